@@ -1,0 +1,286 @@
+"""Benchmark: fused BiGEMM forward (RMSNorm prologue + residual epilogue) on one MI355X.
+
+Workload (one step): the four OmniWeave-T stage shapes 56x56x128 (d=64), 28x28x256 (d=64),
+14x14x512 (d=128), 7x7x1024 (d=128) at batch 128, each with the local, shifted-by-half-window
+and radix (level 1: strided tokens + rotated channel groups) routes: 12 launches of the fused
+kernel, bf16 in/out, fp32 accumulate, RMSNorm weight 1 and LayerScale 1.  Inputs and packed
+weights are resident in HBM before timing; a step is replayed from a HIP graph.
+
+Prints ONE JSON line.  ``value`` = algorithmic TFLOP/s of the whole step (cheapest
+association, F_tile = 6 g d (g + rd) per 16-token x d-channel tile, pad rows included);
+``roofline`` is for the kernel with the largest share of the step time; ``cpu_baseline`` is the
+oracle (the reference backend's algorithm, fp32, PyTorch on the host CPU) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+G = 16
+STAGES = [  # name, H, W, C, d
+    ("s1_56x56x128", 56, 56, 128, 64),
+    ("s2_28x28x256", 28, 28, 256, 64),
+    ("s3_14x14x512", 14, 14, 512, 128),
+    ("s4_7x7x1024", 7, 7, 1024, 128),
+]
+ROUTES = [("local", 0), ("shifted", 0), ("radix", 1)]
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def tile_flops(d: int, rd: int) -> int:
+    return 6 * G * d * (G + rd)
+
+
+def case_work(batch, h, w, c, d, rd=None, elem=2):
+    """(algorithmic flops, algorithmic HBM bytes) of one fused launch."""
+    rd = rd or 2 * d
+    q_s = math.ceil(h * w / G)
+    q_c = math.ceil(c / d)
+    flops = batch * q_s * q_c * tile_flops(d, rd)
+    weights = (3 * G * G + 3 * q_c * d * rd + 2 * c) * elem
+    nbytes = batch * h * w * c * 2 * elem + weights
+    return flops, nbytes
+
+
+def make_inputs(batch, h, w, c, d, route, level, dev, seed):
+    import omniwave_amd
+
+    gen = torch.Generator().manual_seed(seed)
+    rd = 2 * d
+    plan = omniwave_amd.build_route_plan(h, w, c, G, d, route, level)
+    q_c = plan.channel_indices.shape[0]
+    x = torch.randn(batch, h, w, c, generator=gen).to(torch.bfloat16)
+    p = dict(
+        a_u=torch.randn(G, G, generator=gen) / 4, a_v=torch.randn(G, G, generator=gen) / 4,
+        a_o=torch.randn(G, G, generator=gen) / 4,
+        b_u=torch.randn(q_c, d, rd, generator=gen) / math.sqrt(d),
+        b_v=torch.randn(q_c, d, rd, generator=gen) / math.sqrt(d),
+        b_o=torch.randn(q_c, rd, d, generator=gen) / math.sqrt(rd),
+        gamma=torch.ones(c),
+    )
+    p = {k: v.to(torch.bfloat16).to(dev) for k, v in p.items()}
+    return plan, x.to(dev), p, torch.ones(c, dtype=torch.bfloat16, device=dev)
+
+
+def time_graph(graph, replays: int) -> float:
+    """Average ms per replay, HIP events on the current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / replays
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """Oracle (reference backend algorithm, fp32) on the host: every stage x route at batch 8."""
+    from oracle.bigemm import block_reference
+    from oracle.routing import build_route_plan as oracle_plan
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    batch = 8
+    flops_total = 0
+    secs_total = 0.0
+    t_begin = time.perf_counter()
+    cases = 0
+    for (_, h, w, c, d) in STAGES:
+        for (route, level) in ROUTES:
+            gen = torch.Generator().manual_seed(1)
+            plan = oracle_plan(h, w, c, G, d, route, level)
+            q_c = plan.channel_indices.shape[0]
+            params = dict(
+                norm_weight=torch.ones(c), a_u=torch.randn(G, G, generator=gen) / 4,
+                a_v=torch.randn(G, G, generator=gen) / 4, a_o=torch.randn(G, G, generator=gen) / 4,
+                b_u=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
+                b_v=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
+                b_o=torch.randn(q_c, 2 * d, d, generator=gen) / math.sqrt(2 * d), gamma=torch.ones(c),
+            )
+            x = torch.randn(batch, h, w, c, generator=gen)
+            with torch.inference_mode():
+                block_reference(x, plan, params)  # warmup
+                times = []
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    block_reference(x, plan, params)
+                    times.append(time.perf_counter() - t0)
+            times.sort()
+            secs_total += times[1]
+            flops_total += case_work(batch, h, w, c, d)[0]
+            cases += 1
+            if time.perf_counter() - t_begin > budget_s:
+                break
+        if time.perf_counter() - t_begin > budget_s:
+            break
+    return {
+        "value": round(flops_total / secs_total / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle fused block (RMSNorm + pack/einsum/unpack + residual), fp32, batch {batch}, "
+                  f"{cases} of 12 stage x route cases, median of 3 after 1 warmup",
+    }
+
+
+def load_traffic(kernel_case: str) -> int | None:
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), if present."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return int(json.loads(path.read_text())[kernel_case]["hbm_bytes_per_launch"])
+    except (KeyError, ValueError, TypeError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=128)
+    ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the BiGEMM path is data-parallel over images and needs no exchange)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from omniwave_amd import _native
+    from omniwave_amd.hip import bigemm_block_hip
+
+    if _native.load_error() is not None:
+        raise RuntimeError(_native.load_error())
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    cases = []
+    for (name, h, w, c, d) in STAGES:
+        for (route, level) in ROUTES:
+            plan, x, p, nw = make_inputs(args.batch, h, w, c, d, route, level, dev, seed=len(cases))
+            fn = (lambda x=x, nw=nw, plan=plan, p=p: bigemm_block_hip(x, nw, plan, **p))
+            flops, nbytes = case_work(args.batch, h, w, c, d)
+            cases.append(dict(name=f"{name}_{route}{level}", stage=name, d=d, fn=fn, flops=flops, bytes=nbytes))
+
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        for cs in cases:  # pack weights (cached), upload route tables
+            cs["fn"]()
+        torch.cuda.synchronize()
+        setup_ms = (time.perf_counter() - t0) * 1e3
+
+        # Per-case kernel time: graphs of 20 back-to-back launches.
+        per_launch = 20
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        for cs in cases:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(stream):
+                cs["fn"]()
+                torch.cuda.current_stream().synchronize()
+                with torch.cuda.graph(g, stream=stream):
+                    for _ in range(per_launch):
+                        cs["out"] = cs["fn"]()
+            torch.cuda.current_stream().wait_stream(stream)
+            time_graph(g, 3)
+            cs["ms"] = time_graph(g, 10) / per_launch
+            cs["graph"] = g
+
+        # One step = all 12 launches, replayed from one graph.
+        step_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(step_graph, stream=stream):
+                for cs in cases:
+                    cs["fn"]()
+        torch.cuda.current_stream().wait_stream(stream)
+
+        def step():
+            if args.eager:
+                for cs in cases:
+                    cs["fn"]()
+            else:
+                step_graph.replay()
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            step()
+        stop.record()
+        torch.cuda.synchronize()
+        ms_per_step = start.elapsed_time(stop) / args.steps
+
+    total_flops = sum(cs["flops"] for cs in cases)
+    value = total_flops / (ms_per_step * 1e-3) / 1e12
+    stages = {}
+    for cs in cases:
+        tflops = cs["flops"] / (cs["ms"] * 1e-3) / 1e12
+        gbs = cs["bytes"] / (cs["ms"] * 1e-3) / 1e9
+        bound = "hbm" if cs["d"] == 64 else "mfma"
+        frac = gbs / PEAK_HBM_GBS if bound == "hbm" else tflops / PEAK_BF16_TFLOPS
+        stages[cs["name"]] = {"us": round(cs["ms"] * 1e3, 2), "tflops": round(tflops, 1), "gbs": round(gbs, 1),
+                              "bound": bound, "frac": round(frac, 4)}
+    dom = max(cases, key=lambda cs: cs["ms"])
+    dom_bound = "hbm" if dom["d"] == 64 else "mfma"
+    if dom_bound == "hbm":
+        achieved, peak, unit = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    else:
+        achieved, peak, unit = dom["flops"] / (dom["ms"] * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+    roofline = {
+        "bound": dom_bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+        "frac": round(achieved / peak, 4), "traffic": load_traffic(dom["name"]),
+        "kernel": "bigemm_fwd_kernel", "case": dom["name"],
+        "algorithmic_flops": dom["flops"], "algorithmic_bytes": dom["bytes"],
+    }
+    baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
+    line = {
+        "metric": "BiGEMM fwd TFLOP/s (fused RMSNorm+residual, 4 OmniWeave-T stage shapes x 3 routes)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,1/fan_in) weights)",
+        "config": {"workload": "bigemm_fwd_fused_stages_x_routes", "batch": args.batch,
+                   "stages": [s[0] for s in STAGES], "routes": [f"{r}{l}" for r, l in ROUTES],
+                   "launch": "eager" if args.eager else "hip_graph", "setup_ms": round(setup_ms, 1)},
+        "per_case": stages,
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,128 @@
+/*
+ * omniwave_amd — C ABI of the MI355X (gfx950) BiGEMM backend.
+ *
+ * Plain pointers and sizes only.  Every device pointer is caller-owned memory on the current
+ * HIP device; the library never allocates or frees caller memory.  Launches are asynchronous
+ * on the `stream` argument (a hipStream_t passed as void*; NULL = the null stream).  Every
+ * entry point returns OW_OK (0) or an error code; ow_last_error() returns the message of the
+ * calling thread's most recent failure.
+ *
+ * The upstream reference (QuackPhuc/omniwave) is pure Python; the interfaces each entry point
+ * replaces are cited as reference file:line.
+ */
+#ifndef OMNIWAVE_AMD_H
+#define OMNIWAVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define OW_OK 0
+#define OW_ERR_INVALID 1     /* bad argument (null pointer, negative size, inconsistent shape) */
+#define OW_ERR_UNSUPPORTED 2 /* shape/dtype outside the kernel envelope */
+#define OW_ERR_HIP 3         /* HIP runtime error (message names the call) */
+
+/* Route kinds: the `route` strings of omniweave/models/routing.py:152-159. */
+#define OW_ROUTE_LOCAL 0
+#define OW_ROUTE_SHIFTED 1
+#define OW_ROUTE_RADIX 2
+
+/* Element types. */
+#define OW_DTYPE_F32 0
+#define OW_DTYPE_BF16 1
+#define OW_DTYPE_F16 2
+
+/* Fusion flags of ow_bigemm_fwd. */
+#define OW_FUSE_NORM 1     /* x is raw; apply the block's RMSNorm (omniweave/models/block.py:83-85) */
+#define OW_FUSE_RESIDUAL 2 /* write x + delta instead of delta (omniweave/models/block.py:108) */
+
+/*
+ * Route plan descriptor: the arguments of build_route_plan
+ * (omniweave/models/routing.py:128-137) plus the window/shift constants that
+ * _local_token_order / _shifted_token_order hard-code (routing.py:57,71-72).
+ */
+typedef struct OwPlan {
+  int32_t height;
+  int32_t width;
+  int32_t channels;
+  int32_t spatial_tile; /* g */
+  int32_t channel_tile; /* d */
+  int32_t route;        /* OW_ROUTE_* */
+  int32_t radix_level;
+  int32_t window;       /* 4 in the reference */
+  int32_t shift;        /* 2 in the reference */
+} OwPlan;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ow_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* ow_last_error(void);
+
+/*
+ * Q_s = ceil(H*W / g) token groups and Q_c = ceil(C / d) channel groups of a plan
+ * (the shapes of RoutePlan.token_indices / channel_indices, routing.py:25-26).
+ */
+int ow_plan_dims(const OwPlan* plan, int32_t* q_s, int32_t* q_c);
+
+/*
+ * Host-side route tables.  Replaces build_route_plan (omniweave/models/routing.py:128-179):
+ * writes token_index[Q_s*g] (pad = H*W) and channel_index[Q_c*d] (pad = C), identical to
+ * RoutePlan.token_indices / channel_indices flattened row-major.  The masks are
+ * (index < H*W) and (index < C).
+ */
+int ow_route_build(const OwPlan* plan, int32_t* token_index, int32_t* channel_index);
+
+/*
+ * Size in bytes of the packed weight buffer for q_c channel groups, channel tile d,
+ * expanded tile rd and compute dtype (OW_DTYPE_BF16 / OW_DTYPE_F16 / OW_DTYPE_F32).
+ */
+size_t ow_packed_weight_bytes(int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype);
+
+/*
+ * Pack the block's BiGEMM weights into the MFMA operand order the forward kernel reads.
+ * Replaces the per-call weight pre-cast of the accelerated backend
+ * (omniweave/ops/triton.py:221-230).  a_u/a_v/a_o: [g,g]; b_u/b_v: [q_c,d,rd];
+ * b_o: [q_c,rd,d]; all contiguous, element type weight_dtype (any OW_DTYPE_*).  Values are
+ * rounded (nearest-even) to compute_dtype.  `packed` must hold ow_packed_weight_bytes(...).
+ */
+int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o,
+                    const void* b_u, const void* b_v, const void* b_o,
+                    int32_t weight_dtype, int32_t g, int32_t q_c, int32_t d, int32_t rd,
+                    int32_t compute_dtype, void* packed, void* stream);
+
+/*
+ * Fused BiGEMM forward.  Replaces bigemm(..., backend) (omniweave/ops/bigemm.py:24-73) and,
+ * with flags, the RMSNorm -> bigemm -> residual sequence of OmniWeaveBlock.forward
+ * (omniweave/models/block.py:80-108, eval mode).
+ *
+ *   x, out        [batch, H*W, C] NHWC, element type `dtype` (out may not alias x)
+ *   norm_weight   [C] fp32, read when flags & OW_FUSE_NORM (else may be NULL)
+ *   eps           RMSNorm epsilon (1e-6 in the reference)
+ *   gamma         [C] fp32 LayerScale
+ *   packed        ow_pack_weights output for this (q_c, d, rd, dtype)
+ *   packed_bytes  size of `packed`; must equal ow_packed_weight_bytes(q_c, d, rd, dtype)
+ *   token_index   device copy of ow_route_build's token table [Q_s*g]
+ *   channel_index device copy of ow_route_build's channel table [Q_c*d]
+ *
+ * For every tile (b, q_s, q_c): T = rows token_index[q_s,:] x columns channel_index[q_c,:]
+ * of x (pads read as zero), delta = A_o (SiLU(A_u T B_u) * (A_v T B_v)) B_o scaled per
+ * column by gamma; valid rows/columns are written back to their NHWC positions
+ * (omniweave/ops/reference.py:120-173).  Envelope: g = 16, d in {64,128}, rd in {128,256},
+ * dtype in {bf16, f16, f32}.
+ */
+int ow_bigemm_fwd(const void* x, void* out, const float* norm_weight, float eps,
+                  const float* gamma, const void* packed, size_t packed_bytes,
+                  const int32_t* token_index, const int32_t* channel_index,
+                  const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
+                  int32_t flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNIWAVE_AMD_H */

@@ -1,0 +1,108 @@
+"""OmniWeave block: RMSNorm -> BiGEMM -> residual (omniweave/models/block.py:15-108).
+
+Parameter names, shapes and initialisation match the reference so state_dicts interchange.
+When the resolved backend is ``hip`` the whole block runs as one fused kernel
+(``bigemm_block_hip``); otherwise RMSNorm runs here and ``bigemm`` (a module-level import, so
+callers can patch ``omniwave_amd.block.bigemm``) computes the delta.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from omniwave_amd.bigemm import bigemm
+from omniwave_amd.hip import bigemm_block_hip, hip_is_supported
+from omniwave_amd.routing import RoutePlan, build_route_plan
+
+RMS_EPS = 1e-6  # omniweave/models/block.py:84
+
+
+class OmniWeaveBlock(nn.Module):
+    """One OmniWeave block; owns one route plan and returns ``x + delta``."""
+
+    def __init__(
+        self,
+        height: int,
+        width: int,
+        dim: int,
+        channel_tile: int,
+        route: str,
+        radix_level: int,
+        expansion: int = 2,
+        layer_scale_init: float = 1e-5,
+        spatial_tile: int = 16,
+        backend: str = "auto",
+        drop_path_rate: float = 0.0,
+    ) -> None:
+        super().__init__()
+        if not 0.0 <= drop_path_rate < 1.0:
+            raise ValueError("drop_path_rate must be in [0, 1)")
+        self.height = height
+        self.width = width
+        self.dim = dim
+        self.backend = backend
+        self.drop_path_rate = drop_path_rate
+        g = spatial_tile
+        d = channel_tile
+        rd = d * expansion
+        q_c = math.ceil(dim / d)
+        self.plan: RoutePlan = build_route_plan(height, width, dim, g, d, route, radix_level)
+        self.norm_weight = nn.Parameter(torch.ones(dim))
+        self.a_u = nn.Parameter(torch.empty(g, g))
+        self.a_v = nn.Parameter(torch.empty(g, g))
+        self.a_o = nn.Parameter(torch.empty(g, g))
+        self.b_u = nn.Parameter(torch.empty(q_c, d, rd))
+        self.b_v = nn.Parameter(torch.empty(q_c, d, rd))
+        self.b_o = nn.Parameter(torch.empty(q_c, rd, d))
+        self.gamma = nn.Parameter(torch.full((dim,), layer_scale_init))
+        self._init_weights()
+
+    def _init_weights(self) -> None:
+        """omniweave/models/block.py:72-78."""
+        nn.init.orthogonal_(self.a_u)
+        nn.init.orthogonal_(self.a_v)
+        nn.init.eye_(self.a_o)
+        nn.init.xavier_uniform_(self.b_u)
+        nn.init.xavier_uniform_(self.b_v)
+        nn.init.xavier_uniform_(self.b_o)
+
+    def _fused(self, x: Tensor) -> bool:
+        if self.backend not in ("hip", "auto"):
+            return False
+        ok, reason = hip_is_supported(x, self.plan, self.b_u)
+        if not ok and self.backend == "hip":
+            raise RuntimeError(reason)
+        return ok
+
+    def _drop_path(self, delta: Tensor) -> Tensor:
+        """Per-sample stochastic depth in training (omniweave/models/block.py:99-107)."""
+        keep = 1.0 - self.drop_path_rate
+        shape = (delta.shape[0],) + (1,) * (delta.ndim - 1)
+        mask = torch.empty(shape, dtype=delta.dtype, device=delta.device).bernoulli_(keep)
+        return delta * mask / keep
+
+    def forward(self, x: Tensor) -> Tensor:
+        """``x``: ``[B, H, W, C]`` -> ``[B, H, W, C]``."""
+        params = (self.a_u, self.a_v, self.a_o, self.b_u, self.b_v, self.b_o, self.gamma)
+        dropping = self.training and self.drop_path_rate > 0
+        if self._fused(x):
+            if not dropping:
+                return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS)
+            delta = bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, residual=False)
+            return x + self._drop_path(delta)
+        variance = x.float().square().mean(dim=-1, keepdim=True)
+        normalized = x * torch.rsqrt(variance.to(x.dtype) + RMS_EPS)
+        normalized = (normalized * self.norm_weight).to(x.dtype)
+        delta = bigemm(
+            x=normalized, plan=self.plan,
+            a_u=self.a_u, a_v=self.a_v, a_o=self.a_o,
+            b_u=self.b_u, b_v=self.b_v, b_o=self.b_o,
+            gamma=self.gamma, backend=self.backend,
+        )
+        if dropping:
+            delta = self._drop_path(delta)
+        return x + delta

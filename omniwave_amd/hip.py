@@ -1,0 +1,228 @@
+"""HIP backend of the BiGEMM operator (replaces omniweave/ops/triton.py).
+
+* ``hip_is_supported(x, plan, b_u) -> (bool, reason)`` — same tuple contract as
+  ``triton_is_supported`` (omniweave/ops/triton.py:26-55).
+* ``bigemm_delta_hip`` — drop-in for ``bigemm_delta_triton`` (triton.py:58-85): pre-normalised
+  x in, delta out.
+* ``bigemm_block_hip`` — the fused RMSNorm -> BiGEMM -> residual of OmniWeaveBlock.forward
+  (omniweave/models/block.py:80-108) in one kernel.
+
+Both go through the ``omniwave_amd::bigemm_fwd`` torch.library custom op, whose implementation
+calls ``ow_bigemm_fwd`` of libomniwave_amd.so on the current HIP stream.  Weights are packed
+into MFMA operand order by ``ow_pack_weights`` and cached while the parameter tensors are
+unchanged (same object, same version counter).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import weakref
+from collections import OrderedDict
+
+import torch
+from torch import Tensor
+
+from omniwave_amd import _native
+from omniwave_amd.routing import RoutePlan, build_route_plan, device_tables
+
+SPATIAL_TILE = 16
+CHANNEL_TILES = (64, 128)
+EXPANDED_TILES = (128, 256)
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
+_DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
+               torch.float16: _native.OW_DTYPE_F16}
+_ROUTE_NAME = {v: k for k, v in _native.OW_ROUTE.items()}
+
+
+@functools.lru_cache(maxsize=16)
+def _device_arch(index: int) -> str:
+    return str(torch.cuda.get_device_properties(index).gcnArchName)
+
+
+def hip_is_supported(x: Tensor, plan: RoutePlan, b_u: Tensor) -> tuple[bool, str | None]:
+    """Whether the HIP kernels can run these inputs; ``(False, reason)`` otherwise."""
+    err = _native.load_error()
+    if err is not None:
+        return False, f"native library unavailable: {err}"
+    if not x.is_cuda:
+        return False, "CUDA is unavailable"
+    arch = _device_arch(x.device.index if x.device.index is not None else torch.cuda.current_device())
+    if not arch.startswith("gfx950"):
+        return False, f"device architecture {arch} is not gfx950"
+    if x.dtype not in SUPPORTED_DTYPES:
+        return False, f"unsupported dtype {x.dtype}; expected float16 or bfloat16"
+    g = plan.token_indices.shape[1]
+    if g != SPATIAL_TILE:
+        return False, f"unsupported spatial tile g={g}; expected 16"
+    if b_u.dim() != 3:
+        return False, f"b_u must be [Q_c, d, rd], got shape {tuple(b_u.shape)}"
+    q_c, d, rd = b_u.shape
+    if d not in CHANNEL_TILES:
+        return False, f"unsupported channel tile d={d}; expected 64 or 128"
+    if rd not in EXPANDED_TILES:
+        return False, f"unsupported expanded dim rd={rd}; expected 128 or 256"
+    if x.dim() != 4 or tuple(x.shape[1:]) != (plan.height, plan.width, plan.channels):
+        return False, f"input shape {tuple(x.shape)} does not match the plan ({plan.height}, {plan.width}, {plan.channels})"
+    if plan.channel_indices.shape != (q_c, d):
+        return False, f"plan channel tiles {tuple(plan.channel_indices.shape)} do not match b_u {tuple(b_u.shape)}"
+    return True, None
+
+
+# ---------------------------------------------------------------------------------------
+# Packed weights
+
+
+class _PackEntry:
+    __slots__ = ("refs", "versions", "packed", "gamma", "norm_weight")
+
+
+_PACK_CACHE: OrderedDict[tuple, _PackEntry] = OrderedDict()
+_PACK_CACHE_SIZE = 64
+
+
+def _version(t: Tensor) -> int | None:
+    try:
+        return int(t._version)
+    except RuntimeError:  # inference tensors carry no version counter
+        return None
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype) -> Tensor:
+    """Pack the six BiGEMM weights into the kernel's MFMA operand order (uint8 buffer)."""
+    lib = _native.lib()
+    ws = [a_u, a_v, a_o, b_u, b_v, b_o]
+    wdtype = ws[0].dtype
+    if any(w.dtype != wdtype for w in ws) or wdtype not in _DTYPE_CODE:
+        wdtype = torch.float32
+    ws = [w.detach().to(wdtype).contiguous() for w in ws]
+    q_c, d, rd = b_u.shape
+    if tuple(a_u.shape) != (SPATIAL_TILE, SPATIAL_TILE) or tuple(b_o.shape) != (q_c, rd, d) \
+            or tuple(b_v.shape) != (q_c, d, rd) or a_v.shape != a_u.shape or a_o.shape != a_u.shape:
+        raise ValueError("inconsistent BiGEMM weight shapes: "
+                         f"a_u {tuple(a_u.shape)}, b_u {tuple(b_u.shape)}, b_v {tuple(b_v.shape)}, b_o {tuple(b_o.shape)}")
+    cdt = _DTYPE_CODE[compute_dtype]
+    nbytes = lib.ow_packed_weight_bytes(q_c, d, rd, cdt)
+    if nbytes == 0:
+        raise ValueError(f"unsupported packing shape q_c={q_c}, d={d}, rd={rd}")
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=b_u.device)
+    with torch.cuda.device(b_u.device):
+        _native.check(
+            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], SPATIAL_TILE, q_c, d, rd,
+                                cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
+            "ow_pack_weights",
+        )
+    return packed
+
+
+def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype):
+    srcs = (a_u, a_v, a_o, b_u, b_v, b_o, gamma) + ((norm_weight,) if norm_weight is not None else ())
+    versions = tuple(_version(t) for t in srcs)
+    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype,)
+    entry = _PACK_CACHE.get(key)
+    if (entry is not None and None not in versions and entry.versions == versions
+            and all(r() is t for r, t in zip(entry.refs, srcs))):
+        _PACK_CACHE.move_to_end(key)
+        return entry.packed, entry.gamma, entry.norm_weight
+    entry = _PackEntry()
+    entry.refs = tuple(weakref.ref(t) for t in srcs)
+    entry.versions = versions
+    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype)
+    entry.gamma = gamma.detach().float().contiguous()
+    entry.norm_weight = None if norm_weight is None else norm_weight.detach().float().contiguous()
+    if None not in versions:
+        _PACK_CACHE[key] = entry
+        while len(_PACK_CACHE) > _PACK_CACHE_SIZE:
+            _PACK_CACHE.popitem(last=False)
+    return entry.packed, entry.gamma, entry.norm_weight
+
+
+def clear_pack_cache() -> None:
+    _PACK_CACHE.clear()
+
+
+# ---------------------------------------------------------------------------------------
+# Custom op
+
+
+def _plan_desc(plan: RoutePlan) -> list[int]:
+    return [plan.height, plan.width, plan.channels, plan.spatial_tile, plan.channel_tile,
+            _native.OW_ROUTE[plan.route], plan.radix_level]
+
+
+def _plan_from_desc(desc: list[int]) -> RoutePlan:
+    h, w, c, g, d, route, level = desc
+    return build_route_plan(h, w, c, g, d, _ROUTE_NAME[route], level)
+
+
+@torch.library.custom_op("omniwave_amd::bigemm_fwd", mutates_args=())
+def bigemm_fwd(
+    x: Tensor,
+    norm_weight: Tensor | None,
+    gamma: Tensor,
+    a_u: Tensor,
+    a_v: Tensor,
+    a_o: Tensor,
+    b_u: Tensor,
+    b_v: Tensor,
+    b_o: Tensor,
+    plan_desc: list[int],
+    flags: int,
+    eps: float,
+) -> Tensor:
+    """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC."""
+    plan = _plan_from_desc(plan_desc)
+    x = x.contiguous()
+    packed, gamma32, norm32 = _cached_operands(
+        norm_weight if flags & _native.OW_FUSE_NORM else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype
+    )
+    tok, ch = device_tables(plan, x.device)
+    out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    native_plan = plan.native()
+    with torch.cuda.device(x.device):
+        _native.check(
+            _native.lib().ow_bigemm_fwd(
+                x.data_ptr(), out.data_ptr(), 0 if norm32 is None else norm32.data_ptr(), eps,
+                gamma32.data_ptr(), packed.data_ptr(), packed.numel(), tok.data_ptr(), ch.data_ptr(),
+                ctypes.byref(native_plan), x.shape[0], b_u.shape[2], _DTYPE_CODE[x.dtype], flags,
+                _stream_ptr(x.device),
+            ),
+            "ow_bigemm_fwd",
+        )
+    return out
+
+
+@bigemm_fwd.register_fake
+def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _bigemm_fwd_backward(ctx, grad):
+    raise NotImplementedError("omniwave_amd::bigemm_fwd: the hip backward kernels are not built yet")
+
+
+bigemm_fwd.register_autograd(_bigemm_fwd_backward)
+
+
+def _require(x, plan, b_u) -> None:
+    ok, reason = hip_is_supported(x, plan, b_u)
+    if not ok:
+        raise RuntimeError(f"hip backend not supported: {reason}")
+
+
+def bigemm_delta_hip(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma) -> Tensor:
+    """delta for pre-normalised x (omniweave/ops/reference.py:120-173 semantics)."""
+    _require(x, plan, b_u)
+    return bigemm_fwd(x, None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), 0, 0.0)
+
+
+def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, eps: float = 1e-6,
+                     residual: bool = True) -> Tensor:
+    """RMSNorm(x) -> BiGEMM -> (+ x) fused (omniweave/models/block.py:83-108, no drop-path)."""
+    _require(x, plan, b_u)
+    flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0)
+    return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps))

@@ -1,0 +1,206 @@
+"""GPU parity of the HIP forward against the oracle (run with ``-m gpu`` on a gfx950 GPU).
+
+Tolerances (north-star gates, rel-L2 on the BiGEMM delta, which LayerScale 1e-5 would
+otherwise make vacuous): bf16 <= 1e-2, fp16 <= 5e-3.  The oracle runs on the CPU in fp32 on
+the same inputs, with the weights rounded to the kernel's compute dtype.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from oracle.bigemm import bigemm_delta_reference, block_reference, rel_l2, rmsnorm_reference
+from oracle.routing import build_route_plan as oracle_plan
+import omniwave_amd
+from omniwave_amd.hip import bigemm_block_hip, bigemm_delta_hip
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-3}
+STAGES = {  # (H, W, C, d) of OmniWeave-T at 224 px
+    "s1": (56, 56, 128, 64),
+    "s2": (28, 28, 256, 64),
+    "s3": (14, 14, 512, 128),
+    "s4": (7, 7, 1024, 128),
+}
+ROUTES = [("local", 0), ("shifted", 0), ("radix", 1), ("radix", 2)]
+
+
+def announce(msg: str) -> None:
+    print(f"\n[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+def make_case(b, h, w, c, d, route, level, dtype, seed=0, rd=None, gamma=1.0):
+    """Seeded inputs drawn on the CPU in the order x, a_u, a_v, a_o, b_u, b_v, b_o, norm_w, gamma."""
+    rd = rd or 2 * d
+    gen = torch.Generator().manual_seed(seed)
+    plan = omniwave_amd.build_route_plan(h, w, c, 16, d, route, level)
+    q_c = plan.channel_indices.shape[0]
+    x = torch.randn(b, h, w, c, generator=gen).to(dtype)
+    a = [torch.randn(16, 16, generator=gen) / 4.0 for _ in range(3)]
+    b_u = torch.randn(q_c, d, rd, generator=gen) / d ** 0.5
+    b_v = torch.randn(q_c, d, rd, generator=gen) / d ** 0.5
+    b_o = torch.randn(q_c, rd, d, generator=gen) / rd ** 0.5
+    norm_w = torch.rand(c, generator=gen) + 0.5
+    gam = torch.full((c,), gamma) if isinstance(gamma, float) else gamma
+    params = dict(a_u=a[0], a_v=a[1], a_o=a[2], b_u=b_u, b_v=b_v, b_o=b_o, gamma=gam)
+    return plan, x, params, norm_w
+
+
+def to_dev(params):
+    return {k: v.to(DEV) for k, v in params.items()}
+
+
+def rounded(params, dtype):
+    """Weights as the kernel sees them: rounded to the compute dtype, then fp32."""
+    out = {k: v.to(dtype).float() for k, v in params.items() if k != "gamma"}
+    out["gamma"] = params["gamma"].float()
+    return out
+
+
+def oracle_delta(x, plan, params, dtype):
+    p = rounded(params, dtype)
+    oplan = oracle_plan(plan.height, plan.width, plan.channels, plan.spatial_tile, plan.channel_tile,
+                        plan.route, plan.radix_level)
+    return bigemm_delta_reference(x=x.float(), plan=oplan, **p)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("route,level", ROUTES, ids=[f"{r}{l}" for r, l in ROUTES])
+@pytest.mark.parametrize("stage", list(STAGES))
+def test_delta_matches_oracle(stage, route, level, dtype) -> None:
+    h, w, c, d = STAGES[stage]
+    announce(f"delta stage={stage} route={route}{level} dtype={dtype} B=2 seed=0")
+    plan, x, params, _ = make_case(2, h, w, c, d, route, level, dtype)
+    got = bigemm_delta_hip(x=x.to(DEV), plan=plan, **to_dev(params))
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and got.shape == x.shape
+    ref = oracle_delta(x, plan, params, dtype)
+    err = rel_l2(got.cpu(), ref)
+    assert err <= TOL[dtype], f"rel-L2 {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("route,level", ROUTES, ids=[f"{r}{l}" for r, l in ROUTES])
+@pytest.mark.parametrize("stage", list(STAGES))
+def test_fused_block_matches_oracle(stage, route, level, dtype) -> None:
+    """RMSNorm prologue + BiGEMM + residual epilogue in one kernel, gamma = 1."""
+    h, w, c, d = STAGES[stage]
+    announce(f"fused stage={stage} route={route}{level} dtype={dtype} B=2 seed=1")
+    plan, x, params, norm_w = make_case(2, h, w, c, d, route, level, dtype, seed=1)
+    xd = x.to(DEV)
+    dp = to_dev(params)
+    delta = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp, residual=False)
+    out = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp)
+    torch.cuda.synchronize()
+    normalized = rmsnorm_reference(x, norm_w)  # the reference's dtype sequence, on the CPU
+    ref = oracle_delta(normalized, plan, params, dtype)
+    assert rel_l2(delta.cpu(), ref) <= TOL[dtype]
+    # Residual epilogue: out = round(x + round(delta)) element-wise.
+    expected = (x.float() + delta.cpu().float()).to(dtype)
+    assert torch.equal(out.cpu(), expected)
+
+
+def test_config1_shape_local_bf16() -> None:
+    """x [8,14,14,512] ~ N(0,1), local route, g=16, d=128, A ~ N(0,1/16), B ~ N(0,1/fan_in), seed 0."""
+    announce("config1 x[8,14,14,512] local bf16 seed=0")
+    torch.manual_seed(0)
+    x = torch.randn(8, 14, 14, 512)
+    a = [torch.randn(16, 16) / 4.0 for _ in range(3)]
+    b_u, b_v = torch.randn(4, 128, 256) / 128 ** 0.5, torch.randn(4, 128, 256) / 128 ** 0.5
+    b_o = torch.randn(4, 256, 128) / 256 ** 0.5
+    params = dict(a_u=a[0], a_v=a[1], a_o=a[2], b_u=b_u, b_v=b_v, b_o=b_o, gamma=torch.ones(512))
+    plan = omniwave_amd.build_route_plan(14, 14, 512, 16, 128, "local")
+    xb = x.to(torch.bfloat16)
+    got = bigemm_delta_hip(x=xb.to(DEV), plan=plan, **to_dev(params)).cpu()
+    oplan = oracle_plan(14, 14, 512, 16, 128, "local")
+    ref32 = bigemm_delta_reference(x=x, plan=oplan, **params)  # pure fp32 reference inputs
+    assert rel_l2(got, ref32) <= 1e-2
+
+
+@pytest.mark.parametrize("stage", list(STAGES))
+def test_full_batch_sampled_against_oracle(stage) -> None:
+    """B=128 (the benchmark size): two sampled images against the oracle; batch independence
+    is bitwise (image k alone gives the same bytes as image k inside the batch)."""
+    h, w, c, d = STAGES[stage]
+    announce(f"full-batch stage={stage} B=128 shifted bf16 seed=2")
+    plan, x, params, norm_w = make_case(128, h, w, c, d, "shifted", 0, torch.bfloat16, seed=2)
+    dp = to_dev(params)
+    xd = x.to(DEV)
+    out = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp, residual=False)
+    for k in (0, 77):
+        one = bigemm_block_hip(xd[k:k + 1].contiguous(), norm_w.to(DEV), plan, **dp, residual=False)
+        assert torch.equal(one, out[k:k + 1])
+        ref = oracle_delta(rmsnorm_reference(x[k:k + 1], norm_w), plan, params, torch.bfloat16)
+        assert rel_l2(out[k:k + 1].cpu(), ref) <= 1e-2
+
+
+def test_layer_scale_is_exactly_linear() -> None:
+    """gamma -> 2 gamma doubles every output bit-exactly (power-of-two scaling commutes with rounding)."""
+    announce("linearity s3 radix1 bf16")
+    plan, x, params, norm_w = make_case(4, 14, 14, 512, 128, "radix", 1, torch.bfloat16, seed=3,
+                                        gamma=torch.rand(512) + 0.25)
+    dp = to_dev(params)
+    d1 = bigemm_block_hip(x.to(DEV), norm_w.to(DEV), plan, **dp, residual=False)
+    dp["gamma"] = dp["gamma"] * 2
+    d2 = bigemm_block_hip(x.to(DEV), norm_w.to(DEV), plan, **dp, residual=False)
+    assert torch.equal(d2, d1 * 2)
+
+
+def test_ragged_channels_and_rd_variants() -> None:
+    """C=70 with d=64 (pad channels, scalar gather path) and d=64/rd=256, d=128/rd=128."""
+    for (h, w, c, d, rd, route, level) in [(7, 7, 70, 64, 128, "radix", 1), (9, 9, 128, 64, 256, "local", 0),
+                                          (6, 6, 256, 128, 128, "shifted", 0)]:
+        announce(f"ragged h={h} w={w} c={c} d={d} rd={rd} {route}{level}")
+        plan, x, params, norm_w = make_case(3, h, w, c, d, route, level, torch.bfloat16, seed=4, rd=rd)
+        got = bigemm_delta_hip(x=x.to(DEV), plan=plan, **to_dev(params))
+        assert rel_l2(got.cpu(), oracle_delta(x, plan, params, torch.bfloat16)) <= 1e-2
+        fused = bigemm_block_hip(x.to(DEV), norm_w.to(DEV), plan, **to_dev(params), residual=False)
+        ref = oracle_delta(rmsnorm_reference(x, norm_w), plan, params, torch.bfloat16)
+        assert rel_l2(fused.cpu(), ref) <= 1e-2
+
+
+def test_empty_batch_and_noncontiguous_input() -> None:
+    announce("empty batch + non-contiguous x")
+    plan, x, params, _ = make_case(2, 14, 14, 512, 128, "local", 0, torch.bfloat16, seed=5)
+    dp = to_dev(params)
+    empty = bigemm_delta_hip(x=x[:0].to(DEV), plan=plan, **dp)
+    assert empty.shape == (0, 14, 14, 512)
+    xt = x.to(DEV).transpose(1, 2)  # same shape (H == W), non-contiguous
+    got = bigemm_delta_hip(x=xt, plan=plan, **dp)
+    ref = oracle_delta(x.transpose(1, 2).contiguous(), plan, params, torch.bfloat16)
+    assert rel_l2(got.cpu(), ref) <= 1e-2
+
+
+def test_fp32_weights_and_bf16_weights_agree() -> None:
+    """Weights given in bf16 or fp32 pack to the same operands (rounded to bf16)."""
+    announce("weight dtypes s2 local")
+    plan, x, params, _ = make_case(2, 28, 28, 256, 64, "local", 0, torch.bfloat16, seed=6)
+    dp = to_dev(params)
+    d32 = bigemm_delta_hip(x=x.to(DEV), plan=plan, **dp)
+    dbf = bigemm_delta_hip(x=x.to(DEV), plan=plan, **{k: v.to(torch.bfloat16) for k, v in dp.items()})
+    assert torch.equal(d32, dbf)
+
+
+def test_bigemm_front_door_and_block(oracle_backend) -> None:
+    """bigemm(backend='hip'/'auto') and OmniWeaveBlock on the GPU against the registered oracle."""
+    announce("front door + block s3 radix2")
+    plan, x, params, _ = make_case(2, 14, 14, 512, 128, "radix", 2, torch.bfloat16, seed=7)
+    dp = to_dev(params)
+    xd = x.to(DEV)
+    a = omniwave_amd.bigemm(x=xd, plan=plan, backend="hip", **dp)
+    b = omniwave_amd.bigemm(x=xd, plan=plan, backend="auto", **dp)
+    assert torch.equal(a, b)
+    ref = omniwave_amd.bigemm(x=xd, plan=plan, backend="reference", **{k: v.to(torch.bfloat16) for k, v in dp.items()})
+    assert rel_l2(a.cpu(), ref.cpu()) <= 1e-2
+    block = omniwave_amd.block.OmniWeaveBlock(14, 14, 512, 128, "radix", 2).to(DEV).to(torch.bfloat16).eval()
+    with torch.no_grad():
+        block.gamma.fill_(1.0)
+        fused = block(xd)
+        block.backend = "reference"
+        eager = block(xd)
+    assert rel_l2((fused - xd).cpu(), (eager - xd).cpu()) <= 1e-2
