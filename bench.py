@@ -158,6 +158,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
+    ap.add_argument("--only", default="", help="comma-separated substrings: run only matching cases "
+                    "(profiling aid; the full workload is the default)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -177,8 +179,11 @@ def main() -> int:
     torch.cuda.set_device(dev)
 
     cases = []
+    only = [s for s in args.only.split(",") if s]
     for (name, h, w, c, d) in STAGES:
         for (route, level) in ROUTES:
+            if only and not any(s in f"{name}_{route}{level}" for s in only):
+                continue
             plan, x, p, nw = make_inputs(args.batch, h, w, c, d, route, level, dev, seed=len(cases))
             fn = (lambda x=x, nw=nw, plan=plan, p=p: bigemm_block_hip(x, nw, plan, **p))
             flops, nbytes = case_work(args.batch, h, w, c, d)

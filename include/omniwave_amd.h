@@ -87,39 +87,63 @@ size_t ow_packed_weight_bytes(int32_t q_c, int32_t d, int32_t rd, int32_t comput
  * Pack the block's BiGEMM weights into the MFMA operand order the forward kernel reads.
  * Replaces the per-call weight pre-cast of the accelerated backend
  * (omniweave/ops/triton.py:221-230).  a_u/a_v/a_o: [g,g]; b_u/b_v: [q_c,d,rd];
- * b_o: [q_c,rd,d]; all contiguous, element type weight_dtype (any OW_DTYPE_*).  Values are
- * rounded (nearest-even) to compute_dtype.  `packed` must hold ow_packed_weight_bytes(...).
+ * b_o: [q_c,rd,d]; all contiguous, element type weight_dtype (any OW_DTYPE_*).
+ *
+ * Folded into the packed values (then rounded to compute_dtype, nearest-even):
+ *   B_u rows x -log2(e), B_v rows x -ln(2)   (SiLU evaluated as U'V'/(1 + 2^U'));
+ *   B_u / B_v row c of group q x norm_weight[channel_index[q*d + c]] when norm_weight is
+ *   non-NULL (the block's RMSNorm weight; pad channels get 0).
+ * A buffer packed with norm_weight must be used with OW_FUSE_NORM, one packed without it
+ * without OW_FUSE_NORM.  channel_index: device table of ow_route_build (may be NULL when
+ * norm_weight is NULL).  `packed` must hold ow_packed_weight_bytes(...).
  */
 int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o,
                     const void* b_u, const void* b_v, const void* b_o,
-                    int32_t weight_dtype, int32_t g, int32_t q_c, int32_t d, int32_t rd,
+                    int32_t weight_dtype, const float* norm_weight,
+                    const int32_t* channel_index, int32_t channels,
+                    int32_t g, int32_t q_c, int32_t d, int32_t rd,
                     int32_t compute_dtype, void* packed, void* stream);
+
+/*
+ * RMSNorm row scales: scale[i] = rsqrt(mean_c(x[i, c]^2) + eps) for rows x [rows, channels],
+ * with the reference's rounding points (mean in fp32, then var, var + eps and rsqrt each
+ * rounded to `dtype`; omniweave/models/block.py:83-84).  Replaces the variance/rsqrt part of
+ * OmniWeaveBlock.forward's RMSNorm.
+ */
+int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, float eps,
+                 int32_t dtype, void* stream);
+
+/* Workspace bytes ow_bigemm_fwd needs: batch*H*W fp32 row scales with OW_FUSE_NORM, else 0. */
+size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags);
 
 /*
  * Fused BiGEMM forward.  Replaces bigemm(..., backend) (omniweave/ops/bigemm.py:24-73) and,
  * with flags, the RMSNorm -> bigemm -> residual sequence of OmniWeaveBlock.forward
  * (omniweave/models/block.py:80-108, eval mode).
  *
- *   x, out        [batch, H*W, C] NHWC, element type `dtype` (out may not alias x)
- *   norm_weight   [C] fp32, read when flags & OW_FUSE_NORM (else may be NULL)
- *   eps           RMSNorm epsilon (1e-6 in the reference)
+ *   x, out        [batch, H*W, C] NHWC, element type `dtype` (out may not alias x;
+ *                 both may be NULL when batch == 0, which launches nothing)
+ *   eps           RMSNorm epsilon (1e-6 in the reference), used with OW_FUSE_NORM
  *   gamma         [C] fp32 LayerScale
- *   packed        ow_pack_weights output for this (q_c, d, rd, dtype)
+ *   packed        ow_pack_weights output for this (q_c, d, rd, dtype), packed with the
+ *                 RMSNorm weight exactly when flags has OW_FUSE_NORM
  *   packed_bytes  size of `packed`; must equal ow_packed_weight_bytes(q_c, d, rd, dtype)
  *   token_index   device copy of ow_route_build's token table [Q_s*g]
  *   channel_index device copy of ow_route_build's channel table [Q_c*d]
+ *   workspace     ow_fwd_workspace_bytes(plan, batch, flags) bytes of device memory
  *
  * For every tile (b, q_s, q_c): T = rows token_index[q_s,:] x columns channel_index[q_c,:]
- * of x (pads read as zero), delta = A_o (SiLU(A_u T B_u) * (A_v T B_v)) B_o scaled per
- * column by gamma; valid rows/columns are written back to their NHWC positions
- * (omniweave/ops/reference.py:120-173).  Envelope: g = 16, d in {64,128}, rd in {128,256},
- * dtype in {bf16, f16, f32}.
+ * of x (pads read as zero; RMSNorm-scaled with OW_FUSE_NORM), delta = A_o (SiLU(A_u T B_u) *
+ * (A_v T B_v)) B_o scaled per column by gamma; valid rows/columns are written back to their
+ * NHWC positions (omniweave/ops/reference.py:120-173).  With OW_FUSE_NORM the row scales are
+ * computed first (ow_rms_scale into the workspace), on the same stream.  Envelope: g = 16,
+ * d in {64,128}, rd in {128,256}, dtype in {bf16, f16}.
  */
-int ow_bigemm_fwd(const void* x, void* out, const float* norm_weight, float eps,
-                  const float* gamma, const void* packed, size_t packed_bytes,
+int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma,
+                  const void* packed, size_t packed_bytes,
                   const int32_t* token_index, const int32_t* channel_index,
                   const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
-                  int32_t flags, void* stream);
+                  int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -38,15 +38,22 @@ _SIGNATURES = {
     "ow_packed_weight_bytes": (ctypes.c_size_t, [ctypes.c_int32] * 4),
     "ow_pack_weights": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 6 + [ctypes.c_int32] * 6 + [ctypes.c_void_p, ctypes.c_void_p],
+        [ctypes.c_void_p] * 6 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]
+        + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],
     ),
+    "ow_rms_scale": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_int32,
+         ctypes.c_void_p],
+    ),
+    "ow_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32]),
     "ow_bigemm_fwd": (
         ctypes.c_int,
         [
-            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
-            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
             ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-            ctypes.c_int32, ctypes.c_void_p,
+            ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ],
     ),
 }

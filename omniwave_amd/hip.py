@@ -74,7 +74,7 @@ def hip_is_supported(x: Tensor, plan: RoutePlan, b_u: Tensor) -> tuple[bool, str
 
 
 class _PackEntry:
-    __slots__ = ("refs", "versions", "packed", "gamma", "norm_weight")
+    __slots__ = ("refs", "versions", "packed", "gamma")
 
 
 _PACK_CACHE: OrderedDict[tuple, _PackEntry] = OrderedDict()
@@ -92,8 +92,13 @@ def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype) -> Tensor:
-    """Pack the six BiGEMM weights into the kernel's MFMA operand order (uint8 buffer)."""
+def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_weight: Tensor | None = None,
+                 plan: RoutePlan | None = None) -> Tensor:
+    """Pack the six BiGEMM weights into the kernel's MFMA operand order (uint8 buffer).
+
+    With ``norm_weight`` (and the block's ``plan``, whose channel table routes it), the
+    RMSNorm weight is folded into the B_u / B_v rows, as OW_FUSE_NORM expects.
+    """
     lib = _native.lib()
     ws = [a_u, a_v, a_o, b_u, b_v, b_o]
     wdtype = ws[0].dtype
@@ -110,35 +115,42 @@ def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype) -> Te
     if nbytes == 0:
         raise ValueError(f"unsupported packing shape q_c={q_c}, d={d}, rd={rd}")
     packed = torch.empty(nbytes, dtype=torch.uint8, device=b_u.device)
+    nw_ptr = ch_ptr = 0
+    channels = q_c * d
+    if norm_weight is not None:
+        if plan is None:
+            raise ValueError("folding norm_weight needs the block's route plan")
+        nw = norm_weight.detach().to(device=b_u.device, dtype=torch.float32).contiguous()
+        ch = device_tables(plan, b_u.device)[1]
+        nw_ptr, ch_ptr, channels = nw.data_ptr(), ch.data_ptr(), plan.channels
     with torch.cuda.device(b_u.device):
         _native.check(
-            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], SPATIAL_TILE, q_c, d, rd,
-                                cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
+            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], nw_ptr, ch_ptr, channels,
+                                SPATIAL_TILE, q_c, d, rd, cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
             "ow_pack_weights",
         )
     return packed
 
 
-def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype):
+def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, plan: RoutePlan):
     srcs = (a_u, a_v, a_o, b_u, b_v, b_o, gamma) + ((norm_weight,) if norm_weight is not None else ())
     versions = tuple(_version(t) for t in srcs)
-    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype,)
+    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype, plan.key())
     entry = _PACK_CACHE.get(key)
     if (entry is not None and None not in versions and entry.versions == versions
             and all(r() is t for r, t in zip(entry.refs, srcs))):
         _PACK_CACHE.move_to_end(key)
-        return entry.packed, entry.gamma, entry.norm_weight
+        return entry.packed, entry.gamma
     entry = _PackEntry()
     entry.refs = tuple(weakref.ref(t) for t in srcs)
     entry.versions = versions
-    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype)
+    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, norm_weight, plan)
     entry.gamma = gamma.detach().float().contiguous()
-    entry.norm_weight = None if norm_weight is None else norm_weight.detach().float().contiguous()
     if None not in versions:
         _PACK_CACHE[key] = entry
         while len(_PACK_CACHE) > _PACK_CACHE_SIZE:
             _PACK_CACHE.popitem(last=False)
-    return entry.packed, entry.gamma, entry.norm_weight
+    return entry.packed, entry.gamma
 
 
 def clear_pack_cache() -> None:
@@ -177,19 +189,24 @@ def bigemm_fwd(
     """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC."""
     plan = _plan_from_desc(plan_desc)
     x = x.contiguous()
-    packed, gamma32, norm32 = _cached_operands(
-        norm_weight if flags & _native.OW_FUSE_NORM else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype
+    fuse_norm = bool(flags & _native.OW_FUSE_NORM)
+    if fuse_norm and norm_weight is None:
+        raise ValueError("OW_FUSE_NORM needs norm_weight")
+    packed, gamma32 = _cached_operands(
+        norm_weight if fuse_norm else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan
     )
     tok, ch = device_tables(plan, x.device)
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     native_plan = plan.native()
+    lib = _native.lib()
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), x.shape[0], flags)
+    workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
         _native.check(
-            _native.lib().ow_bigemm_fwd(
-                x.data_ptr(), out.data_ptr(), 0 if norm32 is None else norm32.data_ptr(), eps,
-                gamma32.data_ptr(), packed.data_ptr(), packed.numel(), tok.data_ptr(), ch.data_ptr(),
-                ctypes.byref(native_plan), x.shape[0], b_u.shape[2], _DTYPE_CODE[x.dtype], flags,
-                _stream_ptr(x.device),
+            lib.ow_bigemm_fwd(
+                x.data_ptr(), out.data_ptr(), eps, gamma32.data_ptr(), packed.data_ptr(), packed.numel(),
+                tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), x.shape[0], b_u.shape[2],
+                _DTYPE_CODE[x.dtype], flags, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
             ),
             "ow_bigemm_fwd",
         )

@@ -177,13 +177,16 @@ def test_empty_batch_and_noncontiguous_input() -> None:
 
 
 def test_fp32_weights_and_bf16_weights_agree() -> None:
-    """Weights given in bf16 or fp32 pack to the same operands (rounded to bf16)."""
+    """Weights given in bf16 or fp32 both meet the oracle (the packer folds constants before
+    rounding, so bf16 inputs are rounded twice and the two are close, not bit-identical)."""
     announce("weight dtypes s2 local")
     plan, x, params, _ = make_case(2, 28, 28, 256, 64, "local", 0, torch.bfloat16, seed=6)
     dp = to_dev(params)
     d32 = bigemm_delta_hip(x=x.to(DEV), plan=plan, **dp)
     dbf = bigemm_delta_hip(x=x.to(DEV), plan=plan, **{k: v.to(torch.bfloat16) for k, v in dp.items()})
-    assert torch.equal(d32, dbf)
+    ref = oracle_delta(x, plan, params, torch.bfloat16)
+    assert rel_l2(d32.cpu(), ref) <= 1e-2 and rel_l2(dbf.cpu(), ref) <= 1e-2
+    assert rel_l2(d32.cpu(), dbf.cpu()) <= 1e-2
 
 
 def test_bigemm_front_door_and_block(oracle_backend) -> None:
@@ -197,8 +200,12 @@ def test_bigemm_front_door_and_block(oracle_backend) -> None:
     assert torch.equal(a, b)
     ref = omniwave_amd.bigemm(x=xd, plan=plan, backend="reference", **{k: v.to(torch.bfloat16) for k, v in dp.items()})
     assert rel_l2(a.cpu(), ref.cpu()) <= 1e-2
+    # The reference init (xavier on [Q_c, d, rd]) makes delta ~1e-3, below bf16 resolution of
+    # x + delta; O(1)-scale weights and gamma = 1 make the block comparison meaningful.
     block = omniwave_amd.block.OmniWeaveBlock(14, 14, 512, 128, "radix", 2).to(DEV).to(torch.bfloat16).eval()
     with torch.no_grad():
+        for name, value in dp.items():
+            getattr(block, name).copy_(value)
         block.gamma.fill_(1.0)
         fused = block(xd)
         block.backend = "reference"

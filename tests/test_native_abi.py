@@ -61,24 +61,27 @@ def test_packed_weight_bytes() -> None:
 def test_fwd_rejects_bad_arguments_without_touching_the_gpu() -> None:
     lib = _native.lib()
     plan = _native.make_plan(14, 14, 512, 16, 128, "local", 0)
-    rc = lib.ow_bigemm_fwd(None, None, None, 1e-6, None, None, 0, None, None, ctypes.byref(plan), 1, 256,
-                           _native.OW_DTYPE_BF16, 0, None)
-    assert rc == 1 and b"NULL" in lib.ow_last_error()
-    p = ctypes.c_void_p(16)
-    NB = lib.ow_packed_weight_bytes(4, 128, 256, _native.OW_DTYPE_BF16)
-    rc = lib.ow_bigemm_fwd(p, ctypes.c_void_p(32), None, 1e-6, p, p, NB, p, p, ctypes.byref(plan), 1, 256,
-                           _native.OW_DTYPE_BF16, _native.OW_FUSE_NORM, None)
-    assert rc == 1 and b"norm_weight" in lib.ow_last_error()
+    bf16 = _native.OW_DTYPE_BF16
+
+    def fwd(x, out, packed_bytes, p, rd=256, flags=0, ws=None, ws_bytes=0):
+        return lib.ow_bigemm_fwd(x, out, 1e-6, P, P, packed_bytes, P, P, ctypes.byref(p), 1, rd, bf16, flags,
+                                 ws, ws_bytes, None)
+
+    P = None
+    assert fwd(None, None, 0, plan) == 1 and b"NULL" in lib.ow_last_error()
+    P = ctypes.c_void_p(16)
+    NB = lib.ow_packed_weight_bytes(4, 128, 256, bf16)
+    out = ctypes.c_void_p(32)
+    assert fwd(P, out, NB, plan, flags=_native.OW_FUSE_NORM) == 1 and b"workspace" in lib.ow_last_error()
+    assert lib.ow_fwd_workspace_bytes(ctypes.byref(plan), 3, _native.OW_FUSE_NORM) == 3 * 196 * 4
+    assert lib.ow_fwd_workspace_bytes(ctypes.byref(plan), 3, 0) == 0
     bad = _native.make_plan(14, 14, 512, 8, 128, "local", 0)
-    rc = lib.ow_bigemm_fwd(p, ctypes.c_void_p(32), None, 1e-6, p, p, NB, p, p, ctypes.byref(bad), 1, 256,
-                           _native.OW_DTYPE_BF16, 0, None)
-    assert rc == 2 and b"spatial tile" in lib.ow_last_error()
-    rc = lib.ow_bigemm_fwd(p, ctypes.c_void_p(32), None, 1e-6, p, p, NB, p, p, ctypes.byref(plan), 1, 192,
-                           _native.OW_DTYPE_BF16, 0, None)
-    assert rc == 1 and b"rd=192" in lib.ow_last_error()  # packed size cannot match an unsupported rd
-    rc = lib.ow_bigemm_fwd(p, ctypes.c_void_p(32), None, 1e-6, p, p, NB - 2, p, p, ctypes.byref(plan), 1, 256,
-                           _native.OW_DTYPE_BF16, 0, None)
-    assert rc == 1 and b"packed weights" in lib.ow_last_error()
+    assert fwd(P, out, NB, bad) == 2 and b"spatial tile" in lib.ow_last_error()
+    assert fwd(P, out, NB, plan, rd=192) == 1 and b"rd=192" in lib.ow_last_error()
+    assert fwd(P, out, NB - 2, plan) == 1 and b"packed weights" in lib.ow_last_error()
+    assert fwd(P, P, NB, plan) == 1 and b"alias" in lib.ow_last_error()
+    assert lib.ow_rms_scale(None, None, 4, 512, 1e-6, bf16, None) == 1
+    assert lib.ow_rms_scale(None, None, 0, 512, 1e-6, bf16, None) == 0  # empty: nothing launched
 
 
 def test_hip_is_supported_reasons_on_cpu() -> None:
