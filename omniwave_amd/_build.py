@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -18,7 +19,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libomniwave_amd.so"
-SOURCES = ["route.cpp", "bigemm_fwd.hip"]
+SOURCES = ["route.cpp", "bigemm_fwd.hip", "bigemm_fwd_resident.hip"]
 ARCH = "gfx950"
 
 
@@ -39,6 +40,9 @@ def compile_flags() -> list[str]:
         "-Wno-unused-function",
         # Packed-FP32 VALU ops stay off: scalar float code only.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: the SiLU and epilogue read them with VALU instructions,
+        # and values only MFMAs read (resident weights) go to AGPRs instead.
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
     ]
@@ -48,14 +52,14 @@ def build(verbose: bool = False) -> Path:
     """Compile every source into LIB_PATH (always recompiles); returns the library path."""
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="ow_build_") as tmp:
-        objs = []
-        for src in SOURCES:
-            obj = Path(tmp) / (Path(src).stem + ".o")
-            cmd = [cc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)]
-            if verbose:
+        objs = [str(Path(tmp) / (Path(src).stem + ".o")) for src in SOURCES]
+        cmds = [[cc, *compile_flags(), "-c", str(CSRC / src), "-o", obj] for src, obj in zip(SOURCES, objs)]
+        if verbose:
+            for cmd in cmds:
                 print(" ".join(cmd), flush=True)
-            _run(cmd)
-            objs.append(str(obj))
+        with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+            for fut in [pool.submit(_run, cmd) for cmd in cmds]:
+                fut.result()
         out_tmp = Path(tmp) / LIB_PATH.name
         cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(out_tmp)]
         if verbose:

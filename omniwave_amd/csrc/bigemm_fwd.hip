@@ -11,15 +11,8 @@
 // B_u' = -log2(e) B_u, B_v' = -ln(2) B_v give U' = -log2(e) U, V' = -ln(2) V and
 //     SiLU(U) V = U V / (1 + e^-U) = U' V' / (1 + 2^U').
 //
-// MFMA layouts (64 lanes; l16 = lane % 16, h = lane / 16, l32 = lane % 32, hh = lane / 32):
-//   16x16 accumulator        lane holds D[4h + i][l16], i = 0..3
-//   16x16x16 A / B operand   lane holds A[l16][4h + j] / B[4h + j][l16], j = 0..3
-//   32x32 accumulator        lane holds D[8(i/4) + 4hh + i%4][l32], i = 0..15
-//   32x32x16 A / B operand   lane holds 8 K-slots j = 0..7 of row / column l32 for K half hh
-// Only the pairing of A slot (hh, j) with B slot (hh, j) is fixed by the hardware, so each
-// operand may use any K order as long as both sides agree.  All products are computed
-// transposed (tokens on the MFMA N axis) so every result feeds the next contraction from
-// registers:
+// All products are computed transposed (tokens on the MFMA N axis, layouts in ow_device.h) so
+// every result feeds the next contraction from registers:
 //     P^T  = X^T . (A diag r)^T  16x16x16 per token group (K = 16 tokens), X^T from LDS;
 //            two groups' results are merged into one 32-token B operand by a lane exchange
 //     U'^T = B_u'^T . P_u^T      32x32x16 (K = channels, N = 32 tokens), weights from LDS
@@ -32,121 +25,15 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
-#include "ow_common.h"
+#include "ow_device.h"
 
 namespace ow {
 namespace {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kG = 16;        // spatial tile (tokens per group)
 constexpr int kWaves = 4;     // waves per workgroup
 constexpr int kThreads = 256;
-constexpr int kTokFragElems = 256;             // 16x16x16 operand: 64 lanes x 4
-constexpr int kHeadElems = 3 * kTokFragElems;  // A_u^T, A_v^T, A_o at the head of `packed`
-constexpr int kFragElems = 512;                // 32x32x16 operand: 64 lanes x 8
-constexpr float kNegLog2e = -1.4426950408889634f;
-constexpr float kNegLn2 = -0.6931471805599453f;
-
-struct BF16 {
-  static __device__ __forceinline__ uint16_t from_f32(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
-  }
-  static __device__ __forceinline__ float to_f32(uint16_t u) {
-    return __uint_as_float(static_cast<uint32_t>(u) << 16);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
-  }
-  // a.lo^2 + a.hi^2 + acc in fp32
-  static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
-    const bf16x2 v = __builtin_bit_cast(bf16x2, a);
-    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
-  }
-  static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
-                                                     __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
-  }
-};
-
-struct F16 {
-  static __device__ __forceinline__ uint16_t from_f32(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-  }
-  static __device__ __forceinline__ float to_f32(uint16_t u) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, u));
-  }
-  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
-  }
-  static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
-    const f16x2 v = __builtin_bit_cast(f16x2, a);
-    return __builtin_amdgcn_fdot2(v, v, acc, false);
-  }
-  static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
-                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
-  }
-};
-
-template <class Ty>
-__device__ __forceinline__ float round_to(float f) {
-  return Ty::to_f32(Ty::from_f32(f));
-}
-
-// RMSNorm row scale with the reference's dtype sequence (omniweave/models/block.py:83-84):
-// var (fp32) -> x.dtype, + eps in x.dtype, rsqrt in x.dtype.
-template <class Ty>
-__device__ __forceinline__ float rms_scale(float mean_sq, float eps) {
-  const float v = round_to<Ty>(round_to<Ty>(mean_sq) + eps);
-  return round_to<Ty>(rsqrtf(v));
-}
-
-// SiLU(U) V from the folded accumulators U' = -log2(e) U, V' = -ln(2) V.
-__device__ __forceinline__ float silu_gate(float up, float vp) {
-  return up * vp * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(up));
-}
-
-// Separates MFMA results from VALU reads of them by 32 wait states.  Used where the read
-// follows the MFMA across a basic-block boundary (loop exit), or where many accumulator
-// registers are read at once: the hardware does not interlock an MFMA's result against a
-// later VALU read, and a read a few instructions after a 16x16x16 MFMA returns the old value
-// of its last accumulator register.  The scheduling barriers keep the compiler from moving
-// MFMAs or reads across the padding.
-__device__ __forceinline__ void mfma_drain() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Makes this wave's LDS writes visible to its other lanes before they read them.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-__device__ __forceinline__ uint16_t lo16(uint32_t v) { return static_cast<uint16_t>(v & 0xffffu); }
-__device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16_t>(v >> 16); }
 
 // ---------------------------------------------------------------------------------------
 // RMSNorm row scales: scale[row] = rsqrt(mean(x[row]^2) + eps) in the reference's dtype
@@ -225,8 +112,34 @@ struct FwdArgs {
   int32_t batch, n_tok, channels, q_s, q_c;
   int32_t n_chunks;  // ceil(batch * q_s / token groups per workgroup)
   int32_t residual;  // write x + delta instead of delta
-  int32_t gather;    // element-wise channel gather/scatter (rotated or padded channel groups)
+  int32_t mode;      // channel-group access, one of the kMode* values
+  int32_t stride;    // kModeStrided: channel stride n of a group (= q_c)
 };
+
+// Channel-group access modes.
+//   kModeContig   group qc is columns [qc*d, qc*d + d): 16-byte row vectors (radix level 0)
+//   kModeStrided  group qc is columns res + k*n, k < d, n = q_c in {2, 4, 8}, C = n*d (radix
+//                 levels >= 1, omniweave/models/routing.py:107-121): every 16-byte vector of
+//                 a row holds 8/n consecutive tile columns of the group
+//   kModeElement  anything else (padded groups, unaligned or ragged rows): element access
+constexpr int kModeContig = 0;
+constexpr int kModeStrided = 1;
+constexpr int kModeElement = 2;
+constexpr int kBatch = 16;  // global loads kept in flight per thread by the gather / scatter loops
+
+// The M = 8/n elements of a strided channel group held by one 16-byte row vector: element
+// index res + t*n for t < M (res < n is the group's first channel), each in the low 16 bits.
+template <int M>
+__device__ __forceinline__ void strided_elems(const u32x4& v, int res, uint32_t (&e)[M]) {
+  constexpr int N = 8 / M;
+  const uint32_t sh = 16u * static_cast<uint32_t>(res & 1);
+#pragma unroll
+  for (int t = 0; t < M; ++t) {
+    const int w = (res + t * N) >> 1;
+    const uint32_t word = w == 0 ? v[0] : w == 1 ? v[1] : w == 2 ? v[2] : v[3];
+    e[t] = (word >> sh) & 0xffffu;
+  }
+}
 
 // Maps the hardware workgroup id to a logical id so that the q_c workgroups of one row chunk
 // run on the same XCD (workgroups are dispatched round-robin over the 8 XCDs): their gathers
@@ -275,8 +188,6 @@ bigemm_fwd_kernel(FwdArgs a) {
   __shared__ int32_t chx[D];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l16 = lane & 15, h = lane >> 4;
-  const int tau = (lane >> 4) & 1;  // which token group of a pair this lane's MFMA column is in
 
   const int bid = xcd_remap(blockIdx.x, a.n_chunks * a.q_c);
   const int qc = bid % a.q_c, chunk = bid / a.q_c;
@@ -290,17 +201,17 @@ bigemm_fwd_kernel(FwdArgs a) {
   };
   issue_chunk(0);
 
-  for (int r = tid; r < ROWS; r += kThreads) {
-    const int64_t tg = static_cast<int64_t>(chunk) * R + r / kG;
+  static_assert(ROWS <= kThreads, "one row id per thread");
+  if (tid < ROWS) {
+    const int64_t tg = static_cast<int64_t>(chunk) * R + tid / kG;
     int32_t id = -1;
     if (tg < static_cast<int64_t>(a.batch) * a.q_s) {
       const int32_t b = static_cast<int32_t>(tg / a.q_s);
       const int32_t s = static_cast<int32_t>(tg - static_cast<int64_t>(b) * a.q_s);
-      const int32_t t = a.tok[s * kG + (r % kG)];
+      const int32_t t = a.tok[s * kG + (tid % kG)];
       if (t >= 0 && t < a.n_tok) id = b * a.n_tok + t;
     }
-    rowid[r] = id;
-    rsc[r] = (id >= 0 && a.row_scale) ? a.row_scale[id] : 1.0f;
+    rowid[tid] = id;
   }
   for (int k = tid; k < D; k += kThreads) {
     const int c = a.chan[qc * D + k];
@@ -310,8 +221,15 @@ bigemm_fwd_kernel(FwdArgs a) {
   }
   __syncthreads();
 
-  // x tile [ROWS x D] into LDS (pad rows / columns read as zero).
-  if (!a.gather) {
+  // Row scales and the x tile [ROWS x D] into LDS (pad rows / columns read as zero); the
+  // row-scale loads are in flight together with the tile loads.
+  const int strided_res = __builtin_amdgcn_readfirstlane(chx[0]) & (a.stride - 1);
+  float my_rsc = 1.0f;
+  if (tid < ROWS && a.row_scale) {
+    const int64_t id = rowid[tid];
+    if (id >= 0) my_rsc = a.row_scale[id];
+  }
+  if (a.mode == kModeContig) {
     constexpr int VPR = D / 8;
     constexpr int NV = ROWS * VPR / kThreads;
     u32x4 v[NV];
@@ -327,70 +245,89 @@ bigemm_fwd_kernel(FwdArgs a) {
       const int idx = tid + i * kThreads;
       *reinterpret_cast<u32x4*>(&xs[(idx / VPR) * LDX + (idx % VPR) * 8]) = v[i];
     }
+  } else if (a.mode == kModeStrided) {
+    // Full-row 16-byte vectors; vector v of a row holds tile columns [M v, M v + M).
+    auto gather_strided = [&](auto m_tag) {
+      constexpr int M = decltype(m_tag)::value;
+      constexpr int VPR = D / M;  // vectors per row: C / 8 = n d / 8
+      constexpr int NV = ROWS * VPR / kThreads;
+      constexpr int NB = NV < kBatch ? NV : kBatch;
+      static_assert(NV % NB == 0, "whole batches");
+#pragma unroll 1
+      for (int i0 = 0; i0 < NV; i0 += NB) {
+        u32x4 v[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int idx = tid + (i0 + j) * kThreads;
+          const int64_t id = rowid[idx / VPR];
+          v[j] = u32x4{0u, 0u, 0u, 0u};
+          if (id >= 0) v[j] = *reinterpret_cast<const u32x4*>(a.x + id * a.channels + (idx % VPR) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int idx = tid + (i0 + j) * kThreads;
+          uint32_t e[M];
+          strided_elems<M>(v[j], strided_res, e);
+          uint16_t* dst = &xs[(idx / VPR) * LDX + (idx % VPR) * M];
+          if constexpr (M == 4) {
+            *reinterpret_cast<u32x2*>(dst) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+          } else if constexpr (M == 2) {
+            *reinterpret_cast<uint32_t*>(dst) = e[0] | (e[1] << 16);
+          } else {
+            *dst = static_cast<uint16_t>(e[0]);
+          }
+        }
+      }
+    };
+    if (a.stride == 2) gather_strided(std::integral_constant<int, 4>{});
+    else if (a.stride == 4) gather_strided(std::integral_constant<int, 2>{});
+    else gather_strided(std::integral_constant<int, 1>{});
   } else {
-    for (int i = tid; i < ROWS * D; i += kThreads) {
-      const int r = i / D, k = i % D;
-      const int64_t id = rowid[r];
-      const int c = chx[k];
-      xs[r * LDX + k] = (id >= 0 && c >= 0) ? a.x[id * a.channels + c] : static_cast<uint16_t>(0);
+    constexpr int NE = ROWS * D / kThreads;
+    static_assert(NE % kBatch == 0, "whole batches");
+#pragma unroll 1
+    for (int i0 = 0; i0 < NE; i0 += kBatch) {
+      uint16_t v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int i = tid + (i0 + j) * kThreads;
+        const int64_t id = rowid[i / D];
+        const int c = chx[i % D];
+        v[j] = (id >= 0 && c >= 0) ? a.x[id * a.channels + c] : static_cast<uint16_t>(0);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int i = tid + (i0 + j) * kThreads;
+        xs[(i / D) * LDX + i % D] = v[j];
+      }
     }
   }
+  if (tid < ROWS) rsc[tid] = my_rsc;
 
-  const u32x2 fAu = reinterpret_cast<const u32x2*>(a.packed)[lane];
-  const u32x2 fAv = reinterpret_cast<const u32x2*>(a.packed + kTokFragElems)[lane];
-  const u32x2 fAo = reinterpret_cast<const u32x2*>(a.packed + 2 * kTokFragElems)[lane];
+  // Token-operand rows of this lane: A_u, A_v rows for the K step of its token group, A_o row
+  // for the output product.
+  const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
+  const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
+  const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
   __syncthreads();
 
-  // Token side.  For a pair (groups 0, 1) and 16-channel block kb, S_g = 16x16 result of group
-  // g (lane holds channels kb*16 + 4h + i of token l16).  The 32x32x16 B operand wants, in lane
-  // L = 32hh + 16tau + t, channels kb*16 + 8hh + j (j = 0..7) of token t of group tau: slots 0-3
-  // live in lane 32hh + t and slots 4-7 in lane 32hh + 16 + t of S_tau.  A lane of group tau
-  // owns one half and receives the other from lane L ^ 16, which sends its S_(1-tau).
-  const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Token side per pair of groups (32 tokens), block-diagonal 32x32x16 products.
+  const int hh = lane >> 5, l32 = lane & 31;
+  int col[KS / 2];
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) col[cb] = 32 * cb + l32;
   u32x4 Pu[NP][KS], Pv[NP][KS];
+  u32x4 xk[NP][KS / 2][2];  // the lane's x values, kept for the residual
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    u32x2 bu[2], bv[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int row0 = (wave * TPW + 2 * p + g) * kG;
-      bu[g] = fAu;
-      bv[g] = fAv;
-      if (a.row_scale) {  // lane holds A[l16][4h + j]: scale by r of row 4h + j
-        const float r0 = rsc[row0 + 4 * h + 0], r1 = rsc[row0 + 4 * h + 1];
-        const float r2 = rsc[row0 + 4 * h + 2], r3 = rsc[row0 + 4 * h + 3];
-        bu[g] = u32x2{Ty::pack2(Ty::to_f32(lo16(fAu[0])) * r0, Ty::to_f32(hi16(fAu[0])) * r1),
-                      Ty::pack2(Ty::to_f32(lo16(fAu[1])) * r2, Ty::to_f32(hi16(fAu[1])) * r3)};
-        bv[g] = u32x2{Ty::pack2(Ty::to_f32(lo16(fAv[0])) * r0, Ty::to_f32(hi16(fAv[0])) * r1),
-                      Ty::pack2(Ty::to_f32(lo16(fAv[1])) * r2, Ty::to_f32(hi16(fAv[1])) * r3)};
-      }
+    const int row0 = (wave * TPW + 2 * p) * kG;
+    u32x4 bu = fAu, bv = fAv;
+    if (a.row_scale) {  // lane's slots j are tokens 16 tg + kord(j, hh) of its group tg
+      const float* r8 = &rsc[row0 + 16 * ((lane >> 4) & 1) + 4 * hh];
+      bu = scale8<Ty>(fAu, r8);
+      bv = scale8<Ty>(fAv, r8);
     }
-#pragma unroll
-    for (int kb = 0; kb < KS; ++kb) {
-      u32x2 su[2], sv[2];
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int row0 = (wave * TPW + 2 * p + g) * kG;
-        const int k = kb * 16 + l16;
-        const uint32_t e0 = xs[(row0 + 4 * h + 0) * LDX + k];
-        const uint32_t e1 = xs[(row0 + 4 * h + 1) * LDX + k];
-        const uint32_t e2 = xs[(row0 + 4 * h + 2) * LDX + k];
-        const uint32_t e3 = xs[(row0 + 4 * h + 3) * LDX + k];
-        const u32x2 av = {e0 | (e1 << 16), e2 | (e3 << 16)};
-        const f32x4 pu = Ty::mma16(av, bu[g], zero4);
-        const f32x4 pv = Ty::mma16(av, bv[g], zero4);
-        su[g] = u32x2{Ty::pack2(pu[0], pu[1]), Ty::pack2(pu[2], pu[3])};
-        sv[g] = u32x2{Ty::pack2(pv[0], pv[1]), Ty::pack2(pv[2], pv[3])};
-      }
-      const u32x2 send_u = tau ? su[0] : su[1], own_u = tau ? su[1] : su[0];
-      const u32x2 send_v = tau ? sv[0] : sv[1], own_v = tau ? sv[1] : sv[0];
-      const u32x2 recv_u = {static_cast<uint32_t>(__shfl_xor(static_cast<int>(send_u[0]), 16)),
-                            static_cast<uint32_t>(__shfl_xor(static_cast<int>(send_u[1]), 16))};
-      const u32x2 recv_v = {static_cast<uint32_t>(__shfl_xor(static_cast<int>(send_v[0]), 16)),
-                            static_cast<uint32_t>(__shfl_xor(static_cast<int>(send_v[1]), 16))};
-      Pu[p][kb] = tau ? u32x4{recv_u[0], recv_u[1], own_u[0], own_u[1]} : u32x4{own_u[0], own_u[1], recv_u[0], recv_u[1]};
-      Pv[p][kb] = tau ? u32x4{recv_v[0], recv_v[1], own_v[0], own_v[1]} : u32x4{own_v[0], own_v[1], recv_v[0], recv_v[1]};
-    }
+    pair_token_side<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, Pu[p], Pv[p], xk[p]);
   }
 
   // Channel side, streamed over 32-row chunks of the expanded dimension (double-buffered).
@@ -409,114 +346,92 @@ bigemm_fwd_kernel(FwdArgs a) {
     __syncthreads();
     if (ec + 1 < NCH) issue_chunk(ec + 1);
     const uint16_t* cw = chunk_buf(ec);
-    f32x16 U[NP], V[NP];
+    const u32x4* cf = reinterpret_cast<const u32x4*>(cw);
+    auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
+    auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
+    auto fo = [&](int mb, int s) { return cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane]; };
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) U[p][i] = V[p][i] = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 fu = reinterpret_cast<const u32x4*>(cw + ks * kFragElems)[lane];
-      const u32x4 fv = reinterpret_cast<const u32x4*>(cw + (FR_U + ks) * kFragElems)[lane];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        U[p] = Ty::mma32(fu, Pu[p][ks], U[p]);
-        V[p] = Ty::mma32(fv, Pv[p][ks], V[p]);
-      }
-    }
-    // Z^T chunk: accumulator registers 8s..8s+7 are K step s (16 rows) of the next product.
-    u32x4 Z[NP][2];
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          Z[p][s][q] = Ty::pack2(silu_gate(U[p][8 * s + 2 * q], V[p][8 * s + 2 * q]),
-                                 silu_gate(U[p][8 * s + 2 * q + 1], V[p][8 * s + 2 * q + 1]));
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 fo = reinterpret_cast<const u32x4*>(cw + (2 * FR_U + 2 * mb + s) * kFragElems)[lane];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) W[p][mb] = Ty::mma32(fo, Z[p][s], W[p][mb]);
-      }
+    for (int p = 0; p < NP; ++p) pair_chunk<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
   }
 
-  // Output side: each wave stages W^T of a pair into its own 32 rows of xs (transposed to
-  // [token][channel]), computes delta = A_o . W per group with LayerScale, and writes the
-  // rounded delta over the same rows.  W^T lane layout: c = 32mb + 8(i/4) + 4hh + i%4,
-  // token column lane % 32.  No branch separates an MFMA from the reads of its result.
+  // Output side: delta = A_o W per pair (lane = channel 32 mb + l32, registers = tokens) with
+  // LayerScale; the rounded delta, or round(x + delta) with x from the token-side operands, is
+  // written over the pair's own 32 rows of xs.  The barrier first: the odd weight chunks live in
+  // xs.  No branch separates an MFMA from the reads of its result.
   mfma_drain();
-  __syncthreads();  // every wave is done with the last weight chunk
-  const int hh = lane >> 5, l32 = lane & 31;
+  __syncthreads();
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
+    f32x16 dl[MB];
+    pair_output<Ty, MB>(W[p], fAo, lane, dl);
+    mfma_drain();
     uint16_t* st = xs + (wave * TPW + 2 * p) * kG * LDX;
+    if (a.residual) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb) {
+        const float gmv = gm[32 * mb + l32];
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const u32x2 v = {Ty::pack2(W[p][mb][4 * gi + 0], W[p][mb][4 * gi + 1]),
-                         Ty::pack2(W[p][mb][4 * gi + 2], W[p][mb][4 * gi + 3])};
-        *reinterpret_cast<u32x2*>(st + l32 * LDX + mb * 32 + 8 * gi + 4 * hh) = v;
+        for (int i = 0; i < 16; ++i) {
+          const float xv = Ty::to_f32(packed_elem(xk[p][mb][i >> 3], i & 7));
+          st[pair_token_row(i, hh) * LDX + 32 * mb + l32] = Ty::from_f32(xv + round_to<Ty>(dl[mb][i] * gmv));
+        }
       }
-    wave_lds_sync();
+    } else {
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      uint16_t* sg = st + (16 * g) * LDX;
-      f32x4 dl[KS];
+      for (int mb = 0; mb < MB; ++mb) {
+        const float gmv = gm[32 * mb + l32];
 #pragma unroll
-      for (int nb = 0; nb < KS; ++nb) {
-        const int k = nb * 16 + l16;
-        const uint32_t e0 = sg[(4 * h + 0) * LDX + k];
-        const uint32_t e1 = sg[(4 * h + 1) * LDX + k];
-        const uint32_t e2 = sg[(4 * h + 2) * LDX + k];
-        const uint32_t e3 = sg[(4 * h + 3) * LDX + k];
-        const u32x2 bw = {e0 | (e1 << 16), e2 | (e3 << 16)};
-        dl[nb] = Ty::mma16(fAo, bw, zero4);
-      }
-      mfma_drain();  // also orders this group's W reads before the delta writes below
-#pragma unroll
-      for (int nb = 0; nb < KS; ++nb) {
-        const int k = nb * 16 + l16;
-        const float gmv = gm[k];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sg[(4 * h + i) * LDX + k] = Ty::from_f32(dl[nb][i] * gmv);
+        for (int i = 0; i < 16; ++i) st[pair_token_row(i, hh) * LDX + 32 * mb + l32] = Ty::from_f32(dl[mb][i] * gmv);
       }
     }
-    wave_lds_sync();
   }
   __syncthreads();
 
-  // out = round(x + delta) (x re-read from global memory, normally an L2 hit) or delta.
-  if (!a.gather) {
+  // The finished tile to memory.
+  if (a.mode == kModeContig) {
     constexpr int VPR = D / 8;
-    for (int i = tid; i < ROWS * VPR; i += kThreads) {
-      const int r = i / VPR, v = i % VPR;
-      const int64_t id = rowid[r];
-      if (id < 0) continue;
-      u32x4 dv = *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
-      const int64_t off = id * a.channels + qc * D + v * 8;
-      if (a.residual) {
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + off);
+    constexpr int NV = ROWS * VPR / kThreads;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dv[q] = Ty::pack2(Ty::to_f32(lo16(xv[q])) + Ty::to_f32(lo16(dv[q])),
-                            Ty::to_f32(hi16(xv[q])) + Ty::to_f32(hi16(dv[q])));
-      }
-      *reinterpret_cast<u32x4*>(a.out + off) = dv;
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + i * kThreads;
+      const int r = idx / VPR, v = idx % VPR;
+      const int64_t id = rowid[r];
+      if (id >= 0)
+        *reinterpret_cast<u32x4*>(a.out + id * a.channels + qc * D + v * 8) =
+            *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
     }
+  } else if (a.mode == kModeStrided) {
+    // Per 16-byte row vector: M tile columns, stored element by element (the other columns of
+    // the vector belong to other channel groups).
+    auto scatter_strided = [&](auto m_tag) {
+      constexpr int M = decltype(m_tag)::value;
+      constexpr int N = 8 / M;
+      constexpr int VPR = D / M;
+      constexpr int NV = ROWS * VPR / kThreads;
+#pragma unroll 4
+      for (int i = 0; i < NV; ++i) {
+        const int idx = tid + i * kThreads;
+        const int r = idx / VPR, v = idx % VPR;
+        const int64_t id = rowid[r];
+        if (id < 0) continue;
+        const uint16_t* src = &xs[r * LDX + v * M];
+        uint16_t* dst = a.out + id * a.channels + v * 8 + strided_res;
+#pragma unroll
+        for (int t = 0; t < M; ++t) dst[t * N] = src[t];
+      }
+    };
+    if (a.stride == 2) scatter_strided(std::integral_constant<int, 4>{});
+    else if (a.stride == 4) scatter_strided(std::integral_constant<int, 2>{});
+    else scatter_strided(std::integral_constant<int, 1>{});
   } else {
-    for (int i = tid; i < ROWS * D; i += kThreads) {
+    constexpr int NE = ROWS * D / kThreads;
+#pragma unroll 4
+    for (int j = 0; j < NE; ++j) {
+      const int i = tid + j * kThreads;
       const int r = i / D, k = i % D;
       const int64_t id = rowid[r];
       const int c = chx[k];
-      if (id < 0 || c < 0) continue;
-      const int64_t off = id * a.channels + c;
-      const uint16_t dv = xs[r * LDX + k];
-      a.out[off] = a.residual ? Ty::from_f32(Ty::to_f32(a.x[off]) + Ty::to_f32(dv)) : dv;
+      if (id >= 0 && c >= 0) a.out[id * a.channels + c] = xs[r * LDX + k];
     }
   }
 }
@@ -544,24 +459,25 @@ __device__ __forceinline__ float load_f32(const void* p, int64_t i, int dtype) {
   return dtype == OW_DTYPE_BF16 ? BF16::to_f32(u) : F16::to_f32(u);
 }
 
-// Packed order: [A_u^T | A_v^T | A_o] 16x16x16 operands, then per (q, chunk ec): KS B_u'^T
-// fragments, KS B_v'^T fragments, 2*MB B_o^T fragments (32x32x16 A operands, 64 lanes x 8).
-//   B_u'^T / B_v'^T, K step ks: lane l slot j -> row e = 32ec + l32, channel 16ks + 8hh + j
-//                               (the channel order the token-side lane exchange produces)
-//   B_o^T (mb, s):              lane l slot j -> row c = 32mb + l32, expanded index
-//                               32ec + 16s + 8(j/4) + 4hh + j%4 (accumulator rows of U^T)
+// Packed order: three token-operand rows (64 lanes x 8), then per (q, chunk ec): KS B_u'^T
+// fragments, KS B_v'^T fragments, 2*MB B_o fragments (32x32x16 operands, 64 lanes x 8).
+//   A_u / A_v / A_o rows:       lane l slot j -> A[l32 % 16][8(j/4) + 4hh + j%4]
+//   B_u'^T / B_v'^T, K step ks: lane l slot j -> row e = 32ec + l32, channel
+//                               16ks + 8(j/4) + 4hh + j%4 (accumulator rows of P^T)
+//   B_o (mb, s):                lane l slot j -> channel c = 32mb + l32, expanded index
+//                               32ec + 16s + 8(j/4) + 4hh + j%4 (accumulator rows of U'^T)
 template <class Ty>
 __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= p.total) return;
   float val;
   if (idx < kHeadElems) {
-    // Token-side 16x16x16 operands: lane l slot j -> A[l16][4h + j].
-    const int frag = static_cast<int>(idx / kTokFragElems);
-    const int e = static_cast<int>(idx % kTokFragElems);
-    const int lane = e / 4, j = e % 4;
-    const int src = (lane & 15) * kG + 4 * (lane >> 4) + j;
-    val = load_f32(frag == 0 ? p.a_u : frag == 1 ? p.a_v : p.a_o, src, p.wdtype);
+    const int frag = static_cast<int>(idx / kFragElems);
+    const int e = static_cast<int>(idx % kFragElems);
+    const int lane = e / 8, j = e % 8;
+    const int t = lane & 15, hh = lane >> 5;
+    const int k = 8 * (j / 4) + 4 * hh + (j % 4);
+    val = load_f32(frag == 0 ? p.a_u : frag == 1 ? p.a_v : p.a_o, t * kG + k, p.wdtype);
   } else {
     const int ks_n = p.d / 16, mb_n = p.d / 32, nch = p.rd / 32;
     const int64_t ch_elems = static_cast<int64_t>(2 * ks_n + 2 * mb_n) * kFragElems;
@@ -578,7 +494,7 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
       const bool is_u = fr < ks_n;
       const int ks = fr % ks_n;
       const int col = 32 * ec + l32;
-      const int c = 16 * ks + 8 * hh + j;
+      const int c = 16 * ks + 8 * (j / 4) + 4 * hh + (j % 4);
       const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + col;
       float w = 1.0f;
       if (p.norm_w) {
@@ -601,11 +517,6 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
 int64_t packed_elems(int32_t q_c, int32_t d, int32_t rd) {
   const int64_t per_chunk = static_cast<int64_t>(2 * (d / 16) + 2 * (d / 32)) * kFragElems;
   return kHeadElems + static_cast<int64_t>(q_c) * (rd / 32) * per_chunk;
-}
-
-int hip_status(hipError_t e, const char* what) {
-  if (e == hipSuccess) return OW_OK;
-  return fail(OW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
 template <class Ty>
@@ -668,8 +579,6 @@ int dispatch_fwd(const FwdArgs& a, int d, int rd, hipStream_t s) {
   if (d == 128 && rd == 256) return launch_fwd<Ty, 128, 256>(a, s);
   return fail(OW_ERR_UNSUPPORTED, "unsupported channel tile d=%d / expanded dim rd=%d; expected d in {64,128}, rd in {128,256}", d, rd);
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 }  // namespace ow
@@ -770,6 +679,27 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma, const
   OW_CHECK_ARG(workspace_bytes >= need_ws && (need_ws == 0 || workspace),
                "workspace holds %zu bytes; %zu needed", workspace_bytes, need_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) && ow::aligned16(out)) {
+    ow::ResidentArgs r{};
+    r.x = static_cast<const uint16_t*>(x);
+    r.out = static_cast<uint16_t*>(out);
+    r.gamma = gamma;
+    r.packed = static_cast<const uint16_t*>(packed);
+    r.tok = token_index;
+    r.chan = channel_index;
+    r.batch = batch;
+    r.n_tok = n;
+    r.channels = c;
+    r.q_s = q_s;
+    r.q_c = q_c;
+    r.n_pairs = static_cast<int32_t>((static_cast<int64_t>(batch) * q_s + 1) / 2);
+    r.norm = (flags & OW_FUSE_NORM) ? 1 : 0;
+    r.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
+    r.eps = eps;
+    const int rc = ow::launch_fwd_resident(r, dtype, s);
+    if (rc == OW_OK) ow::clear_error();
+    return rc;
+  }
   float* scale = nullptr;
   if (flags & OW_FUSE_NORM) {
     scale = static_cast<float*>(workspace);
@@ -789,9 +719,19 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma, const
   a.q_s = q_s;
   a.q_c = q_c;
   a.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
-  const bool contig = (c % d == 0) && (plan->radix_level == 0 || q_c <= 1);
+  // Channel-group access (routing.py:107-121): identity order at level 0 or with one group;
+  // at levels >= 1 group qc is the channels congruent to (qc + level) mod q_c.
   const bool vec_ok = (c % 8 == 0) && ow::aligned16(x) && ow::aligned16(out);
-  a.gather = !(contig && vec_ok);
+  const bool identity = plan->radix_level == 0 || q_c <= 1;
+  a.stride = 1;
+  if (vec_ok && identity && c % d == 0) {
+    a.mode = ow::kModeContig;
+  } else if (vec_ok && !identity && c == q_c * d && (q_c == 2 || q_c == 4 || q_c == 8)) {
+    a.mode = ow::kModeStrided;
+    a.stride = q_c;
+  } else {
+    a.mode = ow::kModeElement;
+  }
   const int rc = dtype == OW_DTYPE_BF16 ? ow::dispatch_fwd<ow::BF16>(a, d, rd, s)
                                         : ow::dispatch_fwd<ow::F16>(a, d, rd, s);
   if (rc == OW_OK) ow::clear_error();

@@ -1,0 +1,308 @@
+// Device-side helpers shared by the BiGEMM kernels: vector types, per-dtype traits (rounding,
+// packing, MFMA), the reference's RMSNorm dtype sequence and the folded SiLU gate.
+//
+// MFMA layouts (64 lanes; l16 = lane % 16, h = lane / 16, l32 = lane % 32, hh = lane / 32):
+//   16x16 accumulator        lane holds D[4h + i][l16], i = 0..3
+//   16x16x16 A / B operand   lane holds A[l16][4h + j] / B[4h + j][l16], j = 0..3
+//   32x32 accumulator        lane holds D[8(i/4) + 4hh + i%4][l32], i = 0..15
+//   32x32x16 A / B operand   lane holds 8 K-slots j = 0..7 of row / column l32 for K half hh
+// Only the pairing of A slot (hh, j) with B slot (hh, j) is fixed by the hardware, so each
+// operand may use any K order as long as both sides agree.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ow_common.h"
+
+namespace ow {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kG = 16;                      // spatial tile (tokens per group)
+constexpr int kFragElems = 512;             // 32x32x16 operand: 64 lanes x 8
+constexpr int kHeadElems = 3 * kFragElems;  // token-side operands (A_u, A_v, A_o rows) at the head of the packed weights
+constexpr float kNegLog2e = -1.4426950408889634f;
+constexpr float kNegLn2 = -0.6931471805599453f;
+
+struct BF16 {
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t u) {
+    return __uint_as_float(static_cast<uint32_t>(u) << 16);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  }
+  // a.lo^2 + a.hi^2 + acc in fp32
+  static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
+    const bf16x2 v = __builtin_bit_cast(bf16x2, a);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  }
+  static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                     __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t u) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, u));
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
+  static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
+    const f16x2 v = __builtin_bit_cast(f16x2, a);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+  static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+
+template <class Ty>
+__device__ __forceinline__ float round_to(float f) {
+  return Ty::to_f32(Ty::from_f32(f));
+}
+
+// RMSNorm row scale with the reference's dtype sequence (omniweave/models/block.py:83-84):
+// var (fp32) -> x.dtype, + eps in x.dtype, rsqrt in x.dtype.
+template <class Ty>
+__device__ __forceinline__ float rms_scale(float mean_sq, float eps) {
+  const float v = round_to<Ty>(round_to<Ty>(mean_sq) + eps);
+  return round_to<Ty>(rsqrtf(v));
+}
+
+// SiLU(U) V from the folded accumulators U' = -log2(e) U, V' = -ln(2) V:
+// SiLU(U) V = U V / (1 + e^-U) = U' V' / (1 + 2^U').
+__device__ __forceinline__ float silu_gate(float up, float vp) {
+  return up * vp * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(up));
+}
+
+// Separates MFMA results from VALU reads of them by 32 wait states.  Used where the read
+// follows the MFMA across a basic-block boundary (loop exit), or where many accumulator
+// registers are read at once: the hardware does not interlock an MFMA's result against a
+// later VALU read, and a read a few instructions after a 16x16x16 MFMA returns the old value
+// of its last accumulator register.  The scheduling barriers keep the compiler from moving
+// MFMAs or reads across the padding.
+__device__ __forceinline__ void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Makes this wave's LDS writes visible to its other lanes before they read them.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint16_t lo16(uint32_t v) { return static_cast<uint16_t>(v & 0xffffu); }
+__device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16_t>(v >> 16); }
+
+// ---------------------------------------------------------------------------------------
+// One 32-token pair (token groups 0 and 1 of 16 tokens) of a channel group, all on 32x32x16
+// MFMAs.  Token-side products use the block-diagonal 32x32 token matrix: K step g covers the
+// 16 tokens of group g, and lanes whose token (lane % 32) is in the other group get a zero B
+// operand for that step.  Token order within a K step: slot j of lane half hh is token
+// kord(j, hh) = 8(j/4) + 4hh + j%4, the row order of a 32x32 accumulator, so the x values a lane
+// reads for the token side are the ones its output accumulator needs for the residual.
+//
+//   P^T  = X^T (A diag r)^T     A operand X^T: lane (c = l32, hh) slot j = x[16g + kord(j, hh)][c]
+//                               B operand:     lane (t = l32, hh) slot j = A[t % 16][kord(j, hh)] r[16g + kord(j, hh)]
+//        accumulator lane (t, hh) register i = channel kord(i) of the 32-channel block, so
+//        registers 8s..8s+7 are K step s of the next product with channel order
+//        16 ks + kord(j, hh) (the packed B_u'^T / B_v'^T use that order)
+//   U'^T = B_u'^T P_u^T         accumulator lane (t, hh) register i = expanded row kord(i)
+//   W    = Z B_o                A operand Z (lane = token), B operand B_o (lane = channel), K order
+//                               of the expanded dim as held by the U'^T accumulator;
+//        accumulator lane (c = l32, hh) register i = token kord(i)
+//   delta = A_o W               A operand: lane (t, hh) slot j = A_o[t % 16][kord(j, hh)] for
+//                               K step g = t / 16 (zero otherwise), B operand = W registers
+//        accumulator lane (c, hh) register i = delta[token kord(i)][channel c], where register
+//        8g + j is token 16g + kord(j, hh): slot j of the lane's X^T operand for K step g
+
+__device__ __forceinline__ int pair_token_row(int i, int hh) { return 8 * (i >> 2) + 4 * hh + (i & 3); }
+
+// X^T operand: rows p[k ld] for k = 0..3, 8..11 of one LDS column (p = row 16g + 4hh).
+__device__ __forceinline__ u32x4 column8(const uint16_t* p, int ld) {
+  u32x4 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k0 = 8 * (q >> 1) + 2 * (q & 1);
+    v[q] = static_cast<uint32_t>(p[k0 * ld]) | (static_cast<uint32_t>(p[(k0 + 1) * ld]) << 16);
+  }
+  return v;
+}
+
+// Element i (register index of a 32x32 accumulator K half) of a packed operand.
+__device__ __forceinline__ uint16_t packed_elem(const u32x4& v, int j) {
+  return (j & 1) ? hi16(v[j >> 1]) : lo16(v[j >> 1]);
+}
+
+// Sum over aligned groups of N lanes (N in {8, 16, 32}) with DPP; the total lands in the last
+// lane of each group (lane % N == N - 1), the other lanes hold partial sums.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 8 || N == 16 || N == 32, "group of 8, 16 or 32 lanes");
+  v += dpp_f32<0xb1, 0xf>(v);                          // quad_perm 1,0,3,2
+  v += dpp_f32<0x4e, 0xf>(v);                          // quad_perm 2,3,0,1
+  v += dpp_f32<0x141, 0xf>(v);                         // row_half_mirror: quads of 8 lanes
+  if constexpr (N >= 16) v += dpp_f32<0x140, 0xf>(v);  // row_mirror: halves of a 16-lane row
+  if constexpr (N == 32) v += dpp_f32<0x142, 0xa>(v);  // row_bcast15: row 2k into row 2k + 1
+  return v;
+}
+
+// Token-operand row (8 values, packed, slot j <-> token kord(j, hh)) scaled by the RMSNorm
+// scales of those tokens; r points at the scale of token 16g + 4hh.
+template <class Ty>
+__device__ __forceinline__ u32x4 scale8(u32x4 a, const float* r) {
+  u32x4 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k0 = 8 * (q >> 1) + 2 * (q & 1);
+    v[q] = Ty::pack2(Ty::to_f32(lo16(a[q])) * r[k0], Ty::to_f32(hi16(a[q])) * r[k0 + 1]);
+  }
+  return v;
+}
+
+__device__ __forceinline__ u32x4 keep_if(bool keep, u32x4 v) {
+  return keep ? v : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Accumulator registers 8s..8s+7 as a packed K step.
+template <class Ty>
+__device__ __forceinline__ u32x4 pack_kstep(const f32x16& acc, int s) {
+  return u32x4{Ty::pack2(acc[8 * s + 0], acc[8 * s + 1]), Ty::pack2(acc[8 * s + 2], acc[8 * s + 3]),
+               Ty::pack2(acc[8 * s + 4], acc[8 * s + 5]), Ty::pack2(acc[8 * s + 6], acc[8 * s + 7])};
+}
+
+// Token side of a pair: Pu/Pv[ks] (ks < KS) from the pair's 32 LDS rows `tl` (row stride ld).
+// col[cb] is the LDS column holding channel 32 cb + l32 of the group; bu/bv are the lane's
+// (already r-scaled) token-operand rows, used for the K step of the lane's own group.  The X^T
+// operands read are returned in xk[cb][g] (the residual of the lane's output elements).
+template <class Ty, int KS>
+__device__ __forceinline__ void pair_token_side(const uint16_t* tl, int ld, const int (&col)[KS / 2], u32x4 bu,
+                                                u32x4 bv, int lane, u32x4 (&Pu)[KS], u32x4 (&Pv)[KS],
+                                                u32x4 (&xk)[KS / 2][2]) {
+  const int hh = lane >> 5;
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 bu0 = keep_if(g0, bu), bu1 = keep_if(!g0, bu);
+  const u32x4 bv0 = keep_if(g0, bv), bv1 = keep_if(!g0, bv);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    xk[cb][0] = column8(tl + (4 * hh) * ld + col[cb], ld);
+    xk[cb][1] = column8(tl + (16 + 4 * hh) * ld + col[cb], ld);
+  }
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const u32x4 x0 = xk[cb][0], x1 = xk[cb][1];
+    f32x16 pu = Ty::mma32(x0, bu0, zero);
+    f32x16 pv = Ty::mma32(x0, bv0, zero);
+    pu = Ty::mma32(x1, bu1, pu);
+    pv = Ty::mma32(x1, bv1, pv);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Pu[2 * cb + s] = pack_kstep<Ty>(pu, s);
+      Pv[2 * cb + s] = pack_kstep<Ty>(pv, s);
+    }
+  }
+}
+
+// One 32-row chunk of the expanded dimension: U'^T, V'^T from the chunk's B_u'^T / B_v'^T
+// fragments, Z = U'V' / (1 + 2^U'), W[mb] += Z B_o.  fu(ks), fv(ks), fo(mb, s) return fragments.
+template <class Ty, int KS, int MB, class FU, class FV, class FO>
+__device__ __forceinline__ void pair_chunk(const u32x4 (&Pu)[KS], const u32x4 (&Pv)[KS], FU fu, FV fv, FO fo,
+                                           f32x16 (&W)[MB]) {
+  f32x16 U = {}, V = {};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    U = Ty::mma32(fu(ks), Pu[ks], U);
+    V = Ty::mma32(fv(ks), Pv[ks], V);
+  }
+  u32x4 Z[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
+                          silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(mb, s), W[mb]);
+}
+
+// delta[mb] = A_o W[mb] for the pair; ao is the lane's A_o operand row (K step of its group).
+template <class Ty, int MB>
+__device__ __forceinline__ void pair_output(const f32x16 (&W)[MB], u32x4 ao, int lane, f32x16 (&dl)[MB]) {
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 ao0 = keep_if(g0, ao), ao1 = keep_if(!g0, ao);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    dl[mb] = Ty::mma32(ao0, pack_kstep<Ty>(W[mb], 0), zero);
+    dl[mb] = Ty::mma32(ao1, pack_kstep<Ty>(W[mb], 1), dl[mb]);
+  }
+}
+
+inline int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return OW_OK;
+  return fail(OW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Persistent forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4}: weights of a
+// channel group stay in the registers of one wave, one workgroup of q_c waves handles all
+// channel groups of 32 tokens at a time (bigemm_fwd_resident.hip).
+struct ResidentArgs {
+  const uint16_t* x;
+  uint16_t* out;
+  const float* gamma;      // [C]
+  const uint16_t* packed;  // packed weights (same layout as the streamed kernel)
+  const int32_t* tok;      // [q_s * 16]
+  const int32_t* chan;     // [q_c * 64]
+  int32_t batch, n_tok, channels, q_s, q_c;
+  int32_t n_pairs;  // ceil(batch * q_s / 2)
+  int32_t norm;     // fuse the RMSNorm prologue
+  int32_t residual; // write x + delta instead of delta
+  float eps;
+};
+
+bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);
+int launch_fwd_resident(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
+
+}  // namespace ow

@@ -152,9 +152,11 @@ def test_layer_scale_is_exactly_linear() -> None:
 
 
 def test_ragged_channels_and_rd_variants() -> None:
-    """C=70 with d=64 (pad channels, scalar gather path) and d=64/rd=256, d=128/rd=128."""
+    """C=70 with d=64 (pad channels, element gather path), d=64/rd=256 (streamed kernel, contiguous
+    and strided channel groups), d=128/rd=128, and C=64 (one channel group, resident kernel)."""
     for (h, w, c, d, rd, route, level) in [(7, 7, 70, 64, 128, "radix", 1), (9, 9, 128, 64, 256, "local", 0),
-                                          (6, 6, 256, 128, 128, "shifted", 0)]:
+                                          (7, 7, 256, 64, 256, "radix", 1), (6, 6, 256, 128, 128, "shifted", 0),
+                                          (8, 8, 64, 64, 128, "shifted", 0)]:
         announce(f"ragged h={h} w={w} c={c} d={d} rd={rd} {route}{level}")
         plan, x, params, norm_w = make_case(3, h, w, c, d, route, level, torch.bfloat16, seed=4, rd=rd)
         got = bigemm_delta_hip(x=x.to(DEV), plan=plan, **to_dev(params))
@@ -174,6 +176,28 @@ def test_empty_batch_and_noncontiguous_input() -> None:
     got = bigemm_delta_hip(x=xt, plan=plan, **dp)
     ref = oracle_delta(x.transpose(1, 2).contiguous(), plan, params, torch.bfloat16)
     assert rel_l2(got.cpu(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("stage,route,level", [("s1", "radix", 1), ("s3", "local", 0), ("s4", "radix", 2)])
+def test_unaligned_input_uses_element_path(stage, route, level) -> None:
+    """x at a 2-byte offset (not 16-byte aligned) takes the element gather / scatter path; it must
+    agree with the oracle and, for the residual, with round(x + delta)."""
+    h, w, c, d = STAGES[stage]
+    announce(f"unaligned x stage={stage} route={route}{level} bf16 B=2 seed=8")
+    plan, x, params, norm_w = make_case(2, h, w, c, d, route, level, torch.bfloat16, seed=8)
+    store = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=DEV)
+    xd = store[1:].view(x.shape)
+    xd.copy_(x.to(DEV))
+    assert xd.data_ptr() % 16 != 0
+    dp = to_dev(params)
+    got = bigemm_delta_hip(x=xd, plan=plan, **dp)
+    assert rel_l2(got.cpu(), oracle_delta(x, plan, params, torch.bfloat16)) <= 1e-2
+    aligned = bigemm_delta_hip(x=x.to(DEV), plan=plan, **dp)
+    assert torch.equal(got, aligned)  # same arithmetic, different memory access
+    delta = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp, residual=False)
+    out = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), (x.float() + delta.cpu().float()).to(torch.bfloat16))
 
 
 def test_fp32_weights_and_bf16_weights_agree() -> None:

@@ -52,9 +52,9 @@ def test_plan_dims_and_errors() -> None:
 
 def test_packed_weight_bytes() -> None:
     lib = _native.lib()
-    # head (3 x 256 elements) + q_c * 3*d*rd elements, 2 bytes each
-    assert lib.ow_packed_weight_bytes(4, 128, 256, _native.OW_DTYPE_BF16) == 2 * (768 + 4 * 3 * 128 * 256)
-    assert lib.ow_packed_weight_bytes(2, 64, 128, _native.OW_DTYPE_F16) == 2 * (768 + 2 * 3 * 64 * 128)
+    # head (3 token-operand rows of 64 lanes x 8) + q_c * 3*d*rd elements, 2 bytes each
+    assert lib.ow_packed_weight_bytes(4, 128, 256, _native.OW_DTYPE_BF16) == 2 * (1536 + 4 * 3 * 128 * 256)
+    assert lib.ow_packed_weight_bytes(2, 64, 128, _native.OW_DTYPE_F16) == 2 * (1536 + 2 * 3 * 64 * 128)
     assert lib.ow_packed_weight_bytes(0, 64, 128, _native.OW_DTYPE_F16) == 0
 
 
