@@ -92,14 +92,17 @@ size_t ow_packed_weight_bytes(int32_t q_c, int32_t d, int32_t rd, int32_t comput
  * Folded into the packed values (then rounded to compute_dtype, nearest-even):
  *   B_u rows x -log2(e), B_v rows x -ln(2)   (SiLU evaluated as U'V'/(1 + 2^U'));
  *   B_u / B_v row c of group q x norm_weight[channel_index[q*d + c]] when norm_weight is
- *   non-NULL (the block's RMSNorm weight; pad channels get 0).
- * A buffer packed with norm_weight must be used with OW_FUSE_NORM, one packed without it
- * without OW_FUSE_NORM.  channel_index: device table of ow_route_build (may be NULL when
- * norm_weight is NULL).  `packed` must hold ow_packed_weight_bytes(...).
+ *   non-NULL (the block's RMSNorm weight);
+ *   B_o column c of group q x gamma[channel_index[q*d + c]] when gamma is non-NULL (the
+ *   LayerScale, [C] fp32; omniweave/ops/reference.py:168-171 scales delta by it).
+ * With channel_index given, rows / columns of pad channels are packed as 0.  A buffer packed
+ * with norm_weight must be used with OW_FUSE_NORM, one packed without it without
+ * OW_FUSE_NORM.  channel_index: device table of ow_route_build (required when norm_weight or
+ * gamma is non-NULL).  `packed` must hold ow_packed_weight_bytes(...).
  */
 int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o,
                     const void* b_u, const void* b_v, const void* b_o,
-                    int32_t weight_dtype, const float* norm_weight,
+                    int32_t weight_dtype, const float* norm_weight, const float* gamma,
                     const int32_t* channel_index, int32_t channels,
                     int32_t g, int32_t q_c, int32_t d, int32_t rd,
                     int32_t compute_dtype, void* packed, void* stream);
@@ -124,9 +127,9 @@ size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags);
  *   x, out        [batch, H*W, C] NHWC, element type `dtype` (out may not alias x;
  *                 both may be NULL when batch == 0, which launches nothing)
  *   eps           RMSNorm epsilon (1e-6 in the reference), used with OW_FUSE_NORM
- *   gamma         [C] fp32 LayerScale
- *   packed        ow_pack_weights output for this (q_c, d, rd, dtype), packed with the
- *                 RMSNorm weight exactly when flags has OW_FUSE_NORM
+ *   packed        ow_pack_weights output for this (q_c, d, rd, dtype) with the block's
+ *                 LayerScale gamma folded in, packed with the RMSNorm weight exactly when
+ *                 flags has OW_FUSE_NORM
  *   packed_bytes  size of `packed`; must equal ow_packed_weight_bytes(q_c, d, rd, dtype)
  *   token_index   device copy of ow_route_build's token table [Q_s*g]
  *   channel_index device copy of ow_route_build's channel table [Q_c*d]
@@ -135,11 +138,13 @@ size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags);
  * For every tile (b, q_s, q_c): T = rows token_index[q_s,:] x columns channel_index[q_c,:]
  * of x (pads read as zero; RMSNorm-scaled with OW_FUSE_NORM), delta = A_o (SiLU(A_u T B_u) *
  * (A_v T B_v)) B_o scaled per column by gamma; valid rows/columns are written back to their
- * NHWC positions (omniweave/ops/reference.py:120-173).  With OW_FUSE_NORM the row scales are
- * computed first (ow_rms_scale into the workspace), on the same stream.  Envelope: g = 16,
- * d in {64,128}, rd in {128,256}, dtype in {bf16, f16}.
+ * NHWC positions (omniweave/ops/reference.py:120-173).  With OW_FUSE_NORM the row scales
+ * come from the same read of x when d = 64, rd = 128 and C = q_c * 64 with q_c <= 4 (and
+ * x, out 16-byte aligned); otherwise they are computed first (ow_rms_scale into the
+ * workspace), on the same stream.  Envelope: g = 16, d in {64,128}, rd in {128,256}, dtype
+ * in {bf16, f16}.
  */
-int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma,
+int ow_bigemm_fwd(const void* x, void* out, float eps,
                   const void* packed, size_t packed_bytes,
                   const int32_t* token_index, const int32_t* channel_index,
                   const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,

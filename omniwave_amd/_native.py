@@ -38,7 +38,7 @@ _SIGNATURES = {
     "ow_packed_weight_bytes": (ctypes.c_size_t, [ctypes.c_int32] * 4),
     "ow_pack_weights": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 6 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]
+        [ctypes.c_void_p] * 6 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]
         + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],
     ),
     "ow_rms_scale": (
@@ -50,7 +50,7 @@ _SIGNATURES = {
     "ow_bigemm_fwd": (
         ctypes.c_int,
         [
-            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
             ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
             ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,

@@ -6,20 +6,19 @@
 //     delta = A_o . (SiLU(A_u . T . B_u) * (A_v . T . B_v)) . B_o      scaled per column by gamma
 // evaluated with the cheapest association, P = A.T first and Z.B_o before A_o.  With the
 // block's RMSNorm fused, T = diag(r) X diag(w) (r = per-token rsqrt scale, w = norm weight),
-// so P^T = diag(w) X^T (A diag(r))^T: r scales the A operand of each token group and w is
-// folded into the packed B_u / B_v rows.  SiLU's exponent base is folded into the weights too:
-// B_u' = -log2(e) B_u, B_v' = -ln(2) B_v give U' = -log2(e) U, V' = -ln(2) V and
+// so P^T = diag(w) X^T (A diag(r))^T: r scales the token operand of each token group and w is
+// folded into the packed B_u / B_v rows, gamma into the packed B_o columns.  SiLU's exponent
+// base is folded into the weights too: B_u' = -log2(e) B_u, B_v' = -ln(2) B_v give
+// U' = -log2(e) U, V' = -ln(2) V and
 //     SiLU(U) V = U V / (1 + e^-U) = U' V' / (1 + 2^U').
 //
-// All products are computed transposed (tokens on the MFMA N axis, layouts in ow_device.h) so
-// every result feeds the next contraction from registers:
-//     P^T  = X^T . (A diag r)^T  16x16x16 per token group (K = 16 tokens), X^T from LDS;
-//            two groups' results are merged into one 32-token B operand by a lane exchange
-//     U'^T = B_u'^T . P_u^T      32x32x16 (K = channels, N = 32 tokens), weights from LDS
-//     Z^T  = U'V' / (1 + 2^U')   registers; a 32-row accumulator block is two 16-deep
-//                                K steps of the next product
-//     W^T  = B_o^T . Z^T         32x32x16 (K = expanded dim)
-//     delta = A_o . W            16x16x16 per token group, W transposed through LDS
+// Every product is a 32x32x16 MFMA over a pair of token groups (32 tokens), with operand
+// orders chosen so that each accumulator is the next product's operand (ow_device.h):
+//     P^T  = X^T . (A diag r)^T  block-diagonal token matrix, X^T read from the LDS tile
+//     U'^T = B_u'^T . P_u^T      K = channels, weights from LDS
+//     Z    = U'V' / (1 + 2^U')   registers
+//     W    = Z . B_o             K = expanded dim, weights from LDS
+//     delta = A_o . W            block-diagonal token matrix
 // Weights are pre-packed (ow_pack_weights) so each MFMA operand is one 16-byte LDS read per
 // lane, and each chunk of weights is copied global -> LDS directly (global_load_lds).
 #include <hip/hip_runtime.h>
@@ -105,7 +104,6 @@ struct FwdArgs {
   const uint16_t* x;
   uint16_t* out;
   const float* row_scale;  // [batch * n_tok] RMSNorm scale per token, NULL without OW_FUSE_NORM
-  const float* gamma;      // [C]
   const uint16_t* packed;
   const int32_t* tok;
   const int32_t* chan;
@@ -184,7 +182,6 @@ bigemm_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t wb[CH_ELEMS];
   __shared__ int32_t rowid[ROWS];  // b * n_tok + token, -1 for pad rows
   __shared__ float rsc[ROWS];      // RMSNorm scale of each row (1 without norm)
-  __shared__ float gm[D];
   __shared__ int32_t chx[D];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -215,9 +212,7 @@ bigemm_fwd_kernel(FwdArgs a) {
   }
   for (int k = tid; k < D; k += kThreads) {
     const int c = a.chan[qc * D + k];
-    const bool ok = c >= 0 && c < a.channels;
-    chx[k] = ok ? c : -1;
-    gm[k] = ok ? a.gamma[c] : 0.0f;
+    chx[k] = (c >= 0 && c < a.channels) ? c : -1;
   }
   __syncthreads();
 
@@ -354,9 +349,9 @@ bigemm_fwd_kernel(FwdArgs a) {
     for (int p = 0; p < NP; ++p) pair_chunk<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
   }
 
-  // Output side: delta = A_o W per pair (lane = channel 32 mb + l32, registers = tokens) with
-  // LayerScale; the rounded delta, or round(x + delta) with x from the token-side operands, is
-  // written over the pair's own 32 rows of xs.  The barrier first: the odd weight chunks live in
+  // Output side: delta = A_o W per pair (lane = channel 32 mb + l32, registers = tokens;
+  // LayerScale folded into B_o); the rounded delta, or round(x + delta) with x from the
+  // token-side operands, is written over the pair's own 32 rows of xs.  The barrier first: the odd weight chunks live in
   // xs.  No branch separates an MFMA from the reads of its result.
   mfma_drain();
   __syncthreads();
@@ -366,23 +361,13 @@ bigemm_fwd_kernel(FwdArgs a) {
     pair_output<Ty, MB>(W[p], fAo, lane, dl);
     mfma_drain();
     uint16_t* st = xs + (wave * TPW + 2 * p) * kG * LDX;
-    if (a.residual) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const float gmv = gm[32 * mb + l32];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float xv = Ty::to_f32(packed_elem(xk[p][mb][i >> 3], i & 7));
-          st[pair_token_row(i, hh) * LDX + 32 * mb + l32] = Ty::from_f32(xv + round_to<Ty>(dl[mb][i] * gmv));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const float gmv = gm[32 * mb + l32];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st[pair_token_row(i, hh) * LDX + 32 * mb + l32] = Ty::from_f32(dl[mb][i] * gmv);
-      }
+    for (int mb = 0; mb < MB; ++mb) {
+      auto dst = [&](int i) { return &st[pair_token_row(i, hh) * LDX + 32 * mb + l32]; };
+      if (a.residual)
+        pair_store_block<Ty, true>(dl[mb], xk[p][mb], dst);
+      else
+        pair_store_block<Ty, false>(dl[mb], xk[p][mb], dst);
     }
   }
   __syncthreads();
@@ -447,7 +432,8 @@ struct PackArgs {
   const void* b_v;
   const void* b_o;
   const float* norm_w;  // folded into B_u / B_v rows (NULL: weight 1)
-  const int32_t* chan;  // channel table [q_c * d] (routes norm_w to tile rows)
+  const float* gamma;   // folded into B_o columns (NULL: scale 1)
+  const int32_t* chan;  // channel table [q_c * d] (routes norm_w / gamma; pads packed as 0)
   void* packed;
   int32_t wdtype, q_c, d, rd, channels;
   int64_t total;
@@ -497,9 +483,9 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
       const int c = 16 * ks + 8 * (j / 4) + 4 * hh + (j % 4);
       const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + col;
       float w = 1.0f;
-      if (p.norm_w) {
+      if (p.chan) {
         const int gc = p.chan[q * p.d + c];
-        w = (gc >= 0 && gc < p.channels) ? p.norm_w[gc] : 0.0f;
+        w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
       }
       val = load_f32(is_u ? p.b_u : p.b_v, src, p.wdtype) * w * (is_u ? kNegLog2e : kNegLn2);
     } else {
@@ -508,7 +494,12 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
       const int c = 32 * mb + l32;
       const int ee = 32 * ec + 16 * s + 8 * (j / 4) + 4 * hh + (j % 4);
       const int64_t src = (static_cast<int64_t>(q) * p.rd + ee) * p.d + c;
-      val = load_f32(p.b_o, src, p.wdtype);
+      float w = 1.0f;
+      if (p.chan) {
+        const int gc = p.chan[q * p.d + c];
+        w = (gc >= 0 && gc < p.channels) ? (p.gamma ? p.gamma[gc] : 1.0f) : 0.0f;
+      }
+      val = load_f32(p.b_o, src, p.wdtype) * w;
     }
   }
   static_cast<uint16_t*>(p.packed)[idx] = Ty::from_f32(val);
@@ -598,11 +589,11 @@ size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags) 
 }
 
 int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,
-                    const void* b_o, int32_t weight_dtype, const float* norm_weight, const int32_t* channel_index,
-                    int32_t channels, int32_t g, int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype,
-                    void* packed, void* stream) {
+                    const void* b_o, int32_t weight_dtype, const float* norm_weight, const float* gamma,
+                    const int32_t* channel_index, int32_t channels, int32_t g, int32_t q_c, int32_t d, int32_t rd,
+                    int32_t compute_dtype, void* packed, void* stream) {
   OW_CHECK_ARG(a_u && a_v && a_o && b_u && b_v && b_o && packed, "weight or output pointer is NULL");
-  OW_CHECK_ARG(!norm_weight || channel_index, "norm_weight needs channel_index");
+  OW_CHECK_ARG(!(norm_weight || gamma) || channel_index, "norm_weight / gamma need channel_index");
   OW_CHECK_ARG(channels >= 1, "channels must be >= 1 (got %d)", channels);
   OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
   OW_CHECK_SUPPORTED(g == ow::kG, "unsupported spatial tile g=%d; expected 16", g);
@@ -611,7 +602,7 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const voi
                      "unsupported channel tile d=%d / expanded dim rd=%d", d, rd);
   OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16,
                      "unsupported compute dtype %d", compute_dtype);
-  ow::PackArgs p{a_u, a_v, a_o, b_u, b_v, b_o, norm_weight, channel_index, packed,
+  ow::PackArgs p{a_u, a_v, a_o, b_u, b_v, b_o, norm_weight, gamma, channel_index, packed,
                  weight_dtype, q_c, d, rd, channels, ow::packed_elems(q_c, d, rd)};
   const unsigned blocks = static_cast<unsigned>((p.total + 255) / 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -650,14 +641,14 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
   return OW_OK;
 }
 
-int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma, const void* packed,
-                  size_t packed_bytes, const int32_t* token_index, const int32_t* channel_index,
+int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                  const int32_t* token_index, const int32_t* channel_index,
                   const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags, void* workspace,
                   size_t workspace_bytes, void* stream) {
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
-  OW_CHECK_ARG(gamma && packed && token_index && channel_index, "tensor pointer is NULL");
+  OW_CHECK_ARG(packed && token_index && channel_index, "tensor pointer is NULL");
   OW_CHECK_ARG((flags & ~(OW_FUSE_NORM | OW_FUSE_RESIDUAL)) == 0, "unknown flags 0x%x", flags);
   OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16,
@@ -683,7 +674,6 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma, const
     ow::ResidentArgs r{};
     r.x = static_cast<const uint16_t*>(x);
     r.out = static_cast<uint16_t*>(out);
-    r.gamma = gamma;
     r.packed = static_cast<const uint16_t*>(packed);
     r.tok = token_index;
     r.chan = channel_index;
@@ -709,7 +699,6 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const float* gamma, const
   a.x = static_cast<const uint16_t*>(x);
   a.out = static_cast<uint16_t*>(out);
   a.row_scale = scale;
-  a.gamma = gamma;
   a.packed = static_cast<const uint16_t*>(packed);
   a.tok = token_index;
   a.chan = channel_index;

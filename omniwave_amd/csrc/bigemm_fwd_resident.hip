@@ -3,8 +3,11 @@
 //
 // Same math and operand packing as the streamed tile kernel (bigemm_fwd.hip; reference
 // omniweave/ops/reference.py:147-171), organised so that nothing but activations moves:
-//   * one workgroup = q_c waves, wave w owns channel group w; its 48 KB of packed weights
-//     (B_u'^T, B_v'^T, B_o fragments) are loaded into registers once and stay there;
+//   * one workgroup = 2 q_c waves; waves 2g and 2g + 1 own channel group g and split its
+//     expanded dimension: wave half h keeps the packed weights of chunks 2h and 2h + 1
+//     (24 KB) resident in its registers, computes its share of W = Z B_o, and the two halves
+//     exchange partial sums through LDS; each then finishes one 32-channel half of delta.
+//     Two waves per SIMD let one wave's LDS / memory waits overlap the other's work;
 //   * the workgroup walks 32-token pairs of token groups (pair p = groups 2p and 2p + 1 of the
 //     flattened batch x q_s order), persistent over the grid;
 //   * each pair's full rows (32 tokens x C channels) are prefetched into registers one pair
@@ -14,10 +17,11 @@
 //     tile columns a wave reads and writes, so the radix channel rotation costs nothing;
 //   * the residual is added in the LDS tile, which is then written back as whole rows with
 //     16-byte stores.
-// Pipeline per pair i: registers(i) -> RMS scales + LDS tile(i); barrier; store rows of pair
-// i-1 from LDS; issue the loads of pair i+1 (and token-table reads of pair i+2); compute pair
-// i into LDS tile(i).  Three tile buffers: the stores of pair i-1 may still be reading
-// buffer (i-1) % 3 while a faster wave fills buffer (i+1) % 3.
+// Pipeline per pair i: registers(i) -> RMS scales + LDS tile(i); barrier; issue the loads of
+// pair i+1 (and token-table reads of pair i+2), store the rows of pair i-1 from LDS; token side
+// and both chunks of this wave; partial-W exchange (barrier); delta into LDS tile(i).  Three
+// tile buffers: the stores of pair i-1 may still be reading buffer (i-1) % 3 while a faster
+// wave fills buffer (i+1) % 3.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -30,25 +34,37 @@ namespace {
 constexpr int kRD = 128;
 constexpr int kD = 64;
 constexpr int kKS = kD / 16;               // 16-deep K steps over a channel group
-constexpr int kMB = kD / 32;               // 32-channel blocks of W
+constexpr int kMB = kD / 32;               // 32-channel blocks of W (= halves of the group)
 constexpr int kNCH = kRD / 32;             // 32-row chunks of the expanded dimension
+constexpr int kHalfCh = kNCH / 2;          // chunks per wave
 constexpr int kFrU = kKS;                  // B_u'^T fragments per chunk (B_v'^T the same)
 constexpr int kFrCh = 2 * kFrU + 2 * kMB;  // fragments per chunk
 constexpr int kChElems = kFrCh * kFragElems;
 constexpr int kPairRows = 2 * kG;          // 32 tokens per pair
 constexpr int kNBuf = 3;
+static_assert(kMB == 2, "one 32-channel output half per wave of a group");
 
-// Token-table entries of the 4 rows this lane loads and stores in a pair, with the image
+template <int QC>
+struct ResidentLds {
+  static constexpr int C = QC * kD;
+  static constexpr int LDC = C + 8;  // tile row stride (elements)
+  uint16_t tile[kNBuf][kPairRows * LDC];
+  float rsc[kNBuf][kPairRows];
+  u32x4 xch[QC][2][4][64];  // partial W (f32x16 per lane as 4 quarters) by group and writer half
+  u32x4 head[3][64];        // token-operand rows A_u, A_v, A_o
+};
+
+// Token-table entries of the NI rows this lane loads and stores in a pair, with the image
 // index of each row (>= batch past the end).  Only loads: the values are examined one
 // iteration later (row_id), so the loads are not waited on while the row prefetch is in flight.
-template <int RPW, int RPI, int LPR>
+template <int NI, int RPW, int RPI, int LPR>
 __device__ __forceinline__ void pair_row_tok(const ResidentArgs& a, int64_t pair, int wave, int lane,
-                                             int32_t (&t)[4], int32_t (&b)[4]) {
+                                             int32_t (&t)[NI], int32_t (&b)[NI]) {
   const int64_t tg0 = 2 * pair;  // first group of the pair (uniform)
   const int32_t b0 = static_cast<int32_t>(tg0 / a.q_s);
   const int32_t s0 = static_cast<int32_t>(tg0 - static_cast<int64_t>(b0) * a.q_s);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NI; ++j) {
     const int r = wave * RPW + j * RPI + lane / LPR;
     int32_t bb = b0, s = s0 + r / kG;
     if (s == a.q_s) {
@@ -71,82 +87,76 @@ __device__ __forceinline__ u32x4 load_row_vec(const uint16_t* x, int32_t id, int
   return v;
 }
 
-template <class Ty, int QC>
-__global__ void __attribute__((amdgpu_flat_work_group_size(64 * QC, 64 * QC), amdgpu_waves_per_eu(1, 1)))
-bigemm_fwd_resident_kernel(ResidentArgs a) {
+// The persistent loop of one wave: channel group g, expanded-dimension half HF.
+template <class Ty, int QC, int HF>
+__device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds<QC>& sh, int g, int n_iter) {
   constexpr int C = QC * kD;
-  constexpr int LDC = C + 8;           // tile row stride (elements)
-  constexpr int RPW = kPairRows / QC;  // rows each wave loads and stores
+  constexpr int LDC = ResidentLds<QC>::LDC;
+  constexpr int NW = 2 * QC;           // waves per workgroup
+  constexpr int RPW = kPairRows / NW;  // rows each wave loads and stores
   constexpr int LPR = C / 8;           // lanes per row (16-byte vectors)
   constexpr int RPI = 64 / LPR;        // rows per wave-wide vector access
-  static_assert(RPW / RPI == 4, "four row vectors per lane");
-
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kNBuf][kPairRows * LDC];
-  __shared__ __attribute__((aligned(16))) float rsc[kNBuf][kPairRows];
+  constexpr int NI = RPW / RPI;        // row vectors per lane
+  static_assert(NI == 2, "two row vectors per lane");
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
   const int vcol = (lane % LPR) * 8;  // first column of this lane's row vectors
-
   const int64_t n_wg = gridDim.x;
   const int64_t first = blockIdx.x;
-  const int n_iter = first < a.n_pairs ? static_cast<int>((a.n_pairs - 1 - first) / n_wg + 1) : 0;
-  if (n_iter == 0) return;
 
-  // Resident operands of channel group `wave`.
-  const uint16_t* wsrc = a.packed + kHeadElems + static_cast<size_t>(wave) * kNCH * kChElems;
-  u32x4 wt[kNCH][kFrCh];
+  // Resident weights of chunks 2 HF and 2 HF + 1 of channel group g (accumulation registers:
+  // only MFMAs read them).
+  const uint16_t* wsrc = a.packed + kHeadElems + (static_cast<size_t>(g) * kNCH + kHalfCh * HF) * kChElems;
+  u32x4 wt[kHalfCh][kFrCh];
 #pragma unroll
-  for (int ec = 0; ec < kNCH; ++ec)
+  for (int e = 0; e < kHalfCh; ++e)
 #pragma unroll
-    for (int f = 0; f < kFrCh; ++f)
-      wt[ec][f] = reinterpret_cast<const u32x4*>(wsrc + ec * kChElems + f * kFragElems)[lane];
-  const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
-  const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
-  const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
-  int col[kMB];     // tile column of group channel 32 cb + l32
-  float gmv[kMB];   // LayerScale of that column
+    for (int f = 0; f < kFrCh; ++f) {
+      wt[e][f] = reinterpret_cast<const u32x4*>(wsrc + e * kChElems + f * kFragElems)[lane];
+      asm volatile("" : "+a"(wt[e][f]));
+    }
+  int col[kMB];  // tile column of group channel 32 cb + l32
 #pragma unroll
   for (int cb = 0; cb < kMB; ++cb) {
-    int c = a.chan[wave * kD + 32 * cb + l32];
-    c = (c >= 0 && c < C) ? c : 0;  // tables of a plan with C = q_c * d hold no pads
-    col[cb] = c;
-    gmv[cb] = a.gamma[c];
+    const int c = a.chan[g * kD + 32 * cb + l32];
+    col[cb] = (c >= 0 && c < C) ? c : 0;  // tables of a plan with C = q_c * d hold no pads
   }
 
   // ids_prev: rows being stored (pair it - 1); ids_cur: rows of pair it; tok_n / img_n: raw
   // table entries of pair it + 1.
-  int32_t ids_cur[4], ids_prev[4] = {-1, -1, -1, -1};
-  int32_t tok_n[4], img_n[4];
-  u32x4 xr[4];
-  pair_row_tok<RPW, RPI, LPR>(a, first, wave, lane, tok_n, img_n);
+  int32_t ids_cur[NI], ids_prev[NI];
+  int32_t tok_n[NI], img_n[NI];
+  u32x4 xr[NI];
+  pair_row_tok<NI, RPW, RPI, LPR>(a, first, wave, lane, tok_n, img_n);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NI; ++j) {
+    ids_prev[j] = -1;
     ids_cur[j] = row_id(a, tok_n[j], img_n[j]);
     xr[j] = load_row_vec<C>(a.x, ids_cur[j], vcol);
   }
   if (n_iter > 1) {
-    pair_row_tok<RPW, RPI, LPR>(a, first + n_wg, wave, lane, tok_n, img_n);
+    pair_row_tok<NI, RPW, RPI, LPR>(a, first + n_wg, wave, lane, tok_n, img_n);
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) img_n[j] = a.batch;
+    for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
   }
 
 #pragma unroll 1
   for (int it = 0; it < n_iter; ++it) {
     const int buf = it % kNBuf;
-    uint16_t* tl = tile[buf];
+    uint16_t* tl = sh.tile[buf];
 
-    // (1) RMSNorm row scales and the tile of this pair.
+    // (1) RMSNorm row scales and this wave's rows of the pair's tile.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NI; ++j) {
       const int r = wave * RPW + j * RPI + lane / LPR;
       if (a.norm) {
         float acc = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(xr[j][e], acc);
         acc = group_sum<LPR>(acc);
-        if (lane % LPR == LPR - 1) rsc[buf][r] = rms_scale<Ty>(acc / static_cast<float>(C), a.eps);
+        if (lane % LPR == LPR - 1) sh.rsc[buf][r] = rms_scale<Ty>(acc / static_cast<float>(C), a.eps);
       }
       *reinterpret_cast<u32x4*>(&tl[r * LDC + vcol]) = xr[j];
     }
@@ -154,22 +164,22 @@ bigemm_fwd_resident_kernel(ResidentArgs a) {
 
     // (2) Loads first, then stores: rows of pair it + 1, token-table entries of pair it + 2,
     // then the rows of pair it - 1 (complete in their buffer since the barrier) to memory.
-    int32_t ids_next[4];
+    int32_t ids_next[NI];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NI; ++j) {
       ids_next[j] = row_id(a, tok_n[j], img_n[j]);
       xr[j] = load_row_vec<C>(a.x, ids_next[j], vcol);
     }
     if (it + 2 < n_iter) {
-      pair_row_tok<RPW, RPI, LPR>(a, first + (it + 2) * n_wg, wave, lane, tok_n, img_n);
+      pair_row_tok<NI, RPW, RPI, LPR>(a, first + (it + 2) * n_wg, wave, lane, tok_n, img_n);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) img_n[j] = a.batch;
+      for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
     }
     if (it > 0) {
-      const uint16_t* pt = tile[(it + kNBuf - 1) % kNBuf];
+      const uint16_t* pt = sh.tile[(it + kNBuf - 1) % kNBuf];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NI; ++j) {
         const int r = wave * RPW + j * RPI + lane / LPR;
         if (ids_prev[j] >= 0)
           *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(ids_prev[j]) * C + vcol) =
@@ -177,7 +187,7 @@ bigemm_fwd_resident_kernel(ResidentArgs a) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NI; ++j) {
       ids_prev[j] = ids_cur[j];
       ids_cur[j] = ids_next[j];
     }
@@ -185,55 +195,79 @@ bigemm_fwd_resident_kernel(ResidentArgs a) {
     // and the counter it waits on also covers these stores, so they must be issued early.
     __builtin_amdgcn_sched_barrier(0);
 
-    // (4) Token side, (5) channel side with the resident weights, (6) delta = A_o W.
-    u32x4 bu = fAu, bv = fAv;
+    // (3) Token side (the whole group's P, both halves compute it), (4) this wave's chunks.
+    u32x4 bu = sh.head[0][lane], bv = sh.head[1][lane];
     if (a.norm) {  // lane's slots j are tokens 16 tg + kord(j, hh) of its group tg
-      const float* r8 = &rsc[buf][16 * ((lane >> 4) & 1) + 4 * hh];
-      bu = scale8<Ty>(fAu, r8);
-      bv = scale8<Ty>(fAv, r8);
+      const float* r8 = &sh.rsc[buf][16 * ((lane >> 4) & 1) + 4 * hh];
+      bu = scale8<Ty>(bu, r8);
+      bv = scale8<Ty>(bv, r8);
     }
     u32x4 Pu[kKS], Pv[kKS], xk[kMB][2];
     pair_token_side<Ty, kKS>(tl, LDC, col, bu, bv, lane, Pu, Pv, xk);
     f32x16 W[kMB] = {};
 #pragma unroll
-    for (int ec = 0; ec < kNCH; ++ec) {
-      auto fu = [&](int ks) { return wt[ec][ks]; };
-      auto fv = [&](int ks) { return wt[ec][kFrU + ks]; };
-      auto fo = [&](int mb, int s) { return wt[ec][2 * kFrU + 2 * mb + s]; };
+    for (int e = 0; e < kHalfCh; ++e) {
+      auto fu = [&](int ks) { return wt[e][ks]; };
+      auto fv = [&](int ks) { return wt[e][kFrU + ks]; };
+      auto fo = [&](int mb, int s) { return wt[e][2 * kFrU + 2 * mb + s]; };
       pair_chunk<Ty, kKS, kMB>(Pu, Pv, fu, fv, fo, W);
     }
-    f32x16 dl[kMB];
-    pair_output<Ty, kMB>(W, fAo, lane, dl);
-    mfma_drain();
 
-    // (7) delta (rounded, LayerScale applied), plus x from the token-side operands with the
-    // residual, written over the own columns.
-    if (a.residual) {
+    // (5) Partial-W exchange: hand the partner its half (channels 32 (1-HF) ..), take ours.
+    mfma_drain();
 #pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
+    for (int q = 0; q < 4; ++q)
+      sh.xch[g][HF][q][lane] = u32x4{__float_as_uint(W[1 - HF][4 * q]), __float_as_uint(W[1 - HF][4 * q + 1]),
+                                     __float_as_uint(W[1 - HF][4 * q + 2]), __float_as_uint(W[1 - HF][4 * q + 3])};
+    __syncthreads();
+    f32x16 Wh[1];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float xv = Ty::to_f32(packed_elem(xk[mb][i >> 3], i & 7));
-          tl[pair_token_row(i, hh) * LDC + col[mb]] = Ty::from_f32(xv + round_to<Ty>(dl[mb][i] * gmv[mb]));
-        }
-    } else {
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 o = sh.xch[g][1 - HF][q][lane];
 #pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tl[pair_token_row(i, hh) * LDC + col[mb]] = Ty::from_f32(dl[mb][i] * gmv[mb]);
+      for (int k = 0; k < 4; ++k) Wh[0][4 * q + k] = W[HF][4 * q + k] + __uint_as_float(o[k]);
     }
+
+    // (6) delta = A_o W for channels 32 HF + l32, (7) rounded (plus x with the residual) into
+    // the own columns of the tile.
+    f32x16 dl[1];
+    pair_output<Ty, 1>(Wh, sh.head[2][lane], lane, dl);
+    mfma_drain();
+    auto dst = [&](int i) { return &tl[pair_token_row(i, hh) * LDC + col[HF]]; };
+    if (a.residual)
+      pair_store_block<Ty, true>(dl[0], xk[HF], dst);
+    else
+      pair_store_block<Ty, false>(dl[0], xk[HF], dst);
   }
 
   // Rows of the last pair (ids_prev was rotated to it by the last iteration).
   __syncthreads();
-  const uint16_t* pt = tile[(n_iter - 1) % kNBuf];
+  const uint16_t* pt = sh.tile[(n_iter - 1) % kNBuf];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NI; ++j) {
     const int r = wave * RPW + j * RPI + lane / LPR;
     if (ids_prev[j] >= 0)
       *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(ids_prev[j]) * C + vcol) =
           *reinterpret_cast<const u32x4*>(&pt[r * LDC + vcol]);
   }
+}
+
+template <class Ty, int QC>
+__global__ void __attribute__((amdgpu_flat_work_group_size(128 * QC, 128 * QC), amdgpu_waves_per_eu(2, 2)))
+bigemm_fwd_resident_kernel(ResidentArgs a) {
+  __shared__ __attribute__((aligned(16))) ResidentLds<QC> sh;
+  const int64_t n_wg = gridDim.x;
+  const int64_t first = blockIdx.x;
+  const int n_iter = first < a.n_pairs ? static_cast<int>((a.n_pairs - 1 - first) / n_wg + 1) : 0;
+  if (n_iter == 0) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int f = wave; f < 3; f += 2 * QC)  // 2 waves when q_c = 1
+    sh.head[f][lane] = reinterpret_cast<const u32x4*>(a.packed + f * kFragElems)[lane];
+  __syncthreads();
+  if (wave & 1)
+    resident_wave<Ty, QC, 1>(a, sh, wave >> 1, n_iter);
+  else
+    resident_wave<Ty, QC, 0>(a, sh, wave >> 1, n_iter);
 }
 
 // Compute units of the current device (cached per device id).
@@ -251,11 +285,11 @@ int device_cus() {
 
 template <class Ty, int QC>
 int launch_qc(const ResidentArgs& a, hipStream_t stream) {
-  // One wave per SIMD (the weights take most of the register file): 4 / QC workgroups per CU.
+  // Two waves per SIMD, 2 QC waves per workgroup: 4 / QC workgroups per CU.
   const int64_t slots = static_cast<int64_t>(device_cus()) * (4 / QC);
   const int64_t grid = a.n_pairs < slots ? a.n_pairs : slots;
   if (grid <= 0) return OW_OK;
-  hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC>), dim3(static_cast<unsigned>(grid)), dim3(64 * QC), 0,
+  hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC>), dim3(static_cast<unsigned>(grid)), dim3(128 * QC), 0,
                      stream, a);
   return hip_status(hipGetLastError(), "bigemm_fwd_resident_kernel launch");
 }

@@ -150,13 +150,18 @@ __device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16
 
 __device__ __forceinline__ int pair_token_row(int i, int hh) { return 8 * (i >> 2) + 4 * hh + (i & 3); }
 
-// X^T operand: rows p[k ld] for k = 0..3, 8..11 of one LDS column (p = row 16g + 4hh).
+// X^T operand: rows p[k ld] for k = 0..3, 8..11 of one LDS column (p = row 16g + 4hh).  Each
+// 32-bit word is filled half by half (16-bit loads into the low / high half of a register).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 column8(const uint16_t* p, int ld) {
   u32x4 v;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int k0 = 8 * (q >> 1) + 2 * (q & 1);
-    v[q] = static_cast<uint32_t>(p[k0 * ld]) | (static_cast<uint32_t>(p[(k0 + 1) * ld]) << 16);
+    u16x2 w;
+    w.x = p[k0 * ld];
+    w.y = p[(k0 + 1) * ld];
+    v[q] = __builtin_bit_cast(uint32_t, w);
   }
   return v;
 }
@@ -265,6 +270,70 @@ __device__ __forceinline__ void pair_chunk(const u32x4 (&Pu)[KS], const u32x4 (&
     for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(mb, s), W[mb]);
 }
 
+// The whole channel side of a pair (NCH chunks, weights in registers), software-pipelined: the
+// U'/V' MFMAs of chunk ec + 1 are issued ahead of the SiLU of chunk ec and interleaved with
+// it, so the matrix core and the vector unit of one wave work at the same time.
+// fu(ec, ks), fv(ec, ks), fo(ec, mb, s) return fragments.
+template <class Ty, int KS, int MB, int NCH, class FU, class FV, class FO>
+__device__ __forceinline__ void pair_channel_pipelined(const u32x4 (&Pu)[KS], const u32x4 (&Pv)[KS], FU fu, FV fv,
+                                                       FO fo, f32x16 (&W)[MB]) {
+  f32x16 U[2], V[2];
+  auto uv = [&](int ec, f32x16& u, f32x16& v) {
+    u = f32x16{};
+    v = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u = Ty::mma32(fu(ec, ks), Pu[ks], u);
+      v = Ty::mma32(fv(ec, ks), Pv[ks], v);
+    }
+  };
+  uv(0, U[0], V[0]);
+#pragma unroll
+  for (int ec = 0; ec < NCH; ++ec) {
+    const int cur = ec & 1;
+    if (ec + 1 < NCH) uv(ec + 1, U[cur ^ 1], V[cur ^ 1]);
+    u32x4 Z[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        Z[s][q] = Ty::pack2(silu_gate(U[cur][8 * s + 2 * q], V[cur][8 * s + 2 * q]),
+                            silu_gate(U[cur][8 * s + 2 * q + 1], V[cur][8 * s + 2 * q + 1]));
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(ec, mb, s), W[mb]);
+    if (ec + 1 < NCH) {
+      // 2 KS MFMAs of the next chunk spread over the gate's ~100 VALU instructions, then the
+      // 2 MB MFMAs of this chunk's W update.
+#pragma unroll
+      for (int i = 0; i < 2 * KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
+    }
+  }
+}
+
+// Output of one 32-channel block of a pair: dl (lane = channel, register i = token kord(i)) is
+// rounded to Ty; with RESIDUAL, x (the lane's token-side operands xk[0], xk[1], same tokens in
+// the same order) is added and the sum rounded again, the reference's two rounding points
+// (omniweave/models/block.py:87-108).  dst(i) is the element address of register i.
+template <class Ty, bool RESIDUAL, class Dst>
+__device__ __forceinline__ void pair_store_block(const f32x16& dl, const u32x4 (&xk)[2], Dst dst) {
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    uint32_t v = Ty::pack2(dl[i], dl[i + 1]);
+    if constexpr (RESIDUAL) {
+      const uint32_t xp = xk[i >> 3][(i & 7) >> 1];
+      v = Ty::pack2(Ty::to_f32(lo16(xp)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(xp)) + Ty::to_f32(hi16(v)));
+    }
+    *dst(i) = lo16(v);
+    *dst(i + 1) = hi16(v);
+  }
+}
+
 // delta[mb] = A_o W[mb] for the pair; ao is the lane's A_o operand row (K step of its group).
 template <class Ty, int MB>
 __device__ __forceinline__ void pair_output(const f32x16 (&W)[MB], u32x4 ao, int lane, f32x16 (&dl)[MB]) {
@@ -291,8 +360,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 struct ResidentArgs {
   const uint16_t* x;
   uint16_t* out;
-  const float* gamma;      // [C]
-  const uint16_t* packed;  // packed weights (same layout as the streamed kernel)
+  const uint16_t* packed;  // packed weights, LayerScale folded (same layout as the streamed kernel)
   const int32_t* tok;      // [q_s * 16]
   const int32_t* chan;     // [q_c * 64]
   int32_t batch, n_tok, channels, q_s, q_c;

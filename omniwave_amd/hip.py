@@ -74,7 +74,7 @@ def hip_is_supported(x: Tensor, plan: RoutePlan, b_u: Tensor) -> tuple[bool, str
 
 
 class _PackEntry:
-    __slots__ = ("refs", "versions", "packed", "gamma")
+    __slots__ = ("refs", "versions", "packed")
 
 
 _PACK_CACHE: OrderedDict[tuple, _PackEntry] = OrderedDict()
@@ -93,11 +93,12 @@ def _stream_ptr(device: torch.device) -> int:
 
 
 def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_weight: Tensor | None = None,
-                 plan: RoutePlan | None = None) -> Tensor:
+                 plan: RoutePlan | None = None, gamma: Tensor | None = None) -> Tensor:
     """Pack the six BiGEMM weights into the kernel's MFMA operand order (uint8 buffer).
 
-    With ``norm_weight`` (and the block's ``plan``, whose channel table routes it), the
-    RMSNorm weight is folded into the B_u / B_v rows, as OW_FUSE_NORM expects.
+    With the block's ``plan`` (whose channel table routes per-channel vectors), the LayerScale
+    ``gamma`` is folded into the B_o columns and ``norm_weight`` (the RMSNorm weight) into the
+    B_u / B_v rows, as OW_FUSE_NORM expects; pad channels are packed as zero.
     """
     lib = _native.lib()
     ws = [a_u, a_v, a_o, b_u, b_v, b_o]
@@ -115,17 +116,23 @@ def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_
     if nbytes == 0:
         raise ValueError(f"unsupported packing shape q_c={q_c}, d={d}, rd={rd}")
     packed = torch.empty(nbytes, dtype=torch.uint8, device=b_u.device)
-    nw_ptr = ch_ptr = 0
+    nw_ptr = gm_ptr = ch_ptr = 0
     channels = q_c * d
-    if norm_weight is not None:
+    keep = []  # fp32 copies alive until the pack kernel is queued
+    if norm_weight is not None or gamma is not None:
         if plan is None:
-            raise ValueError("folding norm_weight needs the block's route plan")
-        nw = norm_weight.detach().to(device=b_u.device, dtype=torch.float32).contiguous()
+            raise ValueError("folding norm_weight / gamma needs the block's route plan")
         ch = device_tables(plan, b_u.device)[1]
-        nw_ptr, ch_ptr, channels = nw.data_ptr(), ch.data_ptr(), plan.channels
+        ch_ptr, channels = ch.data_ptr(), plan.channels
+        if norm_weight is not None:
+            keep.append(norm_weight.detach().to(device=b_u.device, dtype=torch.float32).contiguous())
+            nw_ptr = keep[-1].data_ptr()
+        if gamma is not None:
+            keep.append(gamma.detach().to(device=b_u.device, dtype=torch.float32).contiguous())
+            gm_ptr = keep[-1].data_ptr()
     with torch.cuda.device(b_u.device):
         _native.check(
-            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], nw_ptr, ch_ptr, channels,
+            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], nw_ptr, gm_ptr, ch_ptr, channels,
                                 SPATIAL_TILE, q_c, d, rd, cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
             "ow_pack_weights",
         )
@@ -140,17 +147,16 @@ def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_d
     if (entry is not None and None not in versions and entry.versions == versions
             and all(r() is t for r, t in zip(entry.refs, srcs))):
         _PACK_CACHE.move_to_end(key)
-        return entry.packed, entry.gamma
+        return entry.packed
     entry = _PackEntry()
     entry.refs = tuple(weakref.ref(t) for t in srcs)
     entry.versions = versions
-    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, norm_weight, plan)
-    entry.gamma = gamma.detach().float().contiguous()
+    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, norm_weight, plan, gamma)
     if None not in versions:
         _PACK_CACHE[key] = entry
         while len(_PACK_CACHE) > _PACK_CACHE_SIZE:
             _PACK_CACHE.popitem(last=False)
-    return entry.packed, entry.gamma
+    return entry.packed
 
 
 def clear_pack_cache() -> None:
@@ -192,9 +198,7 @@ def bigemm_fwd(
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
     if fuse_norm and norm_weight is None:
         raise ValueError("OW_FUSE_NORM needs norm_weight")
-    packed, gamma32 = _cached_operands(
-        norm_weight if fuse_norm else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan
-    )
+    packed = _cached_operands(norm_weight if fuse_norm else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan)
     tok, ch = device_tables(plan, x.device)
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     native_plan = plan.native()
@@ -204,7 +208,7 @@ def bigemm_fwd(
     with torch.cuda.device(x.device):
         _native.check(
             lib.ow_bigemm_fwd(
-                x.data_ptr(), out.data_ptr(), eps, gamma32.data_ptr(), packed.data_ptr(), packed.numel(),
+                x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
                 tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), x.shape[0], b_u.shape[2],
                 _DTYPE_CODE[x.dtype], flags, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
             ),

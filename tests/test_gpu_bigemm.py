@@ -193,7 +193,9 @@ def test_unaligned_input_uses_element_path(stage, route, level) -> None:
     got = bigemm_delta_hip(x=xd, plan=plan, **dp)
     assert rel_l2(got.cpu(), oracle_delta(x, plan, params, torch.bfloat16)) <= 1e-2
     aligned = bigemm_delta_hip(x=x.to(DEV), plan=plan, **dp)
-    assert torch.equal(got, aligned)  # same arithmetic, different memory access
+    # The aligned input may run the other kernel (d=64: expanded dim split over two waves), whose
+    # fp32 sums associate differently: equal up to the last bf16 place, not bitwise.
+    assert rel_l2(got.cpu(), aligned.cpu()) <= 2e-3
     delta = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp, residual=False)
     out = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp)
     torch.cuda.synchronize()

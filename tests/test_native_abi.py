@@ -64,7 +64,7 @@ def test_fwd_rejects_bad_arguments_without_touching_the_gpu() -> None:
     bf16 = _native.OW_DTYPE_BF16
 
     def fwd(x, out, packed_bytes, p, rd=256, flags=0, ws=None, ws_bytes=0):
-        return lib.ow_bigemm_fwd(x, out, 1e-6, P, P, packed_bytes, P, P, ctypes.byref(p), 1, rd, bf16, flags,
+        return lib.ow_bigemm_fwd(x, out, 1e-6, P, packed_bytes, P, P, ctypes.byref(p), 1, rd, bf16, flags,
                                  ws, ws_bytes, None)
 
     P = None
