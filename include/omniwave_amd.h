@@ -150,6 +150,63 @@ int ow_bigemm_fwd(const void* x, void* out, float eps,
                   const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
                   int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Backward building blocks.  Replace the fp32 autograd recompute of the accelerated backend
+ * (omniweave/ops/triton.py:256-292); the plain channel-side GEMMs between them are the
+ * caller's (batched hipBLASLt).  Notation: slots = batch * Q_s * 16 token slots per channel
+ * group (pad slots included), tensors [Q_c][slots][d] are slot-major, compute dtype `dtype`.
+ */
+
+/* Folded weights as plain matrices: B_u'' = -log2(e) w B_u and B_v'' = -ln(2) w B_v
+ * ([q_c][d][rd] and transposed [q_c][rd][d]), B_o'' = B_o diag(gamma) ([q_c][rd][d] and
+ * transposed [q_c][d][rd]); w = norm_weight (NULL: 1), pad channels 0. */
+int ow_fold_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype,
+                    const float* norm_weight, const float* gamma, const int32_t* channel_index,
+                    int32_t channels, int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype,
+                    void* bu, void* bu_t, void* bv, void* bv_t, void* bo, void* bo_t, void* stream);
+
+/* Routed tiles of x * r (r = rscale per row, NULL: 1) and of dy into [Q_c][slots][d]
+ * (pack_tiles, omniweave/ops/reference.py:16-64, for both tensors; pads 0). */
+int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                  const int32_t* channel_index, const OwPlan* plan, int32_t batch, int32_t dtype,
+                  void* xt, void* dyt, void* stream);
+
+/* SiLU-gate backward over n folded values: z = u v s, du = dz v s (1 - ln2 u (1 - s)),
+ * dv = dz u s with s = 1 / (1 + 2^u) (SiLU(U) V and its gradient, reference.py:159). */
+int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du, void* dv, int64_t n,
+                int32_t dtype, void* stream);
+
+/* [Q_c][slots][d] tiles -> g [batch * H * W, C] fp32 at their routed positions
+ * (unpack_tiles, reference.py:67-117; pads dropped). */
+int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* channel_index,
+                   const OwPlan* plan, int32_t batch, int32_t dtype, float* g, void* stream);
+
+/* Token mixing of 16-row tiles (the A_{u,v,o} products of reference.py:155-162 and their
+ * transposes): out_tile = m1 in1_tile (+ m2 in2_tile when in2 is non-NULL); m1, m2 [16][16]
+ * fp32 row-major on the device; in/out [n_tiles][16][d], d % 16 == 0. */
+int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* m2, void* out,
+                int64_t n_tiles, int32_t d, int32_t dtype, void* stream);
+
+/* Gradient of a token matrix: partial[w] = sum over the tiles of wave w of in1_tile in2_tile^T
+ * ([16][16] fp32 each, w < n_waves, tiles assigned round-robin); the caller sums the
+ * n_waves partials (a fixed order, so the result is deterministic). */
+int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_waves, int64_t n_tiles,
+                  int32_t d, int32_t dtype, void* stream);
+
+/* Per row: dx = (residual ? dout : 0) + r g - x r^3 / C sum_c(g x) with rscale, or + g
+ * without it (the RMSNorm and residual of omniweave/models/block.py:83-108). */
+int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx,
+                   int64_t rows, int32_t channels, int32_t residual, int32_t dtype, void* stream);
+
+/* Parameter gradients from the folded ones (dbu, dbv [q_c][d][rd], dbo [q_c][rd][d], fp32):
+ * g_bu, g_bv, g_bo (fp32, parameter shapes), g_gamma [C] and, with norm_weight, g_norm_weight
+ * [C] (each channel written once). */
+int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype,
+                  const float* norm_weight, const float* gamma, const int32_t* channel_index,
+                  int32_t channels, int32_t q_c, int32_t d, int32_t rd, const float* dbu,
+                  const float* dbv, const float* dbo, float* g_bu, float* g_bv, float* g_bo,
+                  float* g_gamma, float* g_norm_weight, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,37 @@ _SIGNATURES = {
             ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ],
     ),
+    "ow_fold_weights": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        + [ctypes.c_int32] * 5 + [ctypes.c_void_p] * 7,
+    ),
+    "ow_bwd_gather": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 5 + [ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32] + [ctypes.c_void_p] * 3,
+    ),
+    "ow_bwd_gate": (ctypes.c_int, [ctypes.c_void_p] * 6 + [ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]),
+    "ow_bwd_scatter": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 3 + [ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                 ctypes.c_void_p],
+    ),
+    "ow_bwd_rmsnorm": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "ow_tile_mix": (
+        ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "ow_tile_outer": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "ow_bwd_params": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        + [ctypes.c_int32] * 4 + [ctypes.c_void_p] * 9,
+    ),
 }
 
 _lock = threading.Lock()

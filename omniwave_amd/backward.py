@@ -1,0 +1,175 @@
+"""Backward of the fused BiGEMM block (dX, dA_u/v/o, dB_u/v/o, dgamma, dnorm_weight).
+
+Replaces the fp32 autograd recompute of the accelerated backend
+(omniweave/ops/triton.py:256-292).  The pass runs in the forward's compute dtype with fp32
+accumulation, entirely on the HIP stream of the gradient:
+
+* routing, RMSNorm, gate and parameter fold-back are the libomniwave_amd.so kernels
+  (``ow_bwd_gather``, ``ow_bwd_gate``, ``ow_bwd_scatter``, ``ow_bwd_rmsnorm``,
+  ``ow_bwd_params``, ``ow_fold_weights``);
+* the 16x16 token-side products are ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA);
+* the channel-side products are plain batched GEMMs over all slots of a channel group
+  (``torch.bmm`` -> hipBLASLt), every right operand contiguous.
+
+Gradients are formed for the folded operands the forward evaluates (B_u'' = -log2(e) w B_u,
+B_v'' = -ln(2) w B_v, B_o'' = B_o diag(gamma), SiLU(U) V = U'V' / (1 + 2^U')) and mapped back
+to the parameters by ``ow_bwd_params``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from omniwave_amd import _native
+from omniwave_amd.routing import RoutePlan, device_tables
+
+_DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
+               torch.float16: _native.OW_DTYPE_F16}
+# Waves of ow_tile_outer: each sums a strided share of the tiles into one [16][16] partial.
+_OUTER_WAVES = 1024
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _tile_mix(lib, in1: Tensor, m1: Tensor, in2: Tensor | None, m2: Tensor | None, d: int, code: int,
+              stream: int) -> Tensor:
+    out = torch.empty_like(in1)
+    n_tiles = in1.numel() // (16 * d)
+    _native.check(lib.ow_tile_mix(in1.data_ptr(), m1.data_ptr(), in2.data_ptr() if in2 is not None else None,
+                                  m2.data_ptr() if m2 is not None else None, out.data_ptr(), n_tiles, d, code,
+                                  stream), "ow_tile_mix")
+    return out
+
+
+def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -> Tensor:
+    n_tiles = in1.numel() // (16 * d)
+    partial = torch.empty(_OUTER_WAVES, 16, 16, dtype=torch.float32, device=in1.device)
+    _native.check(lib.ow_tile_outer(in1.data_ptr(), in2.data_ptr(), partial.data_ptr(), _OUTER_WAVES, n_tiles, d,
+                                    code, stream), "ow_tile_outer")
+    return partial.sum(dim=0)
+
+
+def _fp32(t: Tensor, device) -> Tensor:
+    return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
+                    a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float):
+    """Gradients of ``bigemm_fwd(x, norm_weight, gamma, a_u, .., b_o, plan, flags, eps)``.
+
+    Returns ``(dx, d_norm_weight, d_gamma, d_a_u, d_a_v, d_a_o, d_b_u, d_b_v, d_b_o)``, each in
+    its input's dtype (``d_norm_weight`` is None without OW_FUSE_NORM).
+    """
+    lib = _native.lib()
+    dev = x.device
+    dtype = x.dtype
+    code = _DTYPE_CODE[dtype]
+    fuse_norm = bool(flags & _native.OW_FUSE_NORM)
+    residual = bool(flags & _native.OW_FUSE_RESIDUAL)
+    x = x.contiguous()
+    grad = grad.to(dtype).contiguous()
+    batch = x.shape[0]
+    q_c, d, rd = b_u.shape
+    q_s = plan.token_indices.shape[0]
+    slots = batch * q_s * 16
+    n_rows = batch * plan.height * plan.width
+    tok, ch = device_tables(plan, dev)
+    native_plan = plan.native()
+    stream = _stream(dev)
+
+    ws = [w.detach().contiguous() for w in (b_u, b_v, b_o)]
+    wdtype = ws[0].dtype
+    if any(w.dtype != wdtype for w in ws) or wdtype not in _DTYPE_CODE:
+        wdtype = torch.float32
+        ws = [w.float() for w in ws]
+    nw = _fp32(norm_weight, dev) if fuse_norm else None
+    gm = _fp32(gamma, dev)
+    au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
+    au_t, av_t, ao_t = (a.t().contiguous() for a in (au, av, ao))
+
+    with torch.cuda.device(dev):
+        rscale = None
+        if fuse_norm:
+            rscale = torch.empty(n_rows, dtype=torch.float32, device=dev)
+            _native.check(lib.ow_rms_scale(x.data_ptr(), rscale.data_ptr(), n_rows, plan.channels, eps, code,
+                                           stream), "ow_rms_scale")
+
+        # Folded weights in the compute dtype, plain and transposed (both contiguous).
+        bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
+        bv, bo_t = torch.empty_like(bu), torch.empty_like(bu)
+        bu_t = torch.empty(q_c, rd, d, dtype=dtype, device=dev)
+        bv_t, bo = torch.empty_like(bu_t), torch.empty_like(bu_t)
+        _native.check(lib.ow_fold_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                          nw.data_ptr() if nw is not None else None, gm.data_ptr(), ch.data_ptr(),
+                                          plan.channels, q_c, d, rd, code, bu.data_ptr(), bu_t.data_ptr(),
+                                          bv.data_ptr(), bv_t.data_ptr(), bo.data_ptr(), bo_t.data_ptr(), stream),
+                      "ow_fold_weights")
+
+        # Routed tiles of X' = x r and of dY.
+        xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
+        dyt = torch.empty_like(xt)
+        _native.check(lib.ow_bwd_gather(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale is not None
+                                        else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), batch,
+                                        code, xt.data_ptr(), dyt.data_ptr(), stream), "ow_bwd_gather")
+
+        # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
+        pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
+        pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
+        dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
+
+        # Channel side and gate.
+        u = torch.bmm(pu, bu)
+        v = torch.bmm(pv, bv)
+        dz = torch.bmm(dw, bo_t)
+        z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
+        _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                      dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
+        del u, v, dz
+        d_bu = torch.bmm(pu.transpose(1, 2), du).float()   # [q_c, d, rd]
+        d_bv = torch.bmm(pv.transpose(1, 2), dv).float()
+        d_bo = torch.bmm(z.transpose(1, 2), dw).float()    # [q_c, rd, d]
+        wp = torch.bmm(z, bo)
+        dpu = torch.bmm(du, bu_t)
+        dpv = torch.bmm(dv, bv_t)
+        del z, du, dv, pu, pv, dw
+
+        # Token-matrix gradients and dX'.
+        g_au = _tile_outer(lib, dpu, xt, d, code, stream)
+        g_av = _tile_outer(lib, dpv, xt, d, code, stream)
+        g_ao = _tile_outer(lib, dyt, wp, d, code, stream)
+        dxt = _tile_mix(lib, dpu, au_t, dpv, av_t, d, code, stream)
+        del dpu, dpv, wp, xt, dyt
+
+        # dX' back to NHWC, then through the RMSNorm (+ the residual's identity).
+        g = torch.zeros(n_rows, plan.channels, dtype=torch.float32, device=dev)
+        _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan),
+                                         batch, code, g.data_ptr(), stream), "ow_bwd_scatter")
+        dx = torch.empty_like(x)
+        _native.check(lib.ow_bwd_rmsnorm(x.data_ptr(), g.data_ptr(), rscale.data_ptr() if rscale is not None
+                                         else None, grad.data_ptr(), dx.data_ptr(), n_rows, plan.channels,
+                                         int(residual), code, stream), "ow_bwd_rmsnorm")
+
+        # Parameter gradients from the folded ones.
+        g_bu = torch.empty(q_c, d, rd, dtype=torch.float32, device=dev)
+        g_bv = torch.empty_like(g_bu)
+        g_bo = torch.empty(q_c, rd, d, dtype=torch.float32, device=dev)
+        g_gamma = torch.zeros(plan.channels, dtype=torch.float32, device=dev)
+        g_nw = torch.zeros(plan.channels, dtype=torch.float32, device=dev) if fuse_norm else None
+        _native.check(lib.ow_bwd_params(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                        nw.data_ptr() if nw is not None else None, gm.data_ptr(), ch.data_ptr(),
+                                        plan.channels, q_c, d, rd, d_bu.data_ptr(), d_bv.data_ptr(), d_bo.data_ptr(),
+                                        g_bu.data_ptr(), g_bv.data_ptr(), g_bo.data_ptr(), g_gamma.data_ptr(),
+                                        g_nw.data_ptr() if g_nw is not None else None, stream), "ow_bwd_params")
+
+    return (
+        dx,
+        g_nw.to(norm_weight.dtype) if g_nw is not None else None,
+        g_gamma.to(gamma.dtype),
+        g_au.to(a_u.dtype), g_av.to(a_v.dtype), g_ao.to(a_o.dtype),
+        g_bu.to(b_u.dtype), g_bv.to(b_v.dtype), g_bo.to(b_o.dtype),
+    )

@@ -1,0 +1,478 @@
+// BiGEMM backward: the routing, gating and normalisation parts as HIP kernels; the channel
+// products are plain batched GEMMs the caller runs between them (hipBLASLt).
+//
+// Gradients are taken with respect to the folded weights the forward evaluates (per channel
+// group q, token slot k of the flattened (image, token group, row) order, channel c < d,
+// expanded row e < rd):
+//     X'   = x r                          (r = RMSNorm row scale, 1 without the norm)
+//     P_u  = A_u X'_tile,  P_v = A_v X'_tile                      (token mixing per 16-row tile)
+//     U'   = P_u B_u'',  V' = P_v B_v''   B_u'' = -log2(e) w B_u, B_v'' = -ln(2) w B_v
+//     Z    = U'V' s,  s = 1 / (1 + 2^U')  (= SiLU(U) V, omniweave/ops/reference.py:155-159)
+//     W'   = Z B_o'',  B_o'' = B_o diag(gamma)
+//     delta = A_o W'_tile                                          (reference.py:162-171)
+// Backward for dY = d delta:
+//     dW' = A_o^T dY_tile,  dZ = dW' B_o''^T
+//     dU' = dZ V' s (1 - ln2 U' (1 - s)),  dV' = dZ U' s                   (bwd_gate_kernel)
+//     dB_u'' = P_u^T dU', dB_v'' = P_v^T dV', dB_o'' = Z^T dW'             (GEMMs)
+//     dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,  dX' = A_u^T dP_u + A_v^T dP_v   (GEMMs)
+//     dx = r g - x r^3 / C sum_c(g x),  g = dX' scattered to NHWC    (bwd_rmsnorm_kernel)
+// and the parameter gradients follow from the folded ones (bwd_params_kernel).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ow_device.h"
+
+namespace ow {
+namespace {
+
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == OW_DTYPE_F32) return static_cast<const float*>(p)[i];
+  const uint16_t u = static_cast<const uint16_t*>(p)[i];
+  return dtype == OW_DTYPE_BF16 ? BF16::to_f32(u) : F16::to_f32(u);
+}
+
+// Slot k = (tile, row t) of a channel group -> NHWC row (b * N + token), -1 for pads.
+__device__ __forceinline__ int64_t slot_row(const int32_t* tok, int64_t k, int32_t q_s, int32_t n_tok) {
+  const int64_t tile = k >> 4;
+  const int32_t t = static_cast<int32_t>(k & 15);
+  const int64_t b = tile / q_s;
+  const int32_t s = static_cast<int32_t>(tile - b * q_s);
+  const int32_t tk = tok[s * kG + t];
+  return (tk >= 0 && tk < n_tok) ? b * n_tok + tk : -1;
+}
+
+struct GatherArgs {
+  const uint16_t* x;
+  const uint16_t* dy;
+  const float* rscale;  // NULL: 1
+  const int32_t* tok;
+  const int32_t* chan;
+  uint16_t* xt;   // [q_c][slots][d]: x * r (pads 0)
+  uint16_t* dyt;  // [q_c][slots][d]: dy (pads 0)
+  int64_t slots;  // batch * q_s * 16
+  int32_t n_tok, channels, q_s, d;
+};
+
+// One thread per (q, slot, channel).
+template <class Ty>
+__global__ void __launch_bounds__(256) bwd_gather_kernel(GatherArgs a, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int32_t c = static_cast<int32_t>(i % a.d);
+  const int64_t qk = i / a.d;
+  const int64_t k = qk % a.slots;
+  const int32_t q = static_cast<int32_t>(qk / a.slots);
+  const int64_t row = slot_row(a.tok, k, a.q_s, a.n_tok);
+  const int32_t ch = a.chan[q * a.d + c];
+  uint16_t xv = 0, dv = 0;
+  if (row >= 0 && ch >= 0 && ch < a.channels) {
+    const int64_t off = row * a.channels + ch;
+    const float r = a.rscale ? a.rscale[row] : 1.0f;
+    xv = Ty::from_f32(Ty::to_f32(a.x[off]) * r);
+    dv = a.dy[off];
+  }
+  a.xt[i] = xv;
+  a.dyt[i] = dv;
+}
+
+// Elementwise gate backward over n values (folded operands, see the file comment).
+template <class Ty>
+__global__ void __launch_bounds__(256) bwd_gate_kernel(const uint16_t* u, const uint16_t* v, const uint16_t* dz,
+                                                       uint16_t* z, uint16_t* du, uint16_t* dv, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float up = Ty::to_f32(u[i]), vp = Ty::to_f32(v[i]), g = Ty::to_f32(dz[i]);
+  const float s = 1.0f / (1.0f + exp2f(up));
+  z[i] = Ty::from_f32(up * vp * s);
+  du[i] = Ty::from_f32(g * vp * s * (1.0f - kLn2 * up * (1.0f - s)));
+  dv[i] = Ty::from_f32(g * up * s);
+}
+
+// dX' slots -> g [rows, C] fp32 (every valid (row, channel) is written exactly once: the routes
+// are permutations of tokens and channels).
+template <class Ty>
+__global__ void __launch_bounds__(256) bwd_scatter_kernel(const uint16_t* dxt, const int32_t* tok, const int32_t* chan,
+                                                          float* g, int64_t slots, int32_t n_tok, int32_t channels,
+                                                          int32_t q_s, int32_t d, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int32_t c = static_cast<int32_t>(i % d);
+  const int64_t qk = i / d;
+  const int64_t k = qk % slots;
+  const int32_t q = static_cast<int32_t>(qk / slots);
+  const int64_t row = slot_row(tok, k, q_s, n_tok);
+  const int32_t ch = chan[q * d + c];
+  if (row >= 0 && ch >= 0 && ch < channels) g[row * channels + ch] = Ty::to_f32(dxt[i]);
+}
+
+// One wave per row: dx = (dout) + r g - x r^3 / C sum(g x)   (norm)   or   (dout) + g.
+template <class Ty>
+__global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, const float* g, const float* rscale,
+                                                          const uint16_t* dout, uint16_t* dx, int64_t rows,
+                                                          int32_t channels, int32_t residual) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * channels;
+  const float* gr = g + row * channels;
+  float r = 1.0f, coef = 0.0f;
+  if (rscale) {
+    r = rscale[row];
+    float dot = 0.0f;
+    for (int c = lane; c < channels; c += 64) dot = fmaf(gr[c], Ty::to_f32(xr[c]), dot);
+    for (int m = 32; m > 0; m >>= 1) dot += __shfl_xor(dot, m);
+    coef = dot * r * r * r / static_cast<float>(channels);
+  }
+  for (int c = lane; c < channels; c += 64) {
+    float v = r * gr[c] - coef * Ty::to_f32(xr[c]);
+    if (residual) v += Ty::to_f32(dout[row * channels + c]);
+    dx[row * channels + c] = Ty::from_f32(v);
+  }
+}
+
+struct FoldArgs {
+  const void* b_u;
+  const void* b_v;
+  const void* b_o;
+  const float* norm_w;  // NULL: 1
+  const float* gamma;   // NULL: 1
+  const int32_t* chan;
+  uint16_t* bu;   // [q][d][rd]  B_u''
+  uint16_t* buT;  // [q][rd][d]  B_u''^T
+  uint16_t* bv;
+  uint16_t* bvT;
+  uint16_t* bo;   // [q][rd][d]  B_o''
+  uint16_t* boT;  // [q][d][rd]  B_o''^T
+  int32_t wdtype, q_c, d, rd, channels;
+};
+
+// One thread per (q, c, e).
+template <class Ty>
+__global__ void __launch_bounds__(256) fold_weights_kernel(FoldArgs a, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int32_t e = static_cast<int32_t>(i % a.rd);
+  const int64_t qc = i / a.rd;
+  const int32_t c = static_cast<int32_t>(qc % a.d);
+  const int32_t q = static_cast<int32_t>(qc / a.d);
+  const int32_t ch = a.chan[q * a.d + c];
+  const bool ok = ch >= 0 && ch < a.channels;
+  const float w = ok ? (a.norm_w ? a.norm_w[ch] : 1.0f) : 0.0f;
+  const float gm = ok ? (a.gamma ? a.gamma[ch] : 1.0f) : 0.0f;
+  const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;  // [q][c][e]
+  const int64_t ec = (static_cast<int64_t>(q) * a.rd + e) * a.d + c;  // [q][e][c]
+  const uint16_t u = Ty::from_f32(load_any(a.b_u, cd, a.wdtype) * w * kNegLog2e);
+  const uint16_t v = Ty::from_f32(load_any(a.b_v, cd, a.wdtype) * w * kNegLn2);
+  const uint16_t o = Ty::from_f32(load_any(a.b_o, ec, a.wdtype) * gm);
+  a.bu[cd] = u;
+  a.buT[ec] = u;
+  a.bv[cd] = v;
+  a.bvT[ec] = v;
+  a.bo[ec] = o;
+  a.boT[cd] = o;
+}
+
+struct ParamArgs {
+  const void* b_u;
+  const void* b_v;
+  const void* b_o;
+  const float* norm_w;  // NULL: no RMSNorm weight (its gradient is not produced)
+  const float* gamma;   // NULL: 1
+  const int32_t* chan;
+  const float* dbu;  // [q][d][rd] dB_u''
+  const float* dbv;
+  const float* dbo;  // [q][rd][d] dB_o''
+  float* g_bu;       // [q][d][rd]
+  float* g_bv;
+  float* g_bo;       // [q][rd][d]
+  float* g_gamma;    // [C]
+  float* g_norm_w;   // [C] or NULL
+  int32_t wdtype, q_c, d, rd, channels;
+};
+
+// One thread per (q, c): the folded gradients mapped back to the parameters.
+__global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.q_c) * a.d) return;
+  const int32_t c = static_cast<int32_t>(i % a.d);
+  const int32_t q = static_cast<int32_t>(i / a.d);
+  const int32_t ch = a.chan[q * a.d + c];
+  const bool ok = ch >= 0 && ch < a.channels;
+  const float w = ok ? (a.norm_w ? a.norm_w[ch] : 1.0f) : 0.0f;
+  const float gm = ok ? (a.gamma ? a.gamma[ch] : 1.0f) : 0.0f;
+  float sum_w = 0.0f, sum_g = 0.0f;
+  for (int32_t e = 0; e < a.rd; ++e) {
+    const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;
+    const int64_t ec = (static_cast<int64_t>(q) * a.rd + e) * a.d + c;
+    const float du = a.dbu[cd], dv = a.dbv[cd], dob = a.dbo[ec];
+    a.g_bu[cd] = du * kNegLog2e * w;
+    a.g_bv[cd] = dv * kNegLn2 * w;
+    a.g_bo[ec] = dob * gm;
+    sum_w += du * kNegLog2e * load_any(a.b_u, cd, a.wdtype) + dv * kNegLn2 * load_any(a.b_v, cd, a.wdtype);
+    sum_g += dob * load_any(a.b_o, ec, a.wdtype);
+  }
+  if (ok) {
+    a.g_gamma[ch] = sum_g;
+    if (a.g_norm_w) a.g_norm_w[ch] = sum_w;
+  }
+}
+
+// Token mixing per 16-row tile: out = M1 in1 (+ M2 in2), M* [16][16] fp32, in/out tiles
+// [16][d] of the compute dtype.  One wave per tile, 16x16x16 MFMAs: A operand lane (l16, h)
+// slot j = M[l16][4h + j], B operand = in[4h + j][16 cb + l16].
+template <class Ty, bool TWO>
+__global__ void __launch_bounds__(256) tile_mix_kernel(const uint16_t* in1, const float* m1, const uint16_t* in2,
+                                                       const float* m2, uint16_t* out, int64_t n_tiles, int32_t d) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (tile >= n_tiles) return;
+  const int l16 = lane & 15, h = lane >> 4;
+  auto a_op = [&](const float* m) {
+    return u32x2{Ty::pack2(m[l16 * 16 + 4 * h + 0], m[l16 * 16 + 4 * h + 1]),
+                 Ty::pack2(m[l16 * 16 + 4 * h + 2], m[l16 * 16 + 4 * h + 3])};
+  };
+  const u32x2 a1 = a_op(m1);
+  u32x2 a2 = {0u, 0u};
+  if constexpr (TWO) a2 = a_op(m2);
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t base = tile * 16 * d;
+  for (int cb = 0; cb < d / 16; ++cb) {
+    auto b_op = [&](const uint16_t* in) {
+      const uint16_t* p = in + base + (4 * h) * d + 16 * cb + l16;
+      return u32x2{static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[d]) << 16),
+                   static_cast<uint32_t>(p[2 * d]) | (static_cast<uint32_t>(p[3 * d]) << 16)};
+    };
+    f32x4 acc = Ty::mma16(a1, b_op(in1), zero);
+    if constexpr (TWO) acc = Ty::mma16(a2, b_op(in2), acc);
+    mfma_drain();
+    uint16_t* o = out + base + 16 * cb + l16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[(4 * h + i) * d] = Ty::from_f32(acc[i]);
+  }
+}
+
+// Sum over tiles of in1_tile in2_tile^T ([16][d] x [d][16] -> [16][16]), grid-strided; each wave
+// writes its partial sum (lane (l16, h) register i = out[4h + i][l16]) to partial[wave][256].
+template <class Ty>
+__global__ void __launch_bounds__(256) tile_outer_kernel(const uint16_t* in1, const uint16_t* in2, float* partial,
+                                                         int64_t n_tiles, int32_t d) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
+  const int l16 = lane & 15, h = lane >> 4;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
+    const int64_t base = tile * 16 * d;
+    for (int ks = 0; ks < d / 16; ++ks) {
+      // A: row l16 of in1, K slots 16 ks + 4h + j; B: column l16 = row l16 of in2, same K.
+      const uint2 av = *reinterpret_cast<const uint2*>(in1 + base + l16 * d + 16 * ks + 4 * h);
+      const uint2 bv = *reinterpret_cast<const uint2*>(in2 + base + l16 * d + 16 * ks + 4 * h);
+      acc = Ty::mma16(u32x2{av.x, av.y}, u32x2{bv.x, bv.y}, acc);
+    }
+  }
+  mfma_drain();
+  float* p = partial + wave * 256;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[(4 * h + i) * 16 + l16] = acc[i];
+}
+
+unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
+
+}  // namespace
+}  // namespace ow
+
+extern "C" {
+
+int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                  const int32_t* channel_index, const OwPlan* plan, int32_t batch, int32_t dtype, void* xt, void* dyt,
+                  void* stream) {
+  int32_t q_s = 0, q_c = 0;
+  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
+  OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
+  OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  if (batch == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(x && dy && token_index && channel_index && xt && dyt, "tensor pointer is NULL");
+  ow::GatherArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(dy), rscale, token_index,
+                   channel_index, static_cast<uint16_t*>(xt), static_cast<uint16_t*>(dyt),
+                   static_cast<int64_t>(batch) * q_s * ow::kG, plan->height * plan->width, plan->channels, q_s,
+                   plan->channel_tile};
+  const int64_t total = static_cast<int64_t>(q_c) * a.slots * a.d;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+  else
+    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_gather_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du, void* dv, int64_t n, int32_t dtype,
+                void* stream) {
+  OW_CHECK_ARG(n >= 0, "n must be >= 0");
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  if (n == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(u && v && dz && z && du && dv, "tensor pointer is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::BF16>, dim3(ow::blocks_for(n)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
+                       mu(z), mu(du), mu(dv), n);
+  else
+    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::F16>, dim3(ow::blocks_for(n)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
+                       mu(z), mu(du), mu(dv), n);
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_gate_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan,
+                   int32_t batch, int32_t dtype, float* g, void* stream) {
+  int32_t q_s = 0, q_c = 0;
+  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
+  OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  if (batch == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(dxt && token_index && channel_index && g, "tensor pointer is NULL");
+  const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
+  const int32_t d = plan->channel_tile;
+  const int64_t total = static_cast<int64_t>(q_c) * slots * d;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* src = static_cast<const uint16_t*>(dxt);
+  const int32_t n_tok = plan->height * plan->width;
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, src,
+                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, total);
+  else
+    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, src,
+                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, total);
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_scatter_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx, int64_t rows,
+                   int32_t channels, int32_t residual, int32_t dtype, void* stream) {
+  OW_CHECK_ARG(rows >= 0 && channels >= 1, "bad shape rows=%lld channels=%d", (long long)rows, channels);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  if (rows == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(x && g && dx && (!residual || dout), "tensor pointer is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+                       static_cast<uint16_t*>(dx), rows, channels, residual);
+  else
+    hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+                       static_cast<uint16_t*>(dx), rows, channels, residual);
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_rmsnorm_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_fold_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype, const float* norm_weight,
+                    const float* gamma, const int32_t* channel_index, int32_t channels, int32_t q_c, int32_t d,
+                    int32_t rd, int32_t compute_dtype, void* bu, void* bu_t, void* bv, void* bv_t, void* bo,
+                    void* bo_t, void* stream) {
+  OW_CHECK_ARG(b_u && b_v && b_o && channel_index && bu && bu_t && bv && bv_t && bo && bo_t, "tensor pointer is NULL");
+  OW_CHECK_ARG(q_c >= 1 && d >= 1 && rd >= 1 && channels >= 1, "bad shape q_c=%d d=%d rd=%d C=%d", q_c, d, rd, channels);
+  OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
+  OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16, "unsupported compute dtype %d",
+                     compute_dtype);
+  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  ow::FoldArgs a{b_u, b_v, b_o, norm_weight, gamma, channel_index, mu(bu), mu(bu_t), mu(bv), mu(bv_t), mu(bo), mu(bo_t),
+                 weight_dtype, q_c, d, rd, channels};
+  const int64_t total = static_cast<int64_t>(q_c) * d * rd;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (compute_dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::fold_weights_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+  else
+    hipLaunchKernelGGL(ow::fold_weights_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+  if (int rc = ow::hip_status(hipGetLastError(), "fold_weights_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* m2, void* out, int64_t n_tiles,
+                int32_t d, int32_t dtype, void* stream) {
+  OW_CHECK_ARG(n_tiles >= 0 && d >= 16 && d % 16 == 0, "bad shape n_tiles=%lld d=%d", (long long)n_tiles, d);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  if (n_tiles == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(in1 && m1 && out && (!in2 == !m2), "tensor pointer is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>((n_tiles + 3) / 4);
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (dtype == OW_DTYPE_BF16) {
+    if (in2)
+      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::BF16, true>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+    else
+      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::BF16, false>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+  } else {
+    if (in2)
+      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::F16, true>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+    else
+      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::F16, false>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+  }
+  if (int rc = ow::hip_status(hipGetLastError(), "tile_mix_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_waves, int64_t n_tiles, int32_t d,
+                  int32_t dtype, void* stream) {
+  OW_CHECK_ARG(n_tiles >= 0 && d >= 16 && d % 16 == 0, "bad shape n_tiles=%lld d=%d", (long long)n_tiles, d);
+  OW_CHECK_ARG(n_waves >= 4 && n_waves % 4 == 0, "n_waves must be a positive multiple of 4 (got %d)", n_waves);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(partial && (n_tiles == 0 || (in1 && in2)), "tensor pointer is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::BF16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial, n_tiles, d);
+  else
+    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::F16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial, n_tiles, d);
+  if (int rc = ow::hip_status(hipGetLastError(), "tile_outer_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype, const float* norm_weight,
+                  const float* gamma, const int32_t* channel_index, int32_t channels, int32_t q_c, int32_t d, int32_t rd,
+                  const float* dbu, const float* dbv, const float* dbo, float* g_bu, float* g_bv, float* g_bo,
+                  float* g_gamma, float* g_norm_weight, void* stream) {
+  OW_CHECK_ARG(b_u && b_v && b_o && channel_index && dbu && dbv && dbo && g_bu && g_bv && g_bo && g_gamma,
+               "tensor pointer is NULL");
+  OW_CHECK_ARG(!norm_weight == !g_norm_weight, "norm_weight and its gradient go together");
+  OW_CHECK_ARG(q_c >= 1 && d >= 1 && rd >= 1 && channels >= 1, "bad shape q_c=%d d=%d rd=%d C=%d", q_c, d, rd, channels);
+  OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
+  ow::ParamArgs a{b_u, b_v, b_o, norm_weight, gamma, channel_index, dbu, dbv, dbo, g_bu, g_bv, g_bo, g_gamma,
+                  g_norm_weight, weight_dtype, q_c, d, rd, channels};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ow::bwd_params_kernel, dim3(ow::blocks_for(static_cast<int64_t>(q_c) * d)), dim3(256), 0, s, a);
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_params_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+}  // extern "C"

@@ -222,11 +222,23 @@ def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_d
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
+def _bigemm_fwd_setup_context(ctx, inputs, output):
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps = inputs
+    ctx.save_for_backward(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o)
+    ctx.plan_desc, ctx.flags, ctx.eps = list(plan_desc), int(flags), float(eps)
+
+
 def _bigemm_fwd_backward(ctx, grad):
-    raise NotImplementedError("omniwave_amd::bigemm_fwd: the hip backward kernels are not built yet")
+    from omniwave_amd.backward import bigemm_backward
+
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o = ctx.saved_tensors
+    grads = bigemm_backward(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o,
+                            _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps)
+    grads = tuple(g if need else None for g, need in zip(grads, ctx.needs_input_grad))
+    return grads + (None, None, None)
 
 
-bigemm_fwd.register_autograd(_bigemm_fwd_backward)
+bigemm_fwd.register_autograd(_bigemm_fwd_backward, setup_context=_bigemm_fwd_setup_context)
 
 
 def _require(x, plan, b_u) -> None:
