@@ -149,6 +149,155 @@ def cpu_baseline(budget_s: float) -> dict:
     }
 
 
+_EAGER_TABLES: dict = {}
+
+
+def eager_reference_delta(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma):
+    """The reference backend's operations (omniweave/ops/reference.py:16-173) as PyTorch-eager
+    GPU ops: zero-padded gather of the routed tiles, the token and channel products left to
+    right, SiLU gate, mask, LayerScale and scatter back to NHWC.  Token products run as 2-D
+    matmuls and channel products as batched ones with contiguous right operands.  This is
+    the PyTorch-eager baseline of the model measurement, never part of the HIP path.
+    """
+    b, h, w, c = x.shape
+    n = h * w
+    g, d = G, plan.channel_tile
+    dev = x.device
+    key = (plan.key(), dev)
+    if key not in _EAGER_TABLES:
+        ch = plan.channel_indices.to(dev)
+        gm_mask = (plan.token_mask[:, :, None, None] & plan.channel_mask[None, None, :, :]).to(dev)
+        _EAGER_TABLES[key] = (plan.token_indices.reshape(-1).to(dev), ch.reshape(-1),
+                              ch.clamp_max(c - 1), plan.channel_mask.to(dev), gm_mask)
+    tok, ch, ch_c, ch_mask, mask = _EAGER_TABLES[key]
+    q_s, q_c, rd = plan.token_indices.shape[0], plan.channel_indices.shape[0], b_u.shape[2]
+    flat = torch.nn.functional.pad(x.reshape(b, n, c), (0, 1, 0, 1))   # pad token n, channel c
+    tiles = flat[:, tok][:, :, ch].view(b, q_s, g, q_c, d)              # gather (reference.py:16-64)
+    tiles = tiles * mask.to(x.dtype)[None]
+    tiles = tiles.permute(3, 0, 1, 4, 2).reshape(q_c * b * q_s * d, g)  # rows (q, b, s, k), cols j
+
+    def token_mix(t, a, cols):  # (A T) per tile, t rows (q, b, s, col) x g
+        out = t @ a.t().contiguous()
+        return out.view(q_c, b * q_s, cols, g).transpose(2, 3).reshape(q_c, b * q_s * g, cols)
+
+    u = torch.bmm(token_mix(tiles, a_u, d), b_u.contiguous())
+    v = torch.bmm(token_mix(tiles, a_v, d), b_v.contiguous())
+    z = torch.nn.functional.silu(u) * v
+    z = z.view(q_c, b * q_s, g, rd).transpose(2, 3).reshape(q_c * b * q_s * rd, g)
+    delta = torch.bmm(token_mix(z, a_o, rd), b_o.contiguous())         # [q_c, b*q_s*g, d]
+    delta = delta.view(q_c, b, q_s, g, d) * mask.permute(2, 0, 1, 3)[:, None].to(delta.dtype)
+    delta = delta * (gamma[ch_c] * ch_mask).to(delta.dtype)[:, None, None, None, :]
+    out = x.new_zeros(b, n + 1, c + 1)                                  # scatter (reference.py:67-117)
+    out[:, tok[:, None], ch[None, :]] = delta.permute(1, 2, 3, 0, 4).reshape(b, q_s * g, q_c * d)
+    return out[:, :n, :c].reshape(b, h, w, c)
+
+
+def model_section(batch: int, steps: int, dev) -> dict:
+    """OmniWeave-T forward inference at `batch` x 3 x 224 x 224 bf16 (seeded random init): the
+    HIP path replayed from a HIP graph, against the same model with every block on the
+    PyTorch-eager reference operations (eager_reference_delta) on the same GPU."""
+    import omniwave_amd
+    from omniwave_amd.bigemm import register_backend
+
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").to(device=dev, dtype=torch.bfloat16).eval()
+    blocks = [blk for stage in model.stages for blk in stage.blocks]
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(batch, 3, 224, 224, generator=gen).to(device=dev, dtype=torch.bfloat16)
+    with torch.inference_mode():
+        for blk in blocks:
+            blk.backend = "hip"
+        ref_logits = model(x)  # packs the weights
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            model.forward_features(x)
+            torch.cuda.current_stream().synchronize()
+            with torch.cuda.graph(graph, stream=stream):
+                feats = model.forward_features(x)["stage4"]
+        torch.cuda.current_stream().wait_stream(stream)
+
+        def hip_step():
+            graph.replay()
+            return model.head(feats.mean(dim=(1, 2)))
+
+        replay_err = 0.0
+        for _ in range(3):  # every replay must reproduce the eager HIP logits
+            replay_err = max(replay_err, (hip_step().float() - ref_logits.float()).abs().max().item())
+        hip_ms = _time_fn(hip_step, steps)
+
+        register_backend("reference", eager_reference_delta)
+        try:
+            for blk in blocks:
+                blk.backend = "reference"
+            eager_logits = model(x)
+            eager_ms = _time_fn(lambda: model(x), max(2, steps // 4))
+        finally:
+            register_backend("reference", None)
+            for blk in blocks:
+                blk.backend = "auto"
+    diff = (ref_logits.float() - eager_logits.float()).norm() / eager_logits.float().norm()
+    return {
+        "workload": f"omniweave_t forward, [{batch}, 3, 224, 224] bf16, random init (seed 0)",
+        "images_per_s": round(batch / (hip_ms * 1e-3), 1),
+        "ms_per_batch": round(hip_ms, 3),
+        "eager_images_per_s": round(batch / (eager_ms * 1e-3), 1),
+        "eager_ms_per_batch": round(eager_ms, 3),
+        "speedup_vs_eager": round(eager_ms / hip_ms, 2),
+        "launch": "hip_graph (stem..stage4), eager pool + head",
+        "graph_replay_max_abs_diff": replay_err,
+        "logits_rel_l2_vs_eager": round(float(diff), 5),
+    }
+
+
+def backward_section(batch: int, steps: int, dev) -> dict:
+    """Fused block forward + backward (dx, dA, dB, dgamma, dnorm_weight) at the 56x56x128 and
+    14x14x512 stage shapes, shifted route, bf16, upstream gradient N(0,1)."""
+    from omniwave_amd.hip import bigemm_block_hip
+
+    out = {}
+    for (name, h, w, c, d) in (STAGES[0], STAGES[2]):
+        plan, x, p, nw = make_inputs(batch, h, w, c, d, "shifted", 0, dev, seed=100)
+        x.requires_grad_(True)
+        params = {k: v.clone().requires_grad_(True) for k, v in p.items()}
+        nw = nw.clone().requires_grad_(True)
+        dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).to(dev, torch.bfloat16)
+
+        def fwd():
+            return bigemm_block_hip(x, nw, plan, **params)
+
+        def fwd_bwd():
+            y = fwd()
+            y.backward(dy)
+
+        with torch.no_grad():
+            fwd_ms = _time_fn(fwd, steps)
+        total_ms = _time_fn(fwd_bwd, steps)
+        flops = case_work(batch, h, w, c, d)[0]
+        out[f"{name}_shifted0"] = {
+            "fwd_ms": round(fwd_ms, 3), "fwd_bwd_ms": round(total_ms, 3),
+            "bwd_ms": round(total_ms - fwd_ms, 3),
+            "fwd_bwd_tflops": round(3 * flops / (total_ms * 1e-3) / 1e12, 1),
+        }
+    return {"workload": f"fused block fwd+bwd, batch {batch}, bf16, eager launches", "flops_rule": "3 x forward",
+            "cases": out}
+
+
+def _time_fn(fn, steps: int) -> float:
+    """Average ms per call over `steps` calls after one warm-up, HIP events on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
 def load_traffic(kernel_case: str) -> int | None:
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), if present."""
     path = ROOT / "profiles" / "traffic.json"
@@ -194,6 +343,11 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=128)
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model-batch", type=int, default=256, help="batch of the OmniWeave-T inference section")
+    ap.add_argument("--no-model", action="store_true", help="skip the OmniWeave-T inference section")
+    ap.add_argument("--no-backward", action="store_true", help="skip the forward + backward section")
+    ap.add_argument("--section", choices=["model", "backward"], default=None,
+                    help="profiling aid: run only this section, print its JSON and exit")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--only", default="", help="comma-separated substrings: run only matching cases "
                     "(profiling aid; the full workload is the default)")
@@ -220,6 +374,12 @@ def main() -> int:
         raise RuntimeError(_native.load_error())
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.section == "model":
+        print(json.dumps({"model": model_section(args.model_batch, args.steps, dev)}), flush=True)
+        return 0
+    if args.section == "backward":
+        print(json.dumps({"backward": backward_section(args.batch, args.steps, dev)}), flush=True)
+        return 0
 
     cases = []
     only = [s for s in args.only.split(",") if s]
@@ -309,6 +469,8 @@ def main() -> int:
         "kernel": dom["kernel"], "case": dom["name"],
         "algorithmic_flops": dom["flops"], "algorithmic_bytes": dom["bytes"],
     }
+    model = None if args.no_model else model_section(args.model_batch, 10, dev)
+    backward = None if args.no_backward else backward_section(args.batch, 10, dev)
     baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
     line = {
         "metric": "BiGEMM fwd TFLOP/s (fused RMSNorm+residual, 4 OmniWeave-T stage shapes x 3 routes)",
@@ -328,6 +490,8 @@ def main() -> int:
                    "launch": "eager" if args.eager else "hip_graph", "setup_ms": round(setup_ms, 1)},
         "per_case": stages,
         "roofline": roofline,
+        "model": model,
+        "backward": backward,
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)
