@@ -285,7 +285,9 @@ def backward_section(batch: int, steps: int, dev) -> dict:
 
 
 def _time_fn(fn, steps: int) -> float:
-    """Average ms per call over `steps` calls after one warm-up, HIP events on the current stream."""
+    """Average ms per call over `steps` calls after two warm-up calls (the second one runs the
+    paths the first one set up, e.g. gradient accumulation), HIP events on the current stream."""
+    fn()
     fn()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)

@@ -166,24 +166,26 @@ int ow_fold_weights(const void* b_u, const void* b_v, const void* b_o, int32_t w
                     void* bu, void* bu_t, void* bv, void* bv_t, void* bo, void* bo_t, void* stream);
 
 /* Routed tiles of x * r (r = rscale per row, NULL: 1) and of dy into [Q_c][slots][d]
- * (pack_tiles, omniweave/ops/reference.py:16-64, for both tensors; pads 0). */
+ * (pack_tiles, omniweave/ops/reference.py:16-64, for both tensors; pads 0).  d % 8 == 0;
+ * xt, dyt 16-byte aligned. */
 int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
                   const int32_t* channel_index, const OwPlan* plan, int32_t batch, int32_t dtype,
                   void* xt, void* dyt, void* stream);
 
 /* SiLU-gate backward over n folded values: z = u v s, du = dz v s (1 - ln2 u (1 - s)),
- * dv = dz u s with s = 1 / (1 + 2^u) (SiLU(U) V and its gradient, reference.py:159). */
+ * dv = dz u s with s = 1 / (1 + 2^u) (SiLU(U) V and its gradient, reference.py:159).
+ * n % 8 == 0; all six buffers 16-byte aligned. */
 int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du, void* dv, int64_t n,
                 int32_t dtype, void* stream);
 
 /* [Q_c][slots][d] tiles -> g [batch * H * W, C] fp32 at their routed positions
- * (unpack_tiles, reference.py:67-117; pads dropped). */
+ * (unpack_tiles, reference.py:67-117; pads dropped).  d % 8 == 0; dxt 16-byte aligned. */
 int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* channel_index,
                    const OwPlan* plan, int32_t batch, int32_t dtype, float* g, void* stream);
 
 /* Token mixing of 16-row tiles (the A_{u,v,o} products of reference.py:155-162 and their
  * transposes): out_tile = m1 in1_tile (+ m2 in2_tile when in2 is non-NULL); m1, m2 [16][16]
- * fp32 row-major on the device; in/out [n_tiles][16][d], d % 16 == 0. */
+ * fp32 row-major on the device; in/out [n_tiles][16][d], d in {64, 128}. */
 int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* m2, void* out,
                 int64_t n_tiles, int32_t d, int32_t dtype, void* stream);
 

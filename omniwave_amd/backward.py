@@ -30,6 +30,8 @@ _DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_D
                torch.float16: _native.OW_DTYPE_F16}
 # Waves of ow_tile_outer: each sums a strided share of the tiles into one [16][16] partial.
 _OUTER_WAVES = 1024
+# Most slot chunks of a parameter-gradient GEMM (see _slot_reduce).
+_SPLITS = 64
 
 
 def _stream(device: torch.device) -> int:
@@ -52,6 +54,22 @@ def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -
     _native.check(lib.ow_tile_outer(in1.data_ptr(), in2.data_ptr(), partial.data_ptr(), _OUTER_WAVES, n_tiles, d,
                                     code, stream), "ow_tile_outer")
     return partial.sum(dim=0)
+
+
+def _slot_reduce(a: Tensor, b: Tensor) -> Tensor:
+    """sum over slots of a^T b per channel group ([q_c, S, m] x [q_c, S, n] -> fp32 [q_c, m, n]).
+
+    The slot axis (hundreds of thousands long) is split into up to _SPLITS chunks of whole
+    tiles that run as separate batch entries of one GEMM, so the launch has q_c * splits
+    output blocks instead of q_c; the chunk results are summed in fp32.
+    """
+    q_c, slots, m = a.shape
+    n = b.shape[2]
+    tiles = slots // 16
+    splits = max(s for s in range(1, min(_SPLITS, tiles) + 1) if tiles % s == 0) if tiles else 1
+    chunk = slots // splits
+    part = torch.bmm(a.view(q_c * splits, chunk, m).transpose(1, 2), b.view(q_c * splits, chunk, n))
+    return part.view(q_c, splits, m, n).float().sum(dim=1)
 
 
 def _fp32(t: Tensor, device) -> Tensor:
@@ -130,9 +148,9 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
         _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
                                       dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
         del u, v, dz
-        d_bu = torch.bmm(pu.transpose(1, 2), du).float()   # [q_c, d, rd]
-        d_bv = torch.bmm(pv.transpose(1, 2), dv).float()
-        d_bo = torch.bmm(z.transpose(1, 2), dw).float()    # [q_c, rd, d]
+        d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
+        d_bv = _slot_reduce(pv, dv)
+        d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
         wp = torch.bmm(z, bo)
         dpu = torch.bmm(du, bu_t)
         dpv = torch.bmm(dv, bv_t)

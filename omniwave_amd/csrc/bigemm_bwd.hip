@@ -54,65 +54,202 @@ struct GatherArgs {
   uint16_t* dyt;  // [q_c][slots][d]: dy (pads 0)
   int64_t slots;  // batch * q_s * 16
   int32_t n_tok, channels, q_s, d;
+  int32_t vec;    // x, dy 16-byte aligned and C % 8 == 0: runs of 8 channels load as one vector
 };
 
-// One thread per (q, slot, channel).
+// Channels chan[0..7] are the aligned run c0..c0+7 of one row (one 16-byte access).
+__device__ __forceinline__ bool channel_run8(const int32_t* chan, int32_t channels) {
+  const int32_t c0 = chan[0];
+  bool run = (c0 & 7) == 0 && c0 + 7 < channels;
+#pragma unroll
+  for (int j = 1; j < 8; ++j) run = run && chan[j] == c0 + j;
+  return run;
+}
+
+// One thread per (q, slot, 8 channels): 16-byte stores of both tiles.
 template <class Ty>
-__global__ void __launch_bounds__(256) bwd_gather_kernel(GatherArgs a, int64_t total) {
+__global__ void __launch_bounds__(256) bwd_gather_kernel(GatherArgs a, int64_t total8) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int32_t c = static_cast<int32_t>(i % a.d);
-  const int64_t qk = i / a.d;
+  if (i >= total8) return;
+  const int32_t d8 = a.d >> 3;
+  const int32_t c0 = static_cast<int32_t>(i % d8) * 8;
+  const int64_t qk = i / d8;
   const int64_t k = qk % a.slots;
   const int32_t q = static_cast<int32_t>(qk / a.slots);
   const int64_t row = slot_row(a.tok, k, a.q_s, a.n_tok);
-  const int32_t ch = a.chan[q * a.d + c];
-  uint16_t xv = 0, dv = 0;
-  if (row >= 0 && ch >= 0 && ch < a.channels) {
-    const int64_t off = row * a.channels + ch;
+  const int32_t* chp = a.chan + q * a.d + c0;
+  uint16_t xv[8], dv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xv[j] = dv[j] = 0;
+  if (row >= 0) {
     const float r = a.rscale ? a.rscale[row] : 1.0f;
-    xv = Ty::from_f32(Ty::to_f32(a.x[off]) * r);
-    dv = a.dy[off];
+    const int64_t base = row * a.channels;
+    if (a.vec && channel_run8(chp, a.channels)) {
+      const uint4 xr = *reinterpret_cast<const uint4*>(a.x + base + chp[0]);
+      const uint4 dr = *reinterpret_cast<const uint4*>(a.dy + base + chp[0]);
+      const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, dw[4] = {dr.x, dr.y, dr.z, dr.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xv[j] = static_cast<uint16_t>(xw[j >> 1] >> (16 * (j & 1)));
+        dv[j] = static_cast<uint16_t>(dw[j >> 1] >> (16 * (j & 1)));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int32_t ch = chp[j];
+        if (ch >= 0 && ch < a.channels) {
+          xv[j] = a.x[base + ch];
+          dv[j] = a.dy[base + ch];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = Ty::from_f32(Ty::to_f32(xv[j]) * r);
   }
-  a.xt[i] = xv;
-  a.dyt[i] = dv;
+  auto pack = [](const uint16_t* v) {
+    return uint4{v[0] | (static_cast<uint32_t>(v[1]) << 16), v[2] | (static_cast<uint32_t>(v[3]) << 16),
+                 v[4] | (static_cast<uint32_t>(v[5]) << 16), v[6] | (static_cast<uint32_t>(v[7]) << 16)};
+  };
+  *reinterpret_cast<uint4*>(a.xt + i * 8) = pack(xv);
+  *reinterpret_cast<uint4*>(a.dyt + i * 8) = pack(dv);
 }
 
-// Elementwise gate backward over n values (folded operands, see the file comment).
+// Elementwise gate backward over n values (folded operands, see the file comment), 8 values
+// per thread with 16-byte accesses (n % 8 == 0, all buffers 16-byte aligned).
 template <class Ty>
 __global__ void __launch_bounds__(256) bwd_gate_kernel(const uint16_t* u, const uint16_t* v, const uint16_t* dz,
-                                                       uint16_t* z, uint16_t* du, uint16_t* dv, int64_t n) {
+                                                       uint16_t* z, uint16_t* du, uint16_t* dv, int64_t n8) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float up = Ty::to_f32(u[i]), vp = Ty::to_f32(v[i]), g = Ty::to_f32(dz[i]);
-  const float s = 1.0f / (1.0f + exp2f(up));
-  z[i] = Ty::from_f32(up * vp * s);
-  du[i] = Ty::from_f32(g * vp * s * (1.0f - kLn2 * up * (1.0f - s)));
-  dv[i] = Ty::from_f32(g * up * s);
+  if (i >= n8) return;
+  const uint4 uu = reinterpret_cast<const uint4*>(u)[i];
+  const uint4 vv = reinterpret_cast<const uint4*>(v)[i];
+  const uint4 gg = reinterpret_cast<const uint4*>(dz)[i];
+  const uint32_t uw[4] = {uu.x, uu.y, uu.z, uu.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w}, gw[4] = {gg.x, gg.y, gg.z, gg.w};
+  uint32_t zo[4], uo[4], vo[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float zf[2], uf[2], vf[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float up = Ty::to_f32(static_cast<uint16_t>(uw[w] >> (16 * h)));
+      const float vp = Ty::to_f32(static_cast<uint16_t>(vw[w] >> (16 * h)));
+      const float g = Ty::to_f32(static_cast<uint16_t>(gw[w] >> (16 * h)));
+      const float s = 1.0f / (1.0f + exp2f(up));
+      zf[h] = up * vp * s;
+      uf[h] = g * vp * s * (1.0f - kLn2 * up * (1.0f - s));
+      vf[h] = g * up * s;
+    }
+    zo[w] = Ty::pack2(zf[0], zf[1]);
+    uo[w] = Ty::pack2(uf[0], uf[1]);
+    vo[w] = Ty::pack2(vf[0], vf[1]);
+  }
+  reinterpret_cast<uint4*>(z)[i] = uint4{zo[0], zo[1], zo[2], zo[3]};
+  reinterpret_cast<uint4*>(du)[i] = uint4{uo[0], uo[1], uo[2], uo[3]};
+  reinterpret_cast<uint4*>(dv)[i] = uint4{vo[0], vo[1], vo[2], vo[3]};
 }
 
-// dX' slots -> g [rows, C] fp32 (every valid (row, channel) is written exactly once: the routes
-// are permutations of tokens and channels).
+// dX' slots -> g [rows, C] fp32, 8 channels per thread (every valid (row, channel) is written
+// exactly once: the routes are permutations of tokens and channels).
 template <class Ty>
 __global__ void __launch_bounds__(256) bwd_scatter_kernel(const uint16_t* dxt, const int32_t* tok, const int32_t* chan,
                                                           float* g, int64_t slots, int32_t n_tok, int32_t channels,
-                                                          int32_t q_s, int32_t d, int64_t total) {
+                                                          int32_t q_s, int32_t d, int32_t vec, int64_t total8) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int32_t c = static_cast<int32_t>(i % d);
-  const int64_t qk = i / d;
+  if (i >= total8) return;
+  const int32_t d8 = d >> 3;
+  const int32_t c0 = static_cast<int32_t>(i % d8) * 8;
+  const int64_t qk = i / d8;
   const int64_t k = qk % slots;
   const int32_t q = static_cast<int32_t>(qk / slots);
   const int64_t row = slot_row(tok, k, q_s, n_tok);
-  const int32_t ch = chan[q * d + c];
-  if (row >= 0 && ch >= 0 && ch < channels) g[row * channels + ch] = Ty::to_f32(dxt[i]);
+  if (row < 0) return;
+  const uint4 src = *reinterpret_cast<const uint4*>(dxt + i * 8);
+  const uint32_t sw[4] = {src.x, src.y, src.z, src.w};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = Ty::to_f32(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
+  const int32_t* chp = chan + q * d + c0;
+  float* dst = g + row * channels;
+  if (vec && channel_run8(chp, channels)) {
+    float4* p = reinterpret_cast<float4*>(dst + chp[0]);
+    p[0] = float4{v[0], v[1], v[2], v[3]};
+    p[1] = float4{v[4], v[5], v[6], v[7]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int32_t ch = chp[j];
+      if (ch >= 0 && ch < channels) dst[ch] = v[j];
+    }
+  }
 }
 
-// One wave per row: dx = (dout) + r g - x r^3 / C sum(g x)   (norm)   or   (dout) + g.
+// Rows of `lpr` lanes (a power of two <= 64, 64 / lpr rows per wave), 8 channels per lane
+// step: dx = (dout) + r g - x r^3 / C sum(g x)   (norm)   or   (dout) + g.  C % 8 == 0 and
+// 16-byte aligned x / dout / dx (the caller checks).
 template <class Ty>
 __global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, const float* g, const float* rscale,
                                                           const uint16_t* dout, uint16_t* dx, int64_t rows,
-                                                          int32_t channels, int32_t residual) {
+                                                          int32_t channels, int32_t residual, int32_t lpr) {
+  const int lane = threadIdx.x & 63;
+  const int rows_per_wave = 64 / lpr;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * rows_per_wave + lane / lpr;
+  const int sub = lane % lpr;
+  const bool live = row < rows;
+  const int64_t base = live ? row * channels : 0;
+  const int c8n = channels >> 3;
+  auto unpack8 = [](uint4 q, float* f) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = Ty::to_f32(static_cast<uint16_t>(w[j >> 1] >> (16 * (j & 1))));
+  };
+  float r = 1.0f, coef = 0.0f;
+  if (rscale) {
+    r = live ? rscale[row] : 0.0f;
+    float dot = 0.0f;
+    if (live) {
+      for (int c8 = sub; c8 < c8n; c8 += lpr) {
+        float xf[8];
+        unpack8(*reinterpret_cast<const uint4*>(x + base + 8 * c8), xf);
+        const float4 g0 = *reinterpret_cast<const float4*>(g + base + 8 * c8);
+        const float4 g1 = *reinterpret_cast<const float4*>(g + base + 8 * c8 + 4);
+        dot = fmaf(g0.x, xf[0], dot); dot = fmaf(g0.y, xf[1], dot);
+        dot = fmaf(g0.z, xf[2], dot); dot = fmaf(g0.w, xf[3], dot);
+        dot = fmaf(g1.x, xf[4], dot); dot = fmaf(g1.y, xf[5], dot);
+        dot = fmaf(g1.z, xf[6], dot); dot = fmaf(g1.w, xf[7], dot);
+      }
+    }
+    for (int m = lpr >> 1; m > 0; m >>= 1) dot += __shfl_xor(dot, m);
+    coef = dot * r * r * r / static_cast<float>(channels);
+  }
+  if (!live) return;
+  for (int c8 = sub; c8 < c8n; c8 += lpr) {
+    float xf[8], df[8];
+    unpack8(*reinterpret_cast<const uint4*>(x + base + 8 * c8), xf);
+    if (residual) {
+      unpack8(*reinterpret_cast<const uint4*>(dout + base + 8 * c8), df);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) df[j] = 0.0f;
+    }
+    const float4 g0 = *reinterpret_cast<const float4*>(g + base + 8 * c8);
+    const float4 g1 = *reinterpret_cast<const float4*>(g + base + 8 * c8 + 4);
+    const float gf[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = df[2 * w] + r * gf[2 * w] - coef * xf[2 * w];
+      const float hi = df[2 * w + 1] + r * gf[2 * w + 1] - coef * xf[2 * w + 1];
+      o[w] = Ty::pack2(lo, hi);
+    }
+    *reinterpret_cast<uint4*>(dx + base + 8 * c8) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// Any C and alignment: one wave per row, one channel per lane step.
+template <class Ty>
+__global__ void __launch_bounds__(256) bwd_rmsnorm_scalar_kernel(const uint16_t* x, const float* g, const float* rscale,
+                                                                 const uint16_t* dout, uint16_t* dx, int64_t rows,
+                                                                 int32_t channels, int32_t residual) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -193,9 +330,11 @@ struct ParamArgs {
   int32_t wdtype, q_c, d, rd, channels;
 };
 
-// One thread per (q, c): the folded gradients mapped back to the parameters.
+// One wave per (q, c): the folded gradients mapped back to the parameters, the per-channel
+// sums over the expanded dim reduced across the wave.
 __global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (i >= static_cast<int64_t>(a.q_c) * a.d) return;
   const int32_t c = static_cast<int32_t>(i % a.d);
   const int32_t q = static_cast<int32_t>(i / a.d);
@@ -204,7 +343,7 @@ __global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a) {
   const float w = ok ? (a.norm_w ? a.norm_w[ch] : 1.0f) : 0.0f;
   const float gm = ok ? (a.gamma ? a.gamma[ch] : 1.0f) : 0.0f;
   float sum_w = 0.0f, sum_g = 0.0f;
-  for (int32_t e = 0; e < a.rd; ++e) {
+  for (int32_t e = lane; e < a.rd; e += 64) {
     const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;
     const int64_t ec = (static_cast<int64_t>(q) * a.rd + e) * a.d + c;
     const float du = a.dbu[cd], dv = a.dbv[cd], dob = a.dbo[ec];
@@ -214,18 +353,24 @@ __global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a) {
     sum_w += du * kNegLog2e * load_any(a.b_u, cd, a.wdtype) + dv * kNegLn2 * load_any(a.b_v, cd, a.wdtype);
     sum_g += dob * load_any(a.b_o, ec, a.wdtype);
   }
-  if (ok) {
+  for (int m = 32; m > 0; m >>= 1) {
+    sum_w += __shfl_xor(sum_w, m);
+    sum_g += __shfl_xor(sum_g, m);
+  }
+  if (ok && lane == 0) {
     a.g_gamma[ch] = sum_g;
     if (a.g_norm_w) a.g_norm_w[ch] = sum_w;
   }
 }
 
 // Token mixing per 16-row tile: out = M1 in1 (+ M2 in2), M* [16][16] fp32, in/out tiles
-// [16][d] of the compute dtype.  One wave per tile, 16x16x16 MFMAs: A operand lane (l16, h)
-// slot j = M[l16][4h + j], B operand = in[4h + j][16 cb + l16].
-template <class Ty, bool TWO>
+// [16][NB*16] of the compute dtype.  One wave per tile, 16x16x16 MFMAs: A operand lane (l16, h)
+// slot j = M[l16][4h + j], B operand = in[4h + j][16 cb + l16].  All loads are issued before
+// the MFMAs and all stores after one drain.
+template <class Ty, bool TWO, int NB>
 __global__ void __launch_bounds__(256) tile_mix_kernel(const uint16_t* in1, const float* m1, const uint16_t* in2,
-                                                       const float* m2, uint16_t* out, int64_t n_tiles, int32_t d) {
+                                                       const float* m2, uint16_t* out, int64_t n_tiles) {
+  constexpr int D = NB * 16;
   const int lane = threadIdx.x & 63;
   const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (tile >= n_tiles) return;
@@ -234,23 +379,34 @@ __global__ void __launch_bounds__(256) tile_mix_kernel(const uint16_t* in1, cons
     return u32x2{Ty::pack2(m[l16 * 16 + 4 * h + 0], m[l16 * 16 + 4 * h + 1]),
                  Ty::pack2(m[l16 * 16 + 4 * h + 2], m[l16 * 16 + 4 * h + 3])};
   };
+  const int64_t base = tile * 16 * D + (4 * h) * D + l16;
+  uint16_t e1[NB][4], e2[NB][4];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e1[cb][j] = in1[base + j * D + 16 * cb];
+      if constexpr (TWO) e2[cb][j] = in2[base + j * D + 16 * cb];
+    }
+  }
   const u32x2 a1 = a_op(m1);
   u32x2 a2 = {0u, 0u};
   if constexpr (TWO) a2 = a_op(m2);
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int64_t base = tile * 16 * d;
-  for (int cb = 0; cb < d / 16; ++cb) {
-    auto b_op = [&](const uint16_t* in) {
-      const uint16_t* p = in + base + (4 * h) * d + 16 * cb + l16;
-      return u32x2{static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[d]) << 16),
-                   static_cast<uint32_t>(p[2 * d]) | (static_cast<uint32_t>(p[3 * d]) << 16)};
-    };
-    f32x4 acc = Ty::mma16(a1, b_op(in1), zero);
-    if constexpr (TWO) acc = Ty::mma16(a2, b_op(in2), acc);
-    mfma_drain();
-    uint16_t* o = out + base + 16 * cb + l16;
+  auto b_op = [](const uint16_t* e) {
+    return u32x2{e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16)};
+  };
+  f32x4 acc[NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[(4 * h + i) * d] = Ty::from_f32(acc[i]);
+  for (int cb = 0; cb < NB; ++cb) {
+    acc[cb] = Ty::mma16(a1, b_op(e1[cb]), zero);
+    if constexpr (TWO) acc[cb] = Ty::mma16(a2, b_op(e2[cb]), acc[cb]);
+  }
+  mfma_drain();
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[base + i * D + 16 * cb] = Ty::from_f32(acc[cb][i]);
   }
 }
 
@@ -299,16 +455,19 @@ int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int3
     return OW_OK;
   }
   OW_CHECK_ARG(x && dy && token_index && channel_index && xt && dyt, "tensor pointer is NULL");
+  OW_CHECK_SUPPORTED(plan->channel_tile % 8 == 0, "channel tile %d is not a multiple of 8", plan->channel_tile);
+  OW_CHECK_ARG(ow::aligned16(xt) && ow::aligned16(dyt), "xt / dyt must be 16-byte aligned");
+  const int32_t vec = plan->channels % 8 == 0 && ow::aligned16(x) && ow::aligned16(dy);
   ow::GatherArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(dy), rscale, token_index,
                    channel_index, static_cast<uint16_t*>(xt), static_cast<uint16_t*>(dyt),
                    static_cast<int64_t>(batch) * q_s * ow::kG, plan->height * plan->width, plan->channels, q_s,
-                   plan->channel_tile};
-  const int64_t total = static_cast<int64_t>(q_c) * a.slots * a.d;
+                   plan->channel_tile, vec};
+  const int64_t total8 = static_cast<int64_t>(q_c) * a.slots * (a.d / 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::BF16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, a, total8);
   else
-    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, a, total);
+    hipLaunchKernelGGL(ow::bwd_gather_kernel<ow::F16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, a, total8);
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_gather_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
@@ -323,15 +482,20 @@ int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du,
     return OW_OK;
   }
   OW_CHECK_ARG(u && v && dz && z && du && dv, "tensor pointer is NULL");
+  OW_CHECK_ARG(n % 8 == 0, "n must be a multiple of 8 (got %lld)", (long long)n);
+  OW_CHECK_ARG(ow::aligned16(u) && ow::aligned16(v) && ow::aligned16(dz) && ow::aligned16(z) && ow::aligned16(du) &&
+                   ow::aligned16(dv),
+               "gate buffers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  const int64_t n8 = n / 8;
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::BF16>, dim3(ow::blocks_for(n)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
-                       mu(z), mu(du), mu(dv), n);
+    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::BF16>, dim3(ow::blocks_for(n8)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
+                       mu(z), mu(du), mu(dv), n8);
   else
-    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::F16>, dim3(ow::blocks_for(n)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
-                       mu(z), mu(du), mu(dv), n);
+    hipLaunchKernelGGL(ow::bwd_gate_kernel<ow::F16>, dim3(ow::blocks_for(n8)), dim3(256), 0, s, cu(u), cu(v), cu(dz),
+                       mu(z), mu(du), mu(dv), n8);
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_gate_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
@@ -348,18 +512,21 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
     return OW_OK;
   }
   OW_CHECK_ARG(dxt && token_index && channel_index && g, "tensor pointer is NULL");
+  OW_CHECK_SUPPORTED(plan->channel_tile % 8 == 0, "channel tile %d is not a multiple of 8", plan->channel_tile);
+  OW_CHECK_ARG(ow::aligned16(dxt), "dxt must be 16-byte aligned");
   const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
   const int32_t d = plan->channel_tile;
-  const int64_t total = static_cast<int64_t>(q_c) * slots * d;
+  const int64_t total8 = static_cast<int64_t>(q_c) * slots * (d / 8);
+  const int32_t vec = plan->channels % 8 == 0 && ow::aligned16(g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* src = static_cast<const uint16_t*>(dxt);
   const int32_t n_tok = plan->height * plan->width;
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, src,
-                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, total);
+    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::BF16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, src,
+                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, vec, total8);
   else
-    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, src,
-                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, total);
+    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::F16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, src,
+                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, vec, total8);
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_scatter_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
@@ -375,14 +542,30 @@ int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const voi
   }
   OW_CHECK_ARG(x && g && dx && (!residual || dout), "tensor pointer is NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
-  if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
-                       static_cast<uint16_t*>(dx), rows, channels, residual);
-  else
-    hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
-                       static_cast<uint16_t*>(dx), rows, channels, residual);
+  uint16_t* out = static_cast<uint16_t*>(dx);
+  const bool vec = channels % 8 == 0 && ow::aligned16(x) && ow::aligned16(g) && ow::aligned16(dx) &&
+                   (!residual || ow::aligned16(dout));
+  if (!vec) {
+    const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+    if (dtype == OW_DTYPE_BF16)
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale,
+                         cu(dout), out, rows, channels, residual);
+    else
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale,
+                         cu(dout), out, rows, channels, residual);
+  } else {
+    int32_t lpr = 1;
+    while (lpr < 64 && lpr * 8 < channels) lpr *= 2;
+    const int64_t rows_per_block = 4 * (64 / lpr);
+    const unsigned blocks = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
+    if (dtype == OW_DTYPE_BF16)
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+                         out, rows, channels, residual, lpr);
+    else
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+                         out, rows, channels, residual, lpr);
+  }
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_rmsnorm_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
@@ -413,7 +596,8 @@ int ow_fold_weights(const void* b_u, const void* b_v, const void* b_o, int32_t w
 
 int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* m2, void* out, int64_t n_tiles,
                 int32_t d, int32_t dtype, void* stream) {
-  OW_CHECK_ARG(n_tiles >= 0 && d >= 16 && d % 16 == 0, "bad shape n_tiles=%lld d=%d", (long long)n_tiles, d);
+  OW_CHECK_ARG(n_tiles >= 0, "bad tile count %lld", (long long)n_tiles);
+  OW_CHECK_SUPPORTED(d == 64 || d == 128, "unsupported channel tile d=%d; expected 64 or 128", d);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
   if (n_tiles == 0) {
     ow::clear_error();
@@ -424,17 +608,23 @@ int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* 
   const unsigned blocks = static_cast<unsigned>((n_tiles + 3) / 4);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   uint16_t* o = static_cast<uint16_t*>(out);
+#define OW_TILE_MIX(TY, TWO, NB)                                                                               \
+  hipLaunchKernelGGL((ow::tile_mix_kernel<TY, TWO, NB>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, \
+                     n_tiles)
   if (dtype == OW_DTYPE_BF16) {
-    if (in2)
-      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::BF16, true>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
-    else
-      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::BF16, false>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+    if (d == 64) {
+      if (in2) OW_TILE_MIX(ow::BF16, true, 4); else OW_TILE_MIX(ow::BF16, false, 4);
+    } else {
+      if (in2) OW_TILE_MIX(ow::BF16, true, 8); else OW_TILE_MIX(ow::BF16, false, 8);
+    }
   } else {
-    if (in2)
-      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::F16, true>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
-    else
-      hipLaunchKernelGGL((ow::tile_mix_kernel<ow::F16, false>), dim3(blocks), dim3(256), 0, s, cu(in1), m1, cu(in2), m2, o, n_tiles, d);
+    if (d == 64) {
+      if (in2) OW_TILE_MIX(ow::F16, true, 4); else OW_TILE_MIX(ow::F16, false, 4);
+    } else {
+      if (in2) OW_TILE_MIX(ow::F16, true, 8); else OW_TILE_MIX(ow::F16, false, 8);
+    }
   }
+#undef OW_TILE_MIX
   if (int rc = ow::hip_status(hipGetLastError(), "tile_mix_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
@@ -469,7 +659,8 @@ int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t wei
   ow::ParamArgs a{b_u, b_v, b_o, norm_weight, gamma, channel_index, dbu, dbv, dbo, g_bu, g_bv, g_bo, g_gamma,
                   g_norm_weight, weight_dtype, q_c, d, rd, channels};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(ow::bwd_params_kernel, dim3(ow::blocks_for(static_cast<int64_t>(q_c) * d)), dim3(256), 0, s, a);
+  const unsigned blocks = static_cast<unsigned>((static_cast<int64_t>(q_c) * d + 3) / 4);
+  hipLaunchKernelGGL(ow::bwd_params_kernel, dim3(blocks), dim3(256), 0, s, a);
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_params_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
