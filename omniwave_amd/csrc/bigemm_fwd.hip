@@ -600,8 +600,16 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const voi
   OW_CHECK_ARG(q_c >= 1, "q_c must be >= 1 (got %d)", q_c);
   OW_CHECK_SUPPORTED((d == 64 || d == 128) && (rd == 128 || rd == 256),
                      "unsupported channel tile d=%d / expanded dim rd=%d", d, rd);
-  OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16,
+  OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16 || compute_dtype == OW_DTYPE_F32,
                      "unsupported compute dtype %d", compute_dtype);
+  if (compute_dtype == OW_DTYPE_F32) {
+    if (int rc = ow::pack_weights_f32(a_u, a_v, a_o, b_u, b_v, b_o, weight_dtype, norm_weight, gamma, channel_index,
+                                      channels, q_c, d, rd, ow::packed_elems(q_c, d, rd), packed,
+                                      static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   ow::PackArgs p{a_u, a_v, a_o, b_u, b_v, b_o, norm_weight, gamma, channel_index, packed,
                  weight_dtype, q_c, d, rd, channels, ow::packed_elems(q_c, d, rd)};
   const unsigned blocks = static_cast<unsigned>((p.total + 255) / 256);
@@ -623,7 +631,15 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
     return OW_OK;
   }
   OW_CHECK_ARG(x && scale, "tensor pointer is NULL");
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::rms_scale_f32(static_cast<const float*>(x), scale, rows, channels, eps,
+                                   static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   ow::RmsArgs r{static_cast<const uint16_t*>(x), scale, rows, channels, eps};
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!ow::aligned16(x)) {  // element path
@@ -651,8 +667,8 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   OW_CHECK_ARG(packed && token_index && channel_index, "tensor pointer is NULL");
   OW_CHECK_ARG((flags & ~(OW_FUSE_NORM | OW_FUSE_RESIDUAL)) == 0, "unknown flags 0x%x", flags);
   OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16,
-                     "unsupported dtype %d; expected bf16 or f16", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32,
+                     "unsupported dtype %d; expected bf16, f16 or f32", dtype);
   const int32_t n = plan->height * plan->width, c = plan->channels, d = plan->channel_tile;
   const size_t want = ow_packed_weight_bytes(q_c, d, rd, dtype);
   OW_CHECK_ARG(want != 0 && packed_bytes == want,
@@ -670,6 +686,19 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   OW_CHECK_ARG(workspace_bytes >= need_ws && (need_ws == 0 || workspace),
                "workspace holds %zu bytes; %zu needed", workspace_bytes, need_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OW_DTYPE_F32) {
+    float* scale = nullptr;
+    if (flags & OW_FUSE_NORM) {
+      scale = static_cast<float*>(workspace);
+      if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
+    }
+    if (int rc = ow::launch_fwd_f32(static_cast<const float*>(x), static_cast<float*>(out), scale,
+                                    static_cast<const float*>(packed), token_index, channel_index, batch, n, c, q_s,
+                                    q_c, d, rd, (flags & OW_FUSE_RESIDUAL) ? 1 : 0, s))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   if (ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) && ow::aligned16(out)) {
     ow::ResidentArgs r{};
     r.x = static_cast<const uint16_t*>(x);

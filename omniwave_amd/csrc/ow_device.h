@@ -373,4 +373,14 @@ struct ResidentArgs {
 bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);
 int launch_fwd_resident(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
 
+// fp32 path (bigemm_fwd_f32.hip): operand packing, RMSNorm row scales and the forward.
+int pack_weights_f32(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,
+                     const void* b_o, int32_t weight_dtype, const float* norm_weight, const float* gamma,
+                     const int32_t* channel_index, int32_t channels, int32_t q_c, int32_t d, int32_t rd,
+                     int64_t total, void* packed, hipStream_t stream);
+int rms_scale_f32(const float* x, float* scale, int64_t rows, int32_t channels, float eps, hipStream_t stream);
+int launch_fwd_f32(const float* x, float* out, const float* row_scale, const float* packed, const int32_t* tok,
+                   const int32_t* chan, int32_t batch, int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c,
+                   int32_t d, int32_t rd, int32_t residual, hipStream_t stream);
+
 }  // namespace ow

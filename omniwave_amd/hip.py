@@ -29,7 +29,7 @@ from omniwave_amd.routing import RoutePlan, build_route_plan, device_tables
 SPATIAL_TILE = 16
 CHANNEL_TILES = (64, 128)
 EXPANDED_TILES = (128, 256)
-SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 _DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
                torch.float16: _native.OW_DTYPE_F16}
 _ROUTE_NAME = {v: k for k, v in _native.OW_ROUTE.items()}
@@ -51,7 +51,7 @@ def hip_is_supported(x: Tensor, plan: RoutePlan, b_u: Tensor) -> tuple[bool, str
     if not arch.startswith("gfx950"):
         return False, f"device architecture {arch} is not gfx950"
     if x.dtype not in SUPPORTED_DTYPES:
-        return False, f"unsupported dtype {x.dtype}; expected float16 or bfloat16"
+        return False, f"unsupported dtype {x.dtype}; expected float16, bfloat16 or float32"
     g = plan.token_indices.shape[1]
     if g != SPATIAL_TILE:
         return False, f"unsupported spatial tile g={g}; expected 16"
