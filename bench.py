@@ -38,6 +38,7 @@ STAGES = [  # name, H, W, C, d
 ROUTES = [("local", 0), ("shifted", 0), ("radix", 1)]
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense fp8 MFMA
 
 
 def tile_flops(d: int, rd: int) -> int:
@@ -251,6 +252,62 @@ def model_section(batch: int, steps: int, dev) -> dict:
     }
 
 
+def fp8_section(model_batch: int, steps: int, dev) -> dict:
+    """fp8-e4m3 channel side: the fused block at the 14x14x512 stage shape for B in
+    {64, 256, 1024} (fp8 and bf16 side by side, HIP graphs of 20 launches), and OmniWeave-T
+    inference at `model_batch` with every block on the fp8 variant."""
+    import omniwave_amd
+    from omniwave_amd.hip import bigemm_block_hip
+
+    name, h, w, c, d = STAGES[2]
+    sweep = {}
+    # Inputs are made outside inference mode: parameters that carry a version counter keep
+    # their packed operands cached across calls.
+    inputs = {batch: make_inputs(batch, h, w, c, d, "shifted", 0, dev, seed=200) for batch in (64, 256, 1024)}
+    with torch.inference_mode():
+        for batch in (64, 256, 1024):
+            plan, x, p, nw = inputs[batch]
+            flops = case_work(batch, h, w, c, d)[0]
+            row = {}
+            for label, fp8 in (("fp8", True), ("bf16", False)):
+                fn = (lambda fp8=fp8: bigemm_block_hip(x, nw, plan, **p, fp8=fp8))
+                row[f"{label}_us"] = round(_graph_ms(fn, 20, steps) * 1e3, 2)
+                row[f"{label}_tflops"] = round(flops / (row[f"{label}_us"] * 1e-6) / 1e12, 1)
+            row["fp8_frac_of_fp8_peak"] = round(row["fp8_tflops"] / PEAK_FP8_TFLOPS, 4)
+            sweep[f"B{batch}"] = row
+    del inputs
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").to(device=dev, dtype=torch.bfloat16).eval()
+    omniwave_amd.enable_fp8(model)
+    gen = torch.Generator().manual_seed(0)
+    xi = torch.randn(model_batch, 3, 224, 224, generator=gen).to(device=dev, dtype=torch.bfloat16)
+    with torch.inference_mode():
+        ms = _graph_ms(lambda: model.forward_features(xi), 1, steps)
+    return {
+        "workload": f"fused block fp8 channel side, {name} shifted0; omniweave_t fp8 at [{model_batch},3,224,224]",
+        "stage3_sweep": sweep,
+        "model_images_per_s": round(model_batch / (ms * 1e-3), 1),
+        "model_ms_per_batch": round(ms, 3),
+    }
+
+
+def _graph_ms(fn, per_graph: int, replays: int) -> float:
+    """ms per call of `fn`: captured `per_graph` times into one HIP graph after a warm-up call,
+    replayed `replays` times (plus 2 warm-up replays)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.current_stream().synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(per_graph):
+                fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    time_graph(graph, 2)
+    return time_graph(graph, replays) / per_graph
+
+
 def backward_section(batch: int, steps: int, dev) -> dict:
     """Fused block forward + backward (dx, dA, dB, dgamma, dnorm_weight) at the 56x56x128 and
     14x14x512 stage shapes, shifted route, bf16, upstream gradient N(0,1)."""
@@ -348,7 +405,8 @@ def main() -> int:
     ap.add_argument("--model-batch", type=int, default=256, help="batch of the OmniWeave-T inference section")
     ap.add_argument("--no-model", action="store_true", help="skip the OmniWeave-T inference section")
     ap.add_argument("--no-backward", action="store_true", help="skip the forward + backward section")
-    ap.add_argument("--section", choices=["model", "backward"], default=None,
+    ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 section")
+    ap.add_argument("--section", choices=["model", "backward", "fp8"], default=None,
                     help="profiling aid: run only this section, print its JSON and exit")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--only", default="", help="comma-separated substrings: run only matching cases "
@@ -381,6 +439,9 @@ def main() -> int:
         return 0
     if args.section == "backward":
         print(json.dumps({"backward": backward_section(args.batch, args.steps, dev)}), flush=True)
+        return 0
+    if args.section == "fp8":
+        print(json.dumps({"fp8": fp8_section(args.model_batch, args.steps, dev)}), flush=True)
         return 0
 
     cases = []
@@ -473,6 +534,7 @@ def main() -> int:
     }
     model = None if args.no_model else model_section(args.model_batch, 10, dev)
     backward = None if args.no_backward else backward_section(args.batch, 10, dev)
+    fp8 = None if args.no_fp8 else fp8_section(args.model_batch, 10, dev)
     baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
     line = {
         "metric": "BiGEMM fwd TFLOP/s (fused RMSNorm+residual, 4 OmniWeave-T stage shapes x 3 routes)",
@@ -494,6 +556,7 @@ def main() -> int:
         "roofline": roofline,
         "model": model,
         "backward": backward,
+        "fp8": fp8,
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)

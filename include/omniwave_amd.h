@@ -39,6 +39,7 @@ extern "C" {
 /* Fusion flags of ow_bigemm_fwd. */
 #define OW_FUSE_NORM 1     /* x is raw; apply the block's RMSNorm (omniweave/models/block.py:83-85) */
 #define OW_FUSE_RESIDUAL 2 /* write x + delta instead of delta (omniweave/models/block.py:108) */
+#define OW_FUSE_FP8 4      /* fp8-e4m3 channel side with ow_pack_weights_fp8 weights (needs OW_FUSE_NORM) */
 
 /*
  * Route plan descriptor: the arguments of build_route_plan
@@ -106,6 +107,24 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o,
                     const int32_t* channel_index, int32_t channels,
                     int32_t g, int32_t q_c, int32_t d, int32_t rd,
                     int32_t compute_dtype, void* packed, void* stream);
+
+/*
+ * fp8 inference variant (no counterpart in the reference, which has no fp8 path): the
+ * channel-side products U' = P B_u'' and V' = P B_v'' run on e4m3fn MFMAs with fp32
+ * accumulation; the token side, the gate, Z B_o and A_o W stay in the activation dtype.
+ * Per-tensor scales: B_u'' and B_v'' by their absmax over all channel groups; P by the static
+ * bound ||A||_inf sqrt(C) that the RMSNorm'd rows obey (hence OW_FUSE_NORM).  Packed layout:
+ * the token-side head (act_dtype), 16 scale floats, then per (q, 32-row chunk) the fp8
+ * B_u'' / B_v'' fragments and the act_dtype B_o fragments.  Arguments as ow_pack_weights;
+ * `packed` holds ow_packed_weight_bytes_fp8(q_c, d, rd) bytes.
+ */
+size_t ow_packed_weight_bytes_fp8(int32_t q_c, int32_t d, int32_t rd);
+int ow_pack_weights_fp8(const void* a_u, const void* a_v, const void* a_o,
+                        const void* b_u, const void* b_v, const void* b_o,
+                        int32_t weight_dtype, const float* norm_weight, const float* gamma,
+                        const int32_t* channel_index, int32_t channels,
+                        int32_t g, int32_t q_c, int32_t d, int32_t rd,
+                        int32_t act_dtype, void* packed, void* stream);
 
 /*
  * RMSNorm row scales: scale[i] = rsqrt(mean_c(x[i, c]^2) + eps) for rows x [rows, channels],

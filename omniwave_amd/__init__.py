@@ -7,6 +7,7 @@ Public API mirrors the reference package (omniweave/__init__.py:5-8): ``create_m
 __version__ = "0.1.0"
 
 from omniwave_amd.bigemm import bigemm, register_backend
+from omniwave_amd.block import enable_fp8
 from omniwave_amd.hip import bigemm_block_hip, bigemm_delta_hip, hip_is_supported
 from omniwave_amd.registry import create_model, create_model_from_config
 from omniwave_amd.routing import RoutePlan, build_route_plan, build_stage_schedule
@@ -20,6 +21,7 @@ __all__ = [
     "build_stage_schedule",
     "create_model",
     "create_model_from_config",
+    "enable_fp8",
     "hip_is_supported",
     "register_backend",
 ]

@@ -11,7 +11,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libomniwave_amd.so"
 OW_OK = 0
 OW_ROUTE = {"local": 0, "shifted": 1, "radix": 2}
 OW_DTYPE_F32, OW_DTYPE_BF16, OW_DTYPE_F16 = 0, 1, 2
-OW_FUSE_NORM, OW_FUSE_RESIDUAL = 1, 2
+OW_FUSE_NORM, OW_FUSE_RESIDUAL, OW_FUSE_FP8 = 1, 2, 4
 
 _c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
@@ -37,6 +37,12 @@ _SIGNATURES = {
     "ow_route_build": (ctypes.c_int, [ctypes.POINTER(OwPlan), _c_int32_p, _c_int32_p]),
     "ow_packed_weight_bytes": (ctypes.c_size_t, [ctypes.c_int32] * 4),
     "ow_pack_weights": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 6 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]
+        + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],
+    ),
+    "ow_packed_weight_bytes_fp8": (ctypes.c_size_t, [ctypes.c_int32] * 3),
+    "ow_pack_weights_fp8": (
         ctypes.c_int,
         [ctypes.c_void_p] * 6 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]
         + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],

@@ -59,6 +59,7 @@ class OmniWeaveBlock(nn.Module):
         self.b_v = nn.Parameter(torch.empty(q_c, d, rd))
         self.b_o = nn.Parameter(torch.empty(q_c, rd, d))
         self.gamma = nn.Parameter(torch.full((dim,), layer_scale_init))
+        self.fp8 = False  # e4m3fn channel side (inference with the hip backend); see enable_fp8
         self._init_weights()
 
     def _init_weights(self) -> None:
@@ -89,7 +90,14 @@ class OmniWeaveBlock(nn.Module):
         """``x``: ``[B, H, W, C]`` -> ``[B, H, W, C]``."""
         params = (self.a_u, self.a_v, self.a_o, self.b_u, self.b_v, self.b_o, self.gamma)
         dropping = self.training and self.drop_path_rate > 0
-        if self._fused(x):
+        fused = self._fused(x)
+        if self.fp8:
+            if self.training:
+                raise RuntimeError("the fp8 BiGEMM variant is inference-only; call model.eval()")
+            if not fused:
+                raise RuntimeError("the fp8 BiGEMM variant needs the hip backend on a gfx950 GPU")
+            return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, fp8=True)
+        if fused:
             if not dropping:
                 return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS)
             delta = bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, residual=False)
@@ -106,3 +114,12 @@ class OmniWeaveBlock(nn.Module):
         if dropping:
             delta = self._drop_path(delta)
         return x + delta
+
+
+def enable_fp8(model: nn.Module, enabled: bool = True) -> nn.Module:
+    """Switch every OmniWeaveBlock of ``model`` to the fp8-e4m3 channel side (inference with
+    bf16 / fp16 activations on the hip backend) or back; returns ``model``."""
+    for module in model.modules():
+        if isinstance(module, OmniWeaveBlock):
+            module.fp8 = enabled
+    return model

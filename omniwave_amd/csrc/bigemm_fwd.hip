@@ -158,7 +158,7 @@ __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0
 
 // One workgroup: 4 waves x TPW token groups (TPW/2 pairs of 16 tokens per wave) x one channel
 // group q_c.
-template <class Ty, int D, int RD, int TPW, int OCC>
+template <class Ty, int D, int RD, int TPW, int OCC, bool F8>
 __global__ void __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(OCC)))
 bigemm_fwd_kernel(FwdArgs a) {
   constexpr int NP = TPW / 2;      // token-group pairs per wave (32-token MFMA N blocks)
@@ -171,7 +171,10 @@ bigemm_fwd_kernel(FwdArgs a) {
   constexpr int FR_U = KS;         // B_u'^T fragments per chunk (B_v'^T the same)
   constexpr int FR_O = 2 * MB;     // B_o^T fragments per chunk (MB blocks x 2 K steps)
   constexpr int FR_CH = 2 * FR_U + FR_O;
-  constexpr int CH_ELEMS = FR_CH * kFragElems;
+  // 1 KB copy units per chunk: 2 KS fp8 fragments of 512 bytes + FR_O Ty fragments with F8.
+  constexpr int CH_UNITS = F8 ? FR_U + FR_O : FR_CH;
+  constexpr int CH_ELEMS = CH_UNITS * kFragElems;
+  constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, in 16-bit elements
   static_assert(TPW % 2 == 0, "token groups come in pairs");
   static_assert(CH_ELEMS <= ROWS * LDX, "a weight chunk must fit in the x-tile region");
 
@@ -189,12 +192,12 @@ bigemm_fwd_kernel(FwdArgs a) {
   const int bid = xcd_remap(blockIdx.x, a.n_chunks * a.q_c);
   const int qc = bid % a.q_c, chunk = bid / a.q_c;
 
-  const uint16_t* wsrc = a.packed + kHeadElems + static_cast<size_t>(qc) * NCH * CH_ELEMS;
+  const uint16_t* wsrc = a.packed + HEAD + static_cast<size_t>(qc) * NCH * CH_ELEMS;
   auto chunk_buf = [&](int ec) -> uint16_t* { return (ec & 1) ? xs : wb; };
   auto issue_chunk = [&](int ec) {
     const uint16_t* src = wsrc + static_cast<size_t>(ec) * CH_ELEMS;
     uint16_t* dst = chunk_buf(ec);
-    for (int f = wave; f < FR_CH; f += kWaves) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane);
+    for (int f = wave; f < CH_UNITS; f += kWaves) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane);
   };
   issue_chunk(0);
 
@@ -311,8 +314,10 @@ bigemm_fwd_kernel(FwdArgs a) {
   int col[KS / 2];
 #pragma unroll
   for (int cb = 0; cb < KS / 2; ++cb) col[cb] = 32 * cb + l32;
-  u32x4 Pu[NP][KS], Pv[NP][KS];
+  using POp = std::conditional_t<F8, u32x2, u32x4>;  // P^T operand: fp8 or Ty K steps
+  POp Pu[NP][KS], Pv[NP][KS];
   u32x4 xk[NP][KS / 2][2];  // the lane's x values, kept for the residual
+  const float* f8s = reinterpret_cast<const float*>(a.packed + kHeadElems);  // fp8 scales
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int row0 = (wave * TPW + 2 * p) * kG;
@@ -322,7 +327,11 @@ bigemm_fwd_kernel(FwdArgs a) {
       bu = scale8<Ty>(fAu, r8);
       bv = scale8<Ty>(fAv, r8);
     }
-    pair_token_side<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, Pu[p], Pv[p], xk[p]);
+    if constexpr (F8)
+      pair_token_side_f8<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, f8s[kF8QuantPu], f8s[kF8QuantPv], Pu[p],
+                                 Pv[p], xk[p]);
+    else
+      pair_token_side<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, Pu[p], Pv[p], xk[p]);
   }
 
   // Channel side, streamed over 32-row chunks of the expanded dimension (double-buffered).
@@ -342,11 +351,22 @@ bigemm_fwd_kernel(FwdArgs a) {
     if (ec + 1 < NCH) issue_chunk(ec + 1);
     const uint16_t* cw = chunk_buf(ec);
     const u32x4* cf = reinterpret_cast<const u32x4*>(cw);
-    auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
-    auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
-    auto fo = [&](int mb, int s) { return cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane]; };
+    if constexpr (F8) {
+      const u32x2* c8 = reinterpret_cast<const u32x2*>(cw);
+      const u32x4* co = reinterpret_cast<const u32x4*>(cw + FR_U * kFragElems);
+      auto fu = [&](int ks) { return c8[ks * (kF8FragBytes / 8) + lane]; };
+      auto fv = [&](int ks) { return c8[(FR_U + ks) * (kF8FragBytes / 8) + lane]; };
+      auto fo = [&](int mb, int s) { return co[(2 * mb + s) * (kFragElems / 8) + lane]; };
+      const float du = f8s[kF8DeqU], dv = f8s[kF8DeqV];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) pair_chunk<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
+      for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, du, dv, W[p]);
+    } else {
+      auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
+      auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
+      auto fo = [&](int mb, int s) { return cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane]; };
+#pragma unroll
+      for (int p = 0; p < NP; ++p) pair_chunk<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
+    }
   }
 
   // Output side: delta = A_o W per pair (lane = channel 32 mb + l32, registers = tokens;
@@ -505,6 +525,130 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
   static_cast<uint16_t*>(p.packed)[idx] = Ty::from_f32(val);
 }
 
+// fp8 channel side: per-tensor scales, in three launches (f8_zero, f8_amax, f8_finalize).
+// f8_amax: absmax of the folded B_u'' / B_v'' over all channel groups, 8 values per thread,
+// wave maxima combined with atomic max on the (non-negative) float bits.
+__global__ void __launch_bounds__(64) f8_zero_kernel(float* scales) {
+  if (threadIdx.x < kF8ScaleFloats) scales[threadIdx.x] = 0.0f;
+}
+
+__global__ void __launch_bounds__(256) f8_amax_kernel(PackArgs p, float* scales) {
+  const int n = p.q_c * p.d * p.rd;
+  const int i0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  float mu = 0.0f, mv = 0.0f;
+  for (int i = i0; i < i0 + 8 && i < n; ++i) {
+    const int qc = i / p.rd;  // q * d + c
+    float w = 1.0f;
+    if (p.chan) {
+      const int gc = p.chan[qc];
+      w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
+    }
+    mu = fmaxf(mu, fabsf(load_f32(p.b_u, i, p.wdtype) * w * kNegLog2e));
+    mv = fmaxf(mv, fabsf(load_f32(p.b_v, i, p.wdtype) * w * kNegLn2));
+  }
+  for (int m = 32; m > 0; m >>= 1) {
+    mu = fmaxf(mu, __shfl_xor(mu, m));
+    mv = fmaxf(mv, __shfl_xor(mv, m));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(reinterpret_cast<unsigned int*>(scales + kF8AmaxBu), __float_as_uint(mu));
+    atomicMax(reinterpret_cast<unsigned int*>(scales + kF8AmaxBv), __float_as_uint(mv));
+  }
+}
+
+// The P operand is quantised with the static bound |P| <= ||A||_inf sqrt(C) (1.02): the
+// RMSNorm'd rows satisfy |x_c r| <= sqrt(C), the 2% cover the Ty rounding of r and of the A
+// operand.  One wave: lane i < 16 sums |row i| of the Ty-rounded A_u / A_v.
+template <class Ty>
+__global__ void __launch_bounds__(64) f8_finalize_kernel(PackArgs p, float* scales) {
+  const int lane = threadIdx.x;
+  float su = 0.0f, sv = 0.0f;
+  if (lane < kG) {
+    for (int j = 0; j < kG; ++j) {
+      su += fabsf(Ty::to_f32(Ty::from_f32(load_f32(p.a_u, lane * kG + j, p.wdtype))));
+      sv += fabsf(Ty::to_f32(Ty::from_f32(load_f32(p.a_v, lane * kG + j, p.wdtype))));
+    }
+  }
+  for (int m = 32; m > 0; m >>= 1) {
+    su = fmaxf(su, __shfl_xor(su, m));
+    sv = fmaxf(sv, __shfl_xor(sv, m));
+  }
+  if (lane == 0) {
+    const float au = scales[kF8AmaxBu], av = scales[kF8AmaxBv];
+    const float root_c = sqrtf(static_cast<float>(p.channels)) * 1.02f;
+    const float qu = su > 0.0f ? kF8Max / (su * root_c) : 1.0f;
+    const float qv = sv > 0.0f ? kF8Max / (sv * root_c) : 1.0f;
+    const float sbu = au > 0.0f ? au / kF8Max : 1.0f;
+    const float sbv = av > 0.0f ? av / kF8Max : 1.0f;
+    scales[kF8DeqU] = sbu / qu;
+    scales[kF8DeqV] = sbv / qv;
+    scales[kF8QuantPu] = qu;
+    scales[kF8QuantPv] = qv;
+  }
+}
+
+// fp8 packing, one thread per packed value: the Ty head, then per (q, ec) the e4m3fn
+// B_u'^T / B_v'^T fragments (value / s_b, s_b = absmax / 448) and the Ty B_o fragments, with
+// the lane / slot order of pack_kernel.
+template <class Ty>
+__global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* scales) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= p.total) return;
+  uint8_t* base = static_cast<uint8_t*>(p.packed);
+  if (idx < kHeadElems) {
+    const int frag = static_cast<int>(idx / kFragElems);
+    const int e = static_cast<int>(idx % kFragElems);
+    const int lane = e / 8, j = e % 8;
+    const int t = lane & 15, hh = lane >> 5;
+    const int k = 8 * (j / 4) + 4 * hh + (j % 4);
+    const float val = load_f32(frag == 0 ? p.a_u : frag == 1 ? p.a_v : p.a_o, t * kG + k, p.wdtype);
+    reinterpret_cast<uint16_t*>(base)[idx] = Ty::from_f32(val);
+    return;
+  }
+  const int ks_n = p.d / 16, mb_n = p.d / 32, nch = p.rd / 32;
+  const int64_t ch_units = static_cast<int64_t>(2 * ks_n + 2 * mb_n) * kFragElems;
+  const int64_t ch_bytes = static_cast<int64_t>(2 * ks_n) * kF8FragBytes + static_cast<int64_t>(2 * mb_n) * 2 * kFragElems;
+  int64_t rem = idx - kHeadElems;
+  const int q = static_cast<int>(rem / (nch * ch_units));
+  rem -= static_cast<int64_t>(q) * nch * ch_units;
+  const int ec = static_cast<int>(rem / ch_units);
+  rem -= static_cast<int64_t>(ec) * ch_units;
+  const int fr = static_cast<int>(rem / kFragElems);
+  const int e = static_cast<int>(rem % kFragElems);
+  const int lane = e / 8, j = e % 8;
+  const int l32 = lane & 31, hh = lane >> 5;
+  uint8_t* chunk = base + kF8HeadBytes + (static_cast<int64_t>(q) * nch + ec) * ch_bytes;
+  if (fr < 2 * ks_n) {
+    const bool is_u = fr < ks_n;
+    const int ks = fr % ks_n;
+    const int col = 32 * ec + l32;
+    const int c = 16 * ks + 8 * (j / 4) + 4 * hh + (j % 4);
+    const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + col;
+    float w = 1.0f;
+    if (p.chan) {
+      const int gc = p.chan[q * p.d + c];
+      w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
+    }
+    const float val = load_f32(is_u ? p.b_u : p.b_v, src, p.wdtype) * w * (is_u ? kNegLog2e : kNegLn2);
+    const float amax = scales[is_u ? kF8AmaxBu : kF8AmaxBv];
+    const float mul = amax > 0.0f ? kF8Max / amax : 1.0f;
+    chunk[static_cast<int64_t>(fr) * kF8FragBytes + e] = static_cast<uint8_t>(cvt_fp8x2<false>(val * mul, 0.0f, 0u));
+  } else {
+    const int f = fr - 2 * ks_n;
+    const int mb = f / 2, s = f % 2;
+    const int c = 32 * mb + l32;
+    const int ee = 32 * ec + 16 * s + 8 * (j / 4) + 4 * hh + (j % 4);
+    const int64_t src = (static_cast<int64_t>(q) * p.rd + ee) * p.d + c;
+    float w = 1.0f;
+    if (p.chan) {
+      const int gc = p.chan[q * p.d + c];
+      w = (gc >= 0 && gc < p.channels) ? (p.gamma ? p.gamma[gc] : 1.0f) : 0.0f;
+    }
+    uint16_t* ob = reinterpret_cast<uint16_t*>(chunk + static_cast<int64_t>(2 * ks_n) * kF8FragBytes);
+    ob[static_cast<int64_t>(f) * kFragElems + e] = Ty::from_f32(load_f32(p.b_o, src, p.wdtype) * w);
+  }
+}
+
 int64_t packed_elems(int32_t q_c, int32_t d, int32_t rd) {
   const int64_t per_chunk = static_cast<int64_t>(2 * (d / 16) + 2 * (d / 32)) * kFragElems;
   return kHeadElems + static_cast<int64_t>(q_c) * (rd / 32) * per_chunk;
@@ -545,7 +689,7 @@ int launch_rms(const RmsArgs& a, hipStream_t s) {
 
 // d = 128: 4 token groups per wave (two 32-token MFMA blocks share each weight fragment read
 // from LDS), one workgroup per CU.  d = 64: the same tiling fits two workgroups per CU.
-template <class Ty, int D, int RD>
+template <class Ty, int D, int RD, bool F8>
 int launch_fwd(const FwdArgs& a, hipStream_t stream) {
   constexpr int TPW = D == 64 ? OW_TPW_D64 : OW_TPW_D128;
   constexpr int OCC = D == 64 ? OW_OCC_D64 : OW_OCC_D128;
@@ -557,17 +701,17 @@ int launch_fwd(const FwdArgs& a, hipStream_t stream) {
   if (nwg == 0) return OW_OK;
   if (nwg > 0x7fffffff) return fail(OW_ERR_UNSUPPORTED, "grid too large (%lld workgroups)", (long long)nwg);
   args.n_chunks = static_cast<int32_t>(chunks);
-  hipLaunchKernelGGL((bigemm_fwd_kernel<Ty, D, RD, TPW, OCC>), dim3(static_cast<unsigned>(nwg)), dim3(kThreads),
+  hipLaunchKernelGGL((bigemm_fwd_kernel<Ty, D, RD, TPW, OCC, F8>), dim3(static_cast<unsigned>(nwg)), dim3(kThreads),
                      0, stream, args);
   return hip_status(hipGetLastError(), "bigemm_fwd_kernel launch");
 }
 
-template <class Ty>
+template <class Ty, bool F8>
 int dispatch_fwd(const FwdArgs& a, int d, int rd, hipStream_t s) {
-  if (d == 64 && rd == 128) return launch_fwd<Ty, 64, 128>(a, s);
-  if (d == 64 && rd == 256) return launch_fwd<Ty, 64, 256>(a, s);
-  if (d == 128 && rd == 128) return launch_fwd<Ty, 128, 128>(a, s);
-  if (d == 128 && rd == 256) return launch_fwd<Ty, 128, 256>(a, s);
+  if (d == 64 && rd == 128) return launch_fwd<Ty, 64, 128, F8>(a, s);
+  if (d == 64 && rd == 256) return launch_fwd<Ty, 64, 256, F8>(a, s);
+  if (d == 128 && rd == 128) return launch_fwd<Ty, 128, 128, F8>(a, s);
+  if (d == 128 && rd == 256) return launch_fwd<Ty, 128, 256, F8>(a, s);
   return fail(OW_ERR_UNSUPPORTED, "unsupported channel tile d=%d / expanded dim rd=%d; expected d in {64,128}, rd in {128,256}", d, rd);
 }
 
@@ -623,6 +767,45 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const voi
   return OW_OK;
 }
 
+size_t ow_packed_weight_bytes_fp8(int32_t q_c, int32_t d, int32_t rd) {
+  if (q_c < 1 || d < 32 || rd < 32 || d % 32 || rd % 32) return 0;
+  return static_cast<size_t>(ow::kF8HeadBytes) + static_cast<size_t>(q_c) * (rd / 32) * 128 * static_cast<size_t>(d);
+}
+
+int ow_pack_weights_fp8(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,
+                        const void* b_o, int32_t weight_dtype, const float* norm_weight, const float* gamma,
+                        const int32_t* channel_index, int32_t channels, int32_t g, int32_t q_c, int32_t d, int32_t rd,
+                        int32_t act_dtype, void* packed, void* stream) {
+  OW_CHECK_ARG(a_u && a_v && a_o && b_u && b_v && b_o && packed, "tensor pointer is NULL");
+  OW_CHECK_ARG(!(norm_weight || gamma) || channel_index, "norm_weight / gamma need channel_index");
+  OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
+  OW_CHECK_SUPPORTED(g == ow::kG, "unsupported spatial tile g=%d; expected 16", g);
+  OW_CHECK_ARG(q_c >= 1 && channels >= 1, "bad shape q_c=%d channels=%d", q_c, channels);
+  OW_CHECK_SUPPORTED((d == 64 || d == 128) && (rd == 128 || rd == 256),
+                     "unsupported channel tile d=%d / expanded dim rd=%d", d, rd);
+  OW_CHECK_SUPPORTED(act_dtype == OW_DTYPE_BF16 || act_dtype == OW_DTYPE_F16, "unsupported activation dtype %d",
+                     act_dtype);
+  OW_CHECK_ARG(ow::aligned16(packed), "packed weights must be 16-byte aligned");
+  ow::PackArgs p{a_u, a_v, a_o, b_u, b_v, b_o, norm_weight, gamma, channel_index, packed,
+                 weight_dtype, q_c, d, rd, channels, ow::packed_elems(q_c, d, rd)};
+  float* scales = reinterpret_cast<float*>(static_cast<uint8_t*>(packed) + ow::kHeadElems * 2);
+  const unsigned blocks = static_cast<unsigned>((p.total + 255) / 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int n_b = q_c * d * rd;
+  hipLaunchKernelGGL(ow::f8_zero_kernel, dim3(1), dim3(64), 0, s, scales);
+  hipLaunchKernelGGL(ow::f8_amax_kernel, dim3(static_cast<unsigned>((n_b + 2047) / 2048)), dim3(256), 0, s, p, scales);
+  if (act_dtype == OW_DTYPE_BF16) {
+    hipLaunchKernelGGL(ow::f8_finalize_kernel<ow::BF16>, dim3(1), dim3(64), 0, s, p, scales);
+    hipLaunchKernelGGL(ow::pack_f8_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, p, scales);
+  } else {
+    hipLaunchKernelGGL(ow::f8_finalize_kernel<ow::F16>, dim3(1), dim3(64), 0, s, p, scales);
+    hipLaunchKernelGGL(ow::pack_f8_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, p, scales);
+  }
+  if (int rc = ow::hip_status(hipGetLastError(), "fp8 pack launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
 int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, float eps, int32_t dtype,
                  void* stream) {
   OW_CHECK_ARG(rows >= 0 && channels >= 1, "bad shape rows=%lld channels=%d", (long long)rows, channels);
@@ -665,12 +848,15 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
   OW_CHECK_ARG(packed && token_index && channel_index, "tensor pointer is NULL");
-  OW_CHECK_ARG((flags & ~(OW_FUSE_NORM | OW_FUSE_RESIDUAL)) == 0, "unknown flags 0x%x", flags);
+  OW_CHECK_ARG((flags & ~(OW_FUSE_NORM | OW_FUSE_RESIDUAL | OW_FUSE_FP8)) == 0, "unknown flags 0x%x", flags);
+  const bool fp8 = (flags & OW_FUSE_FP8) != 0;
+  OW_CHECK_SUPPORTED(!fp8 || ((flags & OW_FUSE_NORM) && dtype != OW_DTYPE_F32),
+                     "OW_FUSE_FP8 needs OW_FUSE_NORM and bf16 / f16 activations");
   OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32,
                      "unsupported dtype %d; expected bf16, f16 or f32", dtype);
   const int32_t n = plan->height * plan->width, c = plan->channels, d = plan->channel_tile;
-  const size_t want = ow_packed_weight_bytes(q_c, d, rd, dtype);
+  const size_t want = fp8 ? ow_packed_weight_bytes_fp8(q_c, d, rd) : ow_packed_weight_bytes(q_c, d, rd, dtype);
   OW_CHECK_ARG(want != 0 && packed_bytes == want,
                "packed weights hold %zu bytes; q_c=%d d=%d rd=%d needs %zu", packed_bytes, q_c, d, rd, want);
   OW_CHECK_ARG(ow::aligned16(packed), "packed weights must be 16-byte aligned");
@@ -699,7 +885,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
     ow::clear_error();
     return OW_OK;
   }
-  if (ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) && ow::aligned16(out)) {
+  if (!fp8 && ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) && ow::aligned16(out)) {
     ow::ResidentArgs r{};
     r.x = static_cast<const uint16_t*>(x);
     r.out = static_cast<uint16_t*>(out);
@@ -750,8 +936,12 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   } else {
     a.mode = ow::kModeElement;
   }
-  const int rc = dtype == OW_DTYPE_BF16 ? ow::dispatch_fwd<ow::BF16>(a, d, rd, s)
-                                        : ow::dispatch_fwd<ow::F16>(a, d, rd, s);
+  int rc;
+  if (fp8)
+    rc = dtype == OW_DTYPE_BF16 ? ow::dispatch_fwd<ow::BF16, true>(a, d, rd, s) : ow::dispatch_fwd<ow::F16, true>(a, d, rd, s);
+  else
+    rc = dtype == OW_DTYPE_BF16 ? ow::dispatch_fwd<ow::BF16, false>(a, d, rd, s)
+                                : ow::dispatch_fwd<ow::F16, false>(a, d, rd, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
 }

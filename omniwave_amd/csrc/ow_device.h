@@ -270,6 +270,94 @@ __device__ __forceinline__ void pair_chunk(const u32x4 (&Pu)[KS], const u32x4 (&
     for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(mb, s), W[mb]);
 }
 
+// ---- fp8 (OCP e4m3fn) channel side ----------------------------------------------------------
+// Byte layout of an fp8 packed buffer: the Ty token-side head (kHeadElems elements), then
+// kF8ScaleFloats floats of scales, then per (q, 32-row chunk ec) KS fp8 B_u'^T fragments, KS
+// fp8 B_v'^T fragments (512 bytes each, 8 bytes per lane) and 2 MB Ty B_o fragments (1 KB).
+constexpr int kF8FragBytes = 512;
+constexpr int kF8ScaleFloats = 16;
+constexpr int kF8HeadBytes = kHeadElems * 2 + kF8ScaleFloats * 4;
+// Scale slots: dequantisation factors of the U' / V' accumulators and the P quantisation
+// multipliers (448 / bound of |P|); the raw B''-absmax slots are the packer's.
+constexpr int kF8DeqU = 0, kF8DeqV = 1, kF8QuantPu = 2, kF8QuantPv = 3, kF8AmaxBu = 4, kF8AmaxBv = 5;
+constexpr float kF8Max = 448.0f;
+
+// Two floats -> two e4m3fn bytes (round to nearest even) in the low (HI = false) or high half
+// of `old`.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_fp8x2(float a, float b, uint32_t old) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), HI));
+}
+
+// Accumulator registers 8s..8s+7 times `mul` as a packed fp8 K step (slot order as pack_kstep).
+__device__ __forceinline__ u32x2 pack_kstep_f8(const f32x16& acc, int s, float mul) {
+  uint32_t lo = cvt_fp8x2<false>(acc[8 * s + 0] * mul, acc[8 * s + 1] * mul, 0u);
+  lo = cvt_fp8x2<true>(acc[8 * s + 2] * mul, acc[8 * s + 3] * mul, lo);
+  uint32_t hi = cvt_fp8x2<false>(acc[8 * s + 4] * mul, acc[8 * s + 5] * mul, 0u);
+  hi = cvt_fp8x2<true>(acc[8 * s + 6] * mul, acc[8 * s + 7] * mul, hi);
+  return u32x2{lo, hi};
+}
+
+__device__ __forceinline__ f32x16 mma32_f8(u32x2 a, u32x2 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
+                                                    0, 0);
+}
+
+// Token side of a pair with fp8 outputs: as pair_token_side, the P^T accumulators multiplied by
+// qu / qv and rounded to e4m3fn.
+template <class Ty, int KS>
+__device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, const int (&col)[KS / 2], u32x4 bu,
+                                                   u32x4 bv, int lane, float qu, float qv, u32x2 (&Pu)[KS],
+                                                   u32x2 (&Pv)[KS], u32x4 (&xk)[KS / 2][2]) {
+  const int hh = lane >> 5;
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 bu0 = keep_if(g0, bu), bu1 = keep_if(!g0, bu);
+  const u32x4 bv0 = keep_if(g0, bv), bv1 = keep_if(!g0, bv);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    xk[cb][0] = column8(tl + (4 * hh) * ld + col[cb], ld);
+    xk[cb][1] = column8(tl + (16 + 4 * hh) * ld + col[cb], ld);
+  }
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const u32x4 x0 = xk[cb][0], x1 = xk[cb][1];
+    f32x16 pu = Ty::mma32(x0, bu0, zero);
+    f32x16 pv = Ty::mma32(x0, bv0, zero);
+    pu = Ty::mma32(x1, bu1, pu);
+    pv = Ty::mma32(x1, bv1, pv);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Pu[2 * cb + s] = pack_kstep_f8(pu, s, qu);
+      Pv[2 * cb + s] = pack_kstep_f8(pv, s, qv);
+    }
+  }
+}
+
+// pair_chunk with fp8 U'/V' products: fu(ks), fv(ks) return fp8 fragments (u32x2), the
+// accumulators are dequantised by du / dv before the gate; the Z B_o product stays in Ty.
+template <class Ty, int KS, int MB, class FU, class FV, class FO>
+__device__ __forceinline__ void pair_chunk_f8(const u32x2 (&Pu)[KS], const u32x2 (&Pv)[KS], FU fu, FV fv, FO fo,
+                                              float du, float dv, f32x16 (&W)[MB]) {
+  f32x16 U = {}, V = {};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    U = mma32_f8(fu(ks), Pu[ks], U);
+    V = mma32_f8(fv(ks), Pv[ks], V);
+  }
+  u32x4 Z[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q] * du, V[8 * s + 2 * q] * dv),
+                          silu_gate(U[8 * s + 2 * q + 1] * du, V[8 * s + 2 * q + 1] * dv));
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(mb, s), W[mb]);
+}
+
 // The whole channel side of a pair (NCH chunks, weights in registers), software-pipelined: the
 // U'/V' MFMAs of chunk ec + 1 are issued ahead of the SiLU of chunk ec and interleaved with
 // it, so the matrix core and the vector unit of one wave work at the same time.

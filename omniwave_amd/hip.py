@@ -93,12 +93,13 @@ def _stream_ptr(device: torch.device) -> int:
 
 
 def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_weight: Tensor | None = None,
-                 plan: RoutePlan | None = None, gamma: Tensor | None = None) -> Tensor:
+                 plan: RoutePlan | None = None, gamma: Tensor | None = None, fp8: bool = False) -> Tensor:
     """Pack the six BiGEMM weights into the kernel's MFMA operand order (uint8 buffer).
 
     With the block's ``plan`` (whose channel table routes per-channel vectors), the LayerScale
     ``gamma`` is folded into the B_o columns and ``norm_weight`` (the RMSNorm weight) into the
-    B_u / B_v rows, as OW_FUSE_NORM expects; pad channels are packed as zero.
+    B_u / B_v rows, as OW_FUSE_NORM expects; pad channels are packed as zero.  ``fp8`` packs
+    B_u'' / B_v'' as e4m3fn with per-tensor scales (``ow_pack_weights_fp8``) for OW_FUSE_FP8.
     """
     lib = _native.lib()
     ws = [a_u, a_v, a_o, b_u, b_v, b_o]
@@ -112,7 +113,7 @@ def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_
         raise ValueError("inconsistent BiGEMM weight shapes: "
                          f"a_u {tuple(a_u.shape)}, b_u {tuple(b_u.shape)}, b_v {tuple(b_v.shape)}, b_o {tuple(b_o.shape)}")
     cdt = _DTYPE_CODE[compute_dtype]
-    nbytes = lib.ow_packed_weight_bytes(q_c, d, rd, cdt)
+    nbytes = lib.ow_packed_weight_bytes_fp8(q_c, d, rd) if fp8 else lib.ow_packed_weight_bytes(q_c, d, rd, cdt)
     if nbytes == 0:
         raise ValueError(f"unsupported packing shape q_c={q_c}, d={d}, rd={rd}")
     packed = torch.empty(nbytes, dtype=torch.uint8, device=b_u.device)
@@ -130,19 +131,21 @@ def pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype: torch.dtype, norm_
         if gamma is not None:
             keep.append(gamma.detach().to(device=b_u.device, dtype=torch.float32).contiguous())
             gm_ptr = keep[-1].data_ptr()
+    pack = lib.ow_pack_weights_fp8 if fp8 else lib.ow_pack_weights
     with torch.cuda.device(b_u.device):
         _native.check(
-            lib.ow_pack_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], nw_ptr, gm_ptr, ch_ptr, channels,
-                                SPATIAL_TILE, q_c, d, rd, cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
-            "ow_pack_weights",
+            pack(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype], nw_ptr, gm_ptr, ch_ptr, channels,
+                 SPATIAL_TILE, q_c, d, rd, cdt, packed.data_ptr(), _stream_ptr(b_u.device)),
+            "ow_pack_weights_fp8" if fp8 else "ow_pack_weights",
         )
     return packed
 
 
-def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, plan: RoutePlan):
+def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, plan: RoutePlan,
+                     fp8: bool = False):
     srcs = (a_u, a_v, a_o, b_u, b_v, b_o, gamma) + ((norm_weight,) if norm_weight is not None else ())
     versions = tuple(_version(t) for t in srcs)
-    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype, plan.key())
+    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype, plan.key(), fp8)
     entry = _PACK_CACHE.get(key)
     if (entry is not None and None not in versions and entry.versions == versions
             and all(r() is t for r, t in zip(entry.refs, srcs))):
@@ -151,7 +154,7 @@ def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_d
     entry = _PackEntry()
     entry.refs = tuple(weakref.ref(t) for t in srcs)
     entry.versions = versions
-    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, norm_weight, plan, gamma)
+    entry.packed = pack_weights(a_u, a_v, a_o, b_u, b_v, b_o, compute_dtype, norm_weight, plan, gamma, fp8)
     if None not in versions:
         _PACK_CACHE[key] = entry
         while len(_PACK_CACHE) > _PACK_CACHE_SIZE:
@@ -192,13 +195,16 @@ def bigemm_fwd(
     flags: int,
     eps: float,
 ) -> Tensor:
-    """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC."""
+    """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC; flag
+    OW_FUSE_FP8 selects the fp8 channel side."""
     plan = _plan_from_desc(plan_desc)
     x = x.contiguous()
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
     if fuse_norm and norm_weight is None:
         raise ValueError("OW_FUSE_NORM needs norm_weight")
-    packed = _cached_operands(norm_weight if fuse_norm else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan)
+    fp8 = bool(flags & _native.OW_FUSE_FP8)
+    packed = _cached_operands(norm_weight if fuse_norm else None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan,
+                              fp8)
     tok, ch = device_tables(plan, x.device)
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     native_plan = plan.native()
@@ -231,6 +237,8 @@ def _bigemm_fwd_setup_context(ctx, inputs, output):
 def _bigemm_fwd_backward(ctx, grad):
     from omniwave_amd.backward import bigemm_backward
 
+    if ctx.flags & _native.OW_FUSE_FP8:
+        raise NotImplementedError("the fp8 BiGEMM variant is inference-only (no backward)")
     x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o = ctx.saved_tensors
     grads = bigemm_backward(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o,
                             _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps)
@@ -254,8 +262,14 @@ def bigemm_delta_hip(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma) -> Tensor:
 
 
 def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, eps: float = 1e-6,
-                     residual: bool = True) -> Tensor:
-    """RMSNorm(x) -> BiGEMM -> (+ x) fused (omniweave/models/block.py:83-108, no drop-path)."""
+                     residual: bool = True, fp8: bool = False) -> Tensor:
+    """RMSNorm(x) -> BiGEMM -> (+ x) fused (omniweave/models/block.py:83-108, no drop-path).
+
+    ``fp8=True`` runs the channel-side products on e4m3fn MFMAs (inference only; bf16 / fp16
+    activations).
+    """
     _require(x, plan, b_u)
-    flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0)
+    if fp8 and x.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"hip backend not supported: the fp8 variant takes bf16 or fp16 activations, not {x.dtype}")
+    flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0) | (_native.OW_FUSE_FP8 if fp8 else 0)
     return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps))

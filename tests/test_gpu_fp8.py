@@ -1,0 +1,159 @@
+"""fp8-e4m3 variant on the GPU (``-m gpu``).
+
+Two checks per case:
+
+* against an emulation of the kernel's quantised arithmetic on the CPU (the token operand
+  A_ij r_j in the activation dtype, the same per-tensor scales, e4m3fn rounding of P and of
+  B_u'' / B_v'', fp32 accumulation, activation-dtype rounding of Z, W and delta): rel-L2
+  <= 1e-2 on delta, so the kernel computes what it is designed to compute (the slack covers
+  e4m3 rounding flips from the fp32 summation order);
+* against the fp32 oracle: rel-L2 <= 5e-2 on the block output x + delta (LayerScale 1) and on
+  the model's logits.  delta alone carries the e4m3 error of two chained quantisations
+  (~3% each), which the test prints.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+import sys
+
+import pytest
+import torch
+
+import omniwave_amd
+from omniwave_amd.hip import bigemm_block_hip
+from oracle.bigemm import block_reference, pack_tiles, rel_l2, unpack_tiles
+from oracle.routing import build_route_plan as oracle_plan
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+F8 = torch.float8_e4m3fn
+LOG2E = 1.0 / math.log(2.0)
+LN2 = math.log(2.0)
+STAGES = {"s1": (56, 56, 128, 64), "s2": (28, 28, 256, 64), "s3": (14, 14, 512, 128), "s4": (7, 7, 1024, 128)}
+ROUTES = [("local", 0), ("shifted", 0), ("radix", 1)]
+
+
+def announce(msg: str) -> None:
+    print(f"\n[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+def make_case(b, h, w, c, d, route, level, seed):
+    gen = torch.Generator().manual_seed(seed)
+    plan = omniwave_amd.build_route_plan(h, w, c, 16, d, route, level)
+    q_c, rd = plan.channel_indices.shape[0], 2 * d
+    x = torch.randn(b, h, w, c, generator=gen).to(torch.bfloat16)
+    p = dict(
+        a_u=torch.randn(16, 16, generator=gen) / 4, a_v=torch.randn(16, 16, generator=gen) / 4,
+        a_o=torch.randn(16, 16, generator=gen) / 4,
+        b_u=torch.randn(q_c, d, rd, generator=gen) / d ** 0.5, b_v=torch.randn(q_c, d, rd, generator=gen) / d ** 0.5,
+        b_o=torch.randn(q_c, rd, d, generator=gen) / rd ** 0.5,
+        gamma=torch.ones(c), norm_weight=torch.rand(c, generator=gen) + 0.5,
+    )
+    p = {k: v.to(torch.bfloat16).float() for k, v in p.items()}
+    return plan, x, p
+
+
+def q8(t: torch.Tensor) -> torch.Tensor:
+    return t.to(F8).float()
+
+
+def emulate_fp8_delta(x, plan, p):
+    """The fp8 kernel's arithmetic on the CPU: delta [B,H,W,C] fp32 (rounded as the kernel)."""
+    dt = x.dtype
+    c = plan.channels
+    oplan = oracle_plan(plan.height, plan.width, c, 16, plan.channel_tile, plan.route, plan.radix_level)
+    var = x.float().square().mean(dim=-1, keepdim=True)
+    r = torch.rsqrt(var.to(dt) + 1e-6).float()
+    tiles, mask = pack_tiles(x.float(), oplan)                     # [B, Q_s, Q_c, g, d]
+    r_tok = pack_tiles(r.expand(x.shape).contiguous(), oplan)[0][..., 0]  # [B, Q_s, Q_c, g]
+    ch = oplan.channel_indices.clamp_max(c - 1)
+    valid = oplan.channel_mask.float()
+    w = p["norm_weight"][ch] * valid                                 # [Q_c, d]
+    gm = p["gamma"][ch] * valid
+    bu = -LOG2E * w[:, :, None] * p["b_u"]
+    bv = -LN2 * w[:, :, None] * p["b_v"]
+    s_bu, s_bv = bu.abs().max() / 448.0, bv.abs().max() / 448.0
+    bu_q, bv_q = q8(bu / s_bu) * s_bu, q8(bv / s_bv) * s_bv
+    a_u, a_v, a_o = (p[k].to(dt).float() for k in ("a_u", "a_v", "a_o"))
+    root_c = math.sqrt(c) * 1.02
+    qu = 448.0 / (a_u.abs().sum(1).max() * root_c)
+    qv = 448.0 / (a_v.abs().sum(1).max() * root_c)
+    # Token operand as the kernel forms it: A_ij r_j rounded to the activation dtype.
+    ar_u = (a_u[None, None, None] * r_tok[..., None, :]).to(dt).float()
+    ar_v = (a_v[None, None, None] * r_tok[..., None, :]).to(dt).float()
+    pu = ar_u @ tiles
+    pv = ar_v @ tiles
+    pu, pv = q8(pu * qu) / qu, q8(pv * qv) / qv
+    u = torch.einsum("bsqik,qke->bsqie", pu, bu_q)
+    v = torch.einsum("bsqik,qke->bsqie", pv, bv_q)
+    z = (u * v / (1.0 + torch.exp2(u))).to(dt).float()
+    bo = (p["b_o"] * gm[:, None, :]).to(dt).float()
+    wt = torch.einsum("bsqie,qek->bsqik", z, bo).to(dt).float()
+    delta = torch.einsum("ij,bsqjk->bsqik", a_o, wt).to(dt).float() * mask.float()
+    return unpack_tiles(delta, oplan, x.shape[0])
+
+
+def run_fp8(x, plan, p, residual):
+    dp = {k: v.to(DEV) for k, v in p.items()}
+    nw = dp.pop("norm_weight")
+    return bigemm_block_hip(x.to(DEV), nw, plan, **dp, residual=residual, fp8=True).cpu()
+
+
+@pytest.mark.parametrize("route,level", ROUTES, ids=[f"{r}{l}" for r, l in ROUTES])
+@pytest.mark.parametrize("stage", list(STAGES))
+def test_fp8_block_matches_emulation_and_oracle(stage, route, level) -> None:
+    h, w, c, d = STAGES[stage]
+    announce(f"fp8 block stage={stage} route={route}{level} B=2")
+    plan, x, p = make_case(2, h, w, c, d, route, level, seed=5)
+    delta = run_fp8(x, plan, p, residual=False)
+    out = run_fp8(x, plan, p, residual=True)
+    emu = emulate_fp8_delta(x, plan, p)
+    oplan = oracle_plan(h, w, c, 16, d, route, level)
+    ref_delta = block_reference(x.float(), oplan, p, residual=False)
+    ref_out = x.float() + ref_delta
+    e_emu, e_delta, e_out = rel_l2(delta, emu), rel_l2(delta, ref_delta), rel_l2(out, ref_out)
+    print(f"fp8 {stage} {route}{level}: delta vs emulation {e_emu:.2e}, delta vs fp32 {e_delta:.2e}, "
+          f"block output vs fp32 {e_out:.2e}", flush=True)
+    assert e_emu <= 1e-2
+    assert e_out <= 5e-2
+    # Residual epilogue: out = round(x + round(delta)).
+    assert torch.equal(out, (x.float() + delta.float()).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("layer_scale", [None, 1.0], ids=["init", "gamma1"])
+def test_fp8_model_logits_match_oracle(oracle_backend, layer_scale) -> None:
+    announce(f"omniweave_t fp8 forward B=2 layer_scale={layer_scale}")
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").eval()
+    if layer_scale is not None:
+        with torch.no_grad():
+            for stage in model.stages:
+                for blk in stage.blocks:
+                    blk.gamma.fill_(layer_scale)
+    model = model.to(torch.bfloat16)
+    oracle_model = copy.deepcopy(model).float()
+    for stage in oracle_model.stages:
+        for blk in stage.blocks:
+            blk.backend = "reference"
+    omniwave_amd.enable_fp8(model)
+    x = torch.randn(2, 3, 224, 224, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    with torch.no_grad():
+        want = oracle_model(x.float())
+        got = model.to(DEV)(x.to(DEV)).float().cpu()
+    err = rel_l2(got, want)
+    print(f"fp8 logits rel-L2 {err:.2e}", flush=True)
+    assert err <= 5e-2
+
+
+def test_fp8_rejects_training_and_fp32() -> None:
+    announce("fp8 error paths")
+    blk = omniwave_amd.block.OmniWeaveBlock(14, 14, 512, 128, "local", 0).to(DEV)
+    omniwave_amd.enable_fp8(blk)
+    x = torch.randn(1, 14, 14, 512, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        blk.train()(x)
+    with pytest.raises(RuntimeError, match="fp8 variant"):
+        blk.eval()(x.float())
