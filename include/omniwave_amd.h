@@ -173,7 +173,9 @@ int ow_bigemm_fwd(const void* x, void* out, float eps,
  * Backward building blocks.  Replace the fp32 autograd recompute of the accelerated backend
  * (omniweave/ops/triton.py:256-292); the plain channel-side GEMMs between them are the
  * caller's (batched hipBLASLt).  Notation: slots = batch * Q_s * 16 token slots per channel
- * group (pad slots included), tensors [Q_c][slots][d] are slot-major, compute dtype `dtype`.
+ * group (pad slots included), tensors [Q_c][slots][d] are slot-major, compute dtype `dtype`
+ * (OW_DTYPE_BF16, OW_DTYPE_F16, or OW_DTYPE_F32 for fp32 activations: fp32 tiles and plain
+ * fp32 kernels; the alignment and multiple-of-8 conditions below are for the 16-bit types).
  */
 
 /* Folded weights as plain matrices: B_u'' = -log2(e) w B_u and B_v'' = -ln(2) w B_v

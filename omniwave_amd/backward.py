@@ -86,8 +86,6 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     lib = _native.lib()
     dev = x.device
     dtype = x.dtype
-    if dtype not in (torch.bfloat16, torch.float16):
-        raise NotImplementedError(f"omniwave_amd::bigemm_fwd backward supports bf16 and fp16 activations, not {dtype}")
     code = _DTYPE_CODE[dtype]
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
     residual = bool(flags & _native.OW_FUSE_RESIDUAL)

@@ -449,12 +449,22 @@ int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int3
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
   OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   if (batch == 0) {
     ow::clear_error();
     return OW_OK;
   }
   OW_CHECK_ARG(x && dy && token_index && channel_index && xt && dyt, "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::bwd_gather_f32(static_cast<const float*>(x), static_cast<const float*>(dy), rscale, token_index,
+                                    channel_index, static_cast<float*>(xt), static_cast<float*>(dyt),
+                                    static_cast<int64_t>(batch) * q_s * ow::kG, plan->height * plan->width,
+                                    plan->channels, q_s, q_c, plan->channel_tile, static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   OW_CHECK_SUPPORTED(plan->channel_tile % 8 == 0, "channel tile %d is not a multiple of 8", plan->channel_tile);
   OW_CHECK_ARG(ow::aligned16(xt) && ow::aligned16(dyt), "xt / dyt must be 16-byte aligned");
   const int32_t vec = plan->channels % 8 == 0 && ow::aligned16(x) && ow::aligned16(dy);
@@ -476,12 +486,21 @@ int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int3
 int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du, void* dv, int64_t n, int32_t dtype,
                 void* stream) {
   OW_CHECK_ARG(n >= 0, "n must be >= 0");
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   if (n == 0) {
     ow::clear_error();
     return OW_OK;
   }
   OW_CHECK_ARG(u && v && dz && z && du && dv, "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::bwd_gate_f32(static_cast<const float*>(u), static_cast<const float*>(v),
+                                  static_cast<const float*>(dz), static_cast<float*>(z), static_cast<float*>(du),
+                                  static_cast<float*>(dv), n, static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   OW_CHECK_ARG(n % 8 == 0, "n must be a multiple of 8 (got %lld)", (long long)n);
   OW_CHECK_ARG(ow::aligned16(u) && ow::aligned16(v) && ow::aligned16(dz) && ow::aligned16(z) && ow::aligned16(du) &&
                    ow::aligned16(dv),
@@ -506,12 +525,21 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   if (batch == 0) {
     ow::clear_error();
     return OW_OK;
   }
   OW_CHECK_ARG(dxt && token_index && channel_index && g, "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::bwd_scatter_f32(static_cast<const float*>(dxt), token_index, channel_index, g,
+                                     static_cast<int64_t>(batch) * q_s * ow::kG, plan->height * plan->width,
+                                     plan->channels, q_s, q_c, plan->channel_tile, static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   OW_CHECK_SUPPORTED(plan->channel_tile % 8 == 0, "channel tile %d is not a multiple of 8", plan->channel_tile);
   OW_CHECK_ARG(ow::aligned16(dxt), "dxt must be 16-byte aligned");
   const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
@@ -535,12 +563,21 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
 int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx, int64_t rows,
                    int32_t channels, int32_t residual, int32_t dtype, void* stream) {
   OW_CHECK_ARG(rows >= 0 && channels >= 1, "bad shape rows=%lld channels=%d", (long long)rows, channels);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   if (rows == 0) {
     ow::clear_error();
     return OW_OK;
   }
   OW_CHECK_ARG(x && g && dx && (!residual || dout), "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::bwd_rmsnorm_f32(static_cast<const float*>(x), g, rscale, static_cast<const float*>(dout),
+                                     static_cast<float*>(dx), rows, channels, residual,
+                                     static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   uint16_t* out = static_cast<uint16_t*>(dx);
@@ -578,8 +615,17 @@ int ow_fold_weights(const void* b_u, const void* b_v, const void* b_o, int32_t w
   OW_CHECK_ARG(b_u && b_v && b_o && channel_index && bu && bu_t && bv && bv_t && bo && bo_t, "tensor pointer is NULL");
   OW_CHECK_ARG(q_c >= 1 && d >= 1 && rd >= 1 && channels >= 1, "bad shape q_c=%d d=%d rd=%d C=%d", q_c, d, rd, channels);
   OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
-  OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16, "unsupported compute dtype %d",
-                     compute_dtype);
+  OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16 || compute_dtype == OW_DTYPE_F32,
+                     "unsupported compute dtype %d", compute_dtype);
+  if (compute_dtype == OW_DTYPE_F32) {
+    auto mf = [](void* p) { return static_cast<float*>(p); };
+    if (int rc = ow::fold_weights_f32(b_u, b_v, b_o, weight_dtype, norm_weight, gamma, channel_index, channels, q_c, d,
+                                      rd, mf(bu), mf(bu_t), mf(bv), mf(bv_t), mf(bo), mf(bo_t),
+                                      static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
   ow::FoldArgs a{b_u, b_v, b_o, norm_weight, gamma, channel_index, mu(bu), mu(bu_t), mu(bv), mu(bv_t), mu(bo), mu(bo_t),
                  weight_dtype, q_c, d, rd, channels};
@@ -598,12 +644,20 @@ int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* 
                 int32_t d, int32_t dtype, void* stream) {
   OW_CHECK_ARG(n_tiles >= 0, "bad tile count %lld", (long long)n_tiles);
   OW_CHECK_SUPPORTED(d == 64 || d == 128, "unsupported channel tile d=%d; expected 64 or 128", d);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   if (n_tiles == 0) {
     ow::clear_error();
     return OW_OK;
   }
   OW_CHECK_ARG(in1 && m1 && out && (!in2 == !m2), "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::tile_mix_f32(static_cast<const float*>(in1), m1, static_cast<const float*>(in2), m2,
+                                  static_cast<float*>(out), n_tiles, d, static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned blocks = static_cast<unsigned>((n_tiles + 3) / 4);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
@@ -634,8 +688,16 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
                   int32_t dtype, void* stream) {
   OW_CHECK_ARG(n_tiles >= 0 && d >= 16 && d % 16 == 0, "bad shape n_tiles=%lld d=%d", (long long)n_tiles, d);
   OW_CHECK_ARG(n_waves >= 4 && n_waves % 4 == 0, "n_waves must be a positive multiple of 4 (got %d)", n_waves);
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
   OW_CHECK_ARG(partial && (n_tiles == 0 || (in1 && in2)), "tensor pointer is NULL");
+  if (dtype == OW_DTYPE_F32) {
+    if (int rc = ow::tile_outer_f32(static_cast<const float*>(in1), static_cast<const float*>(in2), partial, n_waves,
+                                    n_tiles, d, static_cast<hipStream_t>(stream)))
+      return rc;
+    ow::clear_error();
+    return OW_OK;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   if (dtype == OW_DTYPE_BF16)

@@ -471,4 +471,22 @@ int launch_fwd_f32(const float* x, float* out, const float* row_scale, const flo
                    const int32_t* chan, int32_t batch, int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c,
                    int32_t d, int32_t rd, int32_t residual, hipStream_t stream);
 
+// fp32 backward building blocks (bigemm_bwd_f32.hip).
+int bwd_gather_f32(const float* x, const float* dy, const float* rscale, const int32_t* tok, const int32_t* chan,
+                   float* xt, float* dyt, int64_t slots, int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c,
+                   int32_t d, hipStream_t s);
+int bwd_gate_f32(const float* u, const float* v, const float* dz, float* z, float* du, float* dv, int64_t n,
+                 hipStream_t s);
+int bwd_scatter_f32(const float* dxt, const int32_t* tok, const int32_t* chan, float* g, int64_t slots,
+                    int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c, int32_t d, hipStream_t s);
+int bwd_rmsnorm_f32(const float* x, const float* g, const float* rscale, const float* dout, float* dx, int64_t rows,
+                    int32_t channels, int32_t residual, hipStream_t s);
+int fold_weights_f32(const void* b_u, const void* b_v, const void* b_o, int32_t wdtype, const float* norm_w,
+                     const float* gamma, const int32_t* chan, int32_t channels, int32_t q_c, int32_t d, int32_t rd,
+                     float* bu, float* buT, float* bv, float* bvT, float* bo, float* boT, hipStream_t s);
+int tile_mix_f32(const float* in1, const float* m1, const float* in2, const float* m2, float* out, int64_t n_tiles,
+                 int32_t d, hipStream_t s);
+int tile_outer_f32(const float* in1, const float* in2, float* partial, int32_t n_waves, int64_t n_tiles, int32_t d,
+                   hipStream_t s);
+
 }  // namespace ow
