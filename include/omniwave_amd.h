@@ -221,6 +221,21 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
 int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx,
                    int64_t rows, int32_t channels, int32_t residual, int32_t dtype, void* stream);
 
+/* Fused channel side of the backward for d = 64 (rd 128 or 256), replacing six channel-side
+ * GEMMs and the gate pass: per 32-slot pair of a channel group, from the token-side tiles
+ * P_u, P_v, dW' ([q_c][slots][64], slots % 32 == 0): U'^T, V'^T, dZ^T per 32-row chunk, the gate
+ * backward (z, du, dv stored to [q_c][slots][rd]), and W' = Z B_o'', dP_u = dU' B_u''^T,
+ * dP_v = dV' B_v''^T stored to [q_c][slots][64].  Weights from ow_pack_bwd_weights (the folded
+ * B_u'', B_v'', B_o'' as the forward's and transposed MFMA operands; ow_bwd_packed_bytes). */
+size_t ow_bwd_packed_bytes(int32_t q_c, int32_t d, int32_t rd);
+int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype,
+                        const float* norm_weight, const float* gamma, const int32_t* channel_index,
+                        int32_t channels, int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype,
+                        void* packed, void* stream);
+int ow_bwd_channel(const void* pu, const void* pv, const void* dw, const void* packed, size_t packed_bytes,
+                   void* z, void* du, void* dv, void* wp, void* dpu, void* dpv, int64_t slots,
+                   int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
+
 /* Parameter gradients from the folded ones (dbu, dbv [q_c][d][rd], dbo [q_c][rd][d], fp32):
  * g_bu, g_bv, g_bo (fp32, parameter shapes), g_gamma [C] and, with norm_weight, g_norm_weight
  * [C] (each channel written once). */

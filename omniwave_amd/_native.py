@@ -88,6 +88,17 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
+    "ow_bwd_packed_bytes": (ctypes.c_size_t, [ctypes.c_int32] * 3),
+    "ow_pack_bwd_weights": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],
+    ),
+    "ow_bwd_channel": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 4 + [ctypes.c_size_t] + [ctypes.c_void_p] * 6
+        + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
     "ow_bwd_params": (
         ctypes.c_int,
         [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]

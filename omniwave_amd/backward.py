@@ -8,8 +8,10 @@ accumulation, entirely on the HIP stream of the gradient:
   (``ow_bwd_gather``, ``ow_bwd_gate``, ``ow_bwd_scatter``, ``ow_bwd_rmsnorm``,
   ``ow_bwd_params``, ``ow_fold_weights``);
 * the 16x16 token-side products are ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA);
-* the channel-side products are plain batched GEMMs over all slots of a channel group
-  (``torch.bmm`` -> hipBLASLt), every right operand contiguous.
+* the channel side (U', V', dZ, the gate, W', dP_u, dP_v) is one fused MFMA kernel for d = 64
+  (``ow_bwd_channel``) and otherwise plain batched GEMMs over all slots of a channel group
+  (``torch.bmm`` -> hipBLASLt, every right operand contiguous) around ``ow_bwd_gate``; the
+  parameter-gradient reductions over slots are batched GEMMs in both cases.
 
 Gradients are formed for the folded operands the forward evaluates (B_u'' = -log2(e) w B_u,
 B_v'' = -ln(2) w B_v, B_o'' = B_o diag(gamma), SiLU(U) V = U'V' / (1 + 2^U')) and mapped back
@@ -140,20 +142,35 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
         pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
         dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
 
-        # Channel side and gate.
-        u = torch.bmm(pu, bu)
-        v = torch.bmm(pv, bv)
-        dz = torch.bmm(dw, bo_t)
-        z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
-        _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
-                                      dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
-        del u, v, dz
+        # Channel side and gate: one fused kernel for d = 64, else batched GEMMs + the gate kernel.
+        if d == 64 and slots % 32 == 0 and dtype != torch.float32:
+            nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
+            wpk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _native.check(lib.ow_pack_bwd_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                                  nw.data_ptr() if nw is not None else None, gm.data_ptr(),
+                                                  ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
+                                                  stream), "ow_pack_bwd_weights")
+            z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
+            du, dv = torch.empty_like(z), torch.empty_like(z)
+            wp, dpu, dpv = torch.empty_like(pu), torch.empty_like(pu), torch.empty_like(pu)
+            _native.check(lib.ow_bwd_channel(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), wpk.data_ptr(), nbytes,
+                                             z.data_ptr(), du.data_ptr(), dv.data_ptr(), wp.data_ptr(),
+                                             dpu.data_ptr(), dpv.data_ptr(), slots, q_c, d, rd, code, stream),
+                          "ow_bwd_channel")
+        else:
+            u = torch.bmm(pu, bu)
+            v = torch.bmm(pv, bv)
+            dz = torch.bmm(dw, bo_t)
+            z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
+            _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                          dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
+            del u, v, dz
+            wp = torch.bmm(z, bo)
+            dpu = torch.bmm(du, bu_t)
+            dpv = torch.bmm(dv, bv_t)
         d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
         d_bv = _slot_reduce(pv, dv)
         d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
-        wp = torch.bmm(z, bo)
-        dpu = torch.bmm(du, bu_t)
-        dpv = torch.bmm(dv, bv_t)
         del z, du, dv, pu, pv, dw
 
         # Token-matrix gradients and dX'.

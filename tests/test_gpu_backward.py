@@ -30,9 +30,9 @@ def announce(msg: str) -> None:
     print(f"\n[gpu-case] {msg}", file=sys.stderr, flush=True)
 
 
-def make_case(b, h, w, c, d, route, level, dtype, seed=0):
+def make_case(b, h, w, c, d, route, level, dtype, seed=0, rd=None):
     """Seeded inputs (x, A ~ N(0, 1/16), B ~ N(0, 1/fan_in), norm_w, gamma in [0.5, 1.5), dy)."""
-    rd = 2 * d
+    rd = rd or 2 * d
     gen = torch.Generator().manual_seed(seed)
     plan = omniwave_amd.build_route_plan(h, w, c, 16, d, route, level)
     q_c = plan.channel_indices.shape[0]
@@ -128,6 +128,18 @@ def test_delta_backward_matches_oracle(name, case) -> None:
     want = oracle_grads(x, plan, params, dy, fused=False, residual=False)
     got = hip_grads(x, plan, params, dy, fused=False, residual=False)
     check(got, want, dy, False, torch.bfloat16, f"delta {name}")
+
+
+@pytest.mark.parametrize("b,h,w,c,d,rd", [(2, 8, 8, 128, 64, 256), (1, 14, 14, 128, 64, 128),
+                                          (2, 8, 8, 256, 128, 128)], ids=["d64-rd256", "odd-pairs", "d128-rd128"])
+def test_backward_rd_variants_and_odd_pair_counts(b, h, w, c, d, rd) -> None:
+    """rd = 4d and rd = d, and a slot count that is not a multiple of 32 (B * Q_s odd: the
+    batched-GEMM channel side instead of the fused d = 64 kernel)."""
+    announce(f"block backward variant B={b} {h}x{w}x{c} d={d} rd={rd}")
+    plan, x, params, dy = make_case(b, h, w, c, d, "shifted", 0, torch.bfloat16, seed=4, rd=rd)
+    want = oracle_grads(x, plan, params, dy, fused=True, residual=True)
+    got = hip_grads(x, plan, params, dy, fused=True, residual=True)
+    check(got, want, dy, True, torch.bfloat16, f"variant d={d} rd={rd}")
 
 
 def test_block_backward_without_residual() -> None:
