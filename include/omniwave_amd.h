@@ -199,10 +199,11 @@ int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int3
 int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du, void* dv, int64_t n,
                 int32_t dtype, void* stream);
 
-/* [Q_c][slots][d] tiles -> g [batch * H * W, C] fp32 at their routed positions
- * (unpack_tiles, reference.py:67-117; pads dropped).  d % 8 == 0; dxt 16-byte aligned. */
+/* [Q_c][slots][d] tiles -> g [batch * H * W, C] (dtype) at their routed positions
+ * (unpack_tiles, reference.py:67-117; pads dropped).  Every element of g is written (the
+ * routes are permutations), so g needs no clearing.  d % 8 == 0; dxt 16-byte aligned. */
 int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* channel_index,
-                   const OwPlan* plan, int32_t batch, int32_t dtype, float* g, void* stream);
+                   const OwPlan* plan, int32_t batch, int32_t dtype, void* g, void* stream);
 
 /* Token mixing of 16-row tiles (the A_{u,v,o} products of reference.py:155-162 and their
  * transposes): out_tile = m1 in1_tile (+ m2 in2_tile when in2 is non-NULL); m1, m2 [16][16]
@@ -218,7 +219,7 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
 
 /* Per row: dx = (residual ? dout : 0) + r g - x r^3 / C sum_c(g x) with rscale, or + g
  * without it (the RMSNorm and residual of omniweave/models/block.py:83-108). */
-int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx,
+int ow_bwd_rmsnorm(const void* x, const void* g, const float* rscale, const void* dout, void* dx,
                    int64_t rows, int32_t channels, int32_t residual, int32_t dtype, void* stream);
 
 /* Fused channel side of the backward for d = 64 (rd 128 or 256), replacing six channel-side

@@ -31,7 +31,7 @@ from omniwave_amd.routing import RoutePlan, device_tables
 _DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
                torch.float16: _native.OW_DTYPE_F16}
 # Waves of ow_tile_outer: each sums a strided share of the tiles into one [16][16] partial.
-_OUTER_WAVES = 1024
+_OUTER_WAVES = 8192
 # Most slot chunks of a parameter-gradient GEMM (see _slot_reduce).
 _SPLITS = 64
 
@@ -71,7 +71,7 @@ def _slot_reduce(a: Tensor, b: Tensor) -> Tensor:
     splits = max(s for s in range(1, min(_SPLITS, tiles) + 1) if tiles % s == 0) if tiles else 1
     chunk = slots // splits
     part = torch.bmm(a.view(q_c * splits, chunk, m).transpose(1, 2), b.view(q_c * splits, chunk, n))
-    return part.view(q_c, splits, m, n).float().sum(dim=1)
+    return part.view(q_c, splits, m, n).sum(dim=1, dtype=torch.float32)
 
 
 def _fp32(t: Tensor, device) -> Tensor:
@@ -181,7 +181,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
         del dpu, dpv, wp, xt, dyt
 
         # dX' back to NHWC, then through the RMSNorm (+ the residual's identity).
-        g = torch.zeros(n_rows, plan.channels, dtype=torch.float32, device=dev)
+        g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing
         _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan),
                                          batch, code, g.data_ptr(), stream), "ow_bwd_scatter")
         dx = torch.empty_like(x)

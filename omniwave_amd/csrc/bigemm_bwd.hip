@@ -148,11 +148,11 @@ __global__ void __launch_bounds__(256) bwd_gate_kernel(const uint16_t* u, const 
   reinterpret_cast<uint4*>(dv)[i] = uint4{vo[0], vo[1], vo[2], vo[3]};
 }
 
-// dX' slots -> g [rows, C] fp32, 8 channels per thread (every valid (row, channel) is written
-// exactly once: the routes are permutations of tokens and channels).
-template <class Ty>
+// dX' slots -> g [rows, C] (activation dtype), 8 channels per thread (every valid (row,
+// channel) is written exactly once: the routes are permutations of tokens and channels, so g
+// needs no clearing).
 __global__ void __launch_bounds__(256) bwd_scatter_kernel(const uint16_t* dxt, const int32_t* tok, const int32_t* chan,
-                                                          float* g, int64_t slots, int32_t n_tok, int32_t channels,
+                                                          uint16_t* g, int64_t slots, int32_t n_tok, int32_t channels,
                                                           int32_t q_s, int32_t d, int32_t vec, int64_t total8) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total8) return;
@@ -164,21 +164,16 @@ __global__ void __launch_bounds__(256) bwd_scatter_kernel(const uint16_t* dxt, c
   const int64_t row = slot_row(tok, k, q_s, n_tok);
   if (row < 0) return;
   const uint4 src = *reinterpret_cast<const uint4*>(dxt + i * 8);
-  const uint32_t sw[4] = {src.x, src.y, src.z, src.w};
-  float v[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = Ty::to_f32(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
   const int32_t* chp = chan + q * d + c0;
-  float* dst = g + row * channels;
+  uint16_t* dst = g + row * channels;
   if (vec && channel_run8(chp, channels)) {
-    float4* p = reinterpret_cast<float4*>(dst + chp[0]);
-    p[0] = float4{v[0], v[1], v[2], v[3]};
-    p[1] = float4{v[4], v[5], v[6], v[7]};
+    *reinterpret_cast<uint4*>(dst + chp[0]) = src;
   } else {
+    const uint32_t sw[4] = {src.x, src.y, src.z, src.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int32_t ch = chp[j];
-      if (ch >= 0 && ch < channels) dst[ch] = v[j];
+      if (ch >= 0 && ch < channels) dst[ch] = static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1)));
     }
   }
 }
@@ -187,7 +182,7 @@ __global__ void __launch_bounds__(256) bwd_scatter_kernel(const uint16_t* dxt, c
 // step: dx = (dout) + r g - x r^3 / C sum(g x)   (norm)   or   (dout) + g.  C % 8 == 0 and
 // 16-byte aligned x / dout / dx (the caller checks).
 template <class Ty>
-__global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, const float* g, const float* rscale,
+__global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, const uint16_t* g, const float* rscale,
                                                           const uint16_t* dout, uint16_t* dx, int64_t rows,
                                                           int32_t channels, int32_t residual, int32_t lpr) {
   const int lane = threadIdx.x & 63;
@@ -208,14 +203,11 @@ __global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, con
     float dot = 0.0f;
     if (live) {
       for (int c8 = sub; c8 < c8n; c8 += lpr) {
-        float xf[8];
+        float xf[8], gf[8];
         unpack8(*reinterpret_cast<const uint4*>(x + base + 8 * c8), xf);
-        const float4 g0 = *reinterpret_cast<const float4*>(g + base + 8 * c8);
-        const float4 g1 = *reinterpret_cast<const float4*>(g + base + 8 * c8 + 4);
-        dot = fmaf(g0.x, xf[0], dot); dot = fmaf(g0.y, xf[1], dot);
-        dot = fmaf(g0.z, xf[2], dot); dot = fmaf(g0.w, xf[3], dot);
-        dot = fmaf(g1.x, xf[4], dot); dot = fmaf(g1.y, xf[5], dot);
-        dot = fmaf(g1.z, xf[6], dot); dot = fmaf(g1.w, xf[7], dot);
+        unpack8(*reinterpret_cast<const uint4*>(g + base + 8 * c8), gf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot = fmaf(gf[j], xf[j], dot);
       }
     }
     for (int m = lpr >> 1; m > 0; m >>= 1) dot += __shfl_xor(dot, m);
@@ -231,9 +223,8 @@ __global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, con
 #pragma unroll
       for (int j = 0; j < 8; ++j) df[j] = 0.0f;
     }
-    const float4 g0 = *reinterpret_cast<const float4*>(g + base + 8 * c8);
-    const float4 g1 = *reinterpret_cast<const float4*>(g + base + 8 * c8 + 4);
-    const float gf[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    float gf[8];
+    unpack8(*reinterpret_cast<const uint4*>(g + base + 8 * c8), gf);
     uint32_t o[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -247,24 +238,24 @@ __global__ void __launch_bounds__(256) bwd_rmsnorm_kernel(const uint16_t* x, con
 
 // Any C and alignment: one wave per row, one channel per lane step.
 template <class Ty>
-__global__ void __launch_bounds__(256) bwd_rmsnorm_scalar_kernel(const uint16_t* x, const float* g, const float* rscale,
+__global__ void __launch_bounds__(256) bwd_rmsnorm_scalar_kernel(const uint16_t* x, const uint16_t* g, const float* rscale,
                                                                  const uint16_t* dout, uint16_t* dx, int64_t rows,
                                                                  int32_t channels, int32_t residual) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const uint16_t* xr = x + row * channels;
-  const float* gr = g + row * channels;
+  const uint16_t* gr = g + row * channels;
   float r = 1.0f, coef = 0.0f;
   if (rscale) {
     r = rscale[row];
     float dot = 0.0f;
-    for (int c = lane; c < channels; c += 64) dot = fmaf(gr[c], Ty::to_f32(xr[c]), dot);
+    for (int c = lane; c < channels; c += 64) dot = fmaf(Ty::to_f32(gr[c]), Ty::to_f32(xr[c]), dot);
     for (int m = 32; m > 0; m >>= 1) dot += __shfl_xor(dot, m);
     coef = dot * r * r * r / static_cast<float>(channels);
   }
   for (int c = lane; c < channels; c += 64) {
-    float v = r * gr[c] - coef * Ty::to_f32(xr[c]);
+    float v = r * Ty::to_f32(gr[c]) - coef * Ty::to_f32(xr[c]);
     if (residual) v += Ty::to_f32(dout[row * channels + c]);
     dx[row * channels + c] = Ty::from_f32(v);
   }
@@ -717,7 +708,7 @@ int ow_bwd_gate(const void* u, const void* v, const void* dz, void* z, void* du,
 }
 
 int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan,
-                   int32_t batch, int32_t dtype, float* g, void* stream) {
+                   int32_t batch, int32_t dtype, void* g, void* stream) {
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
@@ -729,7 +720,7 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
   }
   OW_CHECK_ARG(dxt && token_index && channel_index && g, "tensor pointer is NULL");
   if (dtype == OW_DTYPE_F32) {
-    if (int rc = ow::bwd_scatter_f32(static_cast<const float*>(dxt), token_index, channel_index, g,
+    if (int rc = ow::bwd_scatter_f32(static_cast<const float*>(dxt), token_index, channel_index, static_cast<float*>(g),
                                      static_cast<int64_t>(batch) * q_s * ow::kG, plan->height * plan->width,
                                      plan->channels, q_s, q_c, plan->channel_tile, static_cast<hipStream_t>(stream)))
       return rc;
@@ -745,18 +736,14 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* src = static_cast<const uint16_t*>(dxt);
   const int32_t n_tok = plan->height * plan->width;
-  if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::BF16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, src,
-                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, vec, total8);
-  else
-    hipLaunchKernelGGL(ow::bwd_scatter_kernel<ow::F16>, dim3(ow::blocks_for(total8)), dim3(256), 0, s, src,
-                       token_index, channel_index, g, slots, n_tok, plan->channels, q_s, d, vec, total8);
+  hipLaunchKernelGGL(ow::bwd_scatter_kernel, dim3(ow::blocks_for(total8)), dim3(256), 0, s, src, token_index,
+                     channel_index, static_cast<uint16_t*>(g), slots, n_tok, plan->channels, q_s, d, vec, total8);
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_scatter_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
 }
 
-int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const void* dout, void* dx, int64_t rows,
+int ow_bwd_rmsnorm(const void* x, const void* g, const float* rscale, const void* dout, void* dx, int64_t rows,
                    int32_t channels, int32_t residual, int32_t dtype, void* stream) {
   OW_CHECK_ARG(rows >= 0 && channels >= 1, "bad shape rows=%lld channels=%d", (long long)rows, channels);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
@@ -767,7 +754,8 @@ int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const voi
   }
   OW_CHECK_ARG(x && g && dx && (!residual || dout), "tensor pointer is NULL");
   if (dtype == OW_DTYPE_F32) {
-    if (int rc = ow::bwd_rmsnorm_f32(static_cast<const float*>(x), g, rscale, static_cast<const float*>(dout),
+    if (int rc = ow::bwd_rmsnorm_f32(static_cast<const float*>(x), static_cast<const float*>(g), rscale,
+                                     static_cast<const float*>(dout),
                                      static_cast<float*>(dx), rows, channels, residual,
                                      static_cast<hipStream_t>(stream)))
       return rc;
@@ -782,10 +770,10 @@ int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const voi
   if (!vec) {
     const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
     if (dtype == OW_DTYPE_BF16)
-      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale,
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), cu(g), rscale,
                          cu(dout), out, rows, channels, residual);
     else
-      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale,
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_scalar_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), cu(g), rscale,
                          cu(dout), out, rows, channels, residual);
   } else {
     int32_t lpr = 1;
@@ -793,10 +781,10 @@ int ow_bwd_rmsnorm(const void* x, const float* g, const float* rscale, const voi
     const int64_t rows_per_block = 4 * (64 / lpr);
     const unsigned blocks = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
     if (dtype == OW_DTYPE_BF16)
-      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::BF16>, dim3(blocks), dim3(256), 0, s, cu(x), cu(g), rscale, cu(dout),
                          out, rows, channels, residual, lpr);
     else
-      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), g, rscale, cu(dout),
+      hipLaunchKernelGGL(ow::bwd_rmsnorm_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, cu(x), cu(g), rscale, cu(dout),
                          out, rows, channels, residual, lpr);
   }
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_rmsnorm_kernel launch")) return rc;
