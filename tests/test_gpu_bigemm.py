@@ -237,3 +237,32 @@ def test_bigemm_front_door_and_block(oracle_backend) -> None:
         block.backend = "reference"
         eager = block(xd)
     assert rel_l2((fused - xd).cpu(), (eager - xd).cpu()) <= 1e-2
+
+
+@pytest.mark.parametrize("stage", ["s1", "s3"])
+def test_hip_graph_replays_match_eager(stage) -> None:
+    """The fused block captured in a HIP graph (both kernels, with the statistics pass at d=128):
+    every one of several replays, with eager work and synchronisations between them, reproduces
+    the eager output bitwise."""
+    h, w, c, d = STAGES[stage]
+    announce(f"hip graph replays stage={stage} shifted bf16 B=4")
+    plan, x, params, norm_w = make_case(4, h, w, c, d, "shifted", 0, torch.bfloat16, seed=9)
+    dp, xd, nw = to_dev(params), x.to(DEV), norm_w.to(DEV)
+    eager = bigemm_block_hip(xd, nw, plan, **dp)  # packs the weights before capture
+    static_x = xd.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        bigemm_block_hip(static_x, nw, plan, **dp)
+        torch.cuda.current_stream().synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            out = bigemm_block_hip(static_x, nw, plan, **dp)
+    torch.cuda.current_stream().wait_stream(stream)
+    for k in range(4):
+        scratch = bigemm_block_hip(xd * 0.5, nw, plan, **dp)  # eager work in between
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {k} differs"
+        assert scratch.shape == out.shape
