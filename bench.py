@@ -324,7 +324,10 @@ def backward_section(batch: int, steps: int, dev) -> dict:
         def fwd():
             return bigemm_block_hip(x, nw, plan, **params)
 
-        def fwd_bwd():
+        def fwd_bwd():  # gradients start from None each step, as after zero_grad(set_to_none=True)
+            x.grad = nw.grad = None
+            for t in params.values():
+                t.grad = None
             y = fwd()
             y.backward(dy)
 

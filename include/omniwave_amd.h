@@ -211,9 +211,9 @@ int ow_bwd_scatter(const void* dxt, const int32_t* token_index, const int32_t* c
 int ow_tile_mix(const void* in1, const float* m1, const void* in2, const float* m2, void* out,
                 int64_t n_tiles, int32_t d, int32_t dtype, void* stream);
 
-/* Gradient of a token matrix: partial[w] = sum over the tiles of wave w of in1_tile in2_tile^T
- * ([16][16] fp32 each, w < n_waves, tiles assigned round-robin); the caller sums the
- * n_waves partials (a fixed order, so the result is deterministic). */
+/* Gradient of a token matrix: partial[i][j][w] = (sum over the tiles of wave w of
+ * in1_tile in2_tile^T)[i][j] (fp32, [16][16][n_waves], w < n_waves, tiles assigned
+ * round-robin); the caller sums over w (a fixed order, so the result is deterministic). */
 int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_waves, int64_t n_tiles,
                   int32_t d, int32_t dtype, void* stream);
 

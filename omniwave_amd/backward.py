@@ -52,10 +52,10 @@ def _tile_mix(lib, in1: Tensor, m1: Tensor, in2: Tensor | None, m2: Tensor | Non
 
 def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -> Tensor:
     n_tiles = in1.numel() // (16 * d)
-    partial = torch.empty(_OUTER_WAVES, 16, 16, dtype=torch.float32, device=in1.device)
+    partial = torch.empty(16, 16, _OUTER_WAVES, dtype=torch.float32, device=in1.device)
     _native.check(lib.ow_tile_outer(in1.data_ptr(), in2.data_ptr(), partial.data_ptr(), _OUTER_WAVES, n_tiles, d,
                                     code, stream), "ow_tile_outer")
-    return partial.sum(dim=0)
+    return partial.sum(dim=2)
 
 
 def _slot_reduce(a: Tensor, b: Tensor) -> Tensor:

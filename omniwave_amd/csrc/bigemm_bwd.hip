@@ -402,7 +402,8 @@ __global__ void __launch_bounds__(256) tile_mix_kernel(const uint16_t* in1, cons
 }
 
 // Sum over tiles of in1_tile in2_tile^T ([16][d] x [d][16] -> [16][16]), grid-strided; each wave
-// writes its partial sum (lane (l16, h) register i = out[4h + i][l16]) to partial[wave][256].
+// writes its partial sum (lane (l16, h) register i = out[4h + i][l16]) to partial[256][n_waves]
+// (element-major, so the sum over waves is a contiguous reduction).
 template <class Ty>
 __global__ void __launch_bounds__(256) tile_outer_kernel(const uint16_t* in1, const uint16_t* in2, float* partial,
                                                          int64_t n_tiles, int32_t d) {
@@ -421,9 +422,8 @@ __global__ void __launch_bounds__(256) tile_outer_kernel(const uint16_t* in1, co
     }
   }
   mfma_drain();
-  float* p = partial + wave * 256;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[(4 * h + i) * 16 + l16] = acc[i];
+  for (int i = 0; i < 4; ++i) partial[((4 * h + i) * 16 + l16) * n_waves + wave] = acc[i];
 }
 
 // ---- Fused channel side of the backward, d = 64 -----------------------------------------
@@ -610,16 +610,29 @@ __global__ void __launch_bounds__(256) bwd_channel_d64_kernel(BwdChannelArgs a) 
   }
   mfma_drain();
   if (!live) return;
-  // W', dP_u, dP_v: lane = channel 32 mb + l32, register i = slot pair_token_row(i, hh).
+  // W', dP_u, dP_v (lane = channel 32 mb + l32, register i = slot pair_token_row(i, hh)) go
+  // through a per-wave LDS tile [32 slots][kStageLd] and leave as 16-byte row vectors.  The
+  // buffer of chunk NCH is free: no copy targets it after the last barrier of the loop.
+  constexpr int kStageLd = kBwdD + 8;
+  static_assert(4 * 32 * kStageLd <= CH_ELEMS, "staging tiles fit in one weight buffer");
+  uint16_t* stage = wb[NCH & 1] + wave * 32 * kStageLd;
+  const f32x16* mats[3] = {W, DPu, DPv};
+  uint16_t* outs[3] = {a.wp, a.dpu, a.dpv};
 #pragma unroll
-  for (int mb = 0; mb < kBwdMB; ++mb)
+  for (int m = 0; m < 3; ++m) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t off = (slot0 + pair_token_row(i, hh)) * kBwdD + 32 * mb + l32;
-      a.wp[off] = Ty::from_f32(W[mb][i]);
-      a.dpu[off] = Ty::from_f32(DPu[mb][i]);
-      a.dpv[off] = Ty::from_f32(DPv[mb][i]);
+    for (int mb = 0; mb < kBwdMB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) stage[pair_token_row(i, hh) * kStageLd + 32 * mb + l32] = Ty::from_f32(mats[m][mb][i]);
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+      *reinterpret_cast<u32x4*>(outs[m] + (slot0 + r) * kBwdD + c8) =
+          *reinterpret_cast<const u32x4*>(stage + r * kStageLd + c8);
     }
+    wave_lds_sync();
+  }
 }
 
 unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }

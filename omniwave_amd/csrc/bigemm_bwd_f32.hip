@@ -156,7 +156,7 @@ __global__ void __launch_bounds__(256) tile_mix_f32_kernel(const float* in1, con
   out[idx] = acc;
 }
 
-// partial[w][i][j] = sum over tiles t = w, w + n_waves, ... of sum_c in1[t][i][c] in2[t][j][c];
+// partial[i][j][w] = sum over tiles t = w, w + n_waves, ... of sum_c in1[t][i][c] in2[t][j][c];
 // lane l of wave w owns outputs 4l .. 4l + 3.
 __global__ void __launch_bounds__(256) tile_outer_f32_kernel(const float* in1, const float* in2, float* partial,
                                                              int64_t n_tiles, int32_t d) {
@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(256) tile_outer_f32_kernel(const float* in1, c
     }
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) partial[wave * 256 + 4 * lane + k] = acc[k];
+  for (int k = 0; k < 4; ++k) partial[(4 * lane + k) * n_waves + wave] = acc[k];
 }
 
 }  // namespace
