@@ -148,108 +148,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
 }
 
-// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane), as
-// a buffer load (MUBUF) rather than a global one: the compiler then keeps counting LDS reads
-// that are in flight at the same time exactly, instead of waiting for all of them before each
-// use.  The buffer covers the fragment only; src is wave-uniform.
-__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, int lane, bool valid = true) {
-  // valid = false: a buffer of 0 bytes, so the load reads nothing and writes zeros (no branch).
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), 0, valid ? 1024 : 0, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst), 16, lane * 16, 0, 0, 0);
-}
-
-// The two halves of the channel side of one 32-row chunk for one pair, split so that the
-// gate of chunk ec - 1 can run on the vector unit while the U'/V' products of chunk ec run on
-// the matrix core (same arithmetic, in the same order, as pair_chunk).
-// U'^T, V'^T from the B_u'^T / B_v'^T fragments at f[0, KS) and f[KS, 2 KS).
-template <class Ty, int KS>
-__device__ __forceinline__ void chunk_uv(const u32x4 (&Pu)[KS], const u32x4 (&Pv)[KS], const u32x4* f, int lane,
-                                         f32x16& U, f32x16& V) {
-  U = f32x16{};
-  V = f32x16{};
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    U = Ty::mma32(f[ks * 64 + lane], Pu[ks], U);
-    V = Ty::mma32(f[(KS + ks) * 64 + lane], Pv[ks], V);
-  }
-}
-
-// Z = U'V' / (1 + 2^U') and W[mb] += Z B_o with the B_o fragments at f[2 KS + 2 mb + s].
-template <class Ty, int KS, int MB>
-__device__ __forceinline__ void chunk_gate_w(const f32x16& U, const f32x16& V, const u32x4* f, int lane,
-                                             f32x16 (&W)[MB]) {
-  u32x4 Z[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
-                          silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) W[mb] = Ty::mma32(Z[s], f[(2 * KS + 2 * mb + s) * 64 + lane], W[mb]);
-}
-
-// One steady-state iteration of the channel loop for one pair: the U'/V' products of chunk u
-// (fragments f[0, 2 KS) of the unit) on the matrix core, interleaved in program order with the
-// gate of chunk u - 1 (U, V in: its accumulators) on the vector unit, then W += Z B_o of chunk
-// u - 1 (fragments f[2 KS, 2 KS + 2 MB)); U, V out: chunk u's accumulators.  The scheduling
-// barriers keep each K step's two products next to its share of the gate, with the fragment
-// reads LA products ahead.  Same arithmetic, in the same order, as pair_chunk.
-template <class Ty, int KS, int MB>
-__device__ __forceinline__ void chunk_step(const u32x4 (&Pu)[KS], const u32x4 (&Pv)[KS], const u32x4* f, int lane,
-                                           f32x16& U, f32x16& V, f32x16 (&W)[MB]) {
-  constexpr int NF = 2 * KS + 2 * MB;
-  constexpr int LA = 4;
-  constexpr int EPS = 16 / KS;  // gate elements per K step
-  static_assert(EPS % 2 == 0, "whole packed pairs per K step");
-  // Read order = use order: B_u'^T ks, B_v'^T ks for each ks, then B_o (s, mb) s-major.
-  auto slot = [](int i) {
-    if (i < 2 * KS) return (i & 1) ? KS + (i >> 1) : (i >> 1);
-    const int j = i - 2 * KS, s = j / MB, mb = j % MB;
-    return 2 * KS + 2 * mb + s;
-  };
-  u32x4 fr[NF];
-#pragma unroll
-  for (int i = 0; i < LA; ++i) fr[i] = f[slot(i) * 64 + lane];
-  f32x16 Un = {}, Vn = {};
-  uint32_t z[8];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-    for (int i = 2 * ks + LA; i < 2 * ks + 2 + LA; ++i)
-      if (i < NF) fr[i] = f[slot(i) * 64 + lane];
-    Un = Ty::mma32(fr[2 * ks], Pu[ks], Un);
-    Vn = Ty::mma32(fr[2 * ks + 1], Pv[ks], Vn);
-#pragma unroll
-    for (int e = ks * EPS; e < (ks + 1) * EPS; e += 2)
-      z[e >> 1] = Ty::pack2(silu_gate(U[e], V[e]), silu_gate(U[e + 1], V[e + 1]));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  const u32x4 Z[2] = {u32x4{z[0], z[1], z[2], z[3]}, u32x4{z[4], z[5], z[6], z[7]}};
-#pragma unroll
-  for (int j = 0; j < 2 * MB; ++j) {
-    const int i = 2 * KS + j;
-    if (i + LA < NF) fr[i + LA] = f[slot(i + LA) * 64 + lane];
-    const int s = j / MB, mb = j % MB;
-    W[mb] = Ty::mma32(Z[s], fr[i], W[mb]);
-  }
-  U = Un;
-  V = Vn;
-}
-
-// round(x + d) per element of two packed pairs, the second rounding of the residual
-// (omniweave/models/block.py:87-108; d is already the rounded delta).
-template <class Ty>
-__device__ __forceinline__ uint32_t add_residual2(uint32_t x, uint32_t d) {
-  return Ty::pack2(Ty::to_f32(lo16(x)) + Ty::to_f32(lo16(d)), Ty::to_f32(hi16(x)) + Ty::to_f32(hi16(d)));
-}
-
-template <class Ty>
-__device__ __forceinline__ uint16_t add_residual1(uint16_t x, uint16_t d) {
-  return Ty::from_f32(Ty::to_f32(x) + Ty::to_f32(d));
+// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane).
+__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, int lane) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + lane * 8),
+                                   (__attribute__((address_space(3))) void*)(dst), 16, 0, 0);
 }
 
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -277,21 +179,15 @@ bigemm_fwd_kernel(FwdArgs a) {
   static_assert(CH_ELEMS <= ROWS * LDX, "a weight chunk must fit in the x-tile region");
 
   // LDS regions.  xs: the x tile until the token side has read it; then the odd weight
-  // units; after the channel loop, delta.  wb: the even weight units.
-  //   fp8: unit ec = chunk ec.
-  //   bf16 / fp16: unit u (u = 0..NCH) = the B_u'^T / B_v'^T fragments of chunk u (u < NCH) and
-  //   the B_o fragments of chunk u - 1 (u >= 1), at the fragment slots they have in a chunk:
-  //   iteration u runs the U'/V' products of chunk u on the matrix core while the vector unit
-  //   evaluates the gate of chunk u - 1, then Z B_o of chunk u - 1.
+  // chunks; after the chunk loop, each wave's W^T tile (its own 32 rows) and then delta.
+  // wb: the even weight chunks.
   __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LDX];
   __shared__ __attribute__((aligned(16))) uint16_t wb[CH_ELEMS];
   __shared__ int32_t rowid[ROWS];  // b * n_tok + token, -1 for pad rows
   __shared__ float rsc[ROWS];      // RMSNorm scale of each row (1 without norm)
   __shared__ int32_t chx[D];
 
-  // wave is read through a scalar register so that the weight-copy addresses are provably
-  // uniform (buffer descriptors in scalar registers, no per-lane loop).
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   const int bid = xcd_remap(blockIdx.x, a.n_chunks * a.q_c);
   const int qc = bid % a.q_c, chunk = bid / a.q_c;
@@ -301,22 +197,7 @@ bigemm_fwd_kernel(FwdArgs a) {
   auto issue_chunk = [&](int ec) {
     const uint16_t* src = wsrc + static_cast<size_t>(ec) * CH_ELEMS;
     uint16_t* dst = chunk_buf(ec);
-    if constexpr (F8) {
-      for (int f = wave; f < CH_UNITS; f += kWaves) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane);
-    } else {
-      // U'/V' fragments of chunk ec (ec < NCH), B_o fragments of chunk ec - 1 (ec >= 1); the
-      // slots of the missing part (units 0 and NCH) load nothing.  A fixed count per wave keeps
-      // the channel loop free of branches.
-      static_assert(FR_CH % kWaves == 0, "whole fragments per wave");
-#pragma unroll
-      for (int k = 0; k < FR_CH / kWaves; ++k) {
-        const int f = wave + kWaves * k;
-        const bool uv = f < 2 * FR_U;
-        const bool valid = uv ? ec < NCH : ec >= 1;
-        const uint16_t* s = (uv || ec == 0) ? src : src - CH_ELEMS;
-        copy_frag_to_lds(s + f * kFragElems, dst + f * kFragElems, lane, valid);
-      }
-    }
+    for (int f = wave; f < CH_UNITS; f += kWaves) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane);
   };
   issue_chunk(0);
 
@@ -462,14 +343,15 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) W[p][mb][i] = 0.0f;
 
-  if constexpr (F8) {
-    for (int ec = 0; ec < NCH; ++ec) {
-      wait_lds_dma();
-      // Chunk ec has landed; every wave is done with chunk ec - 1 (and, at ec = 0, with the x
-      // tile), so the buffer of chunk ec + 1 is free.
-      __syncthreads();
-      if (ec + 1 < NCH) issue_chunk(ec + 1);
-      const uint16_t* cw = chunk_buf(ec);
+  for (int ec = 0; ec < NCH; ++ec) {
+    wait_lds_dma();
+    // Chunk ec has landed; every wave is done with chunk ec - 1 (and, at ec = 0, with the x
+    // tile), so the buffer of chunk ec + 1 is free.
+    __syncthreads();
+    if (ec + 1 < NCH) issue_chunk(ec + 1);
+    const uint16_t* cw = chunk_buf(ec);
+    const u32x4* cf = reinterpret_cast<const u32x4*>(cw);
+    if constexpr (F8) {
       const u32x2* c8 = reinterpret_cast<const u32x2*>(cw);
       const u32x4* co = reinterpret_cast<const u32x4*>(cw + FR_U * kFragElems);
       auto fu = [&](int ks) { return c8[ks * (kF8FragBytes / 8) + lane]; };
@@ -478,41 +360,18 @@ bigemm_fwd_kernel(FwdArgs a) {
       const float du = f8s[kF8DeqU], dv = f8s[kF8DeqV];
 #pragma unroll
       for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, du, dv, W[p]);
-    }
-  } else {
-    // Units 0..NCH (see the LDS regions above).  Each iteration starts with unit u landed and
-    // every wave done with unit u - 1 (at u = 0: with the x tile), so unit u + 1 may be issued
-    // into the buffer of unit u - 1.
-    f32x16 Uc[NP], Vc[NP];  // U'^T, V'^T of the chunk whose gate is pending
-    wait_lds_dma();
-    __syncthreads();
-    issue_chunk(1);
-    {
-      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(0));
+    } else {
+      auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
+      auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
+      auto fo = [&](int mb, int s) { return cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane]; };
 #pragma unroll
-      for (int p = 0; p < NP; ++p) chunk_uv<Ty, KS>(Pu[p], Pv[p], cf, lane, Uc[p], Vc[p]);
-    }
-    for (int u = 1; u < NCH; ++u) {
-      mfma_drain();
-      wait_lds_dma();
-      __syncthreads();
-      issue_chunk(u + 1);
-      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(u));
-#pragma unroll
-      for (int p = 0; p < NP; ++p) chunk_step<Ty, KS, MB>(Pu[p], Pv[p], cf, lane, Uc[p], Vc[p], W[p]);
-    }
-    wait_lds_dma();
-    __syncthreads();
-    {
-      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(NCH));
-#pragma unroll
-      for (int p = 0; p < NP; ++p) chunk_gate_w<Ty, KS, MB>(Uc[p], Vc[p], cf, lane, W[p]);
+      for (int p = 0; p < NP; ++p) pair_chunk<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
     }
   }
 
   // Output side: delta = A_o W per pair (lane = channel 32 mb + l32, registers = tokens;
-  // LayerScale folded into B_o); the rounded delta is written over the pair's own 32 rows of
-  // xs, and the residual is added on the way out.  The barrier first: weight units live in
+  // LayerScale folded into B_o); the rounded delta, or round(x + delta) with x from the
+  // token-side operands, is written over the pair's own 32 rows of xs.  The barrier first: the odd weight chunks live in
   // xs.  No branch separates an MFMA from the reads of its result.
   mfma_drain();
   __syncthreads();
@@ -525,13 +384,15 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       auto dst = [&](int i) { return &st[pair_token_row(i, hh) * LDX + 32 * mb + l32]; };
-      pair_store_block<Ty, false>(dl[mb], xk[p][mb], dst);
+      if (a.residual)
+        pair_store_block<Ty, true>(dl[mb], xk[p][mb], dst);
+      else
+        pair_store_block<Ty, false>(dl[mb], xk[p][mb], dst);
     }
   }
   __syncthreads();
 
-  // The finished tile to memory: round(x + delta) with x read again (same addresses, now in
-  // cache), or delta.
+  // The finished tile to memory.
   if (a.mode == kModeContig) {
     constexpr int VPR = D / 8;
     constexpr int NV = ROWS * VPR / kThreads;
@@ -540,15 +401,9 @@ bigemm_fwd_kernel(FwdArgs a) {
       const int idx = tid + i * kThreads;
       const int r = idx / VPR, v = idx % VPR;
       const int64_t id = rowid[r];
-      if (id >= 0) {
-        u32x4 d = *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
-        if (a.residual) {
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + id * a.channels + qc * D + v * 8);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) d[q] = add_residual2<Ty>(xv[q], d[q]);
-        }
-        *reinterpret_cast<u32x4*>(a.out + id * a.channels + qc * D + v * 8) = d;
-      }
+      if (id >= 0)
+        *reinterpret_cast<u32x4*>(a.out + id * a.channels + qc * D + v * 8) =
+            *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
     }
   } else if (a.mode == kModeStrided) {
     // Per 16-byte row vector: M tile columns, stored element by element (the other columns of
@@ -565,17 +420,9 @@ bigemm_fwd_kernel(FwdArgs a) {
         const int64_t id = rowid[r];
         if (id < 0) continue;
         const uint16_t* src = &xs[r * LDX + v * M];
-        const int64_t off = id * a.channels + v * 8 + strided_res;
-        if (a.residual) {
-          // x as the whole 16-byte row vector (one load), the group's M elements picked out.
-          uint32_t e[M];
-          strided_elems<M>(*reinterpret_cast<const u32x4*>(a.x + id * a.channels + v * 8), strided_res, e);
+        uint16_t* dst = a.out + id * a.channels + v * 8 + strided_res;
 #pragma unroll
-          for (int t = 0; t < M; ++t) a.out[off + t * N] = add_residual1<Ty>(static_cast<uint16_t>(e[t]), src[t]);
-        } else {
-#pragma unroll
-          for (int t = 0; t < M; ++t) a.out[off + t * N] = src[t];
-        }
+        for (int t = 0; t < M; ++t) dst[t * N] = src[t];
       }
     };
     if (a.stride == 2) scatter_strided(std::integral_constant<int, 4>{});
@@ -589,10 +436,7 @@ bigemm_fwd_kernel(FwdArgs a) {
       const int r = i / D, k = i % D;
       const int64_t id = rowid[r];
       const int c = chx[k];
-      if (id >= 0 && c >= 0) {
-        const int64_t off = id * a.channels + c;
-        a.out[off] = a.residual ? add_residual1<Ty>(a.x[off], xs[r * LDX + k]) : xs[r * LDX + k];
-      }
+      if (id >= 0 && c >= 0) a.out[id * a.channels + c] = xs[r * LDX + k];
     }
   }
 }

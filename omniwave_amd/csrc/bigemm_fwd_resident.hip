@@ -54,15 +54,36 @@ struct ResidentLds {
   u32x4 head[3][64];        // token-operand rows A_u, A_v, A_o
 };
 
+// Position of a pair's first token group 2 pair = b q_s + s (image b, group s of the image).
+// The loop advances it by the grid stride with additions only: a division per pair would cost
+// a long scalar sequence in every iteration.
+struct PairPos {
+  int32_t b, s;
+};
+
+__device__ __forceinline__ PairPos pair_pos(int64_t pair, int32_t q_s) {
+  const int64_t tg0 = 2 * pair;
+  const int32_t b = static_cast<int32_t>(tg0 / q_s);
+  return PairPos{b, static_cast<int32_t>(tg0 - static_cast<int64_t>(b) * q_s)};
+}
+
+// pos += (step_b, step_s) with step_s < q_s: the position of the pair n_wg further on.
+__device__ __forceinline__ void pair_advance(PairPos& pos, int32_t step_b, int32_t step_s, int32_t q_s) {
+  pos.b += step_b;
+  pos.s += step_s;
+  if (pos.s >= q_s) {
+    pos.s -= q_s;
+    ++pos.b;
+  }
+}
+
 // Token-table entries of the NI rows this lane loads and stores in a pair, with the image
 // index of each row (>= batch past the end).  Only loads: the values are examined one
 // iteration later (row_id), so the loads are not waited on while the row prefetch is in flight.
 template <int NI, int RPW, int RPI, int LPR>
-__device__ __forceinline__ void pair_row_tok(const ResidentArgs& a, int64_t pair, int wave, int lane,
+__device__ __forceinline__ void pair_row_tok(const ResidentArgs& a, PairPos pos, int wave, int lane,
                                              int32_t (&t)[NI], int32_t (&b)[NI]) {
-  const int64_t tg0 = 2 * pair;  // first group of the pair (uniform)
-  const int32_t b0 = static_cast<int32_t>(tg0 / a.q_s);
-  const int32_t s0 = static_cast<int32_t>(tg0 - static_cast<int64_t>(b0) * a.q_s);
+  const int32_t b0 = pos.b, s0 = pos.s;  // uniform
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int r = wave * RPW + j * RPI + lane / LPR;
@@ -128,7 +149,11 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
   int32_t ids_cur[NI], ids_prev[NI];
   int32_t tok_n[NI], img_n[NI];
   u32x4 xr[NI];
-  pair_row_tok<NI, RPW, RPI, LPR>(a, first, wave, lane, tok_n, img_n);
+  // pos: the pair whose table entries are read next; the grid stride in groups is 2 n_wg.
+  const int32_t step_b = static_cast<int32_t>(2 * n_wg / a.q_s);
+  const int32_t step_s = static_cast<int32_t>(2 * n_wg - static_cast<int64_t>(step_b) * a.q_s);
+  PairPos pos = pair_pos(first, a.q_s);
+  pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     ids_prev[j] = -1;
@@ -136,7 +161,8 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
     xr[j] = load_row_vec<C>(a.x, ids_cur[j], vcol);
   }
   if (n_iter > 1) {
-    pair_row_tok<NI, RPW, RPI, LPR>(a, first + n_wg, wave, lane, tok_n, img_n);
+    pair_advance(pos, step_b, step_s, a.q_s);
+    pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
   } else {
 #pragma unroll
     for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
@@ -171,7 +197,8 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
       xr[j] = load_row_vec<C>(a.x, ids_next[j], vcol);
     }
     if (it + 2 < n_iter) {
-      pair_row_tok<NI, RPW, RPI, LPR>(a, first + (it + 2) * n_wg, wave, lane, tok_n, img_n);
+      pair_advance(pos, step_b, step_s, a.q_s);
+      pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
     } else {
 #pragma unroll
       for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
