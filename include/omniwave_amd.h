@@ -237,6 +237,21 @@ int ow_bwd_channel(const void* pu, const void* pv, const void* dw, const void* p
                    void* z, void* du, void* dv, void* wp, void* dpu, void* dpv, int64_t slots,
                    int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
 
+/* The d = 64 backward with the token side fused in (replaces ow_tile_mix x4, ow_tile_outer x3
+ * and ow_bwd_channel; the reference's fp32 autograd recompute, omniweave/ops/triton.py:256-292):
+ * from the routed tiles X' and dY ([q_c][slots][64], ow_bwd_gather) and the fp32 [16][16] token
+ * matrices, per 32-slot pair: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw
+ * for the parameter-gradient GEMMs), the channel side of ow_bwd_channel (z, du, dv stored),
+ * dX' = A_u^T dP_u + A_v^T dP_v (stored to dxt), and the token-matrix gradients dA_u = sum
+ * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
+ * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c); element 16 t + k),
+ * which the caller sums over w.  slots % 32 == 0, bf16 / f16. */
+int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c);
+int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                 void* dv, void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d,
+                 int32_t rd, int32_t dtype, void* stream);
+
 /* Parameter gradients from the folded ones (dbu, dbv [q_c][d][rd], dbo [q_c][rd][d], fp32):
  * g_bu, g_bv, g_bo (fp32, parameter shapes), g_gamma [C] and, with norm_weight, g_norm_weight
  * [C] (each channel written once). */

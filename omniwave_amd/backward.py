@@ -7,11 +7,13 @@ accumulation, entirely on the HIP stream of the gradient:
 * routing, RMSNorm, gate and parameter fold-back are the libomniwave_amd.so kernels
   (``ow_bwd_gather``, ``ow_bwd_gate``, ``ow_bwd_scatter``, ``ow_bwd_rmsnorm``,
   ``ow_bwd_params``, ``ow_fold_weights``);
-* the 16x16 token-side products are ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA);
-* the channel side (U', V', dZ, the gate, W', dP_u, dP_v) is one fused MFMA kernel for d = 64
-  (``ow_bwd_channel``) and otherwise plain batched GEMMs over all slots of a channel group
-  (``torch.bmm`` -> hipBLASLt, every right operand contiguous) around ``ow_bwd_gate``; the
-  parameter-gradient reductions over slots are batched GEMMs in both cases.
+* for d = 64 one fused MFMA kernel (``ow_bwd_fused``) does the token side (P_u, P_v, dW'), the
+  channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u, dP_v), dX' and the token-matrix
+  gradients (per-workgroup partials); otherwise the 16x16 token-side products are
+  ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
+  of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
+  ``ow_bwd_gate``;
+* the parameter-gradient reductions over slots are batched GEMMs in both cases.
 
 Gradients are formed for the folded operands the forward evaluates (B_u'' = -log2(e) w B_u,
 B_v'' = -ln(2) w B_v, B_o'' = B_o diag(gamma), SiLU(U) V = U'V' / (1 + 2^U')) and mapped back
@@ -110,7 +112,6 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     nw = _fp32(norm_weight, dev) if fuse_norm else None
     gm = _fp32(gamma, dev)
     au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
-    au_t, av_t, ao_t = (a.t().contiguous() for a in (au, av, ao))
 
     with torch.cuda.device(dev):
         rscale = None
@@ -119,17 +120,6 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             _native.check(lib.ow_rms_scale(x.data_ptr(), rscale.data_ptr(), n_rows, plan.channels, eps, code,
                                            stream), "ow_rms_scale")
 
-        # Folded weights in the compute dtype, plain and transposed (both contiguous).
-        bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
-        bv, bo_t = torch.empty_like(bu), torch.empty_like(bu)
-        bu_t = torch.empty(q_c, rd, d, dtype=dtype, device=dev)
-        bv_t, bo = torch.empty_like(bu_t), torch.empty_like(bu_t)
-        _native.check(lib.ow_fold_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
-                                          nw.data_ptr() if nw is not None else None, gm.data_ptr(), ch.data_ptr(),
-                                          plan.channels, q_c, d, rd, code, bu.data_ptr(), bu_t.data_ptr(),
-                                          bv.data_ptr(), bv_t.data_ptr(), bo.data_ptr(), bo_t.data_ptr(), stream),
-                      "ow_fold_weights")
-
         # Routed tiles of X' = x r and of dY.
         xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
         dyt = torch.empty_like(xt)
@@ -137,27 +127,49 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                         else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), batch,
                                         code, xt.data_ptr(), dyt.data_ptr(), stream), "ow_bwd_gather")
 
-        # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
-        pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
-        pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
-        dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
-
-        # Channel side and gate: one fused kernel for d = 64, else batched GEMMs + the gate kernel.
         if d == 64 and slots % 32 == 0 and dtype != torch.float32:
+            # One fused kernel: token side, channel side and gate, dX', and the token-matrix
+            # gradients as per-workgroup partials.
             nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
             wpk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
             _native.check(lib.ow_pack_bwd_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
                                                   nw.data_ptr() if nw is not None else None, gm.data_ptr(),
                                                   ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
                                                   stream), "ow_pack_bwd_weights")
+            pu, pv, dw = torch.empty_like(xt), torch.empty_like(xt), torch.empty_like(xt)
             z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
             du, dv = torch.empty_like(z), torch.empty_like(z)
-            wp, dpu, dpv = torch.empty_like(pu), torch.empty_like(pu), torch.empty_like(pu)
-            _native.check(lib.ow_bwd_channel(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), wpk.data_ptr(), nbytes,
-                                             z.data_ptr(), du.data_ptr(), dv.data_ptr(), wp.data_ptr(),
-                                             dpu.data_ptr(), dpv.data_ptr(), slots, q_c, d, rd, code, stream),
-                          "ow_bwd_channel")
+            dxt = torch.empty_like(xt)
+            n_part = lib.ow_bwd_fused_partials(slots, q_c)
+            partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
+            _native.check(lib.ow_bwd_fused(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                           ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
+                                           dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(),
+                                           dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
+                                           stream), "ow_bwd_fused")
+            g_a = partial.sum(dim=0)
+            g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
+            d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
+            d_bv = _slot_reduce(pv, dv)
+            d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
+            del z, du, dv, pu, pv, dw, xt, dyt
         else:
+            # Folded weights in the compute dtype, plain and transposed (both contiguous).
+            bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
+            bv, bo_t = torch.empty_like(bu), torch.empty_like(bu)
+            bu_t = torch.empty(q_c, rd, d, dtype=dtype, device=dev)
+            bv_t, bo = torch.empty_like(bu_t), torch.empty_like(bu_t)
+            _native.check(lib.ow_fold_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                              nw.data_ptr() if nw is not None else None, gm.data_ptr(), ch.data_ptr(),
+                                              plan.channels, q_c, d, rd, code, bu.data_ptr(), bu_t.data_ptr(),
+                                              bv.data_ptr(), bv_t.data_ptr(), bo.data_ptr(), bo_t.data_ptr(), stream),
+                          "ow_fold_weights")
+            au_t, av_t, ao_t = (a.t().contiguous() for a in (au, av, ao))
+            # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
+            pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
+            pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
+            dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
+            # Channel side: batched GEMMs + the gate kernel.
             u = torch.bmm(pu, bu)
             v = torch.bmm(pv, bv)
             dz = torch.bmm(dw, bo_t)
@@ -168,17 +180,17 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             wp = torch.bmm(z, bo)
             dpu = torch.bmm(du, bu_t)
             dpv = torch.bmm(dv, bv_t)
-        d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
-        d_bv = _slot_reduce(pv, dv)
-        d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
-        del z, du, dv, pu, pv, dw
+            d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
+            d_bv = _slot_reduce(pv, dv)
+            d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
+            del z, du, dv, pu, pv, dw
 
-        # Token-matrix gradients and dX'.
-        g_au = _tile_outer(lib, dpu, xt, d, code, stream)
-        g_av = _tile_outer(lib, dpv, xt, d, code, stream)
-        g_ao = _tile_outer(lib, dyt, wp, d, code, stream)
-        dxt = _tile_mix(lib, dpu, au_t, dpv, av_t, d, code, stream)
-        del dpu, dpv, wp, xt, dyt
+            # Token-matrix gradients and dX'.
+            g_au = _tile_outer(lib, dpu, xt, d, code, stream)
+            g_av = _tile_outer(lib, dpv, xt, d, code, stream)
+            g_ao = _tile_outer(lib, dyt, wp, d, code, stream)
+            dxt = _tile_mix(lib, dpu, au_t, dpv, av_t, d, code, stream)
+            del dpu, dpv, wp, xt, dyt
 
         # dX' back to NHWC, then through the RMSNorm (+ the residual's identity).
         g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing

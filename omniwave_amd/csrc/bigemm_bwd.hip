@@ -635,6 +635,287 @@ __global__ void __launch_bounds__(256) bwd_channel_d64_kernel(BwdChannelArgs a) 
   }
 }
 
+// ---- Fused backward, d = 64: token side + channel side + token-side gradients ------------
+// One workgroup = 4 waves; per round, 4 consecutive 32-slot pairs of one channel group (one
+// per wave), rounds grid-strided.  Per pair and wave:
+//   * P_u^T = X'^T (A_u)^T, P_v^T, dW'^T = dY^T A_o (block-diagonal 32x32x16 products over the
+//     pair, as in the forward) from the X' and dY tiles staged in the second weight buffer,
+//     which no copy targets before the first barrier of the chunk loop; P_u, P_v, dW' are also
+//     stored for the parameter-gradient GEMMs;
+//   * the channel loop of bwd_channel_d64_kernel (U'^T, V'^T, dZ^T, gate, Z / dU' / dV' stored,
+//     W' += Z B_o'', dP_u += dU' B_u''^T, dP_v += dV' B_v''^T);
+//   * dX' = A_u^T dP_u + A_v^T dP_v (block-diagonal, the forward's output product), stored;
+//   * dA_u += dP_u X'^T, dA_v += dP_v X'^T, dA_o += dY W'^T per 16-slot tile with 16x16x16
+//     products over the channels (dP_u, dP_v, W' as rows through a per-wave LDS tile, X' and
+//     dY rows from memory), accumulated over all rounds of the wave.
+// At the end the four waves' dA sums are added in a fixed order and the workgroup writes
+// partial[blockIdx][3][256] (dA_u, dA_v, dA_o, element 16 t + k).
+constexpr int64_t kBwdFusedGrid = 1024;  // at most 2 workgroups per CU x 2 rounds in flight
+
+struct BwdFusedArgs {
+  const uint16_t* xt;   // [q_c][slots][64] X' tiles
+  const uint16_t* dyt;  // [q_c][slots][64] dY tiles
+  const float* a_u;     // [16][16] token matrices, fp32
+  const float* a_v;
+  const float* a_o;
+  const uint16_t* packed;  // ow_pack_bwd_weights
+  uint16_t* pu;            // [q_c][slots][64] outputs for the parameter GEMMs
+  uint16_t* pv;
+  uint16_t* dw;
+  uint16_t* z;  // [q_c][slots][rd]
+  uint16_t* du;
+  uint16_t* dv;
+  uint16_t* dxt;   // [q_c][slots][64]
+  float* partial;  // [gridDim][3][256]
+  int64_t slots;
+  int64_t pairs_per_q;  // slots / 32
+  int64_t rounds;       // q_c * ceil(pairs_per_q / 4)
+  int32_t q_c;
+};
+
+// Token-operand fragment of a 16x16 token matrix (lane (t, hh) slot j = M[t % 16][kord(j, hh)],
+// or the transpose with T), rounded to Ty.
+template <class Ty, bool T>
+__device__ __forceinline__ u32x4 token_frag(const float* m, int lane) {
+  const int t = lane & 15, hh = lane >> 5;
+  u32x4 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k0 = 8 * (q >> 1) + 4 * hh + 2 * (q & 1);
+    const float lo = T ? m[k0 * 16 + t] : m[t * 16 + k0];
+    const float hi = T ? m[(k0 + 1) * 16 + t] : m[t * 16 + k0 + 1];
+    v[q] = Ty::pack2(lo, hi);
+  }
+  return v;
+}
+
+template <class Ty, int RD>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+bwd_fused_d64_kernel(BwdFusedArgs a) {
+  constexpr int NCH = RD / 32;
+  constexpr int CH_ELEMS = kBwdFr * kFragElems;
+  constexpr int kLd = kBwdD + 8;  // staged tile row stride (elements): conflict-free columns
+  static_assert(4 * 32 * kLd <= CH_ELEMS, "a tile per wave fits in one weight buffer");
+  __shared__ __attribute__((aligned(16))) uint16_t wb[2][CH_ELEMS];
+  __shared__ __attribute__((aligned(16))) u32x4 tok[5][64];  // A_u, A_v, A_o^T, A_u^T, A_v^T operand rows
+  __shared__ float red[4][3][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, h4 = lane >> 4;
+  const bool g0 = (lane & 16) == 0;
+  const int64_t wg_per_q = (a.pairs_per_q + 3) / 4;
+
+  if (wave == 0) {
+    tok[0][lane] = token_frag<Ty, false>(a.a_u, lane);
+    tok[1][lane] = token_frag<Ty, false>(a.a_v, lane);
+    tok[2][lane] = token_frag<Ty, true>(a.a_o, lane);
+  } else if (wave == 1) {
+    tok[3][lane] = token_frag<Ty, true>(a.a_u, lane);
+    tok[4][lane] = token_frag<Ty, true>(a.a_v, lane);
+  }
+  // red[wave]: the wave's running dA sums (lane (l16, h4) element (4 h4 + i) * 16 + l16), kept
+  // in LDS rather than registers across the channel loop.
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] = 0.0f;
+
+  for (int64_t round = blockIdx.x; round < a.rounds; round += gridDim.x) {
+    const int q = static_cast<int>(round / wg_per_q);
+    const int64_t pair = (round % wg_per_q) * 4 + wave;
+    const bool live = pair < a.pairs_per_q;  // waves past the end still take part in the barriers
+    const uint16_t* wsrc = a.packed + static_cast<int64_t>(q) * NCH * CH_ELEMS;
+    auto issue = [&](int ec) {
+      for (int f = wave; f < kBwdFr; f += 4)
+        bwd_copy_frag(wsrc + static_cast<int64_t>(ec) * CH_ELEMS + f * kFragElems, wb[ec & 1] + f * kFragElems, lane);
+    };
+    __syncthreads();  // the previous round is done with both weight buffers; tok is written
+    issue(0);
+    const int64_t slot0 = static_cast<int64_t>(q) * a.slots + (live ? pair : 0) * 32;
+
+    // Token side, X' first, then dY, through the wave's tile [32][kLd] in the second weight
+    // buffer.
+    uint16_t* tx = wb[1] + wave * 32 * kLd;
+    auto stage_tile = [&](const uint16_t* src) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+        *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+      }
+      wave_lds_sync();
+    };
+    const bool g0b = g0;
+    auto token_side = [&](u32x4 f, u32x4 (&out)[kBwdKS]) {
+      const u32x4 f0 = keep_if(g0b, f), f1 = keep_if(!g0b, f);
+      const f32x16 zero = {};
+#pragma unroll
+      for (int cb = 0; cb < kBwdMB; ++cb) {
+        const u32x4 x0 = column8(tx + (4 * hh) * kLd + 32 * cb + l32, kLd);
+        const u32x4 x1 = column8(tx + (16 + 4 * hh) * kLd + 32 * cb + l32, kLd);
+        f32x16 acc = Ty::mma32(x0, f0, zero);
+        acc = Ty::mma32(x1, f1, acc);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) out[2 * cb + s] = pack_kstep<Ty>(acc, s);
+      }
+    };
+    u32x4 Pu[kBwdKS], Pv[kBwdKS], Dw[kBwdKS];
+    stage_tile(a.xt);
+    token_side(tok[0][lane], Pu);
+    token_side(tok[1][lane], Pv);
+    wave_lds_sync();
+    stage_tile(a.dyt);
+    token_side(tok[2][lane], Dw);
+    const f32x16 zero = {};
+    const int64_t row = slot0 + l32;  // this lane's slot
+    if (live) {
+#pragma unroll
+      for (int ks = 0; ks < kBwdKS; ++ks) {  // inverse of load_kstep
+        const int64_t o = row * kBwdD + 16 * ks + 4 * hh;
+        *reinterpret_cast<u32x2*>(a.pu + o) = u32x2{Pu[ks][0], Pu[ks][1]};
+        *reinterpret_cast<u32x2*>(a.pu + o + 8) = u32x2{Pu[ks][2], Pu[ks][3]};
+        *reinterpret_cast<u32x2*>(a.pv + o) = u32x2{Pv[ks][0], Pv[ks][1]};
+        *reinterpret_cast<u32x2*>(a.pv + o + 8) = u32x2{Pv[ks][2], Pv[ks][3]};
+        *reinterpret_cast<u32x2*>(a.dw + o) = u32x2{Dw[ks][0], Dw[ks][1]};
+        *reinterpret_cast<u32x2*>(a.dw + o + 8) = u32x2{Dw[ks][2], Dw[ks][3]};
+      }
+    }
+
+    // Channel side (as bwd_channel_d64_kernel).
+    f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
+    for (int ec = 0; ec < NCH; ++ec) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1 (ec = 0: its tiles)
+      if (ec + 1 < NCH) issue(ec + 1);
+      const u32x4* cf = reinterpret_cast<const u32x4*>(wb[ec & 1]);
+      auto frag = [&](int f) { return cf[f * (kFragElems / 8) + lane]; };
+      f32x16 U = {}, V = {}, G = {};
+#pragma unroll
+      for (int ks = 0; ks < kBwdKS; ++ks) {
+        U = Ty::mma32(frag(ks), Pu[ks], U);
+        V = Ty::mma32(frag(kBwdKS + ks), Pv[ks], V);
+        G = Ty::mma32(frag(2 * kBwdKS + ks), Dw[ks], G);
+      }
+      mfma_drain();
+      f32x16 Z, DU, DV;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float up = U[i], vp = V[i], g = G[i];
+        const float s = 1.0f / (1.0f + exp2f(up));
+        Z[i] = up * vp * s;
+        DU[i] = g * vp * s * (1.0f - kLn2 * up * (1.0f - s));
+        DV[i] = g * up * s;
+      }
+      u32x4 zs[2], dus[2], dvs[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        zs[s] = pack_kstep<Ty>(Z, s);
+        dus[s] = pack_kstep<Ty>(DU, s);
+        dvs[s] = pack_kstep<Ty>(DV, s);
+      }
+      if (live) {
+        // registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32
+        const int64_t base = row * RD + 32 * ec + 4 * hh;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int s = b >> 1, w = 2 * (b & 1);
+          *reinterpret_cast<u32x2*>(a.z + base + 8 * b) = u32x2{zs[s][w], zs[s][w + 1]};
+          *reinterpret_cast<u32x2*>(a.du + base + 8 * b) = u32x2{dus[s][w], dus[s][w + 1]};
+          *reinterpret_cast<u32x2*>(a.dv + base + 8 * b) = u32x2{dvs[s][w], dvs[s][w + 1]};
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < kBwdMB; ++mb)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          W[mb] = Ty::mma32(zs[s], frag(3 * kBwdKS + 2 * mb + s), W[mb]);
+          DPu[mb] = Ty::mma32(dus[s], frag(3 * kBwdKS + 2 * kBwdMB + 2 * mb + s), DPu[mb]);
+          DPv[mb] = Ty::mma32(dvs[s], frag(3 * kBwdKS + 4 * kBwdMB + 2 * mb + s), DPv[mb]);
+        }
+    }
+    mfma_drain();
+
+    // dX' = A_u^T dP_u + A_v^T dP_v (lane = channel 32 mb + l32, register i = slot
+    // pair_token_row(i, hh)).
+    f32x16 DX[kBwdMB];
+    {
+      const u32x4 tu = tok[3][lane], tv = tok[4][lane];
+      const u32x4 tu0 = keep_if(g0, tu), tu1 = keep_if(!g0, tu);
+      const u32x4 tv0 = keep_if(g0, tv), tv1 = keep_if(!g0, tv);
+#pragma unroll
+      for (int mb = 0; mb < kBwdMB; ++mb) {
+        DX[mb] = Ty::mma32(tu0, pack_kstep<Ty>(DPu[mb], 0), zero);
+        DX[mb] = Ty::mma32(tu1, pack_kstep<Ty>(DPu[mb], 1), DX[mb]);
+        DX[mb] = Ty::mma32(tv0, pack_kstep<Ty>(DPv[mb], 0), DX[mb]);
+        DX[mb] = Ty::mma32(tv1, pack_kstep<Ty>(DPv[mb], 1), DX[mb]);
+      }
+    }
+    mfma_drain();
+
+    // Through the wave's LDS tile [32 slots][kLd] (the buffer of chunk NCH: no copy targets it
+    // after the last barrier of the loop): dP_u, dP_v, W' as rows for the dA products, dX' as
+    // 16-byte row vectors to memory.
+    uint16_t* stage = wb[NCH & 1] + wave * 32 * kLd;
+    auto put = [&](const f32x16 (&m)[kBwdMB]) {
+#pragma unroll
+      for (int mb = 0; mb < kBwdMB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) stage[pair_token_row(i, hh) * kLd + 32 * mb + l32] = Ty::from_f32(m[mb][i]);
+      wave_lds_sync();
+    };
+    // dA_m += sum over the pair's two tiles of rows(stage) rows(other)^T: A operand lane (t, h4)
+    // = stage row 16 g + t, channels 16 ks + 4 h4 .. + 3; B operand = row 16 g + l16 of other.
+    auto outer = [&](f32x4& acc, const uint16_t* other) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) {
+          const u32x2 av = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
+          const u32x2 bv = *reinterpret_cast<const u32x2*>(other + (slot0 + 16 * g + l16) * kBwdD + 16 * ks + 4 * h4);
+          acc = Ty::mma16(av, bv, acc);
+        }
+      wave_lds_sync();
+    };
+    f32x4 dA[3] = {};
+    if (live) {
+      put(DPu);
+      outer(dA[0], a.xt);
+      put(DPv);
+      outer(dA[1], a.xt);
+    }
+    // dA_o = dY W'^T: A operand from dY rows, B from the staged W' rows.
+    if (live) {
+      put(W);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) {
+          const u32x2 av = *reinterpret_cast<const u32x2*>(a.dyt + (slot0 + 16 * g + l16) * kBwdD + 16 * ks + 4 * h4);
+          const u32x2 bv = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
+          dA[2] = Ty::mma16(av, bv, dA[2]);
+        }
+      wave_lds_sync();
+      put(DX);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+        *reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8) =
+            *reinterpret_cast<const u32x4*>(stage + r * kLd + c8);
+      }
+    }
+    mfma_drain();
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] += dA[m][i];
+  }
+
+  // The workgroup's dA sums, the waves added in order 0..3.
+  __syncthreads();
+  for (int e = threadIdx.x; e < 3 * 256; e += 256) {
+    const int m = e >> 8, k = e & 255;
+    a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = ((red[0][m][k] + red[1][m][k]) + red[2][m][k]) + red[3][m][k];
+  }
+}
+
 unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 }  // namespace
@@ -970,6 +1251,60 @@ int ow_bwd_channel(const void* pu, const void* pv, const void* dw, const void* p
       hipLaunchKernelGGL((ow::bwd_channel_d64_kernel<ow::F16, 256>), grid, dim3(256), 0, s, a);
   }
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_channel_d64_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
+
+// Workgroups (and partial rows) of ow_bwd_fused: every workgroup loops over rounds of four
+// pairs, so the dA partials stay few.
+int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c) {
+  if (q_c < 1 || slots <= 0 || slots % 32) return 0;
+  const int64_t rounds = static_cast<int64_t>(q_c) * ((slots / 32 + 3) / 4);
+  return rounds < ow::kBwdFusedGrid ? rounds : ow::kBwdFusedGrid;
+}
+
+int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
+                 void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
+                 int32_t dtype, void* stream) {
+  OW_CHECK_SUPPORTED(d == ow::kBwdD && (rd == 128 || rd == 256), "fused backward needs d = 64, rd in {128, 256}");
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 32 == 0, "bad shape q_c=%d slots=%lld (multiple of 32)", q_c,
+               (long long)slots);
+  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
+               packed_bytes);
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  const int64_t grid = ow_bwd_fused_partials(slots, q_c);
+  OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
+               (long long)n_partial, (long long)grid);
+  OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && z && du && dv && dxt && partial,
+               "tensor pointer is NULL");
+  for (const void* p : {xt, dyt, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
+                        static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
+                        static_cast<const void*>(dv), static_cast<const void*>(dxt)})
+    OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  ow::BwdFusedArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
+                     mu(dxt), partial, slots, slots / 32, 0, q_c};
+  a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16) {
+    if (rd == 128)
+      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::BF16, 128>), g, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::BF16, 256>), g, dim3(256), 0, s, a);
+  } else {
+    if (rd == 128)
+      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::F16, 128>), g, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::F16, 256>), g, dim3(256), 0, s, a);
+  }
+  if (int rc = ow::hip_status(hipGetLastError(), "bwd_fused_d64_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
 }
