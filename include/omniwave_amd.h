@@ -252,6 +252,18 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
                  void* dv, void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d,
                  int32_t rd, int32_t dtype, void* stream);
 
+/* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
+ * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and
+ * ow_bwd_scatter around it as well): X' = x r and dY rows are read from x, dy ([rows][C],
+ * rscale as in ow_bwd_gather, NULL without the RMSNorm) through the token table, and dX' is
+ * written to g ([rows][C], every element once) for ow_bwd_rmsnorm.  The other outputs as in
+ * ow_bwd_fused (slots = batch * q_s * 16). */
+int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                        const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
+                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                        void* dv, void* g, float* partial, int64_t n_partial, int32_t rd, int32_t dtype,
+                        void* stream);
+
 /* Parameter gradients from the folded ones (dbu, dbv [q_c][d][rd], dbo [q_c][rd][d], fp32):
  * g_bu, g_bv, g_bo (fp32, parameter shapes), g_gamma [C] and, with norm_weight, g_norm_weight
  * [C] (each channel written once). */

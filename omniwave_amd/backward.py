@@ -120,14 +120,20 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             _native.check(lib.ow_rms_scale(x.data_ptr(), rscale.data_ptr(), n_rows, plan.channels, eps, code,
                                            stream), "ow_rms_scale")
 
-        # Routed tiles of X' = x r and of dY.
-        xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
-        dyt = torch.empty_like(xt)
-        _native.check(lib.ow_bwd_gather(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale is not None
-                                        else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), batch,
-                                        code, xt.data_ptr(), dyt.data_ptr(), stream), "ow_bwd_gather")
+        fused = d == 64 and slots % 32 == 0 and dtype != torch.float32
+        # The fused kernel reads x / dy and writes g itself when group q is channels
+        # [64 q, 64 q + 64) (routing.py:107-121: radix level 0 or a single group).
+        routed = fused and plan.channels == q_c * d and (plan.radix_level == 0 or q_c == 1)
+        g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing
+        if not routed:
+            # Routed tiles of X' = x r and of dY.
+            xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
+            dyt = torch.empty_like(xt)
+            _native.check(lib.ow_bwd_gather(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale is not None
+                                            else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan),
+                                            batch, code, xt.data_ptr(), dyt.data_ptr(), stream), "ow_bwd_gather")
 
-        if d == 64 and slots % 32 == 0 and dtype != torch.float32:
+        if fused:
             # One fused kernel: token side, channel side and gate, dX', and the token-matrix
             # gradients as per-workgroup partials.
             nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
@@ -136,23 +142,35 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                   nw.data_ptr() if nw is not None else None, gm.data_ptr(),
                                                   ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
                                                   stream), "ow_pack_bwd_weights")
-            pu, pv, dw = torch.empty_like(xt), torch.empty_like(xt), torch.empty_like(xt)
+            pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
+            pv, dw = torch.empty_like(pu), torch.empty_like(pu)
             z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
             du, dv = torch.empty_like(z), torch.empty_like(z)
-            dxt = torch.empty_like(xt)
             n_part = lib.ow_bwd_fused_partials(slots, q_c)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
-            _native.check(lib.ow_bwd_fused(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
-                                           ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
-                                           dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(),
-                                           dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
-                                           stream), "ow_bwd_fused")
+            if routed:
+                _native.check(lib.ow_bwd_fused_routed(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale
+                                                      is not None else None, tok.data_ptr(),
+                                                      ctypes.byref(native_plan), batch, au.data_ptr(),
+                                                      av.data_ptr(), ao.data_ptr(), wpk.data_ptr(), nbytes,
+                                                      pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
+                                                      du.data_ptr(), dv.data_ptr(), g.data_ptr(),
+                                                      partial.data_ptr(), n_part, rd, code, stream),
+                              "ow_bwd_fused_routed")
+            else:
+                dxt = torch.empty_like(xt)
+                _native.check(lib.ow_bwd_fused(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                               ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
+                                               dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(),
+                                               dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
+                                               stream), "ow_bwd_fused")
+                del xt, dyt
             g_a = partial.sum(dim=0)
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
             d_bv = _slot_reduce(pv, dv)
             d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
-            del z, du, dv, pu, pv, dw, xt, dyt
+            del z, du, dv, pu, pv, dw
         else:
             # Folded weights in the compute dtype, plain and transposed (both contiguous).
             bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
@@ -192,10 +210,13 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             dxt = _tile_mix(lib, dpu, au_t, dpv, av_t, d, code, stream)
             del dpu, dpv, wp, xt, dyt
 
-        # dX' back to NHWC, then through the RMSNorm (+ the residual's identity).
-        g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing
-        _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan),
-                                         batch, code, g.data_ptr(), stream), "ow_bwd_scatter")
+        # dX' back to NHWC (unless the fused kernel wrote g), then through the RMSNorm (+ the
+        # residual's identity).
+        if not routed:
+            _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(),
+                                             ctypes.byref(native_plan), batch, code, g.data_ptr(), stream),
+                          "ow_bwd_scatter")
+            del dxt
         dx = torch.empty_like(x)
         _native.check(lib.ow_bwd_rmsnorm(x.data_ptr(), g.data_ptr(), rscale.data_ptr() if rscale is not None
                                          else None, grad.data_ptr(), dx.data_ptr(), n_rows, plan.channels,

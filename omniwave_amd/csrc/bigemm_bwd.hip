@@ -677,7 +677,22 @@ struct BwdFusedArgs {
   int64_t pairs_per_q;  // slots / 32
   int64_t rounds;       // q_c * ceil(pairs_per_q / 4)
   int32_t q_c;
+  // Routed mode (identity channel order, C = q_c * 64): X' and dY rows are read from x, dy
+  // ([rows][C]) through the token table and dX' is written to g ([rows][C]) the same way;
+  // xt, dyt, dxt are unused.
+  const uint16_t* x;
+  const uint16_t* dy;
+  const float* rscale;  // NULL: 1
+  const int32_t* tok;   // [q_s * 16]
+  uint16_t* g;
+  int32_t batch, n_tok, q_s, channels;
 };
+
+// 8 / 4 values of the compute dtype times r, rounded (x r of the gather).
+template <class Ty>
+__device__ __forceinline__ uint32_t scale2(uint32_t v, float r) {
+  return Ty::pack2(Ty::to_f32(static_cast<uint16_t>(v & 0xffffu)) * r, Ty::to_f32(static_cast<uint16_t>(v >> 16)) * r);
+}
 
 // Token-operand fragment of a 16x16 token matrix (lane (t, hh) slot j = M[t % 16][kord(j, hh)],
 // or the transpose with T), rounded to Ty.
@@ -695,7 +710,7 @@ __device__ __forceinline__ u32x4 token_frag(const float* m, int lane) {
   return v;
 }
 
-template <class Ty, int RD>
+template <class Ty, int RD, bool RT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 bwd_fused_d64_kernel(BwdFusedArgs a) {
   constexpr int NCH = RD / 32;
@@ -737,15 +752,48 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     __syncthreads();  // the previous round is done with both weight buffers; tok is written
     issue(0);
     const int64_t slot0 = static_cast<int64_t>(q) * a.slots + (live ? pair : 0) * 32;
+    // Routed mode: the pair's first tile 2 pair = b0 q_s + s0 (uniform), and the NHWC row of
+    // its slot r (-1 for pads and waves past the end).
+    int32_t b0 = 0, s0 = 0;
+    if constexpr (RT) {
+      const uint32_t tile0 = static_cast<uint32_t>(2 * (live ? pair : 0));
+      b0 = static_cast<int32_t>(tile0 / static_cast<uint32_t>(a.q_s));
+      s0 = static_cast<int32_t>(tile0 - static_cast<uint32_t>(b0) * static_cast<uint32_t>(a.q_s));
+    }
+    auto nhwc_row = [&](int r) -> int64_t {
+      int32_t b = b0, st = s0 + (r >> 4);
+      if (st == a.q_s) {
+        st = 0;
+        ++b;
+      }
+      const int32_t tk = a.tok[st * kG + (r & 15)];
+      return (live && b < a.batch && tk >= 0 && tk < a.n_tok) ? static_cast<int64_t>(b) * a.n_tok + tk : -1;
+    };
+    const int64_t cbase = static_cast<int64_t>(q) * kBwdD;  // routed: first channel of group q
 
     // Token side, X' first, then dY, through the wave's tile [32][kLd] in the second weight
     // buffer.
     uint16_t* tx = wb[1] + wave * 32 * kLd;
-    auto stage_tile = [&](const uint16_t* src) {
+    auto stage_tile = [&](const uint16_t* src, bool scale) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-        *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+        u32x4 val;
+        if constexpr (RT) {
+          val = u32x4{0u, 0u, 0u, 0u};
+          const int64_t nr = nhwc_row(r);
+          if (nr >= 0) {
+            val = *reinterpret_cast<const u32x4*>(src + nr * a.channels + cbase + c8);
+            if (scale && a.rscale) {
+              const float rs = a.rscale[nr];
+#pragma unroll
+              for (int w = 0; w < 4; ++w) val[w] = scale2<Ty>(val[w], rs);
+            }
+          }
+        } else {
+          val = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+        }
+        *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = val;
       }
       wave_lds_sync();
     };
@@ -764,11 +812,11 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       }
     };
     u32x4 Pu[kBwdKS], Pv[kBwdKS], Dw[kBwdKS];
-    stage_tile(a.xt);
+    stage_tile(RT ? a.x : a.xt, true);
     token_side(tok[0][lane], Pu);
     token_side(tok[1][lane], Pv);
     wave_lds_sync();
-    stage_tile(a.dyt);
+    stage_tile(RT ? a.dy : a.dyt, false);
     token_side(tok[2][lane], Dw);
     const f32x16 zero = {};
     const int64_t row = slot0 + l32;  // this lane's slot
@@ -869,23 +917,47 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     };
     // dA_m += sum over the pair's two tiles of rows(stage) rows(other)^T: A operand lane (t, h4)
     // = stage row 16 g + t, channels 16 ks + 4 h4 .. + 3; B operand = row 16 g + l16 of other.
-    auto outer = [&](f32x4& acc, const uint16_t* other) {
+    // Rows 16 g + l16 of X' (scaled) or dY, channels 16 ks + 4 h4 .. + 3.
+    int64_t orow[2];
+    float oscale[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if constexpr (RT) {
+        orow[g] = nhwc_row(16 * g + l16);
+        oscale[g] = (orow[g] >= 0 && a.rscale) ? a.rscale[orow[g]] : 1.0f;
+      } else {
+        orow[g] = slot0 + 16 * g + l16;
+        oscale[g] = 1.0f;
+      }
+    }
+    auto other_rows = [&](const uint16_t* tiles, const uint16_t* rows, bool scale, int g, int ks) -> u32x2 {
+      if constexpr (RT) {
+        u32x2 v = {0u, 0u};
+        if (orow[g] >= 0) {
+          v = *reinterpret_cast<const u32x2*>(rows + orow[g] * a.channels + cbase + 16 * ks + 4 * h4);
+          if (scale && a.rscale) v = u32x2{scale2<Ty>(v[0], oscale[g]), scale2<Ty>(v[1], oscale[g])};
+        }
+        return v;
+      } else {
+        return *reinterpret_cast<const u32x2*>(tiles + orow[g] * kBwdD + 16 * ks + 4 * h4);
+      }
+    };
+    auto outer = [&](f32x4& acc) {
 #pragma unroll
       for (int g = 0; g < 2; ++g)
 #pragma unroll
         for (int ks = 0; ks < kBwdKS; ++ks) {
           const u32x2 av = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
-          const u32x2 bv = *reinterpret_cast<const u32x2*>(other + (slot0 + 16 * g + l16) * kBwdD + 16 * ks + 4 * h4);
-          acc = Ty::mma16(av, bv, acc);
+          acc = Ty::mma16(av, other_rows(a.xt, a.x, true, g, ks), acc);
         }
       wave_lds_sync();
     };
     f32x4 dA[3] = {};
     if (live) {
       put(DPu);
-      outer(dA[0], a.xt);
+      outer(dA[0]);
       put(DPv);
-      outer(dA[1], a.xt);
+      outer(dA[1]);
     }
     // dA_o = dY W'^T: A operand from dY rows, B from the staged W' rows.
     if (live) {
@@ -894,17 +966,21 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       for (int g = 0; g < 2; ++g)
 #pragma unroll
         for (int ks = 0; ks < kBwdKS; ++ks) {
-          const u32x2 av = *reinterpret_cast<const u32x2*>(a.dyt + (slot0 + 16 * g + l16) * kBwdD + 16 * ks + 4 * h4);
           const u32x2 bv = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
-          dA[2] = Ty::mma16(av, bv, dA[2]);
+          dA[2] = Ty::mma16(other_rows(a.dyt, a.dy, false, g, ks), bv, dA[2]);
         }
       wave_lds_sync();
       put(DX);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-        *reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8) =
-            *reinterpret_cast<const u32x4*>(stage + r * kLd + c8);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stage + r * kLd + c8);
+        if constexpr (RT) {
+          const int64_t nr = nhwc_row(r);
+          if (nr >= 0) *reinterpret_cast<u32x4*>(a.g + nr * a.channels + cbase + c8) = val;
+        } else {
+          *reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8) = val;
+        }
       }
     }
     mfma_drain();
@@ -920,6 +996,25 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     const int m = e >> 8, k = e & 255;
     a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = ((red[0][m][k] + red[1][m][k]) + red[2][m][k]) + red[3][m][k];
   }
+}
+
+template <bool RT>
+int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dtype, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16) {
+    if (rd == 128)
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 128, RT>), g, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 256, RT>), g, dim3(256), 0, s, a);
+  } else {
+    if (rd == 128)
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 128, RT>), g, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 256, RT>), g, dim3(256), 0, s, a);
+  }
+  if (int rc = hip_status(hipGetLastError(), "bwd_fused_d64_kernel launch")) return rc;
+  clear_error();
+  return OW_OK;
 }
 
 unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
@@ -1297,22 +1392,54 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
   ow::BwdFusedArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
                      mu(dxt), partial, slots, slots / 32, 0, q_c};
   a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 g(static_cast<unsigned>(grid));
-  if (dtype == OW_DTYPE_BF16) {
-    if (rd == 128)
-      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::BF16, 128>), g, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::BF16, 256>), g, dim3(256), 0, s, a);
-  } else {
-    if (rd == 128)
-      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::F16, 128>), g, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((ow::bwd_fused_d64_kernel<ow::F16, 256>), g, dim3(256), 0, s, a);
+  return ow::launch_bwd_fused<false>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
+}
+
+int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                        const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
+                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                        void* dv, void* g, float* partial, int64_t n_partial, int32_t rd, int32_t dtype,
+                        void* stream) {
+  int32_t q_s = 0, q_c = 0;
+  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
+  const int32_t d = plan->channel_tile, c = plan->channels, n = plan->height * plan->width;
+  OW_CHECK_SUPPORTED(d == ow::kBwdD && (rd == 128 || rd == 256), "fused backward needs d = 64, rd in {128, 256}");
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
+  OW_CHECK_SUPPORTED(c == q_c * ow::kBwdD && (plan->radix_level == 0 || q_c == 1),
+                     "routed backward needs the identity channel order with C = q_c * 64");
+  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 31), "bad batch %d", batch);
+  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
+               packed_bytes);
+  const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
   }
-  if (int rc = ow::hip_status(hipGetLastError(), "bwd_fused_d64_kernel launch")) return rc;
-  ow::clear_error();
-  return OW_OK;
+  const int64_t grid = ow_bwd_fused_partials(slots, q_c);
+  OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
+               (long long)n_partial, (long long)grid);
+  OW_CHECK_ARG(x && dy && token_index && a_u && a_v && a_o && pu && pv && dw && z && du && dv && g && partial,
+               "tensor pointer is NULL");
+  for (const void* p : {x, dy, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
+                        static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
+                        static_cast<const void*>(dv), static_cast<const void*>(g)})
+    OW_CHECK_ARG(ow::aligned16(p), "tensors and packed weights must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  ow::BwdFusedArgs a{nullptr, nullptr, a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
+                     nullptr, partial, slots, slots / 32, 0, q_c};
+  a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
+  a.x = cu(x);
+  a.dy = cu(dy);
+  a.rscale = rscale;
+  a.tok = token_index;
+  a.g = mu(g);
+  a.batch = batch;
+  a.n_tok = n;
+  a.q_s = q_s;
+  a.channels = c;
+  return ow::launch_bwd_fused<true>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
 }
 
 int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype, const float* norm_weight,

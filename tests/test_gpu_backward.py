@@ -106,6 +106,7 @@ CASES = [  # (B, H, W, C, d, route, level)
     ("s2-local", (2, 28, 28, 256, 64, "local", 0)),
     ("s4-radix1", (2, 7, 7, 1024, 128, "radix", 1)),
     ("ragged-radix2", (3, 7, 9, 96, 64, "radix", 2)),
+    ("s2-radix1", (2, 28, 28, 256, 64, "radix", 1)),  # d = 64, strided channel groups
 ]
 
 
