@@ -165,7 +165,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                stream), "ow_bwd_fused")
                 del xt, dyt
-            g_a = partial.sum(dim=0)
+            g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
             d_bv = _slot_reduce(pv, dv)
@@ -223,11 +223,15 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                          int(residual), code, stream), "ow_bwd_rmsnorm")
 
         # Parameter gradients from the folded ones.
-        g_bu = torch.empty(q_c, d, rd, dtype=torch.float32, device=dev)
-        g_bv = torch.empty_like(g_bu)
-        g_bo = torch.empty(q_c, rd, d, dtype=torch.float32, device=dev)
-        g_gamma = torch.zeros(plan.channels, dtype=torch.float32, device=dev)
-        g_nw = torch.zeros(plan.channels, dtype=torch.float32, device=dev) if fuse_norm else None
+        # One buffer per output dtype group, so each group is cast with one kernel below; every
+        # element is written (each channel of the permutation exactly once).
+        nb = q_c * d * rd
+        g_b = torch.empty(3 * nb, dtype=torch.float32, device=dev)
+        g_bu, g_bv = g_b[:nb].view(q_c, d, rd), g_b[nb:2 * nb].view(q_c, d, rd)
+        g_bo = g_b[2 * nb:].view(q_c, rd, d)
+        g_c = torch.empty(2 if fuse_norm else 1, plan.channels, dtype=torch.float32, device=dev)
+        g_gamma = g_c[0]
+        g_nw = g_c[1] if fuse_norm else None
         _native.check(lib.ow_bwd_params(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
                                         nw.data_ptr() if nw is not None else None, gm.data_ptr(), ch.data_ptr(),
                                         plan.channels, q_c, d, rd, d_bu.data_ptr(), d_bv.data_ptr(), d_bo.data_ptr(),
@@ -237,7 +241,28 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     return (
         dx,
         g_nw.to(norm_weight.dtype) if g_nw is not None else None,
-        g_gamma.to(gamma.dtype),
-        g_au.to(a_u.dtype), g_av.to(a_v.dtype), g_ao.to(a_o.dtype),
-        g_bu.to(b_u.dtype), g_bv.to(b_v.dtype), g_bo.to(b_o.dtype),
+        *_cast_group((g_gamma,), (gamma.dtype,)),
+        *_cast_group((g_au, g_av, g_ao), (a_u.dtype, a_v.dtype, a_o.dtype)),
+        *_cast_group((g_bu, g_bv, g_bo), (b_u.dtype, b_v.dtype, b_o.dtype)),
     )
+
+
+def _cast_group(ts: tuple[Tensor, ...], dtypes: tuple[torch.dtype, ...]) -> tuple[Tensor, ...]:
+    """Casts each tensor to its dtype; when all share one dtype and one contiguous storage run,
+    with a single kernel (the views of the cast buffer keep their shapes)."""
+    if len(set(dtypes)) == 1 and len(ts) > 1:
+        base = ts[0]
+        flat = [t.reshape(-1) for t in ts]
+        storage = base.untyped_storage().data_ptr()
+        contiguous_run = all(t.is_contiguous() and t.untyped_storage().data_ptr() == storage for t in ts) and all(
+            flat[i + 1].data_ptr() == flat[i].data_ptr() + flat[i].numel() * flat[i].element_size()
+            for i in range(len(ts) - 1))
+        if contiguous_run:
+            n = sum(t.numel() for t in ts)
+            whole = torch.as_strided(base, (n,), (1,)).to(dtypes[0])
+            out, o = [], 0
+            for t in ts:
+                out.append(whole[o:o + t.numel()].view(t.shape))
+                o += t.numel()
+            return tuple(out)
+    return tuple(t.to(dt) for t, dt in zip(ts, dtypes))

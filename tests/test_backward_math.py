@@ -125,3 +125,20 @@ def test_decomposition_matches_autograd(h, w, c, d, route, level) -> None:
     for k in want:
         # 1e-6, not fp64 round-off: the oracle RMSNorm accumulates its variance in fp32.
         assert rel_l2(got[k], want[k]) < 1e-6, k
+
+
+def test_cast_group_one_buffer_and_fallback() -> None:
+    """The parameter gradients are cast per dtype group: views of one buffer with one cast, or
+    tensor by tensor (separate storages, mixed dtypes); values and shapes as a plain .to()."""
+    from omniwave_amd.backward import _cast_group
+
+    buf = torch.randn(3, 256)
+    views = tuple(buf[m].view(16, 16) for m in range(3))
+    out = _cast_group(views, (torch.bfloat16,) * 3)
+    assert all(o.shape == (16, 16) and o.dtype == torch.bfloat16 for o in out)
+    assert all(torch.equal(o, v.to(torch.bfloat16)) for o, v in zip(out, views))
+    assert out[0].untyped_storage().data_ptr() == out[2].untyped_storage().data_ptr()
+    sep = tuple(torch.randn(4, 5) for _ in range(3))
+    out = _cast_group(sep, (torch.bfloat16, torch.float16, torch.float32))
+    assert [o.dtype for o in out] == [torch.bfloat16, torch.float16, torch.float32]
+    assert all(torch.equal(o, s.to(o.dtype)) for o, s in zip(out, sep))
