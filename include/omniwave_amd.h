@@ -222,26 +222,21 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
 int ow_bwd_rmsnorm(const void* x, const void* g, const float* rscale, const void* dout, void* dx,
                    int64_t rows, int32_t channels, int32_t residual, int32_t dtype, void* stream);
 
-/* Fused channel side of the backward for d = 64 (rd 128 or 256), replacing six channel-side
- * GEMMs and the gate pass: per 32-slot pair of a channel group, from the token-side tiles
- * P_u, P_v, dW' ([q_c][slots][64], slots % 32 == 0): U'^T, V'^T, dZ^T per 32-row chunk, the gate
- * backward (z, du, dv stored to [q_c][slots][rd]), and W' = Z B_o'', dP_u = dU' B_u''^T,
- * dP_v = dV' B_v''^T stored to [q_c][slots][64].  Weights from ow_pack_bwd_weights (the folded
- * B_u'', B_v'', B_o'' as the forward's and transposed MFMA operands; ow_bwd_packed_bytes). */
+/* Packed weights of the fused d = 64 backward (rd 128 or 256): per channel group and 32-row
+ * chunk, the folded B_u'', B_v'', B_o'' as the forward's and transposed 32x32x16 MFMA operands
+ * (24 fragments of 1 KB); ow_bwd_packed_bytes gives the size. */
 size_t ow_bwd_packed_bytes(int32_t q_c, int32_t d, int32_t rd);
 int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype,
                         const float* norm_weight, const float* gamma, const int32_t* channel_index,
                         int32_t channels, int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype,
                         void* packed, void* stream);
-int ow_bwd_channel(const void* pu, const void* pv, const void* dw, const void* packed, size_t packed_bytes,
-                   void* z, void* du, void* dv, void* wp, void* dpu, void* dpv, int64_t slots,
-                   int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
 
-/* The d = 64 backward with the token side fused in (replaces ow_tile_mix x4, ow_tile_outer x3
- * and ow_bwd_channel; the reference's fp32 autograd recompute, omniweave/ops/triton.py:256-292):
+/* The d = 64 backward in one kernel (replaces ow_tile_mix x4, ow_tile_outer x3 and the
+ * channel-side GEMMs; the reference's fp32 autograd recompute, omniweave/ops/triton.py:256-292):
  * from the routed tiles X' and dY ([q_c][slots][64], ow_bwd_gather) and the fp32 [16][16] token
  * matrices, per 32-slot pair: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw
- * for the parameter-gradient GEMMs), the channel side of ow_bwd_channel (z, du, dv stored),
+ * for the parameter-gradient GEMMs), U'^T, V'^T, dZ^T and the gate backward per 32-row chunk
+ * (z, du, dv stored to [q_c][slots][rd]), W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
  * dX' = A_u^T dP_u + A_v^T dP_v (stored to dxt), and the token-matrix gradients dA_u = sum
  * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
  * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c); element 16 t + k),

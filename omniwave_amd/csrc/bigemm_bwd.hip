@@ -501,144 +501,9 @@ __global__ void __launch_bounds__(256) pack_bwd_kernel(BwdPackArgs p) {
   p.packed[idx] = Ty::from_f32(val);
 }
 
-struct BwdChannelArgs {
-  const uint16_t* pu;   // [q_c][slots][64]
-  const uint16_t* pv;
-  const uint16_t* dw;
-  const uint16_t* packed;
-  uint16_t* z;          // [q_c][slots][rd]
-  uint16_t* du;
-  uint16_t* dv;
-  uint16_t* wp;         // [q_c][slots][64]
-  uint16_t* dpu;
-  uint16_t* dpv;
-  int64_t slots;
-  int64_t pairs_per_q;  // slots / 32
-  int32_t q_c;
-};
-
 __device__ __forceinline__ void bwd_copy_frag(const uint16_t* src, uint16_t* dst, int lane) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + lane * 8),
                                    (__attribute__((address_space(3))) void*)(dst), 16, 0, 0);
-}
-
-// K-step ks of a [32 slots][64] tile as a 32x32x16 B operand (lane = slot l32, slot j ->
-// channel 16 ks + kord(j, hh)): two 8-byte loads.
-__device__ __forceinline__ u32x4 load_kstep(const uint16_t* rowp, int ks, int hh) {
-  const u32x2 a = *reinterpret_cast<const u32x2*>(rowp + 16 * ks + 4 * hh);
-  const u32x2 b = *reinterpret_cast<const u32x2*>(rowp + 16 * ks + 8 + 4 * hh);
-  return u32x4{a.x, a.y, b.x, b.y};
-}
-
-// One workgroup = 4 waves = 4 consecutive 32-slot pairs of one channel group; weight chunks
-// (24 KB) double-buffered in LDS.  Per chunk and pair: U'^T, V'^T, dZ^T (K = channels), the
-// gate backward, Z / dU' / dV' stored, and W' += Z B_o'', dP_u += dU' B_u''^T,
-// dP_v += dV' B_v''^T (K = expanded rows).  Finally W', dP_u, dP_v are stored.
-template <class Ty, int RD>
-__global__ void __launch_bounds__(256) bwd_channel_d64_kernel(BwdChannelArgs a) {
-  constexpr int NCH = RD / 32;
-  constexpr int CH_ELEMS = kBwdFr * kFragElems;
-  __shared__ __attribute__((aligned(16))) uint16_t wb[2][CH_ELEMS];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int hh = lane >> 5, l32 = lane & 31;
-  const int64_t wg_per_q = (a.pairs_per_q + 3) / 4;
-  const int q = static_cast<int>(blockIdx.x / wg_per_q);
-  const int64_t pair = (blockIdx.x % wg_per_q) * 4 + wave;
-  const bool live = pair < a.pairs_per_q;  // waves past the end still take part in the barriers
-
-  const uint16_t* wsrc = a.packed + static_cast<int64_t>(q) * NCH * CH_ELEMS;
-  auto issue = [&](int ec) {
-    for (int f = wave; f < kBwdFr; f += 4)
-      bwd_copy_frag(wsrc + static_cast<int64_t>(ec) * CH_ELEMS + f * kFragElems, wb[ec & 1] + f * kFragElems, lane);
-  };
-  issue(0);
-
-  const int64_t slot0 = static_cast<int64_t>(q) * a.slots + (live ? pair : 0) * 32;
-  const int64_t row = slot0 + l32;  // this lane's slot (row of the [slots][..] tiles)
-  u32x4 Pu[kBwdKS], Pv[kBwdKS], Dw[kBwdKS];
-#pragma unroll
-  for (int ks = 0; ks < kBwdKS; ++ks) {
-    Pu[ks] = load_kstep(a.pu + row * kBwdD, ks, hh);
-    Pv[ks] = load_kstep(a.pv + row * kBwdD, ks, hh);
-    Dw[ks] = load_kstep(a.dw + row * kBwdD, ks, hh);
-  }
-  f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
-
-  for (int ec = 0; ec < NCH; ++ec) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1
-    if (ec + 1 < NCH) issue(ec + 1);
-    const u32x4* cf = reinterpret_cast<const u32x4*>(wb[ec & 1]);
-    auto frag = [&](int f) { return cf[f * (kFragElems / 8) + lane]; };
-    f32x16 U = {}, V = {}, G = {};
-#pragma unroll
-    for (int ks = 0; ks < kBwdKS; ++ks) {
-      U = Ty::mma32(frag(ks), Pu[ks], U);
-      V = Ty::mma32(frag(kBwdKS + ks), Pv[ks], V);
-      G = Ty::mma32(frag(2 * kBwdKS + ks), Dw[ks], G);
-    }
-    mfma_drain();
-    f32x16 Z, DU, DV;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float up = U[i], vp = V[i], g = G[i];
-      const float s = gate_sigmoid(up);
-      Z[i] = up * vp * s;
-      DU[i] = g * vp * s * (1.0f - kLn2 * up * (1.0f - s));
-      DV[i] = g * up * s;
-    }
-    u32x4 zs[2], dus[2], dvs[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      zs[s] = pack_kstep<Ty>(Z, s);
-      dus[s] = pack_kstep<Ty>(DU, s);
-      dvs[s] = pack_kstep<Ty>(DV, s);
-    }
-    if (live) {
-      // registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32
-      const int64_t base = row * RD + 32 * ec + 4 * hh;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int s = b >> 1, w = 2 * (b & 1);
-        *reinterpret_cast<u32x2*>(a.z + base + 8 * b) = u32x2{zs[s][w], zs[s][w + 1]};
-        *reinterpret_cast<u32x2*>(a.du + base + 8 * b) = u32x2{dus[s][w], dus[s][w + 1]};
-        *reinterpret_cast<u32x2*>(a.dv + base + 8 * b) = u32x2{dvs[s][w], dvs[s][w + 1]};
-      }
-    }
-#pragma unroll
-    for (int mb = 0; mb < kBwdMB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        W[mb] = Ty::mma32(zs[s], frag(3 * kBwdKS + 2 * mb + s), W[mb]);
-        DPu[mb] = Ty::mma32(dus[s], frag(3 * kBwdKS + 2 * kBwdMB + 2 * mb + s), DPu[mb]);
-        DPv[mb] = Ty::mma32(dvs[s], frag(3 * kBwdKS + 4 * kBwdMB + 2 * mb + s), DPv[mb]);
-      }
-  }
-  mfma_drain();
-  if (!live) return;
-  // W', dP_u, dP_v (lane = channel 32 mb + l32, register i = slot pair_token_row(i, hh)) go
-  // through a per-wave LDS tile [32 slots][kStageLd] and leave as 16-byte row vectors.  The
-  // buffer of chunk NCH is free: no copy targets it after the last barrier of the loop.
-  constexpr int kStageLd = kBwdD + 8;
-  static_assert(4 * 32 * kStageLd <= CH_ELEMS, "staging tiles fit in one weight buffer");
-  uint16_t* stage = wb[NCH & 1] + wave * 32 * kStageLd;
-  const f32x16* mats[3] = {W, DPu, DPv};
-  uint16_t* outs[3] = {a.wp, a.dpu, a.dpv};
-#pragma unroll
-  for (int m = 0; m < 3; ++m) {
-#pragma unroll
-    for (int mb = 0; mb < kBwdMB; ++mb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) stage[pair_token_row(i, hh) * kStageLd + 32 * mb + l32] = Ty::from_f32(mats[m][mb][i]);
-    wave_lds_sync();
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-      *reinterpret_cast<u32x4*>(outs[m] + (slot0 + r) * kBwdD + c8) =
-          *reinterpret_cast<const u32x4*>(stage + r * kStageLd + c8);
-    }
-    wave_lds_sync();
-  }
 }
 
 // ---- Fused backward, d = 64: token side + channel side + token-side gradients ------------
@@ -648,7 +513,7 @@ __global__ void __launch_bounds__(256) bwd_channel_d64_kernel(BwdChannelArgs a) 
 //     pair, as in the forward) from the X' and dY tiles staged in the second weight buffer,
 //     which no copy targets before the first barrier of the chunk loop; P_u, P_v, dW' are also
 //     stored for the parameter-gradient GEMMs;
-//   * the channel loop of bwd_channel_d64_kernel (U'^T, V'^T, dZ^T, gate, Z / dU' / dV' stored,
+//   * the channel loop (U'^T, V'^T, dZ^T per 32-row chunk, gate, Z / dU' / dV' stored,
 //     W' += Z B_o'', dP_u += dU' B_u''^T, dP_v += dV' B_v''^T);
 //   * dX' = A_u^T dP_u + A_v^T dP_v (block-diagonal, the forward's output product), stored;
 //   * dA_u += dP_u X'^T, dA_v += dP_v X'^T, dA_o += dY W'^T per 16-slot tile with 16x16x16
@@ -822,7 +687,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     const int64_t row = slot0 + l32;  // this lane's slot
     if (live) {
 #pragma unroll
-      for (int ks = 0; ks < kBwdKS; ++ks) {  // inverse of load_kstep
+      for (int ks = 0; ks < kBwdKS; ++ks) {  // lane = slot l32, slot j -> channel 16 ks + kord(j, hh)
         const int64_t o = row * kBwdD + 16 * ks + 4 * hh;
         *reinterpret_cast<u32x2*>(a.pu + o) = u32x2{Pu[ks][0], Pu[ks][1]};
         *reinterpret_cast<u32x2*>(a.pu + o + 8) = u32x2{Pu[ks][2], Pu[ks][3]};
@@ -833,7 +698,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       }
     }
 
-    // Channel side (as bwd_channel_d64_kernel).
+    // Channel side.
     f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
     for (int ec = 0; ec < NCH; ++ec) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1311,47 +1176,6 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
   else
     hipLaunchKernelGGL(ow::pack_bwd_kernel<ow::F16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, p);
   if (int rc = ow::hip_status(hipGetLastError(), "pack_bwd_kernel launch")) return rc;
-  ow::clear_error();
-  return OW_OK;
-}
-
-int ow_bwd_channel(const void* pu, const void* pv, const void* dw, const void* packed, size_t packed_bytes, void* z,
-                   void* du, void* dv, void* wp, void* dpu, void* dpv, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
-                   int32_t dtype, void* stream) {
-  OW_CHECK_SUPPORTED(d == ow::kBwdD && (rd == 128 || rd == 256), "fused backward needs d = 64, rd in {128, 256}");
-  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
-  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 32 == 0, "bad shape q_c=%d slots=%lld (multiple of 32)", q_c,
-               (long long)slots);
-  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
-               packed_bytes);
-  if (slots == 0) {
-    ow::clear_error();
-    return OW_OK;
-  }
-  OW_CHECK_ARG(pu && pv && dw && z && du && dv && wp && dpu && dpv, "tensor pointer is NULL");
-  for (const void* p : {pu, pv, dw, packed, static_cast<const void*>(z), static_cast<const void*>(du),
-                        static_cast<const void*>(dv)})
-    OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
-  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
-  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
-  ow::BwdChannelArgs a{cu(pu), cu(pv), cu(dw), cu(packed), mu(z), mu(du), mu(dv), mu(wp), mu(dpu), mu(dpv),
-                       slots, slots / 32, q_c};
-  const int64_t wgs = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
-  OW_CHECK_ARG(wgs < (int64_t(1) << 31), "grid too large");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(wgs));
-  if (dtype == OW_DTYPE_BF16) {
-    if (rd == 128)
-      hipLaunchKernelGGL((ow::bwd_channel_d64_kernel<ow::BF16, 128>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((ow::bwd_channel_d64_kernel<ow::BF16, 256>), grid, dim3(256), 0, s, a);
-  } else {
-    if (rd == 128)
-      hipLaunchKernelGGL((ow::bwd_channel_d64_kernel<ow::F16, 128>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((ow::bwd_channel_d64_kernel<ow::F16, 256>), grid, dim3(256), 0, s, a);
-  }
-  if (int rc = ow::hip_status(hipGetLastError(), "bwd_channel_d64_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
 }

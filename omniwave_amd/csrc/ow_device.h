@@ -166,11 +166,6 @@ __device__ __forceinline__ u32x4 column8(const uint16_t* p, int ld) {
   return v;
 }
 
-// Element i (register index of a 32x32 accumulator K half) of a packed operand.
-__device__ __forceinline__ uint16_t packed_elem(const u32x4& v, int j) {
-  return (j & 1) ? hi16(v[j >> 1]) : lo16(v[j >> 1]);
-}
-
 // Sum over aligned groups of N lanes (N in {8, 16, 32}) with DPP; the total lands in the last
 // lane of each group (lane % N == N - 1), the other lanes hold partial sums.
 template <int CTRL, int ROW_MASK>
@@ -356,52 +351,6 @@ __device__ __forceinline__ void pair_chunk_f8(const u32x2 (&Pu)[KS], const u32x2
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(mb, s), W[mb]);
-}
-
-// The whole channel side of a pair (NCH chunks, weights in registers), software-pipelined: the
-// U'/V' MFMAs of chunk ec + 1 are issued ahead of the SiLU of chunk ec and interleaved with
-// it, so the matrix core and the vector unit of one wave work at the same time.
-// fu(ec, ks), fv(ec, ks), fo(ec, mb, s) return fragments.
-template <class Ty, int KS, int MB, int NCH, class FU, class FV, class FO>
-__device__ __forceinline__ void pair_channel_pipelined(const u32x4 (&Pu)[KS], const u32x4 (&Pv)[KS], FU fu, FV fv,
-                                                       FO fo, f32x16 (&W)[MB]) {
-  f32x16 U[2], V[2];
-  auto uv = [&](int ec, f32x16& u, f32x16& v) {
-    u = f32x16{};
-    v = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u = Ty::mma32(fu(ec, ks), Pu[ks], u);
-      v = Ty::mma32(fv(ec, ks), Pv[ks], v);
-    }
-  };
-  uv(0, U[0], V[0]);
-#pragma unroll
-  for (int ec = 0; ec < NCH; ++ec) {
-    const int cur = ec & 1;
-    if (ec + 1 < NCH) uv(ec + 1, U[cur ^ 1], V[cur ^ 1]);
-    u32x4 Z[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        Z[s][q] = Ty::pack2(silu_gate(U[cur][8 * s + 2 * q], V[cur][8 * s + 2 * q]),
-                            silu_gate(U[cur][8 * s + 2 * q + 1], V[cur][8 * s + 2 * q + 1]));
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) W[mb] = Ty::mma32(Z[s], fo(ec, mb, s), W[mb]);
-    if (ec + 1 < NCH) {
-      // 2 KS MFMAs of the next chunk spread over the gate's ~100 VALU instructions, then the
-      // 2 MB MFMAs of this chunk's W update.
-#pragma unroll
-      for (int i = 0; i < 2 * KS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0);
-    }
-  }
 }
 
 // Output of one 32-channel block of a pair: dl (lane = channel, register i = token kord(i)) is
