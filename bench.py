@@ -213,15 +213,15 @@ def model_section(batch: int, steps: int, dev) -> dict:
         stream.wait_stream(torch.cuda.current_stream())
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
-            model.forward_features(x)
+            model(x)
             torch.cuda.current_stream().synchronize()
             with torch.cuda.graph(graph, stream=stream):
-                feats = model.forward_features(x)["stage4"]
+                logits = model(x)
         torch.cuda.current_stream().wait_stream(stream)
 
         def hip_step():
             graph.replay()
-            return model.head(feats.mean(dim=(1, 2)))
+            return logits
 
         replay_err = 0.0
         for _ in range(3):  # every replay must reproduce the eager HIP logits
@@ -246,7 +246,7 @@ def model_section(batch: int, steps: int, dev) -> dict:
         "eager_images_per_s": round(batch / (eager_ms * 1e-3), 1),
         "eager_ms_per_batch": round(eager_ms, 3),
         "speedup_vs_eager": round(eager_ms / hip_ms, 2),
-        "launch": "hip_graph (stem..stage4), eager pool + head",
+        "launch": "hip_graph (whole forward)",
         "graph_replay_max_abs_diff": replay_err,
         "logits_rel_l2_vs_eager": round(float(diff), 5),
     }
@@ -282,7 +282,7 @@ def fp8_section(model_batch: int, steps: int, dev) -> dict:
     gen = torch.Generator().manual_seed(0)
     xi = torch.randn(model_batch, 3, 224, 224, generator=gen).to(device=dev, dtype=torch.bfloat16)
     with torch.inference_mode():
-        ms = _graph_ms(lambda: model.forward_features(xi), 1, steps)
+        ms = _graph_ms(lambda: model(xi), 1, steps)
     return {
         "workload": f"fused block fp8 channel side, {name} shifted0; omniweave_t fp8 at [{model_batch},3,224,224]",
         "stage3_sweep": sweep,

@@ -79,6 +79,14 @@ int ow_plan_dims(const OwPlan* plan, int32_t* q_s, int32_t* q_c);
 int ow_route_build(const OwPlan* plan, int32_t* token_index, int32_t* channel_index);
 
 /*
+ * Output-row table for a block whose output feeds space_to_depth(factor) (omniweave/models/
+ * backbone.py:14-27,183-186): out_rows[i] = the row, within its image, that token
+ * token_index[i] occupies in space_to_depth(out, factor) viewed as [H*W, C] rows (pad = H*W).
+ * Pass it to ow_bigemm_fwd_rows to write the block output directly in that layout.
+ */
+int ow_route_s2d_rows(const OwPlan* plan, int32_t factor, const int32_t* token_index, int32_t* out_rows);
+
+/*
  * Size in bytes of the packed weight buffer for q_c channel groups, channel tile d,
  * expanded tile rd and compute dtype (OW_DTYPE_BF16 / OW_DTYPE_F16 / OW_DTYPE_F32).
  */
@@ -168,6 +176,31 @@ int ow_bigemm_fwd(const void* x, void* out, float eps,
                   const int32_t* token_index, const int32_t* channel_index,
                   const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
                   int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ow_bigemm_fwd with the output rows permuted: token slot i (token_index[i] of image b) is
+ * written to row b*H*W + out_rows[i] of out instead of row b*H*W + token_index[i]; the input
+ * rows, residual and RMSNorm are unchanged.  out_rows (device, [Q_s*g], pad = H*W) must map
+ * the valid slots one-to-one onto [0, H*W), e.g. ow_route_s2d_rows, so that the block and the
+ * space_to_depth after it (omniweave/models/backbone.py:183-186) are one pass over HBM.
+ * bf16 / f16 activations only.
+ */
+int ow_bigemm_fwd_rows(const void* x, void* out, float eps,
+                       const void* packed, size_t packed_bytes,
+                       const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
+                       const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
+                       int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Backbone stem as one gather-GEMM (omniweave/models/backbone.py:121,173-176): image
+ * [batch, 3, height, width] (NCHW) -> space_to_depth(4) -> x W^T with weight [n_out, 48]
+ * (nn.Linear(48, n_out, bias=False), input order (row offset, column offset, channel)) ->
+ * out [batch, height/4, width/4, n_out] (NHWC).  fp32 accumulation, one rounding to dtype
+ * (OW_DTYPE_BF16 or OW_DTYPE_F16; image, weight and out share it).  height, width divisible
+ * by 4; n_out in {32, 64, 96, 128, 192, 256}; image 8-byte, out 16-byte aligned.
+ */
+int ow_stem_fwd(const void* image, const void* weight, void* out, int32_t batch, int32_t height,
+                int32_t width, int32_t n_out, int32_t dtype, void* stream);
 
 /*
  * Backward building blocks.  Replace the fp32 autograd recompute of the accelerated backend

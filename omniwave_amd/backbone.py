@@ -10,10 +10,12 @@ from __future__ import annotations
 
 from collections import OrderedDict
 
+import torch
 import torch.nn as nn
 from torch import Tensor
 
 from omniwave_amd.block import OmniWeaveBlock
+from omniwave_amd.hip import stem_hip, stem_is_supported
 from omniwave_amd.routing import build_stage_schedule
 
 
@@ -48,6 +50,16 @@ class _Stage(nn.Module):
         for block in self.blocks:
             x = block(x)
         return x
+
+    def forward_s2d(self, x: Tensor, factor: int) -> Tensor:
+        """``space_to_depth(self(x), factor)``; the last block writes that layout itself when it
+        can (``OmniWeaveBlock.forward_s2d``)."""
+        if self.anchor is not None:
+            x = self.anchor(x)
+        for block in self.blocks[:-1]:
+            x = block(x)
+        y = self.blocks[-1].forward_s2d(x, factor)
+        return y if y is not None else space_to_depth_nhwc(self.blocks[-1](x), factor)
 
 
 class OmniWeaveBackbone(nn.Module):
@@ -98,11 +110,22 @@ class OmniWeaveBackbone(nn.Module):
         self.head = nn.Linear(widths[-1], num_classes)
         self._widths = widths
 
+    def _hip_glue(self, x: Tensor) -> bool:
+        """Inference with every block on the hip backend: run the stem and the block before each
+        downsample as the fused kernels (``stem_hip``, ``OmniWeaveBlock.forward_s2d``)."""
+        if torch.is_grad_enabled() or not x.is_cuda:
+            return False
+        return all(blk.backend in ("hip", "auto") for stage in self.stages for blk in stage.blocks)
+
+    def _stem(self, x: Tensor) -> Tensor:
+        """NCHW image -> NHWC stem features (backbone.py:173-176)."""
+        if self._hip_glue(x) and stem_is_supported(x, self.stem_proj.weight)[0]:
+            return stem_hip(x, self.stem_proj.weight)
+        return self.stem_proj(space_to_depth_nhwc(x.permute(0, 2, 3, 1), 4))
+
     def forward_features(self, x: Tensor) -> OrderedDict[str, Tensor]:
         """NCHW image -> OrderedDict ``stage1..stage4`` of NHWC feature maps (backbone.py:165-189)."""
-        x = x.permute(0, 2, 3, 1)
-        x = space_to_depth_nhwc(x, 4)
-        x = self.stem_proj(x)
+        x = self._stem(x)
         features: OrderedDict[str, Tensor] = OrderedDict()
         for i, stage in enumerate(self.stages):
             x = stage(x)
@@ -113,5 +136,16 @@ class OmniWeaveBackbone(nn.Module):
         return features
 
     def forward(self, x: Tensor) -> Tensor:
-        stage4 = self.forward_features(x)["stage4"]
-        return self.head(stage4.mean(dim=(1, 2)))
+        """NCHW image -> logits (backbone.py:191-197).  Under ``torch.no_grad`` /
+        ``inference_mode`` with the blocks on the hip backend, the stem and each stage's last
+        block write the layout the next Linear reads, so no space_to_depth copy is made."""
+        if not self._hip_glue(x):
+            stage4 = self.forward_features(x)["stage4"]
+            return self.head(stage4.mean(dim=(1, 2)))
+        x = self._stem(x)
+        for i, stage in enumerate(self.stages):
+            if i < 3:
+                x = self.downsamples[i](stage.forward_s2d(x, 2))
+            else:
+                x = stage(x)
+        return self.head(x.mean(dim=(1, 2)))

@@ -15,7 +15,7 @@ import torch.nn as nn
 from torch import Tensor
 
 from omniwave_amd.bigemm import bigemm
-from omniwave_amd.hip import bigemm_block_hip, hip_is_supported
+from omniwave_amd.hip import bigemm_block_hip, bigemm_block_s2d_hip, hip_is_supported
 from omniwave_amd.routing import RoutePlan, build_route_plan
 
 RMS_EPS = 1e-6  # omniweave/models/block.py:84
@@ -85,6 +85,21 @@ class OmniWeaveBlock(nn.Module):
         shape = (delta.shape[0],) + (1,) * (delta.ndim - 1)
         mask = torch.empty(shape, dtype=delta.dtype, device=delta.device).bernoulli_(keep)
         return delta * mask / keep
+
+    def forward_s2d(self, x: Tensor, factor: int = 2) -> Tensor | None:
+        """``space_to_depth(self(x), factor)`` as one kernel — the block writes its output rows
+        straight into the ``[B, H/f, W/f, C f^2]`` layout (omniweave/models/backbone.py:14-27,
+        183-186) — when nothing needs a gradient and the fused hip path takes ``x`` (bf16 /
+        fp16); ``None`` otherwise, and the caller composes the two."""
+        if torch.is_grad_enabled() or (self.training and (self.drop_path_rate > 0 or self.fp8)):
+            return None
+        if x.dtype not in (torch.bfloat16, torch.float16) or not self._fused(x):
+            return None
+        if x.shape[1] % factor or x.shape[2] % factor:
+            return None
+        params = (self.a_u, self.a_v, self.a_o, self.b_u, self.b_v, self.b_o, self.gamma)
+        return bigemm_block_s2d_hip(x, self.norm_weight, self.plan, *params, factor=factor, eps=RMS_EPS,
+                                    fp8=self.fp8)
 
     def forward(self, x: Tensor) -> Tensor:
         """``x``: ``[B, H, W, C]`` -> ``[B, H, W, C]``."""

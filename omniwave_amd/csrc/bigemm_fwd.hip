@@ -107,6 +107,7 @@ struct FwdArgs {
   const uint16_t* packed;
   const int32_t* tok;
   const int32_t* chan;
+  const int32_t* out_tok;  // [q_s * 16] output row of each token slot; NULL: the token table
   int32_t batch, n_tok, channels, q_s, q_c;
   int32_t n_chunks;  // ceil(batch * q_s / token groups per workgroup)
   int32_t residual;  // write x + delta instead of delta
@@ -183,7 +184,8 @@ bigemm_fwd_kernel(FwdArgs a) {
   // wb: the even weight chunks.
   __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LDX];
   __shared__ __attribute__((aligned(16))) uint16_t wb[CH_ELEMS];
-  __shared__ int32_t rowid[ROWS];  // b * n_tok + token, -1 for pad rows
+  __shared__ int32_t rowid[ROWS];   // b * n_tok + token, -1 for pad rows
+  __shared__ int32_t rowout[ROWS];  // output row of each tile row, -1 for pad rows
   __shared__ float rsc[ROWS];      // RMSNorm scale of each row (1 without norm)
   __shared__ int32_t chx[D];
 
@@ -204,14 +206,22 @@ bigemm_fwd_kernel(FwdArgs a) {
   static_assert(ROWS <= kThreads, "one row id per thread");
   if (tid < ROWS) {
     const int64_t tg = static_cast<int64_t>(chunk) * R + tid / kG;
-    int32_t id = -1;
+    int32_t id = -1, od = -1;
     if (tg < static_cast<int64_t>(a.batch) * a.q_s) {
       const int32_t b = static_cast<int32_t>(tg / a.q_s);
       const int32_t s = static_cast<int32_t>(tg - static_cast<int64_t>(b) * a.q_s);
       const int32_t t = a.tok[s * kG + (tid % kG)];
-      if (t >= 0 && t < a.n_tok) id = b * a.n_tok + t;
+      if (t >= 0 && t < a.n_tok) {
+        id = b * a.n_tok + t;
+        od = id;
+        if (a.out_tok) {
+          const int32_t to = a.out_tok[s * kG + (tid % kG)];
+          od = (to >= 0 && to < a.n_tok) ? b * a.n_tok + to : -1;
+        }
+      }
     }
     rowid[tid] = id;
+    rowout[tid] = od;
   }
   for (int k = tid; k < D; k += kThreads) {
     const int c = a.chan[qc * D + k];
@@ -400,7 +410,7 @@ bigemm_fwd_kernel(FwdArgs a) {
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + i * kThreads;
       const int r = idx / VPR, v = idx % VPR;
-      const int64_t id = rowid[r];
+      const int64_t id = rowout[r];
       if (id >= 0)
         *reinterpret_cast<u32x4*>(a.out + id * a.channels + qc * D + v * 8) =
             *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
@@ -417,7 +427,7 @@ bigemm_fwd_kernel(FwdArgs a) {
       for (int i = 0; i < NV; ++i) {
         const int idx = tid + i * kThreads;
         const int r = idx / VPR, v = idx % VPR;
-        const int64_t id = rowid[r];
+        const int64_t id = rowout[r];
         if (id < 0) continue;
         const uint16_t* src = &xs[r * LDX + v * M];
         uint16_t* dst = a.out + id * a.channels + v * 8 + strided_res;
@@ -434,7 +444,7 @@ bigemm_fwd_kernel(FwdArgs a) {
     for (int j = 0; j < NE; ++j) {
       const int i = tid + j * kThreads;
       const int r = i / D, k = i % D;
-      const int64_t id = rowid[r];
+      const int64_t id = rowout[r];
       const int c = chx[k];
       if (id >= 0 && c >= 0) a.out[id * a.channels + c] = xs[r * LDX + k];
     }
@@ -840,10 +850,10 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
   return OW_OK;
 }
 
-int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
-                  const int32_t* token_index, const int32_t* channel_index,
-                  const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags, void* workspace,
-                  size_t workspace_bytes, void* stream) {
+static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                            const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
+                            const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
+                            void* workspace, size_t workspace_bytes, void* stream) {
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
@@ -872,6 +882,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   OW_CHECK_ARG(workspace_bytes >= need_ws && (need_ws == 0 || workspace),
                "workspace holds %zu bytes; %zu needed", workspace_bytes, need_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  OW_CHECK_SUPPORTED(!out_rows || dtype != OW_DTYPE_F32, "an output-row table needs bf16 or f16 activations");
   if (dtype == OW_DTYPE_F32) {
     float* scale = nullptr;
     if (flags & OW_FUSE_NORM) {
@@ -892,6 +903,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
     r.packed = static_cast<const uint16_t*>(packed);
     r.tok = token_index;
     r.chan = channel_index;
+    r.out_tok = out_rows;
     r.batch = batch;
     r.n_tok = n;
     r.channels = c;
@@ -917,6 +929,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
   a.packed = static_cast<const uint16_t*>(packed);
   a.tok = token_index;
   a.chan = channel_index;
+  a.out_tok = out_rows;
   a.batch = batch;
   a.n_tok = n;
   a.channels = c;
@@ -944,6 +957,22 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
                                 : ow::dispatch_fwd<ow::F16, false>(a, d, rd, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
+}
+
+int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                  const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan, int32_t batch,
+                  int32_t rd, int32_t dtype, int32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
+  return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, nullptr, plan, batch, rd,
+                          dtype, flags, workspace, workspace_bytes, stream);
+}
+
+int ow_bigemm_fwd_rows(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                       const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
+                       const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  OW_CHECK_ARG(out_rows, "out_rows is NULL");
+  return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
+                          dtype, flags, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -77,12 +77,13 @@ __device__ __forceinline__ void pair_advance(PairPos& pos, int32_t step_b, int32
   }
 }
 
-// Token-table entries of the NI rows this lane loads and stores in a pair, with the image
-// index of each row (>= batch past the end).  Only loads: the values are examined one
-// iteration later (row_id), so the loads are not waited on while the row prefetch is in flight.
-template <int NI, int RPW, int RPI, int LPR>
+// Token-table entries of the NI rows this lane loads and stores in a pair (with OM, also the
+// output-row table entries), with the image index of each row (>= batch past the end).  Only
+// loads: the values are examined one iteration later (row_id), so the loads are not waited on
+// while the row prefetch is in flight.
+template <int NI, int RPW, int RPI, int LPR, bool OM>
 __device__ __forceinline__ void pair_row_tok(const ResidentArgs& a, PairPos pos, int wave, int lane,
-                                             int32_t (&t)[NI], int32_t (&b)[NI]) {
+                                             int32_t (&t)[NI], int32_t (&to)[NI], int32_t (&b)[NI]) {
   const int32_t b0 = pos.b, s0 = pos.s;  // uniform
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
@@ -94,11 +95,19 @@ __device__ __forceinline__ void pair_row_tok(const ResidentArgs& a, PairPos pos,
     }
     b[j] = bb;
     t[j] = a.tok[s * kG + (r % kG)];  // s < q_s: in bounds even for rows past the end
+    if (OM) to[j] = a.out_tok[s * kG + (r % kG)];
   }
 }
 
 __device__ __forceinline__ int32_t row_id(const ResidentArgs& a, int32_t t, int32_t b) {
   return (b < a.batch && t >= 0 && t < a.n_tok) ? b * a.n_tok + t : -1;
+}
+
+// Output row of a token slot whose input row is `in` (-1: pad slot, not stored).
+template <bool OM>
+__device__ __forceinline__ int32_t out_id(const ResidentArgs& a, int32_t in, int32_t to, int32_t b) {
+  if (!OM) return in;
+  return in >= 0 ? row_id(a, to, b) : -1;
 }
 
 template <int C>
@@ -108,8 +117,9 @@ __device__ __forceinline__ u32x4 load_row_vec(const uint16_t* x, int32_t id, int
   return v;
 }
 
-// The persistent loop of one wave: channel group g, expanded-dimension half HF.
-template <class Ty, int QC, int HF>
+// The persistent loop of one wave: channel group g, expanded-dimension half HF.  OM: rows are
+// stored at the output-row table's positions instead of their input positions.
+template <class Ty, int QC, int HF, bool OM>
 __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds<QC>& sh, int g, int n_iter) {
   constexpr int C = QC * kD;
   constexpr int LDC = ResidentLds<QC>::LDC;
@@ -144,25 +154,26 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
     col[cb] = (c >= 0 && c < C) ? c : 0;  // tables of a plan with C = q_c * d hold no pads
   }
 
-  // ids_prev: rows being stored (pair it - 1); ids_cur: rows of pair it; tok_n / img_n: raw
-  // table entries of pair it + 1.
+  // ids_prev: output rows being stored (pair it - 1); ids_cur: output rows of pair it; tok_n /
+  // tout_n / img_n: raw table entries of pair it + 1.
   int32_t ids_cur[NI], ids_prev[NI];
-  int32_t tok_n[NI], img_n[NI];
+  int32_t tok_n[NI], tout_n[NI], img_n[NI];
   u32x4 xr[NI];
   // pos: the pair whose table entries are read next; the grid stride in groups is 2 n_wg.
   const int32_t step_b = static_cast<int32_t>(2 * n_wg / a.q_s);
   const int32_t step_s = static_cast<int32_t>(2 * n_wg - static_cast<int64_t>(step_b) * a.q_s);
   PairPos pos = pair_pos(first, a.q_s);
-  pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
+  pair_row_tok<NI, RPW, RPI, LPR, OM>(a, pos, wave, lane, tok_n, tout_n, img_n);
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     ids_prev[j] = -1;
-    ids_cur[j] = row_id(a, tok_n[j], img_n[j]);
-    xr[j] = load_row_vec<C>(a.x, ids_cur[j], vcol);
+    const int32_t in = row_id(a, tok_n[j], img_n[j]);
+    ids_cur[j] = out_id<OM>(a, in, tout_n[j], img_n[j]);
+    xr[j] = load_row_vec<C>(a.x, in, vcol);
   }
   if (n_iter > 1) {
     pair_advance(pos, step_b, step_s, a.q_s);
-    pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
+    pair_row_tok<NI, RPW, RPI, LPR, OM>(a, pos, wave, lane, tok_n, tout_n, img_n);
   } else {
 #pragma unroll
     for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
@@ -193,12 +204,13 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
     int32_t ids_next[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      ids_next[j] = row_id(a, tok_n[j], img_n[j]);
-      xr[j] = load_row_vec<C>(a.x, ids_next[j], vcol);
+      const int32_t in = row_id(a, tok_n[j], img_n[j]);
+      ids_next[j] = out_id<OM>(a, in, tout_n[j], img_n[j]);
+      xr[j] = load_row_vec<C>(a.x, in, vcol);
     }
     if (it + 2 < n_iter) {
       pair_advance(pos, step_b, step_s, a.q_s);
-      pair_row_tok<NI, RPW, RPI, LPR>(a, pos, wave, lane, tok_n, img_n);
+      pair_row_tok<NI, RPW, RPI, LPR, OM>(a, pos, wave, lane, tok_n, tout_n, img_n);
     } else {
 #pragma unroll
       for (int j = 0; j < NI; ++j) img_n[j] = a.batch;
@@ -279,7 +291,7 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
   }
 }
 
-template <class Ty, int QC>
+template <class Ty, int QC, bool OM>
 __global__ void __attribute__((amdgpu_flat_work_group_size(128 * QC, 128 * QC), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_resident_kernel(ResidentArgs a) {
   __shared__ __attribute__((aligned(16))) ResidentLds<QC> sh;
@@ -292,22 +304,9 @@ bigemm_fwd_resident_kernel(ResidentArgs a) {
     sh.head[f][lane] = reinterpret_cast<const u32x4*>(a.packed + f * kFragElems)[lane];
   __syncthreads();
   if (wave & 1)
-    resident_wave<Ty, QC, 1>(a, sh, wave >> 1, n_iter);
+    resident_wave<Ty, QC, 1, OM>(a, sh, wave >> 1, n_iter);
   else
-    resident_wave<Ty, QC, 0>(a, sh, wave >> 1, n_iter);
-}
-
-// Compute units of the current device (cached per device id).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
+    resident_wave<Ty, QC, 0, OM>(a, sh, wave >> 1, n_iter);
 }
 
 template <class Ty, int QC>
@@ -316,8 +315,12 @@ int launch_qc(const ResidentArgs& a, hipStream_t stream) {
   const int64_t slots = static_cast<int64_t>(device_cus()) * (4 / QC);
   const int64_t grid = a.n_pairs < slots ? a.n_pairs : slots;
   if (grid <= 0) return OW_OK;
-  hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC>), dim3(static_cast<unsigned>(grid)), dim3(128 * QC), 0,
-                     stream, a);
+  if (a.out_tok)
+    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, true>), dim3(static_cast<unsigned>(grid)), dim3(128 * QC),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, false>), dim3(static_cast<unsigned>(grid)),
+                       dim3(128 * QC), 0, stream, a);
   return hip_status(hipGetLastError(), "bigemm_fwd_resident_kernel launch");
 }
 

@@ -391,6 +391,19 @@ inline int hip_status(hipError_t e, const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compute units of the current device (cached per device id).
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Persistent forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4}: weights of a
 // channel group stay in the registers of one wave, one workgroup of q_c waves handles all
 // channel groups of 32 tokens at a time (bigemm_fwd_resident.hip).
@@ -400,6 +413,7 @@ struct ResidentArgs {
   const uint16_t* packed;  // packed weights, LayerScale folded (same layout as the streamed kernel)
   const int32_t* tok;      // [q_s * 16]
   const int32_t* chan;     // [q_c * 64]
+  const int32_t* out_tok;  // [q_s * 16] output row of each token slot; NULL: the token table
   int32_t batch, n_tok, channels, q_s, q_c;
   int32_t n_pairs;  // ceil(batch * q_s / 2)
   int32_t norm;     // fuse the RMSNorm prologue

@@ -177,4 +177,24 @@ int ow_route_build(const OwPlan* plan, int32_t* token_index, int32_t* channel_in
   return OW_OK;
 }
 
+int ow_route_s2d_rows(const OwPlan* plan, int32_t factor, const int32_t* token_index, int32_t* out_rows) {
+  if (int rc = ow::validate(plan)) return rc;
+  OW_CHECK_ARG(token_index && out_rows, "table pointers are NULL");
+  const int32_t h = plan->height, w = plan->width, n = h * w, g = plan->spatial_tile;
+  OW_CHECK_ARG(factor >= 1 && h % factor == 0 && w % factor == 0,
+               "height %d and width %d must be divisible by factor %d", h, w, factor);
+  const int32_t q_s = (n + g - 1) / g, wf = w / factor;
+  for (int32_t i = 0; i < q_s * g; ++i) {
+    const int32_t t = token_index[i];
+    if (t < 0 || t >= n) {
+      out_rows[i] = n;
+      continue;
+    }
+    const int32_t r = t / w, c = t % w;
+    out_rows[i] = ((r / factor) * wf + c / factor) * factor * factor + (r % factor) * factor + c % factor;
+  }
+  ow::clear_error();
+  return OW_OK;
+}
+
 }  // extern "C"

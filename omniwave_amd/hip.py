@@ -6,6 +6,9 @@
   x in, delta out.
 * ``bigemm_block_hip`` — the fused RMSNorm -> BiGEMM -> residual of OmniWeaveBlock.forward
   (omniweave/models/block.py:80-108) in one kernel.
+* ``bigemm_block_s2d_hip`` — the same block with its output written directly in
+  ``space_to_depth`` layout (inference; the block before a downsample).
+* ``stem_hip`` — the backbone stem (NCHW image -> space_to_depth(4) -> Linear) in one kernel.
 
 Both go through the ``omniwave_amd::bigemm_fwd`` torch.library custom op, whose implementation
 calls ``ow_bigemm_fwd`` of libomniwave_amd.so on the current HIP stream.  Weights are packed
@@ -24,7 +27,7 @@ import torch
 from torch import Tensor
 
 from omniwave_amd import _native
-from omniwave_amd.routing import RoutePlan, build_route_plan, device_tables
+from omniwave_amd.routing import RoutePlan, build_route_plan, device_tables, s2d_rows_table
 
 SPATIAL_TILE = 16
 CHANNEL_TILES = (64, 128)
@@ -273,3 +276,130 @@ def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, 
         raise RuntimeError(f"hip backend not supported: the fp8 variant takes bf16 or fp16 activations, not {x.dtype}")
     flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0) | (_native.OW_FUSE_FP8 if fp8 else 0)
     return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps))
+
+
+# ---------------------------------------------------------------------------------------
+# Backbone glue (inference): a block whose output feeds space_to_depth, and the stem.
+
+
+@torch.library.custom_op("omniwave_amd::bigemm_fwd_s2d", mutates_args=())
+def bigemm_fwd_s2d(
+    x: Tensor,
+    norm_weight: Tensor,
+    gamma: Tensor,
+    a_u: Tensor,
+    a_v: Tensor,
+    a_o: Tensor,
+    b_u: Tensor,
+    b_v: Tensor,
+    b_o: Tensor,
+    plan_desc: list[int],
+    flags: int,
+    eps: float,
+    factor: int,
+) -> Tensor:
+    """``space_to_depth(x + delta, factor)`` ([B, H/f, W/f, C f^2]) with the block's RMSNorm
+    fused: ``ow_bigemm_fwd_rows`` with the ``ow_route_s2d_rows`` table, one pass over HBM.
+    Inference only (no autograd)."""
+    plan = _plan_from_desc(plan_desc)
+    x = x.contiguous()
+    b, h, w, c = x.shape
+    if h % factor or w % factor:
+        raise ValueError(f"height {h} and width {w} must be divisible by factor {factor}")
+    fp8 = bool(flags & _native.OW_FUSE_FP8)
+    packed = _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan, fp8)
+    tok, ch = device_tables(plan, x.device)
+    rows = s2d_rows_table(plan, factor, x.device)
+    out = torch.empty((b, h // factor, w // factor, c * factor * factor), dtype=x.dtype, device=x.device)
+    native_plan = plan.native()
+    lib = _native.lib()
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), b, flags)
+    workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _native.check(
+            lib.ow_bigemm_fwd_rows(
+                x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
+                tok.data_ptr(), ch.data_ptr(), rows.data_ptr(), ctypes.byref(native_plan), b, b_u.shape[2],
+                _DTYPE_CODE[x.dtype], flags, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
+            ),
+            "ow_bigemm_fwd_rows",
+        )
+    return out
+
+
+@bigemm_fwd_s2d.register_fake
+def _bigemm_fwd_s2d_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, factor):
+    b, h, w, c = x.shape
+    return x.new_empty((b, h // factor, w // factor, c * factor * factor))
+
+
+def bigemm_block_s2d_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, factor: int = 2,
+                         eps: float = 1e-6, fp8: bool = False) -> Tensor:
+    """``space_to_depth(bigemm_block_hip(x, ...), factor)`` as one kernel (omniweave/models/
+    block.py:80-108 then backbone.py:14-27,183-186); bf16 / fp16 activations, inference only."""
+    _require(x, plan, b_u)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"hip backend not supported: the space_to_depth output takes bf16 or fp16, not {x.dtype}")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, norm_weight, gamma, a_u, b_u)):
+        raise RuntimeError("bigemm_block_s2d_hip is inference-only (no backward); run it under torch.no_grad()")
+    flags = _native.OW_FUSE_NORM | _native.OW_FUSE_RESIDUAL | (_native.OW_FUSE_FP8 if fp8 else 0)
+    return bigemm_fwd_s2d(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps),
+                          int(factor))
+
+
+STEM_CHANNELS = (32, 64, 96, 128, 192, 256)
+
+
+def stem_is_supported(image: Tensor, weight: Tensor) -> tuple[bool, str | None]:
+    """Whether ``stem_hip`` can run these inputs; ``(False, reason)`` otherwise."""
+    err = _native.load_error()
+    if err is not None:
+        return False, f"native library unavailable: {err}"
+    if not image.is_cuda:
+        return False, "CUDA is unavailable"
+    arch = _device_arch(image.device.index if image.device.index is not None else torch.cuda.current_device())
+    if not arch.startswith("gfx950"):
+        return False, f"device architecture {arch} is not gfx950"
+    if image.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != image.dtype:
+        return False, f"stem takes bf16 or fp16 image and weight of one dtype, not {image.dtype} / {weight.dtype}"
+    if image.dim() != 4 or image.shape[1] != 3 or image.shape[2] % 4 or image.shape[3] % 4:
+        return False, f"image must be [B, 3, H, W] with H, W divisible by 4, got {tuple(image.shape)}"
+    if weight.dim() != 2 or weight.shape[1] != 48 or weight.shape[0] not in STEM_CHANNELS:
+        return False, f"weight must be [N, 48] with N in {STEM_CHANNELS}, got {tuple(weight.shape)}"
+    return True, None
+
+
+@torch.library.custom_op("omniwave_amd::stem_fwd", mutates_args=())
+def stem_fwd(image: Tensor, weight: Tensor) -> Tensor:
+    """``Linear(space_to_depth(image.permute(0, 2, 3, 1), 4))`` ([B, H/4, W/4, N]) in one kernel
+    (``ow_stem_fwd``).  Inference only (no autograd)."""
+    image = image.contiguous()
+    weight = weight.contiguous()
+    b, _, h, w = image.shape
+    n = weight.shape[0]
+    out = torch.empty((b, h // 4, w // 4, n), dtype=image.dtype, device=image.device)
+    with torch.cuda.device(image.device):
+        _native.check(
+            _native.lib().ow_stem_fwd(image.data_ptr(), weight.data_ptr(), out.data_ptr(), b, h, w, n,
+                                      _DTYPE_CODE[image.dtype], _stream_ptr(image.device)),
+            "ow_stem_fwd",
+        )
+    return out
+
+
+@stem_fwd.register_fake
+def _stem_fwd_fake(image, weight):
+    b, _, h, w = image.shape
+    return image.new_empty((b, h // 4, w // 4, weight.shape[0]))
+
+
+def stem_hip(image: Tensor, weight: Tensor) -> Tensor:
+    """Backbone stem (omniweave/models/backbone.py:121,173-176) on the HIP kernel; raises if
+    unsupported or if a gradient is needed."""
+    ok, reason = stem_is_supported(image, weight)
+    if not ok:
+        raise RuntimeError(f"hip stem not supported: {reason}")
+    if torch.is_grad_enabled() and (image.requires_grad or weight.requires_grad):
+        raise RuntimeError("stem_hip is inference-only (no backward); run it under torch.no_grad()")
+    return stem_fwd(image, weight)
+

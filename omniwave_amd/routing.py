@@ -130,3 +130,27 @@ def device_tables(plan: RoutePlan, device: torch.device) -> tuple[torch.Tensor, 
         hit = (tok, ch)
         _DEVICE_TABLES[key] = hit
     return hit
+
+
+_S2D_ROWS: dict[tuple, torch.Tensor] = {}
+
+
+def s2d_rows_table(plan: RoutePlan, factor: int, device: torch.device) -> torch.Tensor:
+    """int32 ``[Q_s * g]`` output-row table on ``device`` (``ow_route_s2d_rows``): the row each
+    token slot occupies in ``space_to_depth(out, factor)`` viewed as ``[H*W, C]`` rows per image
+    (omniweave/models/backbone.py:14-27); pad slots hold H*W."""
+    dev = torch.device(device)
+    key = plan.key() + (int(factor), dev.type, dev.index)
+    hit = _S2D_ROWS.get(key)
+    if hit is None:
+        lib = _native.lib()
+        tok = np.ascontiguousarray(plan.token_indices.reshape(-1).numpy(), dtype=np.int32)
+        rows = np.empty_like(tok)
+        ptr = _native._c_int32_p
+        native = plan.native()
+        _native.check(lib.ow_route_s2d_rows(_native.ctypes.byref(native), int(factor), tok.ctypes.data_as(ptr),
+                                            rows.ctypes.data_as(ptr)), "ow_route_s2d_rows")
+        hit = torch.from_numpy(rows).to(dev)
+        _S2D_ROWS[key] = hit
+    return hit
+

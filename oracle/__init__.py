@@ -11,6 +11,7 @@ Modules
 ``oracle.routing``  literal loop restatement of the route plans (integer work).
 ``oracle.bigemm``   pack -> gated two-sided einsum -> unpack in PyTorch on the CPU, the
                     block's RMSNorm/residual sequence, and an fp64 per-tile brute force.
+``oracle.backbone`` the backbone's space_to_depth layout and stem (fp32).
 
 How each function is pinned (tests named in brackets):
 
@@ -24,4 +25,7 @@ How each function is pinned (tests named in brackets):
   code with the pack/einsum path [tests/test_oracle_ops.py].
 * ``rmsnorm_reference`` - textbook RMS formula in fp64 and the reference's dtype sequence
   checked element-wise [tests/test_oracle_ops.py].
+* ``space_to_depth_nhwc`` - an element loop over the definition (``space_to_depth_loops``)
+  and the inverse property on an index image; ``stem_reference`` - a per-pixel fp64 dot
+  product over the 4x4x3 patch written from the NCHW image directly [tests/test_backbone_glue.py].
 """

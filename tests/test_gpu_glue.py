@@ -1,0 +1,130 @@
+"""Backbone glue on the GPU (``-m gpu``): the stem kernel against the oracle stem, the block
+output written in space_to_depth layout against space_to_depth of the fused block's output
+(bit-exact: the same kernel math, only the output rows move), and the model's fused-glue
+forward against its forward_features composition (bit-exact)."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+import omniwave_amd
+from omniwave_amd.backbone import space_to_depth_nhwc
+from omniwave_amd.hip import bigemm_block_hip, bigemm_block_s2d_hip, stem_hip, stem_is_supported
+from oracle.backbone import stem_reference
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+# Relative rounding bound of one conversion to the dtype (half an ulp), doubled for the
+# fp32 accumulation-order difference.
+ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+
+
+def announce(msg: str) -> None:
+    print(f"\n[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+STEM_CASES = [(2, 224, 224, 128), (3, 36, 44, 96), (1, 288, 272, 64), (2, 16, 8, 256), (1, 8, 8, 32), (2, 12, 20, 192)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("case", STEM_CASES, ids=[f"b{b}_{h}x{w}_n{n}" for b, h, w, n in STEM_CASES])
+def test_stem_matches_oracle(case, dtype) -> None:
+    b, h, w, n = case
+    announce(f"stem B={b} {h}x{w} N={n} dtype={dtype}")
+    gen = torch.Generator().manual_seed(h * w + n)
+    img = torch.randn(b, 3, h, w, generator=gen).to(dtype)
+    wt = (torch.randn(n, 48, generator=gen) / 48 ** 0.5).to(dtype)
+    with torch.no_grad():
+        got = stem_hip(img.to(DEV), wt.to(DEV))
+    torch.cuda.synchronize()
+    want = stem_reference(img, wt)
+    assert got.shape == want.shape and got.dtype == dtype
+    err = (got.float().cpu() - want).abs()
+    bound = want.abs() * ULP[dtype] + 1e-5
+    assert bool((err <= bound).all()), f"max excess {(err - bound).max().item():.3e}"
+
+
+def test_stem_rejects_unsupported_inputs() -> None:
+    announce("stem argument checks")
+    img = torch.zeros(1, 3, 8, 8, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(128, 48, dtype=torch.bfloat16, device=DEV)
+    assert stem_is_supported(img, w)[0]
+    assert not stem_is_supported(img[:, :, :6], w)[0]
+    assert not stem_is_supported(img, w[:, :47])[0]
+    assert not stem_is_supported(img, w[:100])[0]
+    assert not stem_is_supported(img.float(), w.float())[0]
+    with pytest.raises(RuntimeError):
+        stem_hip(img.float(), w.float())
+    with pytest.raises(RuntimeError, match="inference-only"):
+        stem_hip(img, w.clone().requires_grad_(True))
+
+
+STAGES = {"s1": (56, 56, 128, 64), "s2": (28, 28, 256, 64), "s3": (14, 14, 512, 128), "pad": (6, 10, 96, 64)}
+S2D_CASES = [("s1", "local", 0), ("s1", "shifted", 0), ("s1", "radix", 1), ("s2", "local", 0), ("s2", "radix", 2),
+             ("s3", "local", 0), ("s3", "shifted", 0), ("s3", "radix", 1), ("s3", "radix", 2), ("pad", "local", 0)]
+
+
+def make_case(b, h, w, c, d, route, level, dtype, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    plan = omniwave_amd.build_route_plan(h, w, c, 16, d, route, level)
+    q_c, rd = plan.channel_indices.shape[0], 2 * d
+    x = torch.randn(b, h, w, c, generator=gen).to(dtype).to(DEV)
+    p = dict(a_u=torch.randn(16, 16, generator=gen) / 4.0, a_v=torch.randn(16, 16, generator=gen) / 4.0,
+             a_o=torch.randn(16, 16, generator=gen) / 4.0, b_u=torch.randn(q_c, d, rd, generator=gen) / d ** 0.5,
+             b_v=torch.randn(q_c, d, rd, generator=gen) / d ** 0.5, b_o=torch.randn(q_c, rd, d, generator=gen) / rd ** 0.5,
+             gamma=torch.full((c,), 1.0))
+    nw = (torch.rand(c, generator=gen) + 0.5).to(DEV)
+    return plan, x, {k: v.to(DEV) for k, v in p.items()}, nw
+
+
+@pytest.mark.parametrize("variant", ["bf16", "f16", "fp8"])
+@pytest.mark.parametrize("stage,route,level", S2D_CASES, ids=[f"{s}-{r}{l}" for s, r, l in S2D_CASES])
+def test_block_s2d_equals_space_to_depth_of_block(stage, route, level, variant) -> None:
+    h, w, c, d = STAGES[stage]
+    dtype = torch.float16 if variant == "f16" else torch.bfloat16
+    fp8 = variant == "fp8"
+    announce(f"block s2d stage={stage} route={route}{level} variant={variant} B=3")
+    plan, x, p, nw = make_case(3, h, w, c, d, route, level, dtype)
+    with torch.no_grad():
+        want = space_to_depth_nhwc(bigemm_block_hip(x, nw, plan, **p, fp8=fp8), 2)
+        got = bigemm_block_s2d_hip(x, nw, plan, **p, factor=2, fp8=fp8)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    assert torch.equal(got, want)
+
+
+def test_block_s2d_is_inference_only() -> None:
+    announce("block s2d under autograd")
+    plan, x, p, nw = make_case(1, 14, 14, 512, 128, "local", 0, torch.bfloat16)
+    p["b_u"].requires_grad_(True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        bigemm_block_s2d_hip(x, nw, plan, **p)
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
+def test_model_fused_glue_matches_forward_features(fp8) -> None:
+    announce(f"omniweave_t fused glue vs forward_features B=2 fp8={fp8}")
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").eval()
+    with torch.no_grad():
+        for stage in model.stages:
+            for blk in stage.blocks:
+                blk.gamma.fill_(1.0)
+    model = model.to(device=DEV, dtype=torch.bfloat16)
+    if fp8:
+        omniwave_amd.enable_fp8(model)
+    x = torch.randn(2, 3, 224, 224, generator=torch.Generator().manual_seed(1)).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        got = model(x)
+        feats = model.forward_features(x)
+        want = model.head(feats["stage4"].mean(dim=(1, 2)))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    if not fp8:  # with autograd on, the reference composition runs (no fused glue)
+        eager = model(x)
+        rel = ((eager.float() - got.float()).norm() / got.float().norm()).item()
+        assert rel <= 1e-2, rel
