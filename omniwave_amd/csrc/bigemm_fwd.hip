@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(kThreads) rms_rows_generic_kernel(RmsArgs a) {
 struct FwdArgs {
   const uint16_t* x;
   uint16_t* out;
-  const float* row_scale;  // [batch * n_tok] RMSNorm scale per token, NULL without OW_FUSE_NORM
+  const float* row_scale;  // [batch * n_tok] RMSNorm scale per token (norm == kNormBuffer)
   const uint16_t* packed;
   const int32_t* tok;
   const int32_t* chan;
@@ -113,7 +113,18 @@ struct FwdArgs {
   int32_t residual;  // write x + delta instead of delta
   int32_t mode;      // channel-group access, one of the kMode* values
   int32_t stride;    // kModeStrided: channel stride n of a group (= q_c)
+  int32_t norm;      // RMSNorm row scales: kNormNone, kNormBuffer (row_scale) or kNormInline
+  float eps;         // kNormInline: RMSNorm epsilon
 };
+
+// Where the RMSNorm row scales come from.
+//   kNormBuffer  row_scale, computed by a statistics pass before the launch
+//   kNormInline  the tile load reads whole rows (C / 8 16-byte vectors, 16 lanes per row) and
+//                sums the squares itself; the other channel groups' workgroups of the same
+//                tokens read the same rows, mostly from L2 (they run on the same XCD)
+constexpr int kNormNone = 0;
+constexpr int kNormBuffer = 1;
+constexpr int kNormInline = 2;
 
 // Channel-group access modes.
 //   kModeContig   group qc is columns [qc*d, qc*d + d): 16-byte row vectors (radix level 0)
@@ -233,11 +244,79 @@ bigemm_fwd_kernel(FwdArgs a) {
   // row-scale loads are in flight together with the tile loads.
   const int strided_res = __builtin_amdgcn_readfirstlane(chx[0]) & (a.stride - 1);
   float my_rsc = 1.0f;
-  if (tid < ROWS && a.row_scale) {
+  if (tid < ROWS && a.norm == kNormBuffer) {
     const int64_t id = rowid[tid];
     if (id >= 0) my_rsc = a.row_scale[id];
   }
-  if (a.mode == kModeContig) {
+  // Whole rows, 16 lanes per row: lane l16 reads vectors l16 + 16 j (j < J = C / 128) of its
+  // row, sums their squares for the row scale and keeps this group's tile columns: with M = 0
+  // the group is contiguous (vector v holds columns 8 (v - qc D / 8) .. + 8 when it belongs
+  // to group qc), with M > 0 strided (vector v holds tile columns M v .. M v + M).
+  auto gather_rows = [&](auto j_tag, auto m_tag) {
+    constexpr int J = decltype(j_tag)::value;
+    constexpr int M = decltype(m_tag)::value;
+    constexpr int RS = kThreads / 16;         // rows per pass
+    constexpr int NI = ROWS / RS;             // passes
+    constexpr int IB = J <= 4 ? NI : NI / 2;  // passes whose loads are in flight together
+    static_assert(NI % IB == 0, "whole batches");
+    const int l16 = tid & 15, rs = tid >> 4;
+#pragma unroll 1
+    for (int i0 = 0; i0 < NI; i0 += IB) {
+      u32x4 v[IB][J];
+#pragma unroll
+      for (int i = 0; i < IB; ++i) {
+        const int64_t id = rowid[rs + RS * (i0 + i)];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          v[i][j] = u32x4{0u, 0u, 0u, 0u};
+          if (id >= 0) v[i][j] = *reinterpret_cast<const u32x4*>(a.x + id * a.channels + (l16 + 16 * j) * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < IB; ++i) {
+        const int r = rs + RS * (i0 + i);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(v[i][j][e], acc);
+        acc = group_sum<16>(acc);
+        if (l16 == 0) rsc[r] = rms_scale<Ty>(acc / static_cast<float>(a.channels), a.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int vv = l16 + 16 * j;
+          if constexpr (M == 0) {
+            if (vv / (D / 8) == qc) *reinterpret_cast<u32x4*>(&xs[r * LDX + (vv % (D / 8)) * 8]) = v[i][j];
+          } else {
+            uint32_t e[M];
+            strided_elems<M>(v[i][j], strided_res, e);
+            uint16_t* dst = &xs[r * LDX + vv * M];
+            if constexpr (M == 4) {
+              *reinterpret_cast<u32x2*>(dst) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+            } else if constexpr (M == 2) {
+              *reinterpret_cast<uint32_t*>(dst) = e[0] | (e[1] << 16);
+            } else {
+              *dst = static_cast<uint16_t>(e[0]);
+            }
+          }
+        }
+      }
+    }
+  };
+  auto gather_rows_m = [&](auto m_tag) {
+    switch (a.channels / 128) {
+      case 1: gather_rows(std::integral_constant<int, 1>{}, m_tag); break;
+      case 2: gather_rows(std::integral_constant<int, 2>{}, m_tag); break;
+      case 4: gather_rows(std::integral_constant<int, 4>{}, m_tag); break;
+      default: gather_rows(std::integral_constant<int, 8>{}, m_tag); break;
+    }
+  };
+  if (a.norm == kNormInline) {
+    if (a.mode == kModeContig) gather_rows_m(std::integral_constant<int, 0>{});
+    else if (a.stride == 2) gather_rows_m(std::integral_constant<int, 4>{});
+    else if (a.stride == 4) gather_rows_m(std::integral_constant<int, 2>{});
+    else gather_rows_m(std::integral_constant<int, 1>{});
+  } else if (a.mode == kModeContig) {
     constexpr int VPR = D / 8;
     constexpr int NV = ROWS * VPR / kThreads;
     u32x4 v[NV];
@@ -310,7 +389,7 @@ bigemm_fwd_kernel(FwdArgs a) {
       }
     }
   }
-  if (tid < ROWS) rsc[tid] = my_rsc;
+  if (tid < ROWS && a.norm != kNormInline) rsc[tid] = my_rsc;
 
   // Token-operand rows of this lane: A_u, A_v rows for the K step of its token group, A_o row
   // for the output product.
@@ -332,7 +411,7 @@ bigemm_fwd_kernel(FwdArgs a) {
   for (int p = 0; p < NP; ++p) {
     const int row0 = (wave * TPW + 2 * p) * kG;
     u32x4 bu = fAu, bv = fAv;
-    if (a.row_scale) {  // lane's slots j are tokens 16 tg + kord(j, hh) of its group tg
+    if (a.norm != kNormNone) {  // lane's slots j are tokens 16 tg + kord(j, hh) of its group tg
       const float* r8 = &rsc[row0 + 16 * ((lane >> 4) & 1) + 4 * hh];
       bu = scale8<Ty>(fAu, r8);
       bv = scale8<Ty>(fAv, r8);
@@ -917,15 +996,9 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }
-  float* scale = nullptr;
-  if (flags & OW_FUSE_NORM) {
-    scale = static_cast<float*>(workspace);
-    if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
-  }
   ow::FwdArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.out = static_cast<uint16_t*>(out);
-  a.row_scale = scale;
   a.packed = static_cast<const uint16_t*>(packed);
   a.tok = token_index;
   a.chan = channel_index;
@@ -936,6 +1009,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   a.q_s = q_s;
   a.q_c = q_c;
   a.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
+  a.eps = eps;
   // Channel-group access (routing.py:107-121): identity order at level 0 or with one group;
   // at levels >= 1 group qc is the channels congruent to (qc + level) mod q_c.
   const bool vec_ok = (c % 8 == 0) && ow::aligned16(x) && ow::aligned16(out);
@@ -948,6 +1022,20 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     a.stride = q_c;
   } else {
     a.mode = ow::kModeElement;
+  }
+  // RMSNorm row scales: read with the tile when whole rows are 16 lanes x 1, 2, 4 or 8 vectors,
+  // otherwise from a statistics pass into the workspace.
+  a.norm = ow::kNormNone;
+  if (flags & OW_FUSE_NORM) {
+    const int32_t j = c / 128;
+    if (a.mode != ow::kModeElement && c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8)) {
+      a.norm = ow::kNormInline;
+    } else {
+      float* scale = static_cast<float*>(workspace);
+      if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
+      a.norm = ow::kNormBuffer;
+      a.row_scale = scale;
+    }
   }
   int rc;
   if (fp8)

@@ -59,17 +59,13 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(kStemThreads, kStemTh
     }
 
   uint16_t* o = ot[wave];
-  for (int64_t u = blockIdx.x; u < a.units; u += gridDim.x) {
+  auto load_unit = [&](int64_t u, u32x4 (&xb)[kStemIn]) {
     const int32_t pb = static_cast<int32_t>(u % a.wblocks);
-    const int64_t bi = u / a.wblocks;  // b * ho + i
+    const int64_t bi = u / a.wblocks;
     const int32_t i = static_cast<int32_t>(bi % a.ho);
     const int64_t b = bi / a.ho;
-    const int32_t p0 = pb * kStemPix + wave * 32;  // first output pixel of this wave
-    const int32_t p = p0 + l32;
-    const bool valid = p < a.wo;
-
-    // B operand of K step c: lane (pixel p, hh) slot j = image[b, c, 4i + 2hh + j/4, 4p + j%4].
-    u32x4 xb[kStemIn];
+    const int32_t p = pb * kStemPix + wave * 32 + l32;
+    const bool valid = u < a.units && p < a.wo;
 #pragma unroll
     for (int c = 0; c < kStemIn; ++c) {
       const uint16_t* src =
@@ -81,6 +77,17 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(kStemThreads, kStemTh
       }
       xb[c] = u32x4{r0.x, r0.y, r1.x, r1.y};
     }
+  };
+  u32x4 xn[kStemIn];
+  load_unit(blockIdx.x, xn);
+  for (int64_t u = blockIdx.x; u < a.units; u += gridDim.x) {
+    const int32_t pb = static_cast<int32_t>(u % a.wblocks);
+    const int64_t bi = u / a.wblocks;  // b * ho + i
+    const int32_t p0 = pb * kStemPix + wave * 32;  // first output pixel of this wave
+    u32x4 xb[kStemIn];
+#pragma unroll
+    for (int c = 0; c < kStemIn; ++c) xb[c] = xn[c];
+    load_unit(u + gridDim.x, xn);
     f32x16 acc[NB];
 #pragma unroll
     for (int cb = 0; cb < NB; ++cb) {
@@ -114,21 +121,39 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(kStemThreads, kStemTh
   }
 }
 
+// Persistent over units (the weight operands are gathered once per workgroup), with exactly as
+// many workgroups as fit on the device at once: a grid beyond that leaves a second, partial
+// wave of workgroups that each run a full share of units after the first ones finish.
+template <class Ty, int NB>
+int launch_stem_nb(const StemArgs& a, hipStream_t stream) {
+  static int per_cu[64] = {0};
+  int dev = 0;
+  if (int rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  int fit = dev >= 0 && dev < 64 ? per_cu[dev] : 0;
+  if (fit == 0) {
+    if (int rc = hip_status(hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, stem_kernel<Ty, NB>, kStemThreads, 0),
+                            "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+      return rc;
+    fit = fit > 0 ? fit : 1;
+    if (dev >= 0 && dev < 64) per_cu[dev] = fit;
+  }
+  const int64_t slots = static_cast<int64_t>(device_cus()) * fit;
+  const unsigned grid = static_cast<unsigned>(a.units < slots ? a.units : slots);
+  hipLaunchKernelGGL((stem_kernel<Ty, NB>), dim3(grid), dim3(kStemThreads), 0, stream, a);
+  return hip_status(hipGetLastError(), "stem_kernel launch");
+}
+
 template <class Ty>
 int launch_stem(const StemArgs& a, int32_t n_out, hipStream_t stream) {
-  // Persistent over units: the weight operands are gathered once per workgroup.
-  const int64_t slots = static_cast<int64_t>(device_cus()) * 8;
-  const unsigned grid = static_cast<unsigned>(a.units < slots ? a.units : slots);
   switch (n_out / 32) {
-    case 1: hipLaunchKernelGGL((stem_kernel<Ty, 1>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((stem_kernel<Ty, 2>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL((stem_kernel<Ty, 3>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((stem_kernel<Ty, 4>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
-    case 6: hipLaunchKernelGGL((stem_kernel<Ty, 6>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
-    case 8: hipLaunchKernelGGL((stem_kernel<Ty, 8>), dim3(grid), dim3(kStemThreads), 0, stream, a); break;
+    case 1: return launch_stem_nb<Ty, 1>(a, stream);
+    case 2: return launch_stem_nb<Ty, 2>(a, stream);
+    case 3: return launch_stem_nb<Ty, 3>(a, stream);
+    case 4: return launch_stem_nb<Ty, 4>(a, stream);
+    case 6: return launch_stem_nb<Ty, 6>(a, stream);
+    case 8: return launch_stem_nb<Ty, 8>(a, stream);
     default: return fail(OW_ERR_UNSUPPORTED, "stem: %d output channels; expected 32, 64, 96, 128, 192 or 256", n_out);
   }
-  return hip_status(hipGetLastError(), "stem_kernel launch");
 }
 
 }  // namespace
