@@ -12,6 +12,7 @@ from collections import OrderedDict
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 from torch import Tensor
 
 from omniwave_amd.block import OmniWeaveBlock
@@ -51,11 +52,9 @@ class _Stage(nn.Module):
             x = block(x)
         return x
 
-    def forward_s2d(self, x: Tensor, factor: int) -> Tensor:
-        """``space_to_depth(self(x), factor)``; the last block writes that layout itself when it
-        can (``OmniWeaveBlock.forward_s2d``)."""
-        if self.anchor is not None:
-            x = self.anchor(x)
+    def forward_blocks_s2d(self, x: Tensor, factor: int) -> Tensor:
+        """``space_to_depth`` of the blocks' output (the anchor is the caller's); the last block
+        writes that layout itself when it can (``OmniWeaveBlock.forward_s2d``)."""
         for block in self.blocks[:-1]:
             x = block(x)
         y = self.blocks[-1].forward_s2d(x, factor)
@@ -109,6 +108,26 @@ class OmniWeaveBackbone(nn.Module):
             offset += depths[i]
         self.head = nn.Linear(widths[-1], num_classes)
         self._widths = widths
+        self._entry_cache: dict[int, tuple[tuple, Tensor]] = {}
+
+    def _entry_weight(self, i: int) -> Tensor:
+        """Weight of the Linear that enters stage ``i`` (> 0) from the previous stage's
+        space_to_depth output: the downsample, with the stage's anchor folded in when it has
+        one — both are bias-free, so ``anchor(downsample(x)) = x (W_a W_ds)^T``; the product is
+        formed in fp32 and rounded once.  Cached while both weights are unchanged."""
+        w_ds = self.downsamples[i - 1].weight
+        anchor = self.stages[i].anchor
+        if anchor is None:
+            return w_ds
+        w_a = anchor.weight
+        key = tuple((t.data_ptr(), t.dtype, t.device, t._version) for t in (w_ds, w_a))
+        hit = self._entry_cache.get(i)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                fused = (w_a.float() @ w_ds.float()).to(w_ds.dtype)
+            hit = (key, fused)
+            self._entry_cache[i] = hit
+        return hit[1]
 
     def _hip_glue(self, x: Tensor) -> bool:
         """Inference with every block on the hip backend: run the stem and the block before each
@@ -138,14 +157,20 @@ class OmniWeaveBackbone(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         """NCHW image -> logits (backbone.py:191-197).  Under ``torch.no_grad`` /
         ``inference_mode`` with the blocks on the hip backend, the stem and each stage's last
-        block write the layout the next Linear reads, so no space_to_depth copy is made."""
+        block write the layout the next Linear reads, so no space_to_depth copy is made, and a
+        stage's anchor Linear is folded into the downsample before it (``_entry_weight``)."""
         if not self._hip_glue(x):
             stage4 = self.forward_features(x)["stage4"]
             return self.head(stage4.mean(dim=(1, 2)))
         x = self._stem(x)
         for i, stage in enumerate(self.stages):
+            if i > 0:  # downsample (+ anchor) on the previous stage's space_to_depth output
+                x = F.linear(x, self._entry_weight(i))
+            elif stage.anchor is not None:
+                x = stage.anchor(x)
             if i < 3:
-                x = self.downsamples[i](stage.forward_s2d(x, 2))
+                x = stage.forward_blocks_s2d(x, 2)
             else:
-                x = stage(x)
+                for block in stage.blocks:
+                    x = block(x)
         return self.head(x.mean(dim=(1, 2)))

@@ -122,9 +122,24 @@ def test_model_fused_glue_matches_forward_features(fp8) -> None:
         got = model(x)
         feats = model.forward_features(x)
         want = model.head(feats["stage4"].mean(dim=(1, 2)))
+        # The same composition with the anchors unfolded: downsample, then anchor.
+        h = model._stem(x)
+        for i, stage in enumerate(model.stages):
+            if i > 0:
+                h = model.downsamples[i - 1](h)
+            if stage.anchor is not None:
+                h = stage.anchor(h)
+            h = stage.forward_blocks_s2d(h, 2) if i < 3 else stage.blocks[1](stage.blocks[0](h))
+        unfolded = model.head(h.mean(dim=(1, 2)))
     torch.cuda.synchronize()
-    assert torch.equal(got, want)
-    if not fp8:  # with autograd on, the reference composition runs (no fused glue)
+    # Stages 1-2 and the space_to_depth layout are exact (checked per block above); folding
+    # the anchor into the downsample changes one bf16 rounding of the stage-3/4 entry.
+    rel = ((got.float() - want.float()).norm() / want.float().norm()).item()
+    rel_unfolded = ((unfolded.float() - want.float()).norm() / want.float().norm()).item()
+    print(f"fused glue vs forward_features rel-L2 {rel:.2e}; unfolded anchors {rel_unfolded:.2e}", flush=True)
+    assert rel <= 1e-2, rel
+    assert rel_unfolded == 0.0, rel_unfolded
+    if not fp8:  # with autograd on, the reference composition runs (no fused glue, no stem kernel)
         eager = model(x)
-        rel = ((eager.float() - got.float()).norm() / got.float().norm()).item()
-        assert rel <= 1e-2, rel
+        rel_eager = ((eager.float() - want.float()).norm() / want.float().norm()).item()
+        assert rel_eager <= 1e-2, rel_eager
