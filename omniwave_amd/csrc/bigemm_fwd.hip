@@ -137,17 +137,26 @@ constexpr int kModeStrided = 1;
 constexpr int kModeElement = 2;
 constexpr int kBatch = 16;  // global loads kept in flight per thread by the gather / scatter loops
 
-// The M = 8/n elements of a strided channel group held by one 16-byte row vector: element
-// index res + t*n for t < M (res < n is the group's first channel), each in the low 16 bits.
+// The M = 8/n elements of a strided channel group held by one 16-byte row vector (element
+// index res + t n for t < M, res < n the group's first channel), packed in order: M = 4 and
+// M = 2 as 16-bit halves of two / one word, M = 1 in the low half.  res is wave-uniform, so
+// the word choices are uniform selects and each pair of halves is one v_perm_b32 (result
+// bytes 0-1 from the low operand, 2-3 from the high one).
 template <int M>
-__device__ __forceinline__ void strided_elems(const u32x4& v, int res, uint32_t (&e)[M]) {
-  constexpr int N = 8 / M;
-  const uint32_t sh = 16u * static_cast<uint32_t>(res & 1);
-#pragma unroll
-  for (int t = 0; t < M; ++t) {
-    const int w = (res + t * N) >> 1;
+using StridedPack = std::conditional_t<M == 4, u32x2, uint32_t>;
+
+template <int M>
+__device__ __forceinline__ StridedPack<M> strided_pack(const u32x4& v, int res) {
+  const uint32_t sel = (res & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+  if constexpr (M == 4) {  // n = 2: halves (res & 1) of words 0..3
+    return u32x2{__builtin_amdgcn_perm(v[1], v[0], sel), __builtin_amdgcn_perm(v[3], v[2], sel)};
+  } else if constexpr (M == 2) {  // n = 4: words res / 2 and res / 2 + 2
+    const bool w1 = (res & 2) != 0;
+    return __builtin_amdgcn_perm(w1 ? v[3] : v[2], w1 ? v[1] : v[0], sel);
+  } else {  // n = 8: word res / 2
+    const int w = res >> 1;
     const uint32_t word = w == 0 ? v[0] : w == 1 ? v[1] : w == 2 ? v[2] : v[3];
-    e[t] = (word >> sh) & 0xffffu;
+    return (res & 1) ? word >> 16 : word;
   }
 }
 
@@ -288,16 +297,12 @@ bigemm_fwd_kernel(FwdArgs a) {
           if constexpr (M == 0) {
             if (vv / (D / 8) == qc) *reinterpret_cast<u32x4*>(&xs[r * LDX + (vv % (D / 8)) * 8]) = v[i][j];
           } else {
-            uint32_t e[M];
-            strided_elems<M>(v[i][j], strided_res, e);
+            const StridedPack<M> e = strided_pack<M>(v[i][j], strided_res);
             uint16_t* dst = &xs[r * LDX + vv * M];
-            if constexpr (M == 4) {
-              *reinterpret_cast<u32x2*>(dst) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-            } else if constexpr (M == 2) {
-              *reinterpret_cast<uint32_t*>(dst) = e[0] | (e[1] << 16);
-            } else {
-              *dst = static_cast<uint16_t>(e[0]);
-            }
+            if constexpr (M == 1)
+              *dst = static_cast<uint16_t>(e);
+            else
+              *reinterpret_cast<StridedPack<M>*>(dst) = e;
           }
         }
       }
@@ -353,16 +358,12 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
           const int idx = tid + (i0 + j) * kThreads;
-          uint32_t e[M];
-          strided_elems<M>(v[j], strided_res, e);
+          const StridedPack<M> e = strided_pack<M>(v[j], strided_res);
           uint16_t* dst = &xs[(idx / VPR) * LDX + (idx % VPR) * M];
-          if constexpr (M == 4) {
-            *reinterpret_cast<u32x2*>(dst) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-          } else if constexpr (M == 2) {
-            *reinterpret_cast<uint32_t*>(dst) = e[0] | (e[1] << 16);
-          } else {
-            *dst = static_cast<uint16_t>(e[0]);
-          }
+          if constexpr (M == 1)
+            *dst = static_cast<uint16_t>(e);
+          else
+            *reinterpret_cast<StridedPack<M>*>(dst) = e;
         }
       }
     };
@@ -481,42 +482,69 @@ bigemm_fwd_kernel(FwdArgs a) {
   }
   __syncthreads();
 
-  // The finished tile to memory.
-  if (a.mode == kModeContig) {
-    constexpr int VPR = D / 8;
-    constexpr int NV = ROWS * VPR / kThreads;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int idx = tid + i * kThreads;
-      const int r = idx / VPR, v = idx % VPR;
-      const int64_t id = rowout[r];
-      if (id >= 0)
-        *reinterpret_cast<u32x4*>(a.out + id * a.channels + qc * D + v * 8) =
-            *reinterpret_cast<const u32x4*>(&xs[r * LDX + v * 8]);
-    }
-  } else if (a.mode == kModeStrided) {
-    // Per 16-byte row vector: M tile columns, stored element by element (the other columns of
-    // the vector belong to other channel groups).
-    auto scatter_strided = [&](auto m_tag) {
+  // The finished tile to memory.  Each wave stores rows [32 wave, 32 wave + 32) of the tile;
+  // the output-row ids and the tile data of a batch of rows are read from LDS first, then the
+  // stores are issued without waiting in between (an LDS round trip per store would leave
+  // the loop latency-bound).
+  if (a.mode == kModeContig || a.mode == kModeStrided) {
+    constexpr int WR = ROWS / kWaves;  // rows per wave
+    static_assert(WR == 32, "32 rows per wave");
+    // M tile columns per 16-byte row vector of out: 8 (contiguous) or 8 / stride.
+    auto store_rows = [&](auto m_tag) {
       constexpr int M = decltype(m_tag)::value;
-      constexpr int N = 8 / M;
-      constexpr int VPR = D / M;
-      constexpr int NV = ROWS * VPR / kThreads;
-#pragma unroll 4
-      for (int i = 0; i < NV; ++i) {
-        const int idx = tid + i * kThreads;
-        const int r = idx / VPR, v = idx % VPR;
-        const int64_t id = rowout[r];
-        if (id < 0) continue;
-        const uint16_t* src = &xs[r * LDX + v * M];
-        uint16_t* dst = a.out + id * a.channels + v * 8 + strided_res;
+      constexpr int N = 8 / M;                   // element stride of the group in a vector
+      constexpr int VPR = D / M;                 // row vectors holding the group's columns
+      constexpr int LPR = VPR < 64 ? VPR : 64;   // lanes per row
+      constexpr int RPI = 64 / LPR;              // rows per pass
+      constexpr int NIT = WR / RPI;              // passes (rows per lane)
+      constexpr int VPL = VPR / LPR;             // vectors per lane and row
+      constexpr int KB = NIT < 8 ? NIT : 8;      // passes per batch
+      static_assert(NIT % KB == 0, "whole batches");
+      using Elt = std::conditional_t<M == 8, u32x4, std::conditional_t<M == 4, u32x2,
+                                     std::conditional_t<M == 2, uint32_t, uint16_t>>>;
+      const int sub = lane % LPR, rsub = lane / LPR;
+      const int64_t col0 = M == 8 ? static_cast<int64_t>(qc) * D : strided_res;
+#pragma unroll 1
+      for (int k0 = 0; k0 < NIT; k0 += KB) {
+        int32_t ids[KB];
+        Elt val[KB][VPL];
 #pragma unroll
-        for (int t = 0; t < M; ++t) dst[t * N] = src[t];
+        for (int k = 0; k < KB; ++k) {
+          const int r = wave * WR + rsub + RPI * (k0 + k);
+          ids[k] = rowout[r];
+#pragma unroll
+          for (int q = 0; q < VPL; ++q)
+            val[k][q] = *reinterpret_cast<const Elt*>(&xs[r * LDX + (sub + q * LPR) * M]);
+        }
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+          if (ids[k] < 0) continue;
+          uint16_t* row = a.out + static_cast<int64_t>(ids[k]) * a.channels + col0;
+#pragma unroll
+          for (int q = 0; q < VPL; ++q) {
+            uint16_t* dst = row + (sub + q * LPR) * 8;
+            const Elt e = val[k][q];
+            if constexpr (M == 8) {
+              *reinterpret_cast<u32x4*>(dst) = e;
+            } else if constexpr (M == 4) {
+              dst[0] = lo16(e.x);
+              dst[N] = hi16(e.x);
+              dst[2 * N] = lo16(e.y);
+              dst[3 * N] = hi16(e.y);
+            } else if constexpr (M == 2) {
+              dst[0] = lo16(e);
+              dst[N] = hi16(e);
+            } else {
+              dst[0] = e;
+            }
+          }
+        }
       }
     };
-    if (a.stride == 2) scatter_strided(std::integral_constant<int, 4>{});
-    else if (a.stride == 4) scatter_strided(std::integral_constant<int, 2>{});
-    else scatter_strided(std::integral_constant<int, 1>{});
+    if (a.mode == kModeContig) store_rows(std::integral_constant<int, 8>{});
+    else if (a.stride == 2) store_rows(std::integral_constant<int, 4>{});
+    else if (a.stride == 4) store_rows(std::integral_constant<int, 2>{});
+    else store_rows(std::integral_constant<int, 1>{});
   } else {
     constexpr int NE = ROWS * D / kThreads;
 #pragma unroll 4

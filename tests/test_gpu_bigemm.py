@@ -153,10 +153,12 @@ def test_layer_scale_is_exactly_linear() -> None:
 
 def test_ragged_channels_and_rd_variants() -> None:
     """C=70 with d=64 (pad channels, element gather path), d=64/rd=256 (streamed kernel, contiguous
-    and strided channel groups), d=128/rd=128, and C=64 (one channel group, resident kernel)."""
+    and strided channel groups: 4, 2 and 8 groups), d=128/rd=128, d=128 with two strided groups,
+    and C=64 (one channel group, resident kernel)."""
     for (h, w, c, d, rd, route, level) in [(7, 7, 70, 64, 128, "radix", 1), (9, 9, 128, 64, 256, "local", 0),
-                                          (7, 7, 256, 64, 256, "radix", 1), (6, 6, 256, 128, 128, "shifted", 0),
-                                          (8, 8, 64, 64, 128, "shifted", 0)]:
+                                          (7, 7, 256, 64, 256, "radix", 1), (10, 6, 128, 64, 256, "radix", 2),
+                                          (5, 5, 512, 64, 256, "radix", 1), (6, 6, 256, 128, 128, "shifted", 0),
+                                          (6, 6, 256, 128, 256, "radix", 1), (8, 8, 64, 64, 128, "shifted", 0)]:
         announce(f"ragged h={h} w={w} c={c} d={d} rd={rd} {route}{level}")
         plan, x, params, norm_w = make_case(3, h, w, c, d, route, level, torch.bfloat16, seed=4, rd=rd)
         got = bigemm_delta_hip(x=x.to(DEV), plan=plan, **to_dev(params))
