@@ -40,8 +40,7 @@ def compile_flags() -> list[str]:
         "-Wno-unused-function",
         # Packed-FP32 VALU ops stay off: scalar float code only.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # MFMA accumulators in VGPRs: the SiLU and epilogue read them with VALU instructions,
-        # and values only MFMAs read (resident weights) go to AGPRs instead.
+        # MFMA accumulators in VGPRs: the SiLU and epilogue read them with VALU instructions.
         "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         f"-I{INCLUDE}",
         f"-I{CSRC}",

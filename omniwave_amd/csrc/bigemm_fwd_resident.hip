@@ -136,17 +136,16 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
   const int64_t n_wg = gridDim.x;
   const int64_t first = blockIdx.x;
 
-  // Resident weights of chunks 2 HF and 2 HF + 1 of channel group g (accumulation registers:
-  // only MFMAs read them).
+  // Resident weights of chunks 2 HF and 2 HF + 1 of channel group g (96 registers).  They stay
+  // in ordinary VGPRs: with 2 waves per SIMD a wave has 256 registers, and pinning the weights
+  // to AGPRs would split that budget 128 / 128 and spill the loop's VGPRs into AGPRs (a copy
+  // each way per spilled value, ~50 VALU instructions per pair).
   const uint16_t* wsrc = a.packed + kHeadElems + (static_cast<size_t>(g) * kNCH + kHalfCh * HF) * kChElems;
   u32x4 wt[kHalfCh][kFrCh];
 #pragma unroll
   for (int e = 0; e < kHalfCh; ++e)
 #pragma unroll
-    for (int f = 0; f < kFrCh; ++f) {
-      wt[e][f] = reinterpret_cast<const u32x4*>(wsrc + e * kChElems + f * kFragElems)[lane];
-      asm volatile("" : "+a"(wt[e][f]));
-    }
+    for (int f = 0; f < kFrCh; ++f) wt[e][f] = reinterpret_cast<const u32x4*>(wsrc + e * kChElems + f * kFragElems)[lane];
   int col[kMB];  // tile column of group channel 32 cb + l32
 #pragma unroll
   for (int cb = 0; cb < kMB; ++cb) {
