@@ -143,3 +143,30 @@ def test_model_fused_glue_matches_forward_features(fp8) -> None:
         eager = model(x)
         rel_eager = ((eager.float() - want.float()).norm() / want.float().norm()).item()
         assert rel_eager <= 1e-2, rel_eager
+
+
+def test_model_fused_glue_graph_replays_match_eager() -> None:
+    """The inference path (stem kernel, s2d-layout blocks, folded entry GEMMs) captured in one
+    HIP graph: every replay, with eager work and synchronisation in between, reproduces the
+    eager logits exactly."""
+    announce("omniweave_t fused glue under HIP graph capture, B=4")
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").to(device=DEV, dtype=torch.bfloat16).eval()
+    x = torch.randn(4, 3, 224, 224, generator=torch.Generator().manual_seed(3)).to(DEV, torch.bfloat16)
+    with torch.inference_mode():
+        eager = model(x).clone()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            model(x)
+            torch.cuda.current_stream().synchronize()
+            with torch.cuda.graph(graph, stream=stream):
+                logits = model(x)
+        torch.cuda.current_stream().wait_stream(stream)
+        for k in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(logits, eager), f"replay {k}"
+            model(x[:2])  # eager work between replays
+            torch.cuda.synchronize()
