@@ -32,8 +32,16 @@ from omniwave_amd.routing import RoutePlan, device_tables
 
 _DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
                torch.float16: _native.OW_DTYPE_F16}
-# Waves of ow_tile_outer: each sums a strided share of the tiles into one [16][16] partial.
-_OUTER_WAVES = 8192
+# Waves of ow_tile_outer: each sums a strided share of the tiles into one [16][16] partial;
+# about 8 tiles per wave (two in flight per loop step), between 256 and 8192 waves.
+_OUTER_TILES_PER_WAVE = 8
+_OUTER_WAVES_MIN, _OUTER_WAVES_MAX = 256, 8192
+
+
+def _outer_waves(n_tiles: int) -> int:
+    waves = -(-n_tiles // _OUTER_TILES_PER_WAVE)
+    waves = -(-waves // 4) * 4
+    return max(_OUTER_WAVES_MIN, min(_OUTER_WAVES_MAX, waves))
 # Most slot chunks of a parameter-gradient GEMM (see _slot_reduce).
 _SPLITS = 64
 
@@ -54,8 +62,9 @@ def _tile_mix(lib, in1: Tensor, m1: Tensor, in2: Tensor | None, m2: Tensor | Non
 
 def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -> Tensor:
     n_tiles = in1.numel() // (16 * d)
-    partial = torch.empty(16, 16, _OUTER_WAVES, dtype=torch.float32, device=in1.device)
-    _native.check(lib.ow_tile_outer(in1.data_ptr(), in2.data_ptr(), partial.data_ptr(), _OUTER_WAVES, n_tiles, d,
+    n_waves = _outer_waves(n_tiles)
+    partial = torch.empty(16, 16, n_waves, dtype=torch.float32, device=in1.device)
+    _native.check(lib.ow_tile_outer(in1.data_ptr(), in2.data_ptr(), partial.data_ptr(), n_waves, n_tiles, d,
                                     code, stream), "ow_tile_outer")
     return partial.sum(dim=2)
 

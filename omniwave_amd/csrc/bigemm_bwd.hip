@@ -409,22 +409,71 @@ __global__ void __launch_bounds__(256) tile_mix_kernel(const uint16_t* in1, cons
 
 // Sum over tiles of in1_tile in2_tile^T ([16][d] x [d][16] -> [16][16]), grid-strided; each wave
 // writes its partial sum (lane (l16, h) register i = out[4h + i][l16]) to partial[256][n_waves]
-// (element-major, so the sum over waves is a contiguous reduction).
+// (element-major, so the sum over waves is a contiguous reduction).  With d % 32 == 0 the K
+// order inside each pair of 16-deep steps is lane-major: lane (l16, h) holds channels
+// 32 s + 8 h .. + 8 of row l16 (one 16-byte load per operand), the first MFMA of the pair takes
+// elements 0..3 and the second 4..7 — both operands use the same order, so the sum is the full
+// contraction — and two tiles are loaded before their MFMAs, so each wave keeps 4 d / 32 loads
+// in flight.
 template <class Ty>
 __global__ void __launch_bounds__(256) tile_outer_kernel(const uint16_t* in1, const uint16_t* in2, float* partial,
-                                                         int64_t n_tiles, int32_t d) {
+                                                         int64_t n_tiles, int32_t d, int32_t vec) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
   const int l16 = lane & 15, h = lane >> 4;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
-    const int64_t base = tile * 16 * d;
-    for (int ks = 0; ks < d / 16; ++ks) {
-      // A: row l16 of in1, K slots 16 ks + 4h + j; B: column l16 = row l16 of in2, same K.
-      const uint2 av = *reinterpret_cast<const uint2*>(in1 + base + l16 * d + 16 * ks + 4 * h);
-      const uint2 bv = *reinterpret_cast<const uint2*>(in2 + base + l16 * d + 16 * ks + 4 * h);
-      acc = Ty::mma16(u32x2{av.x, av.y}, u32x2{bv.x, bv.y}, acc);
+  auto tile_pair = [&](auto nk_tag) {
+    constexpr int NK = decltype(nk_tag)::value;  // 16-byte loads per row and operand (d / 32)
+    constexpr int D = 32 * NK;
+    auto mma_pair = [&](const u32x4& a, const u32x4& b) {
+      acc = Ty::mma16(u32x2{a.x, a.y}, u32x2{b.x, b.y}, acc);
+      acc = Ty::mma16(u32x2{a.z, a.w}, u32x2{b.z, b.w}, acc);
+    };
+    int64_t tile = wave;
+    for (; tile + n_waves < n_tiles; tile += 2 * n_waves) {
+      const uint16_t* p0 = in1 + tile * 16 * D + l16 * D + 8 * h;
+      const uint16_t* q0 = in2 + tile * 16 * D + l16 * D + 8 * h;
+      const int64_t step = n_waves * 16 * D;
+      u32x4 a0[NK], b0[NK], a1[NK], b1[NK];
+#pragma unroll
+      for (int s = 0; s < NK; ++s) {
+        a0[s] = *reinterpret_cast<const u32x4*>(p0 + 32 * s);
+        b0[s] = *reinterpret_cast<const u32x4*>(q0 + 32 * s);
+        a1[s] = *reinterpret_cast<const u32x4*>(p0 + step + 32 * s);
+        b1[s] = *reinterpret_cast<const u32x4*>(q0 + step + 32 * s);
+      }
+#pragma unroll
+      for (int s = 0; s < NK; ++s) mma_pair(a0[s], b0[s]);
+#pragma unroll
+      for (int s = 0; s < NK; ++s) mma_pair(a1[s], b1[s]);
+    }
+    if (tile < n_tiles) {
+      const uint16_t* p0 = in1 + tile * 16 * D + l16 * D + 8 * h;
+      const uint16_t* q0 = in2 + tile * 16 * D + l16 * D + 8 * h;
+      u32x4 a0[NK], b0[NK];
+#pragma unroll
+      for (int s = 0; s < NK; ++s) {
+        a0[s] = *reinterpret_cast<const u32x4*>(p0 + 32 * s);
+        b0[s] = *reinterpret_cast<const u32x4*>(q0 + 32 * s);
+      }
+#pragma unroll
+      for (int s = 0; s < NK; ++s) mma_pair(a0[s], b0[s]);
+    }
+  };
+  if (vec && d == 64) {
+    tile_pair(std::integral_constant<int, 2>{});
+  } else if (vec && d == 128) {
+    tile_pair(std::integral_constant<int, 4>{});
+  } else {
+    for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
+      const int64_t base = tile * 16 * d;
+      for (int ks = 0; ks < d / 16; ++ks) {
+        // A: row l16 of in1, K slots 16 ks + 4h + j; B: column l16 = row l16 of in2, same K.
+        const uint2 av = *reinterpret_cast<const uint2*>(in1 + base + l16 * d + 16 * ks + 4 * h);
+        const uint2 bv = *reinterpret_cast<const uint2*>(in2 + base + l16 * d + 16 * ks + 4 * h);
+        acc = Ty::mma16(u32x2{av.x, av.y}, u32x2{bv.x, bv.y}, acc);
+      }
     }
   }
   mfma_drain();
@@ -1144,10 +1193,13 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  const int32_t vec = ow::aligned16(in1) && ow::aligned16(in2) ? 1 : 0;  // 16-byte row loads
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::BF16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial, n_tiles, d);
+    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::BF16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial,
+                       n_tiles, d, vec);
   else
-    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::F16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial, n_tiles, d);
+    hipLaunchKernelGGL(ow::tile_outer_kernel<ow::F16>, dim3(n_waves / 4), dim3(256), 0, s, cu(in1), cu(in2), partial,
+                       n_tiles, d, vec);
   if (int rc = ow::hip_status(hipGetLastError(), "tile_outer_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
