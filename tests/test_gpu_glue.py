@@ -12,6 +12,7 @@ import torch
 
 import omniwave_amd
 from omniwave_amd.backbone import space_to_depth_nhwc
+from omniwave_amd.block import OmniWeaveBlock
 from omniwave_amd.hip import bigemm_block_hip, bigemm_block_s2d_hip, stem_hip, stem_is_supported
 from oracle.backbone import stem_reference
 
@@ -170,3 +171,40 @@ def test_model_fused_glue_graph_replays_match_eager() -> None:
             assert torch.equal(logits, eager), f"replay {k}"
             model(x[:2])  # eager work between replays
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("size", [64, 160])
+def test_model_fused_glue_other_sizes_and_dtypes(size, dtype) -> None:
+    """Other input resolutions (stage grids 16/8/4/2 and 40/20/10/5) and fp16: the inference
+    path against the reference composition on the same GPU (forward_features with autograd
+    on, which uses neither the stem kernel nor the space_to_depth output)."""
+    announce(f"omniweave_t fused glue input {size} dtype={dtype} B=2")
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t", input_size=size).eval()
+    with torch.no_grad():
+        for stage in model.stages:
+            for blk in stage.blocks:
+                blk.gamma.fill_(0.5)
+    model = model.to(device=DEV, dtype=dtype)
+    x = torch.randn(2, 3, size, size, generator=torch.Generator().manual_seed(5)).to(DEV, dtype)
+    with torch.no_grad():
+        got = model(x)
+    want = model.head(model.forward_features(x)["stage4"].mean(dim=(1, 2)))  # autograd on: reference glue
+    torch.cuda.synchronize()
+    rel = ((got.float() - want.float()).norm() / want.float().norm()).item()
+    print(f"input {size} {dtype}: rel-L2 {rel:.2e}", flush=True)
+    assert rel <= 1e-2, rel
+
+
+def test_block_s2d_falls_back_when_unsupported() -> None:
+    """fp32 activations and odd grids: forward_s2d returns None (the caller composes
+    space_to_depth); the backbone path then matches the reference composition."""
+    announce("block forward_s2d fallbacks")
+    blk = OmniWeaveBlock(height=14, width=14, dim=512, channel_tile=128, route="local", radix_level=0).to(DEV).eval()
+    x32 = torch.randn(1, 14, 14, 512, device=DEV)
+    with torch.no_grad():
+        assert blk.forward_s2d(x32, 2) is None
+        assert blk.to(torch.bfloat16).forward_s2d(x32.to(torch.bfloat16), 3) is None  # 14 % 3 != 0
+        y = blk.forward_s2d(x32.to(torch.bfloat16), 2)
+    assert y is not None and y.shape == (1, 7, 7, 2048)
