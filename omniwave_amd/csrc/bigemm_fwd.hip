@@ -177,6 +177,13 @@ __device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* 
 
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Waits until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // One workgroup: 4 waves x TPW token groups (TPW/2 pairs of 16 tokens per wave) x one channel
 // group q_c.
 template <class Ty, int D, int RD, int TPW, int OCC, bool F8>
@@ -198,11 +205,20 @@ bigemm_fwd_kernel(FwdArgs a) {
   constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, in 16-bit elements
   static_assert(TPW % 2 == 0, "token groups come in pairs");
   static_assert(CH_ELEMS <= ROWS * LDX, "a weight chunk must fit in the x-tile region");
+  // Weight-chunk copies per wave and chunk (every wave issues the same number).
+  constexpr int DPW = CH_UNITS / kWaves;
+  static_assert(CH_UNITS % kWaves == 0, "chunk copy units split evenly over the waves");
+  // Software-pipelined chunk loop (d = 128, bf16 / fp16 channel side, one pair per wave): chunk
+  // ec + 1's U'/V' MFMAs are issued before chunk ec's gate, so chunks ec and ec + 1 are resident
+  // while ec + 2 is copied — three chunk buffers.  (The d = 64 instance runs at 3 waves per SIMD,
+  // where the second set of U'/V' accumulators would spill.)
+  constexpr bool PIPE = !F8 && NP == 1 && NCH % 2 == 0 && D == 128;
+  constexpr int XS_ELEMS = (PIPE && 2 * CH_ELEMS > ROWS * LDX) ? 2 * CH_ELEMS : ROWS * LDX;
 
-  // LDS regions.  xs: the x tile until the token side has read it; then the odd weight
-  // chunks; after the chunk loop, each wave's W^T tile (its own 32 rows) and then delta.
-  // wb: the even weight chunks.
-  __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LDX];
+  // LDS regions.  xs: the x tile until the token side has read it; then weight chunks (PIPE:
+  // chunks 3k + 1 at xs and 3k + 2 at xs + CH_ELEMS; otherwise the odd chunks); after the
+  // chunk loop, each wave's rows of the output tile.  wb: chunks 3k (PIPE) or the even chunks.
+  __shared__ __attribute__((aligned(16))) uint16_t xs[XS_ELEMS];
   __shared__ __attribute__((aligned(16))) uint16_t wb[CH_ELEMS];
   __shared__ int32_t rowid[ROWS];   // b * n_tok + token, -1 for pad rows
   __shared__ int32_t rowout[ROWS];  // output row of each tile row, -1 for pad rows
@@ -215,7 +231,14 @@ bigemm_fwd_kernel(FwdArgs a) {
   const int qc = bid % a.q_c, chunk = bid / a.q_c;
 
   const uint16_t* wsrc = a.packed + HEAD + static_cast<size_t>(qc) * NCH * CH_ELEMS;
-  auto chunk_buf = [&](int ec) -> uint16_t* { return (ec & 1) ? xs : wb; };
+  auto chunk_buf = [&](int ec) -> uint16_t* {
+    if constexpr (PIPE) {
+      const int k = ec % 3;
+      return k == 0 ? wb : xs + (k - 1) * CH_ELEMS;
+    } else {
+      return (ec & 1) ? xs : wb;
+    }
+  };
   auto issue_chunk = [&](int ec) {
     const uint16_t* src = wsrc + static_cast<size_t>(ec) * CH_ELEMS;
     uint16_t* dst = chunk_buf(ec);
@@ -433,6 +456,59 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) W[p][mb][i] = 0.0f;
 
+  if constexpr (PIPE) {
+    auto uv = [&](int ec, f32x16& U, f32x16& V) {
+      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
+      U = f32x16{};
+      V = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[0][ks], U);
+        V = Ty::mma32(cf[(FR_U + ks) * (kFragElems / 8) + lane], Pv[0][ks], V);
+      }
+    };
+    auto gate_w = [&](int ec, const f32x16& U, const f32x16& V) {
+      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
+      u32x4 Z[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
+                              silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) W[0][mb] = Ty::mma32(Z[s], cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane], W[0][mb]);
+    };
+    // Step ec: wait for chunk ec + 1 (at ec = 0 chunk 2 may still be in flight: nothing else is
+    // outstanding during the loop, so the count is exact); the barrier also means every wave is
+    // done with chunk ec - 1, whose buffer then takes chunk ec + 2; chunk ec + 1's U'/V'
+    // products are issued, then chunk ec's gate and Z B_o run while they execute.
+    auto step = [&](int ec, f32x16& Uc, f32x16& Vc, f32x16& Un, f32x16& Vn) {
+      if (ec + 1 < NCH) {
+        if (ec == 0 && NCH > 2)
+          wait_vmcnt<DPW>();
+        else
+          wait_lds_dma();
+        __syncthreads();
+        if (ec >= 1 && ec + 2 < NCH) issue_chunk(ec + 2);
+        uv(ec + 1, Un, Vn);
+      }
+      gate_w(ec, Uc, Vc);
+    };
+    wait_lds_dma();
+    __syncthreads();
+    if (NCH > 1) issue_chunk(1);
+    if (NCH > 2) issue_chunk(2);
+    f32x16 Ua, Va, Ub, Vb;
+    uv(0, Ua, Va);
+#pragma unroll
+    for (int ec = 0; ec < NCH; ec += 2) {
+      step(ec, Ua, Va, Ub, Vb);
+      step(ec + 1, Ub, Vb, Ua, Va);
+    }
+  } else
   for (int ec = 0; ec < NCH; ++ec) {
     wait_lds_dma();
     // Chunk ec has landed; every wave is done with chunk ec - 1 (and, at ec = 0, with the x
