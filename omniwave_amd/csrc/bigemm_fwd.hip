@@ -208,11 +208,11 @@ bigemm_fwd_kernel(FwdArgs a) {
   // Weight-chunk copies per wave and chunk (every wave issues the same number).
   constexpr int DPW = CH_UNITS / kWaves;
   static_assert(CH_UNITS % kWaves == 0, "chunk copy units split evenly over the waves");
-  // Software-pipelined chunk loop (d = 128, bf16 / fp16 channel side, one pair per wave): chunk
+  // Software-pipelined chunk loop (d = 128, one pair per wave): chunk
   // ec + 1's U'/V' MFMAs are issued before chunk ec's gate, so chunks ec and ec + 1 are resident
   // while ec + 2 is copied — three chunk buffers.  (The d = 64 instance runs at 3 waves per SIMD,
   // where the second set of U'/V' accumulators would spill.)
-  constexpr bool PIPE = !F8 && NP == 1 && NCH % 2 == 0 && D == 128;
+  constexpr bool PIPE = NP == 1 && NCH % 2 == 0 && D == 128;
   constexpr int XS_ELEMS = (PIPE && 2 * CH_ELEMS > ROWS * LDX) ? 2 * CH_ELEMS : ROWS * LDX;
 
   // LDS regions.  xs: the x tile until the token side has read it; then weight chunks (PIPE:
@@ -457,29 +457,45 @@ bigemm_fwd_kernel(FwdArgs a) {
       for (int i = 0; i < 16; ++i) W[p][mb][i] = 0.0f;
 
   if constexpr (PIPE) {
+    // U'/V' of chunk ec (fp8: e4m3 fragments and P operands, dequantised in the gate).
     auto uv = [&](int ec, f32x16& U, f32x16& V) {
-      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
       U = f32x16{};
       V = f32x16{};
+      if constexpr (F8) {
+        const u32x2* c8 = reinterpret_cast<const u32x2*>(chunk_buf(ec));
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[0][ks], U);
-        V = Ty::mma32(cf[(FR_U + ks) * (kFragElems / 8) + lane], Pv[0][ks], V);
+        for (int ks = 0; ks < KS; ++ks) {
+          U = mma32_f8(c8[ks * (kF8FragBytes / 8) + lane], Pu[0][ks], U);
+          V = mma32_f8(c8[(FR_U + ks) * (kF8FragBytes / 8) + lane], Pv[0][ks], V);
+        }
+      } else {
+        const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[0][ks], U);
+          V = Ty::mma32(cf[(FR_U + ks) * (kFragElems / 8) + lane], Pv[0][ks], V);
+        }
       }
     };
+    // Gate and W += Z B_o of chunk ec.
     auto gate_w = [&](int ec, const f32x16& U, const f32x16& V) {
-      const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
+      const uint16_t* cw = chunk_buf(ec);
+      const u32x4* co = reinterpret_cast<const u32x4*>(F8 ? cw + FR_U * kFragElems : cw + 2 * FR_U * kFragElems);
+      const float du = F8 ? f8s[kF8DeqU] : 1.0f, dv = F8 ? f8s[kF8DeqV] : 1.0f;
       u32x4 Z[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
-                              silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
+        for (int q = 0; q < 4; ++q) {
+          const float u0 = U[8 * s + 2 * q], u1 = U[8 * s + 2 * q + 1];
+          const float v0 = V[8 * s + 2 * q], v1 = V[8 * s + 2 * q + 1];
+          Z[s][q] = F8 ? Ty::pack2(silu_gate(u0 * du, v0 * dv), silu_gate(u1 * du, v1 * dv))
+                       : Ty::pack2(silu_gate(u0, v0), silu_gate(u1, v1));
+        }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) W[0][mb] = Ty::mma32(Z[s], cf[(2 * FR_U + 2 * mb + s) * (kFragElems / 8) + lane], W[0][mb]);
+        for (int s = 0; s < 2; ++s) W[0][mb] = Ty::mma32(Z[s], co[(2 * mb + s) * (kFragElems / 8) + lane], W[0][mb]);
     };
     // Step ec: wait for chunk ec + 1 (at ec = 0 chunk 2 may still be in flight: nothing else is
     // outstanding during the loop, so the count is exact); the barrier also means every wave is
