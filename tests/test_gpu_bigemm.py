@@ -1,6 +1,6 @@
 """GPU parity of the HIP forward against the oracle (run with ``-m gpu`` on a gfx950 GPU).
 
-Tolerances (north-star gates, rel-L2 on the BiGEMM delta, which LayerScale 1e-5 would
+Tolerances (the operator's parity gates, rel-L2 on the BiGEMM delta, which LayerScale 1e-5 would
 otherwise make vacuous): bf16 <= 1e-2, fp16 <= 5e-3.  The oracle runs on the CPU in fp32 on
 the same inputs, with the weights rounded to the kernel's compute dtype.
 """
