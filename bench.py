@@ -340,8 +340,36 @@ def backward_section(batch: int, steps: int, dev) -> dict:
             "bwd_ms": round(total_ms - fwd_ms, 3),
             "fwd_bwd_tflops": round(3 * flops / (total_ms * 1e-3) / 1e12, 1),
         }
-    return {"workload": f"fused block fwd+bwd, batch {batch}, bf16, eager launches", "flops_rule": "3 x forward",
-            "cases": out}
+        out[f"{name}_shifted0"].update(_graph_fwd_bwd(fwd_bwd, [x, nw, *params.values()], steps, flops))
+    return {"workload": f"fused block fwd+bwd, batch {batch}, bf16, eager launches; also replayed from one HIP graph "
+                        "(every replay's gradients checked against the eager ones)",
+            "flops_rule": "3 x forward", "cases": out}
+
+
+def _graph_fwd_bwd(fwd_bwd, leaves, steps: int, flops: int) -> dict:
+    """fwd_bwd captured in one HIP graph: ms per replay, and the largest difference of any
+    replay's gradients from the eager gradients (replays interleaved with eager work)."""
+    fwd_bwd()
+    torch.cuda.synchronize()
+    want = [t.grad.detach().clone() for t in leaves]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fwd_bwd()
+        torch.cuda.current_stream().synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            fwd_bwd()
+    torch.cuda.current_stream().wait_stream(stream)
+    diff = 0.0
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        diff = max(diff, max((t.grad.float() - w.float()).abs().max().item() for t, w in zip(leaves, want)))
+        torch.cuda.synchronize()
+    ms = _time_fn(graph.replay, steps)
+    return {"fwd_bwd_graph_ms": round(ms, 3), "fwd_bwd_graph_tflops": round(3 * flops / (ms * 1e-3) / 1e12, 1),
+            "graph_replay_grad_max_abs_diff": diff}
 
 
 def _time_fn(fn, steps: int) -> float:
