@@ -477,11 +477,13 @@ bigemm_fwd_kernel(FwdArgs a) {
         }
       }
     };
-    // Gate and W += Z B_o of chunk ec.
+    // Gate and W += Z B_o of chunk ec.  The fp8 dequantisation factors are read once, before
+    // the loop: a global load inside it would make the waits for the chunk copies (which count
+    // all outstanding vector-memory operations) wait for the copy of chunk ec + 2 as well.
+    const float du = F8 ? f8s[kF8DeqU] : 1.0f, dv = F8 ? f8s[kF8DeqV] : 1.0f;
     auto gate_w = [&](int ec, const f32x16& U, const f32x16& V) {
       const uint16_t* cw = chunk_buf(ec);
       const u32x4* co = reinterpret_cast<const u32x4*>(F8 ? cw + FR_U * kFragElems : cw + 2 * FR_U * kFragElems);
-      const float du = F8 ? f8s[kF8DeqU] : 1.0f, dv = F8 ? f8s[kF8DeqV] : 1.0f;
       u32x4 Z[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s)
