@@ -15,6 +15,7 @@ oracle (the reference backend's algorithm, fp32, PyTorch on the host CPU) on a b
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -88,15 +89,21 @@ def make_inputs(batch, h, w, c, d, route, level, dev, seed):
 
 
 def time_graph(graph, replays: int) -> float:
-    """Average ms per replay, HIP events on the current stream."""
+    """Average ms per replay, HIP events on the current stream; the garbage collector is paused
+    while the replays are issued (see _time_fn)."""
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    gc.collect()
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    stop.record()
-    stop.synchronize()
+    gc.disable()
+    try:
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        stop.record()
+        stop.synchronize()
+    finally:
+        gc.enable()
     return start.elapsed_time(stop) / replays
 
 
@@ -308,29 +315,35 @@ def _graph_ms(fn, per_graph: int, replays: int) -> float:
     return time_graph(graph, replays) / per_graph
 
 
+def _block_fwd_bwd(batch: int, h: int, w: int, c: int, d: int, dev):
+    """One fused block case with trainable leaves: (forward, forward+backward, leaves)."""
+    from omniwave_amd.hip import bigemm_block_hip
+
+    plan, x, p, nw = make_inputs(batch, h, w, c, d, "shifted", 0, dev, seed=100)
+    x.requires_grad_(True)
+    params = {k: v.clone().requires_grad_(True) for k, v in p.items()}
+    nw = nw.clone().requires_grad_(True)
+    dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).to(dev, torch.bfloat16)
+
+    def fwd():
+        return bigemm_block_hip(x, nw, plan, **params)
+
+    def fwd_bwd():  # gradients start from None each step, as after zero_grad(set_to_none=True)
+        x.grad = nw.grad = None
+        for t in params.values():
+            t.grad = None
+        y = fwd()
+        y.backward(dy)
+
+    return fwd, fwd_bwd, [x, nw, *params.values()]
+
+
 def backward_section(batch: int, steps: int, dev) -> dict:
     """Fused block forward + backward (dx, dA, dB, dgamma, dnorm_weight) at the 56x56x128 and
     14x14x512 stage shapes, shifted route, bf16, upstream gradient N(0,1)."""
-    from omniwave_amd.hip import bigemm_block_hip
-
-    out = {}
+    out, graphed = {}, []
     for (name, h, w, c, d) in (STAGES[0], STAGES[2]):
-        plan, x, p, nw = make_inputs(batch, h, w, c, d, "shifted", 0, dev, seed=100)
-        x.requires_grad_(True)
-        params = {k: v.clone().requires_grad_(True) for k, v in p.items()}
-        nw = nw.clone().requires_grad_(True)
-        dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).to(dev, torch.bfloat16)
-
-        def fwd():
-            return bigemm_block_hip(x, nw, plan, **params)
-
-        def fwd_bwd():  # gradients start from None each step, as after zero_grad(set_to_none=True)
-            x.grad = nw.grad = None
-            for t in params.values():
-                t.grad = None
-            y = fwd()
-            y.backward(dy)
-
+        fwd, fwd_bwd, leaves = _block_fwd_bwd(batch, h, w, c, d, dev)
         with torch.no_grad():
             fwd_ms = _time_fn(fwd, steps)
         total_ms = _time_fn(fwd_bwd, steps)
@@ -340,15 +353,47 @@ def backward_section(batch: int, steps: int, dev) -> dict:
             "bwd_ms": round(total_ms - fwd_ms, 3),
             "fwd_bwd_tflops": round(3 * flops / (total_ms * 1e-3) / 1e12, 1),
         }
-        out[f"{name}_shifted0"].update(_graph_fwd_bwd(fwd_bwd, [x, nw, *params.values()], steps, flops))
+        graphed.append((name, fwd_bwd, leaves, flops))
+    # The graphs are captured after every eager timing, so no eager number follows a capture.
+    for (name, fwd_bwd, leaves, flops) in graphed:
+        out[f"{name}_shifted0"].update(_graph_fwd_bwd(fwd_bwd, leaves, steps, flops))
     return {"workload": f"fused block fwd+bwd, batch {batch}, bf16, eager launches; also replayed from one HIP graph "
                         "(every replay's gradients checked against the eager ones)",
             "flops_rule": "3 x forward", "cases": out}
 
 
+_KEEP_GRAPHS = []
+
+
+def _init_graph_state(dev) -> None:
+    """Capture one trivial graph outside inference mode before any other capture, and keep it
+    for the life of the process.  PyTorch creates the CUDA generator's graph-capture state when
+    a graph is registered while none is alive; state created inside inference_mode cannot be
+    updated by a later capture outside it (the graph-replayed backward), so one graph made here
+    stays alive and every later capture reuses its state."""
+    graph = torch.cuda.CUDAGraph()
+    _KEEP_GRAPHS.append(graph)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        t = torch.zeros(1, device=dev)
+        with torch.cuda.graph(graph, stream=stream):
+            t.add_(1)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+
+
 def _graph_fwd_bwd(fwd_bwd, leaves, steps: int, flops: int) -> dict:
     """fwd_bwd captured in one HIP graph: ms per replay, and the largest difference of any
-    replay's gradients from the eager gradients (replays interleaved with eager work)."""
+    replay's gradients from the eager gradients (replays interleaved with eager work).  A
+    capture failure is reported in the result rather than raised."""
+    try:
+        return _graph_fwd_bwd_run(fwd_bwd, leaves, steps, flops)
+    except RuntimeError as err:
+        return {"fwd_bwd_graph_ms": None, "graph_error": str(err)[:200]}
+
+
+def _graph_fwd_bwd_run(fwd_bwd, leaves, steps: int, flops: int) -> dict:
     fwd_bwd()
     torch.cuda.synchronize()
     want = [t.grad.detach().clone() for t in leaves]
@@ -374,17 +419,25 @@ def _graph_fwd_bwd(fwd_bwd, leaves, steps: int, flops: int) -> dict:
 
 def _time_fn(fn, steps: int) -> float:
     """Average ms per call over `steps` calls after two warm-up calls (the second one runs the
-    paths the first one set up, e.g. gradient accumulation), HIP events on the current stream."""
+    paths the first one set up, e.g. gradient accumulation), HIP events on the current stream.
+    Python's cyclic garbage collector is run before and paused during the timed calls, as
+    timeit does: one full collection over the objects the earlier sections left (~270K) takes
+    tens of ms and, landing in a short timed window, was measured as a tenfold slower call."""
     fn()
     fn()
+    gc.collect()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        fn()
-    stop.record()
-    stop.synchronize()
+    gc.disable()
+    try:
+        start.record()
+        for _ in range(steps):
+            fn()
+        stop.record()
+        stop.synchronize()
+    finally:
+        gc.enable()
     return start.elapsed_time(stop) / steps
 
 
@@ -465,6 +518,7 @@ def main() -> int:
         raise RuntimeError(_native.load_error())
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    _init_graph_state(dev)
     if args.section == "model":
         print(json.dumps({"model": model_section(args.model_batch, args.steps, dev)}), flush=True)
         return 0
@@ -535,14 +589,17 @@ def main() -> int:
 
         for _ in range(args.warmup):
             step()
+        gc.collect()
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
+        gc.disable()
         start.record()
         for _ in range(args.steps):
             step()
         stop.record()
         torch.cuda.synchronize()
+        gc.enable()
         ms_per_step = start.elapsed_time(stop) / args.steps
 
     total_flops = sum(cs["flops"] for cs in cases)
