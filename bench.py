@@ -89,21 +89,15 @@ def make_inputs(batch, h, w, c, d, route, level, dev, seed):
 
 
 def time_graph(graph, replays: int) -> float:
-    """Average ms per replay, HIP events on the current stream; the garbage collector is paused
-    while the replays are issued (see _time_fn)."""
+    """Average ms per replay, HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    gc.collect()
     torch.cuda.synchronize()
-    gc.disable()
-    try:
-        start.record()
-        for _ in range(replays):
-            graph.replay()
-        stop.record()
-        stop.synchronize()
-    finally:
-        gc.enable()
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    stop.synchronize()
     return start.elapsed_time(stop) / replays
 
 
@@ -419,25 +413,17 @@ def _graph_fwd_bwd_run(fwd_bwd, leaves, steps: int, flops: int) -> dict:
 
 def _time_fn(fn, steps: int) -> float:
     """Average ms per call over `steps` calls after two warm-up calls (the second one runs the
-    paths the first one set up, e.g. gradient accumulation), HIP events on the current stream.
-    Python's cyclic garbage collector is run before and paused during the timed calls, as
-    timeit does: one full collection over the objects the earlier sections left (~270K) takes
-    tens of ms and, landing in a short timed window, was measured as a tenfold slower call."""
+    paths the first one set up, e.g. gradient accumulation), HIP events on the current stream."""
     fn()
     fn()
-    gc.collect()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    gc.disable()
-    try:
-        start.record()
-        for _ in range(steps):
-            fn()
-        stop.record()
-        stop.synchronize()
-    finally:
-        gc.enable()
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    stop.synchronize()
     return start.elapsed_time(stop) / steps
 
 
@@ -519,6 +505,13 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _init_graph_state(dev)
+    # Python's cyclic garbage collector stays off for the run and is called explicitly between
+    # sections, ahead of their warm-ups: a full collection over the ~270K objects the earlier
+    # sections leave takes tens of ms, and one landing inside a short timed window was measured
+    # as a tenfold slower call; one placed between warm-up and timing idles the GPU long enough
+    # to drop its clocks (~8% slower kernels in the following timed replays).
+    gc.collect()
+    gc.disable()
     if args.section == "model":
         print(json.dumps({"model": model_section(args.model_batch, args.steps, dev)}), flush=True)
         return 0
@@ -589,17 +582,14 @@ def main() -> int:
 
         for _ in range(args.warmup):
             step()
-        gc.collect()
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
-        gc.disable()
         start.record()
         for _ in range(args.steps):
             step()
         stop.record()
         torch.cuda.synchronize()
-        gc.enable()
         ms_per_step = start.elapsed_time(stop) / args.steps
 
     total_flops = sum(cs["flops"] for cs in cases)
@@ -624,9 +614,13 @@ def main() -> int:
         "kernel": dom["kernel"], "case": dom["name"],
         "algorithmic_flops": dom["flops"], "algorithmic_bytes": dom["bytes"],
     }
+    gc.collect()
     model = None if args.no_model else model_section(args.model_batch, 10, dev)
+    gc.collect()
     backward = None if args.no_backward else backward_section(args.batch, 10, dev)
+    gc.collect()
     fp8 = None if args.no_fp8 else fp8_section(args.model_batch, 10, dev)
+    gc.collect()
     baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
     line = {
         "metric": "BiGEMM fwd TFLOP/s (fused RMSNorm+residual, 4 OmniWeave-T stage shapes x 3 routes)",
