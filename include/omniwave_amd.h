@@ -192,6 +192,25 @@ int ow_bigemm_fwd_rows(const void* x, void* out, float eps,
                        int32_t flags, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ow_bigemm_fwd / ow_bigemm_fwd_rows (out_rows may be NULL) for consecutive blocks of a stage
+ * (omniweave/models/backbone.py:75-80, each block's RMSNorm at omniweave/models/block.py:83-84
+ * reading the previous block's output).  With stats_out non-NULL ([batch*H*W, Q_c] floats)
+ * the launch may also write, per output row and channel group, the sum of squares of the
+ * stored values of the group's columns; *stats_written (host) says whether it did (bf16 /
+ * f16, contiguous channel groups, the streamed d = 128 kernel, out_rows NULL).  Passing those
+ * sums to the next block as stats_in (stats_in_parts = that block's predecessor's Q_c) gives
+ * it its RMSNorm statistics without reading whole rows; the result equals ow_bigemm_fwd's up
+ * to the summation order of the mean of squares.  Needs OW_FUSE_NORM with stats_in; bf16 /
+ * f16 activations only.
+ */
+int ow_bigemm_fwd_chain(const void* x, void* out, float eps,
+                        const void* packed, size_t packed_bytes,
+                        const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
+                        const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
+                        const float* stats_in, int32_t stats_in_parts, float* stats_out,
+                        int32_t* stats_written, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Backbone stem as one gather-GEMM (omniweave/models/backbone.py:121,173-176): image
  * [batch, 3, height, width] (NCHW) -> space_to_depth(4) -> x W^T with weight [n_out, 48]
  * (nn.Linear(48, n_out, bias=False), input order (row offset, column offset, channel)) ->

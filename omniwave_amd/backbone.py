@@ -54,11 +54,29 @@ class _Stage(nn.Module):
 
     def forward_blocks_s2d(self, x: Tensor, factor: int) -> Tensor:
         """``space_to_depth`` of the blocks' output (the anchor is the caller's); the last block
-        writes that layout itself when it can (``OmniWeaveBlock.forward_s2d``)."""
-        for block in self.blocks[:-1]:
-            x = block(x)
+        writes that layout itself when it can, and each block hands the next its RMSNorm
+        statistics when it can (``OmniWeaveBlock.forward_chain``)."""
+        x, stats = self._chain(self.blocks[:-1], x)
+        r = self.blocks[-1].forward_chain(x, stats, factor)
+        if r is not None:
+            return r[0]
         y = self.blocks[-1].forward_s2d(x, factor)
         return y if y is not None else space_to_depth_nhwc(self.blocks[-1](x), factor)
+
+    def forward_blocks(self, x: Tensor) -> Tensor:
+        """The blocks (the anchor is the caller's), chained as in ``forward_blocks_s2d``."""
+        return self._chain(self.blocks, x)[0]
+
+    @staticmethod
+    def _chain(blocks, x: Tensor) -> tuple[Tensor, Tensor | None]:
+        stats = None
+        for block in blocks:
+            r = block.forward_chain(x, stats)
+            if r is None:
+                x, stats = block(x), None
+            else:
+                x, stats = r
+        return x, stats
 
 
 class OmniWeaveBackbone(nn.Module):
@@ -171,6 +189,5 @@ class OmniWeaveBackbone(nn.Module):
             if i < 3:
                 x = stage.forward_blocks_s2d(x, 2)
             else:
-                for block in stage.blocks:
-                    x = block(x)
+                x = stage.forward_blocks(x)
         return self.head(x.mean(dim=(1, 2)))

@@ -15,7 +15,7 @@ import torch.nn as nn
 from torch import Tensor
 
 from omniwave_amd.bigemm import bigemm
-from omniwave_amd.hip import bigemm_block_hip, bigemm_block_s2d_hip, hip_is_supported
+from omniwave_amd.hip import bigemm_block_chain_hip, bigemm_block_hip, bigemm_block_s2d_hip, hip_is_supported
 from omniwave_amd.routing import RoutePlan, build_route_plan
 
 RMS_EPS = 1e-6  # omniweave/models/block.py:84
@@ -100,6 +100,21 @@ class OmniWeaveBlock(nn.Module):
         params = (self.a_u, self.a_v, self.a_o, self.b_u, self.b_v, self.b_o, self.gamma)
         return bigemm_block_s2d_hip(x, self.norm_weight, self.plan, *params, factor=factor, eps=RMS_EPS,
                                     fp8=self.fp8)
+
+    def forward_chain(self, x: Tensor, stats: Tensor | None, factor: int = 0) -> tuple[Tensor, Tensor | None] | None:
+        """``self(x)`` (factor 0) or ``forward_s2d(x, factor)`` for a block of a stage's chain
+        (inference): returns ``(y, stats)``, ``stats`` being the RMSNorm statistics of ``y`` for
+        the next block (or None), given ``stats`` of ``x`` from the previous block; ``None``
+        when the chained hip path does not apply and the caller uses the plain calls."""
+        if torch.is_grad_enabled() or (self.training and (self.drop_path_rate > 0 or self.fp8)):
+            return None
+        if x.dtype not in (torch.bfloat16, torch.float16) or not self._fused(x):
+            return None
+        if factor and (x.shape[1] % factor or x.shape[2] % factor):
+            return None
+        params = (self.a_u, self.a_v, self.a_o, self.b_u, self.b_v, self.b_o, self.gamma)
+        return bigemm_block_chain_hip(x, stats, self.norm_weight, self.plan, *params, factor=factor, eps=RMS_EPS,
+                                      fp8=self.fp8)
 
     def forward(self, x: Tensor) -> Tensor:
         """``x``: ``[B, H, W, C]`` -> ``[B, H, W, C]``."""

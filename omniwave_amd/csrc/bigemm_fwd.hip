@@ -113,8 +113,10 @@ struct FwdArgs {
   int32_t residual;  // write x + delta instead of delta
   int32_t mode;      // channel-group access, one of the kMode* values
   int32_t stride;    // kModeStrided: channel stride n of a group (= q_c)
-  int32_t norm;      // RMSNorm row scales: kNormNone, kNormBuffer (row_scale) or kNormInline
-  float eps;         // kNormInline: RMSNorm epsilon
+  int32_t norm;      // RMSNorm row scales: one of the kNorm* values
+  float eps;         // kNormInline / kNormPartials: RMSNorm epsilon
+  int32_t parts;     // kNormPartials: partial sums per row in row_scale ([batch * n_tok, parts])
+  float* stats_out;  // NULL, or [batch * n_tok, q_c]: sum of squares of each stored row's group columns
 };
 
 // Where the RMSNorm row scales come from.
@@ -122,9 +124,13 @@ struct FwdArgs {
 //   kNormInline  the tile load reads whole rows (C / 8 16-byte vectors, 16 lanes per row) and
 //                sums the squares itself; the other channel groups' workgroups of the same
 //                tokens read the same rows, mostly from L2 (they run on the same XCD)
+//   kNormPartials row_scale holds `parts` partial sums of squares per row, written by the
+//                previous block's launch (stats_out); the tile load reads only the group's
+//                columns
 constexpr int kNormNone = 0;
 constexpr int kNormBuffer = 1;
 constexpr int kNormInline = 2;
+constexpr int kNormPartials = 3;
 
 // Channel-group access modes.
 //   kModeContig   group qc is columns [qc*d, qc*d + d): 16-byte row vectors (radix level 0)
@@ -279,6 +285,13 @@ bigemm_fwd_kernel(FwdArgs a) {
   if (tid < ROWS && a.norm == kNormBuffer) {
     const int64_t id = rowid[tid];
     if (id >= 0) my_rsc = a.row_scale[id];
+  } else if (tid < ROWS && a.norm == kNormPartials) {
+    const int64_t id = rowid[tid];
+    if (id >= 0) {
+      float acc = 0.0f;
+      for (int q = 0; q < a.parts; ++q) acc += a.row_scale[id * a.parts + q];
+      my_rsc = rms_scale<Ty>(acc / static_cast<float>(a.channels), a.eps);
+    }
   }
   // Whole rows, 16 lanes per row: lane l16 reads vectors l16 + 16 j (j < J = C / 128) of its
   // row, sums their squares for the row scale and keeps this group's tile columns: with M = 0
@@ -609,6 +622,20 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int q = 0; q < VPL; ++q)
             val[k][q] = *reinterpret_cast<const Elt*>(&xs[r * LDX + (sub + q * LPR) * M]);
+        }
+        if constexpr (M == 8) {
+          // Sum of squares of the stored values of each row's group columns: the next block's
+          // RMSNorm statistics (kNormPartials).  Contiguous groups only: 16 lanes per row.
+          if (a.stats_out) {
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+              float acc = 0.0f;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(val[k][0][e], acc);
+              acc = group_sum<LPR>(acc);
+              if (sub == 0 && ids[k] >= 0) a.stats_out[static_cast<int64_t>(ids[k]) * a.q_c + qc] = acc;
+            }
+          }
         }
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
@@ -1054,7 +1081,9 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
 static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
                             const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
                             const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+                            const float* stats_in, int32_t stats_in_parts, float* stats_out,
+                            int32_t* stats_written, void* workspace, size_t workspace_bytes, void* stream) {
+  if (stats_written) *stats_written = 0;
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
@@ -1145,12 +1174,17 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   } else {
     a.mode = ow::kModeElement;
   }
-  // RMSNorm row scales: read with the tile when whole rows are 16 lanes x 1, 2, 4 or 8 vectors,
-  // otherwise from a statistics pass into the workspace.
+  // RMSNorm row scales: from the previous launch's partial sums when given, read with the tile
+  // when whole rows are 16 lanes x 1, 2, 4 or 8 vectors, otherwise from a statistics pass into
+  // the workspace.
   a.norm = ow::kNormNone;
   if (flags & OW_FUSE_NORM) {
     const int32_t j = c / 128;
-    if (a.mode != ow::kModeElement && c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8)) {
+    if (stats_in && a.mode != ow::kModeElement) {
+      a.norm = ow::kNormPartials;
+      a.row_scale = stats_in;
+      a.parts = stats_in_parts;
+    } else if (a.mode != ow::kModeElement && c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8)) {
       a.norm = ow::kNormInline;
     } else {
       float* scale = static_cast<float*>(workspace);
@@ -1158,6 +1192,10 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
       a.norm = ow::kNormBuffer;
       a.row_scale = scale;
     }
+  }
+  if (stats_out && a.mode == ow::kModeContig && !out_rows) {
+    a.stats_out = stats_out;
+    if (stats_written) *stats_written = 1;
   }
   int rc;
   if (fp8)
@@ -1173,7 +1211,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
                   const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan, int32_t batch,
                   int32_t rd, int32_t dtype, int32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, nullptr, plan, batch, rd,
-                          dtype, flags, workspace, workspace_bytes, stream);
+                          dtype, flags, nullptr, 0, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 int ow_bigemm_fwd_rows(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
@@ -1182,7 +1220,23 @@ int ow_bigemm_fwd_rows(const void* x, void* out, float eps, const void* packed, 
                        size_t workspace_bytes, void* stream) {
   OW_CHECK_ARG(out_rows, "out_rows is NULL");
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
-                          dtype, flags, workspace, workspace_bytes, stream);
+                          dtype, flags, nullptr, 0, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+int ow_bigemm_fwd_chain(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                        const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
+                        const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
+                        const float* stats_in, int32_t stats_in_parts, float* stats_out, int32_t* stats_written,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  OW_CHECK_ARG(stats_written, "stats_written is NULL");
+  *stats_written = 0;
+  OW_CHECK_SUPPORTED(dtype != OW_DTYPE_F32, "row statistics between launches need bf16 or f16 activations");
+  OW_CHECK_ARG(!stats_in || (stats_in_parts >= 1 && stats_in_parts <= 64),
+               "stats_in_parts must be in [1, 64] (got %d)", stats_in_parts);
+  OW_CHECK_ARG(!stats_in || (flags & OW_FUSE_NORM), "stats_in without OW_FUSE_NORM");
+  return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
+                          dtype, flags, stats_in, stats_in_parts, stats_out, stats_written, workspace,
+                          workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -347,6 +347,103 @@ def bigemm_block_s2d_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gam
                           int(factor))
 
 
+@torch.library.custom_op("omniwave_amd::bigemm_fwd_chain", mutates_args=())
+def bigemm_fwd_chain(
+    x: Tensor,
+    norm_weight: Tensor,
+    gamma: Tensor,
+    a_u: Tensor,
+    a_v: Tensor,
+    a_o: Tensor,
+    b_u: Tensor,
+    b_v: Tensor,
+    b_o: Tensor,
+    plan_desc: list[int],
+    flags: int,
+    eps: float,
+    stats_in: Tensor | None,
+    factor: int,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """One block of a stage's chain (``ow_bigemm_fwd_chain``), inference only: ``out`` as
+    ``bigemm_fwd`` (factor 0) or ``bigemm_fwd_s2d`` (factor > 0); ``stats`` ([B*H*W, Q_c] fp32,
+    [0, Q_c] with factor > 0): per output row and channel group, the sum of squares of the
+    stored values, valid when ``written`` (a CPU int32 [1]) is 1; ``stats_in``: the previous
+    block's ``stats`` (its RMSNorm statistics, so the launch reads only its groups' columns)."""
+    plan = _plan_from_desc(plan_desc)
+    x = x.contiguous()
+    b, h, w, c = x.shape
+    fp8 = bool(flags & _native.OW_FUSE_FP8)
+    packed = _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan, fp8)
+    tok, ch = device_tables(plan, x.device)
+    q_c = ch.numel() // plan.channel_tile
+    if factor > 0:
+        if h % factor or w % factor:
+            raise ValueError(f"height {h} and width {w} must be divisible by factor {factor}")
+        rows = s2d_rows_table(plan, factor, x.device).data_ptr()
+        out = torch.empty((b, h // factor, w // factor, c * factor * factor), dtype=x.dtype, device=x.device)
+        stats = torch.empty((0, q_c), dtype=torch.float32, device=x.device)
+    else:
+        rows = None
+        out = torch.empty_like(x)
+        stats = torch.empty((b * h * w, q_c), dtype=torch.float32, device=x.device)
+    parts = 0
+    if stats_in is not None:
+        if stats_in.dtype != torch.float32 or stats_in.dim() != 2 or stats_in.shape[0] != b * h * w:
+            raise ValueError(f"stats_in must be float32 [{b * h * w}, parts], got {stats_in.dtype} "
+                             f"{tuple(stats_in.shape)}")
+        stats_in = stats_in.contiguous()
+        parts = stats_in.shape[1]
+    native_plan = plan.native()
+    lib = _native.lib()
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), b, flags)
+    workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
+    written = ctypes.c_int32(0)
+    with torch.cuda.device(x.device):
+        _native.check(
+            lib.ow_bigemm_fwd_chain(
+                x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
+                tok.data_ptr(), ch.data_ptr(), rows, ctypes.byref(native_plan), b, b_u.shape[2],
+                _DTYPE_CODE[x.dtype], flags, None if stats_in is None else stats_in.data_ptr(), parts,
+                stats.data_ptr() if stats.numel() else None, ctypes.byref(written),
+                workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
+            ),
+            "ow_bigemm_fwd_chain",
+        )
+    return out, stats, torch.tensor([written.value], dtype=torch.int32)
+
+
+@bigemm_fwd_chain.register_fake
+def _bigemm_fwd_chain_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, stats_in,
+                           factor):
+    b, h, w, c = x.shape
+    q_c = -(-plan_desc[2] // plan_desc[4])
+    if factor > 0:
+        out = x.new_empty((b, h // factor, w // factor, c * factor * factor))
+        stats = x.new_empty((0, q_c), dtype=torch.float32)
+    else:
+        out = x.new_empty(x.shape)
+        stats = x.new_empty((b * h * w, q_c), dtype=torch.float32)
+    return out, stats, torch.empty((1,), dtype=torch.int32)
+
+
+def bigemm_block_chain_hip(x, stats_in, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, factor: int = 0,
+                           eps: float = 1e-6, fp8: bool = False) -> tuple[Tensor, Tensor | None]:
+    """``bigemm_block_hip`` (factor 0) or ``bigemm_block_s2d_hip`` (factor > 0) for consecutive
+    blocks of a stage (omniweave/models/backbone.py:75-80): returns ``(out, stats)``, where
+    ``stats`` is the next block's ``stats_in`` (its RMSNorm statistics) or None when this
+    launch wrote none.  The output equals the unchained call's up to the summation order of the
+    RMSNorm mean of squares.  bf16 / fp16 activations, inference only."""
+    _require(x, plan, b_u)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"hip backend not supported: chained blocks take bf16 or fp16, not {x.dtype}")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, norm_weight, gamma, a_u, b_u)):
+        raise RuntimeError("bigemm_block_chain_hip is inference-only (no backward); run it under torch.no_grad()")
+    flags = _native.OW_FUSE_NORM | _native.OW_FUSE_RESIDUAL | (_native.OW_FUSE_FP8 if fp8 else 0)
+    out, stats, written = bigemm_fwd_chain(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan),
+                                           flags, float(eps), stats_in, int(factor))
+    return out, (stats if int(written[0]) else None)
+
+
 STEM_CHANNELS = (32, 64, 96, 128, 192, 256)
 
 

@@ -13,7 +13,8 @@ import torch
 import omniwave_amd
 from omniwave_amd.backbone import space_to_depth_nhwc
 from omniwave_amd.block import OmniWeaveBlock
-from omniwave_amd.hip import bigemm_block_hip, bigemm_block_s2d_hip, stem_hip, stem_is_supported
+from omniwave_amd.hip import (bigemm_block_chain_hip, bigemm_block_hip, bigemm_block_s2d_hip, stem_hip,
+                              stem_is_supported)
 from oracle.backbone import stem_reference
 
 pytestmark = pytest.mark.gpu
@@ -133,13 +134,15 @@ def test_model_fused_glue_matches_forward_features(fp8) -> None:
             h = stage.forward_blocks_s2d(h, 2) if i < 3 else stage.blocks[1](stage.blocks[0](h))
         unfolded = model.head(h.mean(dim=(1, 2)))
     torch.cuda.synchronize()
-    # Stages 1-2 and the space_to_depth layout are exact (checked per block above); folding
-    # the anchor into the downsample changes one bf16 rounding of the stage-3/4 entry.
+    # Stages 1-2 and the space_to_depth layout are exact (checked per block above); in stages
+    # 3-4 each block after the first takes its RMSNorm statistics from its predecessor's
+    # launch (another summation order of the mean of squares: rare one-ulp differences), and
+    # folding the anchor into the downsample changes one bf16 rounding of the stage-3/4 entry.
     rel = ((got.float() - want.float()).norm() / want.float().norm()).item()
     rel_unfolded = ((unfolded.float() - want.float()).norm() / want.float().norm()).item()
     print(f"fused glue vs forward_features rel-L2 {rel:.2e}; unfolded anchors {rel_unfolded:.2e}", flush=True)
     assert rel <= 1e-2, rel
-    assert rel_unfolded == 0.0, rel_unfolded
+    assert rel_unfolded <= 2e-3, rel_unfolded
     if not fp8:  # with autograd on, the reference composition runs (no fused glue, no stem kernel)
         eager = model(x)
         rel_eager = ((eager.float() - want.float()).norm() / want.float().norm()).item()
@@ -208,3 +211,94 @@ def test_block_s2d_falls_back_when_unsupported() -> None:
         assert blk.to(torch.bfloat16).forward_s2d(x32.to(torch.bfloat16), 3) is None  # 14 % 3 != 0
         y = blk.forward_s2d(x32.to(torch.bfloat16), 2)
     assert y is not None and y.shape == (1, 7, 7, 2048)
+
+
+def _rel(a, b) -> float:
+    return ((a.float() - b.float()).norm() / b.float().norm()).item()
+
+
+CHAIN_CASES = [("s3", 14, 14, 512, 128), ("s4", 7, 7, 1024, 128), ("s3b", 14, 14, 256, 128)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("name,h,w,c,d", CHAIN_CASES, ids=[k[0] for k in CHAIN_CASES])
+def test_chain_stats_are_group_sums_of_squares(name, h, w, c, d, dtype) -> None:
+    """A contiguous-group d = 128 launch writes, per output row and channel group, the sum of
+    squares of the stored values; its output is the unchained launch's, bit for bit."""
+    announce(f"chain stats {name} {dtype} B=3")
+    plan, x, p, nw = make_case(3, h, w, c, d, "shifted", 0, dtype)
+    q_c = c // d
+    with torch.no_grad():
+        y, stats = bigemm_block_chain_hip(x, None, nw, plan, **p)
+        want = bigemm_block_hip(x, nw, plan, **p)
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
+    assert stats is not None and stats.shape == (3 * h * w, q_c)
+    ref = want.float().reshape(3 * h * w, q_c, d).square().sum(-1)
+    torch.testing.assert_close(stats, ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("route,level", [("local", 0), ("shifted", 0), ("radix", 1), ("radix", 2)])
+@pytest.mark.parametrize("variant", ["bf16", "f16", "fp8"])
+def test_chain_consumer_matches_unchained_block(route, level, variant) -> None:
+    """A block given its predecessor's statistics (stats_in) reads only its groups' columns; the
+    result equals the unchained block's up to the summation order of the mean of squares, and
+    both are within the bf16 tolerance of the oracle."""
+    from oracle.bigemm import block_reference
+    from oracle.routing import build_route_plan as oracle_plan
+
+    dtype = torch.float16 if variant == "f16" else torch.bfloat16
+    fp8 = variant == "fp8"
+    announce(f"chain consumer s3 {route}{level} {variant} B=4")
+    plan0, x0, p0, nw0 = make_case(4, 14, 14, 512, 128, "local", 0, dtype, seed=1)
+    plan, _, p, nw = make_case(4, 14, 14, 512, 128, route, level, dtype, seed=2)
+    with torch.no_grad():
+        x, stats = bigemm_block_chain_hip(x0, None, nw0, plan0, **p0)
+        got, nxt = bigemm_block_chain_hip(x, stats, nw, plan, **p, fp8=fp8)
+        want = bigemm_block_hip(x, nw, plan, **p, fp8=fp8)
+    torch.cuda.synchronize()
+    assert stats is not None
+    assert (nxt is not None) == (level == 0)
+    rel = _rel(got, want)
+    equal = (got == want).float().mean().item()
+    print(f"chained vs unchained rel-L2 {rel:.2e}, {equal:.4%} elements equal", flush=True)
+    assert rel <= 2e-3, rel
+    oplan = oracle_plan(14, 14, 512, 16, 128, route, level)
+    params = {k: v.to(dtype).float().cpu() for k, v in p.items()}
+    params["norm_weight"] = nw.to(dtype).float().cpu()
+    ref = block_reference(x.float().cpu(), oplan, params)
+    tol = 5e-2 if fp8 else 1e-2
+    assert _rel(got.cpu(), ref) <= tol
+
+
+def test_chain_s2d_consumer_and_resident_producer() -> None:
+    """factor 2: the chained launch writes the space_to_depth layout and no statistics; a d = 64
+    block (the resident kernel) takes no statistics and writes none."""
+    announce("chain s2d consumer + d=64 producer")
+    plan0, x0, p0, nw0 = make_case(2, 14, 14, 512, 128, "local", 0, torch.bfloat16, seed=3)
+    plan, _, p, nw = make_case(2, 14, 14, 512, 128, "shifted", 0, torch.bfloat16, seed=4)
+    with torch.no_grad():
+        x, stats = bigemm_block_chain_hip(x0, None, nw0, plan0, **p0)
+        got, nxt = bigemm_block_chain_hip(x, stats, nw, plan, **p, factor=2)
+        want = bigemm_block_s2d_hip(x, nw, plan, **p, factor=2)
+        plan1, x1, p1, nw1 = make_case(2, 28, 28, 256, 64, "local", 0, torch.bfloat16, seed=5)
+        y1, s1 = bigemm_block_chain_hip(x1, None, nw1, plan1, **p1)
+        want1 = bigemm_block_hip(x1, nw1, plan1, **p1)
+    torch.cuda.synchronize()
+    assert nxt is None and got.shape == want.shape
+    assert _rel(got, want) <= 2e-3
+    assert s1 is None and torch.equal(y1, want1)
+
+
+def test_chain_rejects_bad_stats() -> None:
+    announce("chain rejects bad stats_in")
+    plan, x, p, nw = make_case(1, 14, 14, 512, 128, "local", 0, torch.bfloat16)
+    with torch.no_grad():
+        with pytest.raises(ValueError, match="stats_in"):
+            bigemm_block_chain_hip(x, torch.zeros(5, 4, device=DEV), nw, plan, **p)
+        with pytest.raises(ValueError, match="stats_in"):
+            bigemm_block_chain_hip(x, torch.zeros(196, 4, device=DEV, dtype=torch.float64), nw, plan, **p)
+        with pytest.raises(ValueError, match="stats_in_parts"):
+            bigemm_block_chain_hip(x, torch.zeros(196, 65, device=DEV), nw, plan, **p)
+        with pytest.raises(RuntimeError):
+            bigemm_block_chain_hip(x.float(), None, nw, plan, **p)
