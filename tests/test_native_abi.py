@@ -84,6 +84,27 @@ def test_fwd_rejects_bad_arguments_without_touching_the_gpu() -> None:
     assert lib.ow_rms_scale(None, None, 0, 512, 1e-6, bf16, None) == 0  # empty: nothing launched
 
 
+def test_fwd_chain_rejects_bad_arguments_without_touching_the_gpu() -> None:
+    lib = _native.lib()
+    plan = _native.make_plan(14, 14, 512, 16, 128, "local", 0)
+    bf16, f32 = _native.OW_DTYPE_BF16, _native.OW_DTYPE_F32
+    P, out = ctypes.c_void_p(16), ctypes.c_void_p(32)
+    NB = lib.ow_packed_weight_bytes(4, 128, 256, bf16)
+    written = ctypes.c_int32(7)
+
+    def chain(dtype=bf16, flags=_native.OW_FUSE_NORM, stats_in=None, parts=0, w=ctypes.byref(written)):
+        return lib.ow_bigemm_fwd_chain(P, out, 1e-6, P, NB, P, P, None, ctypes.byref(plan), 1, 256, dtype, flags,
+                                       stats_in, parts, None, w, None, 0, None)
+
+    assert chain(w=None) == 1 and b"stats_written" in lib.ow_last_error()
+    assert chain(dtype=f32) == 2 and written.value == 0
+    assert chain(stats_in=P, parts=0) == 1 and b"stats_in_parts" in lib.ow_last_error()
+    assert chain(stats_in=P, parts=65) == 1 and b"stats_in_parts" in lib.ow_last_error()
+    assert chain(stats_in=P, parts=4, flags=0) == 1 and b"OW_FUSE_NORM" in lib.ow_last_error()
+    written.value = 7
+    assert chain() == 1 and b"workspace" in lib.ow_last_error() and written.value == 0
+
+
 def test_hip_is_supported_reasons_on_cpu() -> None:
     plan = build_route_plan(14, 14, 512, 16, 128, "local")
     ok, reason = hip_is_supported(torch.randn(1, 14, 14, 512), plan, torch.randn(4, 128, 256))
