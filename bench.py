@@ -101,53 +101,98 @@ def time_graph(graph, replays: int) -> float:
     return start.elapsed_time(stop) / replays
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """Oracle (reference backend algorithm, fp32) on the host: every stage x route at batch 8."""
+def _cpu_model_name() -> str:
+    """The host CPU model (lscpu's "Model name"), or the platform string."""
+    import platform
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _median_time(fn, warmup: int, iters: int) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline(budget_s: float, batch: int, min_s: float = 10.0) -> dict:
+    """The oracle (the reference backend's algorithm, fp32 PyTorch) on the host, in the same run
+    as the GPU measurement: every stage x route of the bench workload at `batch`, with all CPUs
+    of this process's affinity mask; warm-up 2, then timed passes over all cases (at least 5,
+    and more until `min_s` seconds of timed work), the median per case.  Also config 1
+    (x [8, 14, 14, 512] fp32, local route) on its own.  Cases are skipped, and said so, once
+    `budget_s` is spent."""
     from oracle.bigemm import block_reference
     from oracle.routing import build_route_plan as oracle_plan
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    batch = 8
-    flops_total = 0
-    secs_total = 0.0
+    warmup, min_iters = 2, 5
+
+    def make(h, w, c, d, route, level, b):
+        gen = torch.Generator().manual_seed(0)
+        plan = oracle_plan(h, w, c, G, d, route, level)
+        q_c = plan.channel_indices.shape[0]
+        x = torch.randn(b, h, w, c, generator=gen)
+        params = dict(
+            a_u=torch.randn(G, G, generator=gen) / 4, a_v=torch.randn(G, G, generator=gen) / 4,
+            a_o=torch.randn(G, G, generator=gen) / 4,
+            b_u=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
+            b_v=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
+            b_o=torch.randn(q_c, 2 * d, d, generator=gen) / math.sqrt(2 * d), gamma=torch.ones(c),
+            norm_weight=torch.ones(c),
+        )
+        return lambda: block_reference(x, plan, params)
+
     t_begin = time.perf_counter()
-    cases = 0
-    for (_, h, w, c, d) in STAGES:
-        for (route, level) in ROUTES:
-            gen = torch.Generator().manual_seed(1)
-            plan = oracle_plan(h, w, c, G, d, route, level)
-            q_c = plan.channel_indices.shape[0]
-            params = dict(
-                norm_weight=torch.ones(c), a_u=torch.randn(G, G, generator=gen) / 4,
-                a_v=torch.randn(G, G, generator=gen) / 4, a_o=torch.randn(G, G, generator=gen) / 4,
-                b_u=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
-                b_v=torch.randn(q_c, d, 2 * d, generator=gen) / math.sqrt(d),
-                b_o=torch.randn(q_c, 2 * d, d, generator=gen) / math.sqrt(2 * d), gamma=torch.ones(c),
-            )
-            x = torch.randn(batch, h, w, c, generator=gen)
-            with torch.inference_mode():
-                block_reference(x, plan, params)  # warmup
-                times = []
-                for _ in range(3):
-                    t0 = time.perf_counter()
-                    block_reference(x, plan, params)
-                    times.append(time.perf_counter() - t0)
-            times.sort()
-            secs_total += times[1]
-            flops_total += case_work(batch, h, w, c, d)[0]
-            cases += 1
-            if time.perf_counter() - t_begin > budget_s:
-                break
-        if time.perf_counter() - t_begin > budget_s:
-            break
+    with torch.inference_mode():
+        config1_s = _median_time(make(14, 14, 512, 128, "local", 0, 8), warmup, min_iters)
+        cases = []
+        for (_, h, w, c, d) in STAGES:
+            for (route, level) in ROUTES:
+                if time.perf_counter() - t_begin > budget_s:
+                    break
+                fn = make(h, w, c, d, route, level, batch)
+                for _ in range(warmup):
+                    fn()
+                cases.append((fn, case_work(batch, h, w, c, d)[0], []))
+        timed, passes = 0.0, 0
+        while passes < min_iters or (timed < min_s and time.perf_counter() - t_begin < budget_s):
+            for fn, _, times in cases:
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+                timed += times[-1]
+            passes += 1
+    secs_total = sum(sorted(t)[len(t) // 2] for _, _, t in cases)
+    flops_total = sum(f for _, f, _ in cases)
     return {
         "value": round(flops_total / secs_total / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "sample": f"oracle fused block (RMSNorm + pack/einsum/unpack + residual), fp32, batch {batch}, "
-                  f"{cases} of 12 stage x route cases, median of 3 after 1 warmup",
+                  f"{len(cases)} of 12 stage x route cases, warm-up {warmup} then the median of {passes} timed "
+                  f"passes ({timed:.1f} s timed)",
+        "config1_ms": round(config1_s * 1e3, 3),
+        "config1_gflop_per_s": round(case_work(8, 14, 14, 512, 128)[0] / config1_s / 1e9, 2),
+        "torch_threads": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model_name(),
+        "wall_s": round(time.perf_counter() - t_begin, 1),
     }
 
 
@@ -163,9 +208,11 @@ def eager_reference_delta(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma):
     """
     b, h, w, c = x.shape
     n = h * w
-    g, d = G, plan.channel_tile
+    g, d = G, int(plan.channel_indices.shape[1])
     dev = x.device
-    key = (plan.key(), dev)
+    from omniwave_amd.routing import plan_key
+
+    key = (plan_key(plan), dev)
     if key not in _EAGER_TABLES:
         ch = plan.channel_indices.to(dev)
         gm_mask = (plan.token_mask[:, :, None, None] & plan.channel_mask[None, None, :, :]).to(dev)
@@ -240,6 +287,7 @@ def model_section(batch: int, steps: int, dev) -> dict:
             for blk in blocks:
                 blk.backend = "auto"
     diff = (ref_logits.float() - eager_logits.float()).norm() / eager_logits.float().norm()
+    gamma1 = _model_parity_gamma1(model, x[:8])
     return {
         "workload": f"omniweave_t forward, [{batch}, 3, 224, 224] bf16, random init (seed 0)",
         "images_per_s": round(batch / (hip_ms * 1e-3), 1),
@@ -250,7 +298,35 @@ def model_section(batch: int, steps: int, dev) -> dict:
         "launch": "hip_graph (whole forward)",
         "graph_replay_max_abs_diff": replay_err,
         "logits_rel_l2_vs_eager": round(float(diff), 5),
+        "logits_rel_l2_gamma1_vs_fp32_eager": gamma1,
     }
+
+
+def _model_parity_gamma1(model, x) -> float:
+    """Logits parity where it is not vacuous: with every LayerScale at 1 (at its initial 1e-5 the
+    blocks barely move the logits), the HIP path in bf16 against the same weights in fp32 on
+    the PyTorch-eager reference operations, rel-L2 over the given images."""
+    import copy
+
+    from omniwave_amd.bigemm import register_backend
+
+    m1 = copy.deepcopy(model)
+    with torch.no_grad():
+        for stage in m1.stages:
+            for blk in stage.blocks:
+                blk.gamma.fill_(1.0)
+    m32 = copy.deepcopy(m1).float()
+    with torch.inference_mode():
+        got = m1(x).float()
+        register_backend("reference", eager_reference_delta)
+        try:
+            for stage in m32.stages:
+                for blk in stage.blocks:
+                    blk.backend = "reference"
+            want = m32(x.float())
+        finally:
+            register_backend("reference", None)
+    return round(float((got - want).norm() / want.norm()), 5)
 
 
 def fp8_section(model_batch: int, steps: int, dev) -> dict:
@@ -471,6 +547,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=128)
     ap.add_argument("--cpu-budget", type=float, default=30.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-batch", type=int, default=8,
+                    help="batch of the CPU baseline's stage x route cases (8: config 1's batch, the CPU's best "
+                         "throughput; larger batches run slower per flop on the host)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--model-batch", type=int, default=256, help="batch of the OmniWeave-T inference section")
     ap.add_argument("--no-model", action="store_true", help="skip the OmniWeave-T inference section")
@@ -621,7 +700,7 @@ def main() -> int:
     gc.collect()
     fp8 = None if args.no_fp8 else fp8_section(args.model_batch, 10, dev)
     gc.collect()
-    baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
+    baseline = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.cpu_batch)
     line = {
         "metric": "BiGEMM fwd TFLOP/s (fused RMSNorm+residual, 4 OmniWeave-T stage shapes x 3 routes)",
         "value": round(value, 2),

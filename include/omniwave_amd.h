@@ -143,7 +143,12 @@ int ow_pack_weights_fp8(const void* a_u, const void* a_v, const void* a_o,
 int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, float eps,
                  int32_t dtype, void* stream);
 
-/* Workspace bytes ow_bigemm_fwd needs: batch*H*W fp32 row scales with OW_FUSE_NORM, else 0. */
+/*
+ * Workspace bytes ow_bigemm_fwd may need: batch*H*W fp32 row scales with OW_FUSE_NORM, else 0.
+ * Only launches whose RMSNorm statistics come from a separate pass use it (fp32 activations,
+ * element access for ragged / unaligned rows, or a channel count the in-kernel statistics do
+ * not cover); for the others `workspace` may be NULL and workspace_bytes 0.
+ */
 size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags);
 
 /*
@@ -160,7 +165,8 @@ size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags);
  *   packed_bytes  size of `packed`; must equal ow_packed_weight_bytes(q_c, d, rd, dtype)
  *   token_index   device copy of ow_route_build's token table [Q_s*g]
  *   channel_index device copy of ow_route_build's channel table [Q_c*d]
- *   workspace     ow_fwd_workspace_bytes(plan, batch, flags) bytes of device memory
+ *   workspace     ow_fwd_workspace_bytes(plan, batch, flags) bytes of device memory when the
+ *                 launch needs it (see ow_fwd_workspace_bytes), else may be NULL
  *
  * For every tile (b, q_s, q_c): T = rows token_index[q_s,:] x columns channel_index[q_c,:]
  * of x (pads read as zero; RMSNorm-scaled with OW_FUSE_NORM), delta = A_o (SiLU(A_u T B_u) *
@@ -201,7 +207,8 @@ int ow_bigemm_fwd_rows(const void* x, void* out, float eps,
  * sums to the next block as stats_in (stats_in_parts = that block's predecessor's Q_c) gives
  * it its RMSNorm statistics without reading whole rows; the result equals ow_bigemm_fwd's up
  * to the summation order of the mean of squares.  Needs OW_FUSE_NORM with stats_in; bf16 /
- * f16 activations only.
+ * f16 activations only.  stats_in and stats_out must not overlap (the launch reads one while
+ * other workgroups write the other; overlapping ranges are rejected with OW_ERR_INVALID).
  */
 int ow_bigemm_fwd_chain(const void* x, void* out, float eps,
                         const void* packed, size_t packed_bytes,
@@ -209,6 +216,22 @@ int ow_bigemm_fwd_chain(const void* x, void* out, float eps,
                         const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
                         const float* stats_in, int32_t stats_in_parts, float* stats_out,
                         int32_t* stats_written, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ow_bigemm_fwd for training with per-sample drop-path (stochastic depth,
+ * omniweave/models/block.py:99-107): drop_scale [batch] (fp32, device) multiplies each image's
+ * rounded delta before the residual, out = round(x + round(round(delta) * drop_scale[b])) (or
+ * round(round(delta) * drop_scale[b]) without OW_FUSE_RESIDUAL; fp32 activations: one fp32
+ * product).  drop_scale[b] = keep_mask[b] * (1 / keep_probability) reproduces the reference's
+ * delta * keep_mask / keep_probability, whose division by a scalar PyTorch evaluates on the
+ * GPU as a product with the fp32 reciprocal.  Other arguments as ow_bigemm_fwd.
+ */
+int ow_bigemm_fwd_drop(const void* x, void* out, float eps,
+                       const void* packed, size_t packed_bytes,
+                       const int32_t* token_index, const int32_t* channel_index,
+                       const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
+                       int32_t flags, const float* drop_scale, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /*
  * Backbone stem as one gather-GEMM (omniweave/models/backbone.py:121,173-176): image
@@ -229,6 +252,13 @@ int ow_stem_fwd(const void* image, const void* weight, void* out, int32_t batch,
  * (OW_DTYPE_BF16, OW_DTYPE_F16, or OW_DTYPE_F32 for fp32 activations: fp32 tiles and plain
  * fp32 kernels; the alignment and multiple-of-8 conditions below are for the 16-bit types).
  */
+
+/* out[b][i] = x[b][i] * scale[b] rounded to dtype, for b < batch and i < per_sample: the
+ * gradient of the delta branch under drop-path (the autograd of delta * keep_mask /
+ * keep_probability, omniweave/models/block.py:99-107, with scale = keep_mask / keep_probability
+ * as in ow_bigemm_fwd_drop).  out may alias x. */
+int ow_scale_samples(const void* x, const float* scale, void* out, int32_t batch, int64_t per_sample,
+                     int32_t dtype, void* stream);
 
 /* Folded weights as plain matrices: B_u'' = -log2(e) w B_u and B_v'' = -ln(2) w B_v
  * ([q_c][d][rd] and transposed [q_c][rd][d]), B_o'' = B_o diag(gamma) ([q_c][rd][d] and

@@ -81,6 +81,20 @@ _SIGNATURES = {
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ],
     ),
+    "ow_bigemm_fwd_drop": (
+        ctypes.c_int,
+        [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ],
+    ),
+    "ow_scale_samples": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+         ctypes.c_void_p],
+    ),
     "ow_route_s2d_rows": (ctypes.c_int, [ctypes.POINTER(OwPlan), ctypes.c_int32, _c_int32_p, _c_int32_p]),
     "ow_stem_fwd": (
         ctypes.c_int,

@@ -28,7 +28,7 @@ import torch
 from torch import Tensor
 
 from omniwave_amd import _native
-from omniwave_amd.routing import RoutePlan, device_tables
+from omniwave_amd.routing import RoutePlan, device_tables, native_plan
 
 _DTYPE_CODE = {torch.float32: _native.OW_DTYPE_F32, torch.bfloat16: _native.OW_DTYPE_BF16,
                torch.float16: _native.OW_DTYPE_F16}
@@ -90,11 +90,14 @@ def _fp32(t: Tensor, device) -> Tensor:
 
 
 def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
-                    a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float):
-    """Gradients of ``bigemm_fwd(x, norm_weight, gamma, a_u, .., b_o, plan, flags, eps)``.
+                    a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float,
+                    drop_scale: Tensor | None = None):
+    """Gradients of ``bigemm_fwd(x, norm_weight, gamma, a_u, .., b_o, plan, flags, eps, drop_scale)``.
 
     Returns ``(dx, d_norm_weight, d_gamma, d_a_u, d_a_v, d_a_o, d_b_u, d_b_v, d_b_o)``, each in
-    its input's dtype (``d_norm_weight`` is None without OW_FUSE_NORM).
+    its input's dtype (``d_norm_weight`` is None without OW_FUSE_NORM).  With ``drop_scale``
+    (per-image drop-path factors of the forward) the delta branch receives the upstream
+    gradient scaled per image and rounded (``ow_scale_samples``), the residual the plain one.
     """
     lib = _native.lib()
     dev = x.device
@@ -110,8 +113,9 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     slots = batch * q_s * 16
     n_rows = batch * plan.height * plan.width
     tok, ch = device_tables(plan, dev)
-    native_plan = plan.native()
+    oplan = native_plan(plan)
     stream = _stream(dev)
+    grad_delta = grad  # upstream gradient of the delta branch (drop-path scaled below)
 
     ws = [w.detach().contiguous() for w in (b_u, b_v, b_o)]
     wdtype = ws[0].dtype
@@ -123,6 +127,11 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
 
     with torch.cuda.device(dev):
+        if drop_scale is not None:
+            scale = drop_scale.to(device=dev, dtype=torch.float32).contiguous()
+            grad_delta = torch.empty_like(grad)
+            _native.check(lib.ow_scale_samples(grad.data_ptr(), scale.data_ptr(), grad_delta.data_ptr(), batch,
+                                               grad.numel() // max(batch, 1), code, stream), "ow_scale_samples")
         rscale = None
         if fuse_norm:
             rscale = torch.empty(n_rows, dtype=torch.float32, device=dev)
@@ -138,8 +147,8 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             # Routed tiles of X' = x r and of dY.
             xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
             dyt = torch.empty_like(xt)
-            _native.check(lib.ow_bwd_gather(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale is not None
-                                            else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan),
+            _native.check(lib.ow_bwd_gather(x.data_ptr(), grad_delta.data_ptr(), rscale.data_ptr() if rscale is not None
+                                            else None, tok.data_ptr(), ch.data_ptr(), ctypes.byref(oplan),
                                             batch, code, xt.data_ptr(), dyt.data_ptr(), stream), "ow_bwd_gather")
 
         if fused:
@@ -158,9 +167,9 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             n_part = lib.ow_bwd_fused_partials(slots, q_c)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
             if routed:
-                _native.check(lib.ow_bwd_fused_routed(x.data_ptr(), grad.data_ptr(), rscale.data_ptr() if rscale
+                _native.check(lib.ow_bwd_fused_routed(x.data_ptr(), grad_delta.data_ptr(), rscale.data_ptr() if rscale
                                                       is not None else None, tok.data_ptr(),
-                                                      ctypes.byref(native_plan), batch, au.data_ptr(),
+                                                      ctypes.byref(oplan), batch, au.data_ptr(),
                                                       av.data_ptr(), ao.data_ptr(), wpk.data_ptr(), nbytes,
                                                       pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
                                                       du.data_ptr(), dv.data_ptr(), g.data_ptr(),
@@ -223,7 +232,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
         # residual's identity).
         if not routed:
             _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(),
-                                             ctypes.byref(native_plan), batch, code, g.data_ptr(), stream),
+                                             ctypes.byref(oplan), batch, code, g.data_ptr(), stream),
                           "ow_bwd_scatter")
             del dxt
         dx = torch.empty_like(x)

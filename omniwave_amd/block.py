@@ -15,7 +15,8 @@ import torch.nn as nn
 from torch import Tensor
 
 from omniwave_amd.bigemm import bigemm
-from omniwave_amd.hip import bigemm_block_chain_hip, bigemm_block_hip, bigemm_block_s2d_hip, hip_is_supported
+from omniwave_amd.hip import (bigemm_block_chain_hip, bigemm_block_hip, bigemm_block_s2d_hip, drop_path_scale,
+                              hip_is_supported)
 from omniwave_amd.routing import RoutePlan, build_route_plan
 
 RMS_EPS = 1e-6  # omniweave/models/block.py:84
@@ -128,10 +129,10 @@ class OmniWeaveBlock(nn.Module):
                 raise RuntimeError("the fp8 BiGEMM variant needs the hip backend on a gfx950 GPU")
             return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, fp8=True)
         if fused:
-            if not dropping:
-                return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS)
-            delta = bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, residual=False)
-            return x + self._drop_path(delta)
+            # Drop-path (block.py:99-107) fused: the kernel scales each image's rounded delta
+            # before the residual; the keep mask is drawn as the reference draws it.
+            scale = drop_path_scale(x.shape[0], self.drop_path_rate, x.dtype, x.device) if dropping else None
+            return bigemm_block_hip(x, self.norm_weight, self.plan, *params, eps=RMS_EPS, drop_scale=scale)
         variance = x.float().square().mean(dim=-1, keepdim=True)
         normalized = x * torch.rsqrt(variance.to(x.dtype) + RMS_EPS)
         normalized = (normalized * self.norm_weight).to(x.dtype)

@@ -933,10 +933,78 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
 
 unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
+// out[b][i] = round(x[b][i] * scale[b]): the upstream gradient of the delta branch under
+// per-sample drop-path (omniweave/models/block.py:99-107; the autograd of delta * keep_mask /
+// keep_probability multiplies the gradient by the same per-image factor and rounds once).
+// V = 8 elements per thread (16-bit types, 16-byte accesses) or V = 1.
+template <class Ty, int V>
+__global__ void __launch_bounds__(256) scale_samples_kernel(const uint16_t* x, const float* scale, uint16_t* out,
+                                                            int64_t per_sample, int64_t total) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * V;
+  if (i >= total) return;
+  const float sc = scale[i / per_sample];
+  if constexpr (V == 8) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = Ty::pack2(Ty::to_f32(lo16(v[w])) * sc, Ty::to_f32(hi16(v[w])) * sc);
+    *reinterpret_cast<u32x4*>(out + i) = o;
+  } else {
+    out[i] = Ty::from_f32(Ty::to_f32(x[i]) * sc);
+  }
+}
+
+__global__ void __launch_bounds__(256) scale_samples_f32_kernel(const float* x, const float* scale, float* out,
+                                                                int64_t per_sample, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < total) out[i] = x[i] * scale[i / per_sample];
+}
+
 }  // namespace
 }  // namespace ow
 
 extern "C" {
+
+int ow_scale_samples(const void* x, const float* scale, void* out, int32_t batch, int64_t per_sample, int32_t dtype,
+                     void* stream) {
+  OW_CHECK_ARG(batch >= 0 && per_sample >= 0, "bad shape batch=%d per_sample=%lld", batch, (long long)per_sample);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32, "unsupported dtype %d",
+                     dtype);
+  const int64_t total = static_cast<int64_t>(batch) * per_sample;
+  if (total == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(x && scale && out, "tensor pointer is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OW_DTYPE_F32) {
+    hipLaunchKernelGGL(ow::scale_samples_f32_kernel, dim3(ow::blocks_for(total)), dim3(256), 0, s,
+                       static_cast<const float*>(x), scale, static_cast<float*>(out), per_sample, total);
+  } else {
+    const auto* xi = static_cast<const uint16_t*>(x);
+    auto* oi = static_cast<uint16_t*>(out);
+    const bool vec = per_sample % 8 == 0 && ow::aligned16(x) && ow::aligned16(out);
+    const unsigned blocks = ow::blocks_for(vec ? total / 8 : total);
+    if (dtype == OW_DTYPE_BF16) {
+      if (vec)
+        hipLaunchKernelGGL((ow::scale_samples_kernel<ow::BF16, 8>), dim3(blocks), dim3(256), 0, s, xi, scale, oi,
+                           per_sample, total);
+      else
+        hipLaunchKernelGGL((ow::scale_samples_kernel<ow::BF16, 1>), dim3(blocks), dim3(256), 0, s, xi, scale, oi,
+                           per_sample, total);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((ow::scale_samples_kernel<ow::F16, 8>), dim3(blocks), dim3(256), 0, s, xi, scale, oi,
+                           per_sample, total);
+      else
+        hipLaunchKernelGGL((ow::scale_samples_kernel<ow::F16, 1>), dim3(blocks), dim3(256), 0, s, xi, scale, oi,
+                           per_sample, total);
+    }
+  }
+  if (int rc = ow::hip_status(hipGetLastError(), "scale_samples_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
+}
 
 int ow_bwd_gather(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
                   const int32_t* channel_index, const OwPlan* plan, int32_t batch, int32_t dtype, void* xt, void* dyt,

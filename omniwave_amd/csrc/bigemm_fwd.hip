@@ -117,6 +117,7 @@ struct FwdArgs {
   float eps;         // kNormInline / kNormPartials: RMSNorm epsilon
   int32_t parts;     // kNormPartials: partial sums per row in row_scale ([batch * n_tok, parts])
   float* stats_out;  // NULL, or [batch * n_tok, q_c]: sum of squares of each stored row's group columns
+  const float* drop_scale;  // NULL, or [batch]: per-image multiplier of the rounded delta (drop-path)
 };
 
 // Where the RMSNorm row scales come from.
@@ -229,6 +230,7 @@ bigemm_fwd_kernel(FwdArgs a) {
   __shared__ int32_t rowid[ROWS];   // b * n_tok + token, -1 for pad rows
   __shared__ int32_t rowout[ROWS];  // output row of each tile row, -1 for pad rows
   __shared__ float rsc[ROWS];      // RMSNorm scale of each row (1 without norm)
+  __shared__ float dsc[R];         // drop-path scale of each token group's image (1 without)
   __shared__ int32_t chx[D];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -271,6 +273,11 @@ bigemm_fwd_kernel(FwdArgs a) {
     }
     rowid[tid] = id;
     rowout[tid] = od;
+    if (tid % kG == 0) {
+      float ds = 1.0f;
+      if (a.drop_scale && tg < static_cast<int64_t>(a.batch) * a.q_s) ds = a.drop_scale[tg / a.q_s];
+      dsc[tid / kG] = ds;
+    }
   }
   for (int k = tid; k < D; k += kThreads) {
     const int c = a.chan[qc * D + k];
@@ -578,13 +585,20 @@ bigemm_fwd_kernel(FwdArgs a) {
     pair_output<Ty, MB>(W[p], fAo, lane, dl);
     mfma_drain();
     uint16_t* st = xs + (wave * TPW + 2 * p) * kG * LDX;
+    const float s0 = dsc[wave * TPW + 2 * p], s1 = dsc[wave * TPW + 2 * p + 1];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       auto dst = [&](int i) { return &st[pair_token_row(i, hh) * LDX + 32 * mb + l32]; };
-      if (a.residual)
+      if (a.drop_scale) {
+        if (a.residual)
+          pair_store_block<Ty, true, true>(dl[mb], xk[p][mb], dst, s0, s1);
+        else
+          pair_store_block<Ty, false, true>(dl[mb], xk[p][mb], dst, s0, s1);
+      } else if (a.residual) {
         pair_store_block<Ty, true>(dl[mb], xk[p][mb], dst);
-      else
+      } else {
         pair_store_block<Ty, false>(dl[mb], xk[p][mb], dst);
+      }
     }
   }
   __syncthreads();
@@ -1078,11 +1092,25 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
   return OW_OK;
 }
 
+// The RMSNorm row scales of a launch come from one of four places (kNorm*); only kNormBuffer
+// (and the fp32 kernel with OW_FUSE_NORM) uses the workspace, for batch * H * W floats.
+// Returns true when the launch needs it.
+static bool fwd_needs_scale_buffer(bool fp32, bool norm, bool resident, int32_t mode, bool stats_in, int32_t c) {
+  if (!norm) return false;
+  if (fp32) return true;
+  if (resident) return false;
+  if (mode == ow::kModeElement) return true;
+  if (stats_in) return false;
+  const int32_t j = c / 128;
+  return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));
+}
+
 static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
                             const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
                             const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
                             const float* stats_in, int32_t stats_in_parts, float* stats_out,
-                            int32_t* stats_written, void* workspace, size_t workspace_bytes, void* stream) {
+                            int32_t* stats_written, const float* drop_scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   if (stats_written) *stats_written = 0;
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
@@ -1090,7 +1118,8 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   OW_CHECK_ARG(packed && token_index && channel_index, "tensor pointer is NULL");
   OW_CHECK_ARG((flags & ~(OW_FUSE_NORM | OW_FUSE_RESIDUAL | OW_FUSE_FP8)) == 0, "unknown flags 0x%x", flags);
   const bool fp8 = (flags & OW_FUSE_FP8) != 0;
-  OW_CHECK_SUPPORTED(!fp8 || ((flags & OW_FUSE_NORM) && dtype != OW_DTYPE_F32),
+  const bool norm = (flags & OW_FUSE_NORM) != 0;
+  OW_CHECK_SUPPORTED(!fp8 || (norm && dtype != OW_DTYPE_F32),
                      "OW_FUSE_FP8 needs OW_FUSE_NORM and bf16 / f16 activations");
   OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16 || dtype == OW_DTYPE_F32,
@@ -1100,6 +1129,8 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   OW_CHECK_ARG(want != 0 && packed_bytes == want,
                "packed weights hold %zu bytes; q_c=%d d=%d rd=%d needs %zu", packed_bytes, q_c, d, rd, want);
   OW_CHECK_ARG(ow::aligned16(packed), "packed weights must be 16-byte aligned");
+  OW_CHECK_SUPPORTED(!out_rows || dtype != OW_DTYPE_F32, "an output-row table needs bf16 or f16 activations");
+  OW_CHECK_SUPPORTED(!(out_rows && drop_scale), "a drop-path scale with an output-row table");
   if (batch == 0) {  // empty tensors may carry NULL data pointers; nothing to launch
     ow::clear_error();
     return OW_OK;
@@ -1108,25 +1139,38 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   OW_CHECK_ARG(x != out, "out must not alias x");
   OW_CHECK_ARG(static_cast<int64_t>(batch) * n * c < (int64_t(1) << 40), "tensor too large");
   OW_CHECK_ARG(static_cast<int64_t>(batch) * n < (int64_t(1) << 31), "batch * H * W must be < 2^31");
-  const size_t need_ws = ow_fwd_workspace_bytes(plan, batch, flags);
-  OW_CHECK_ARG(workspace_bytes >= need_ws && (need_ws == 0 || workspace),
-               "workspace holds %zu bytes; %zu needed", workspace_bytes, need_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  OW_CHECK_SUPPORTED(!out_rows || dtype != OW_DTYPE_F32, "an output-row table needs bf16 or f16 activations");
-  if (dtype == OW_DTYPE_F32) {
-    float* scale = nullptr;
-    if (flags & OW_FUSE_NORM) {
-      scale = static_cast<float*>(workspace);
-      if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
-    }
+
+  // Kernel and channel-group access (routing.py:107-121): identity order at level 0 or with one
+  // group; at levels >= 1 group qc is the channels congruent to (qc + level) mod q_c.
+  const bool fp32 = dtype == OW_DTYPE_F32;
+  const bool resident = !fp32 && !fp8 && ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) &&
+                        ow::aligned16(out);
+  const bool vec_ok = (c % 8 == 0) && ow::aligned16(x) && ow::aligned16(out);
+  const bool identity = plan->radix_level == 0 || q_c <= 1;
+  int32_t mode = ow::kModeElement;
+  if (vec_ok && identity && c % d == 0)
+    mode = ow::kModeContig;
+  else if (vec_ok && !identity && c == q_c * d && (q_c == 2 || q_c == 4 || q_c == 8))
+    mode = ow::kModeStrided;
+  float* scale = nullptr;
+  if (fwd_needs_scale_buffer(fp32, norm, resident, mode, stats_in != nullptr, c)) {
+    const size_t need = ow_fwd_workspace_bytes(plan, batch, flags);
+    OW_CHECK_ARG(workspace && workspace_bytes >= need, "workspace holds %zu bytes; %zu needed", workspace_bytes,
+                 need);
+    scale = static_cast<float*>(workspace);
+    if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
+  }
+
+  if (fp32) {
     if (int rc = ow::launch_fwd_f32(static_cast<const float*>(x), static_cast<float*>(out), scale,
                                     static_cast<const float*>(packed), token_index, channel_index, batch, n, c, q_s,
-                                    q_c, d, rd, (flags & OW_FUSE_RESIDUAL) ? 1 : 0, s))
+                                    q_c, d, rd, (flags & OW_FUSE_RESIDUAL) ? 1 : 0, drop_scale, s))
       return rc;
     ow::clear_error();
     return OW_OK;
   }
-  if (!fp8 && ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) && ow::aligned16(out)) {
+  if (resident) {
     ow::ResidentArgs r{};
     r.x = static_cast<const uint16_t*>(x);
     r.out = static_cast<uint16_t*>(out);
@@ -1140,9 +1184,10 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.q_s = q_s;
     r.q_c = q_c;
     r.n_pairs = static_cast<int32_t>((static_cast<int64_t>(batch) * q_s + 1) / 2);
-    r.norm = (flags & OW_FUSE_NORM) ? 1 : 0;
+    r.norm = norm ? 1 : 0;
     r.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
     r.eps = eps;
+    r.drop_scale = drop_scale;
     const int rc = ow::launch_fwd_resident(r, dtype, s);
     if (rc == OW_OK) ow::clear_error();
     return rc;
@@ -1161,36 +1206,23 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   a.q_c = q_c;
   a.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
   a.eps = eps;
-  // Channel-group access (routing.py:107-121): identity order at level 0 or with one group;
-  // at levels >= 1 group qc is the channels congruent to (qc + level) mod q_c.
-  const bool vec_ok = (c % 8 == 0) && ow::aligned16(x) && ow::aligned16(out);
-  const bool identity = plan->radix_level == 0 || q_c <= 1;
-  a.stride = 1;
-  if (vec_ok && identity && c % d == 0) {
-    a.mode = ow::kModeContig;
-  } else if (vec_ok && !identity && c == q_c * d && (q_c == 2 || q_c == 4 || q_c == 8)) {
-    a.mode = ow::kModeStrided;
-    a.stride = q_c;
-  } else {
-    a.mode = ow::kModeElement;
-  }
-  // RMSNorm row scales: from the previous launch's partial sums when given, read with the tile
-  // when whole rows are 16 lanes x 1, 2, 4 or 8 vectors, otherwise from a statistics pass into
-  // the workspace.
+  a.drop_scale = drop_scale;
+  a.mode = mode;
+  a.stride = mode == ow::kModeStrided ? q_c : 1;
+  // RMSNorm row scales: the statistics pass above (element access, or whole rows that are not
+  // 16 lanes x 1, 2, 4 or 8 vectors), else the previous launch's partial sums when given, else
+  // read with the tile.
   a.norm = ow::kNormNone;
-  if (flags & OW_FUSE_NORM) {
-    const int32_t j = c / 128;
-    if (stats_in && a.mode != ow::kModeElement) {
+  if (norm) {
+    if (scale) {
+      a.norm = ow::kNormBuffer;
+      a.row_scale = scale;
+    } else if (stats_in) {
       a.norm = ow::kNormPartials;
       a.row_scale = stats_in;
       a.parts = stats_in_parts;
-    } else if (a.mode != ow::kModeElement && c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8)) {
-      a.norm = ow::kNormInline;
     } else {
-      float* scale = static_cast<float*>(workspace);
-      if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
-      a.norm = ow::kNormBuffer;
-      a.row_scale = scale;
+      a.norm = ow::kNormInline;
     }
   }
   if (stats_out && a.mode == ow::kModeContig && !out_rows) {
@@ -1211,7 +1243,7 @@ int ow_bigemm_fwd(const void* x, void* out, float eps, const void* packed, size_
                   const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan, int32_t batch,
                   int32_t rd, int32_t dtype, int32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, nullptr, plan, batch, rd,
-                          dtype, flags, nullptr, 0, nullptr, nullptr, workspace, workspace_bytes, stream);
+                          dtype, flags, nullptr, 0, nullptr, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 int ow_bigemm_fwd_rows(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
@@ -1220,7 +1252,7 @@ int ow_bigemm_fwd_rows(const void* x, void* out, float eps, const void* packed, 
                        size_t workspace_bytes, void* stream) {
   OW_CHECK_ARG(out_rows, "out_rows is NULL");
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
-                          dtype, flags, nullptr, 0, nullptr, nullptr, workspace, workspace_bytes, stream);
+                          dtype, flags, nullptr, 0, nullptr, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 int ow_bigemm_fwd_chain(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
@@ -1234,9 +1266,30 @@ int ow_bigemm_fwd_chain(const void* x, void* out, float eps, const void* packed,
   OW_CHECK_ARG(!stats_in || (stats_in_parts >= 1 && stats_in_parts <= 64),
                "stats_in_parts must be in [1, 64] (got %d)", stats_in_parts);
   OW_CHECK_ARG(!stats_in || (flags & OW_FUSE_NORM), "stats_in without OW_FUSE_NORM");
+  if (stats_in && stats_out && batch > 0 && plan) {
+    // The launch reads stats_in while it writes stats_out, from different workgroups: the two
+    // must not share memory.
+    int32_t q_s_chk = 0, q_c_chk = 0;
+    if (int rc = ow_plan_dims(plan, &q_s_chk, &q_c_chk)) return rc;
+    const int64_t rows = static_cast<int64_t>(batch) * plan->height * plan->width;
+    const auto in0 = reinterpret_cast<uintptr_t>(stats_in), out0 = reinterpret_cast<uintptr_t>(stats_out);
+    const uintptr_t in1 = in0 + static_cast<uintptr_t>(rows) * stats_in_parts * sizeof(float);
+    const uintptr_t out1 = out0 + static_cast<uintptr_t>(rows) * q_c_chk * sizeof(float);
+    OW_CHECK_ARG(in1 <= out0 || out1 <= in0, "stats_in and stats_out overlap");
+  }
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
-                          dtype, flags, stats_in, stats_in_parts, stats_out, stats_written, workspace,
+                          dtype, flags, stats_in, stats_in_parts, stats_out, stats_written, nullptr, workspace,
                           workspace_bytes, stream);
+}
+
+int ow_bigemm_fwd_drop(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                       const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan, int32_t batch,
+                       int32_t rd, int32_t dtype, int32_t flags, const float* drop_scale, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  OW_CHECK_ARG(drop_scale || batch == 0, "drop_scale is NULL");
+  return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, nullptr, plan, batch, rd,
+                          dtype, flags, nullptr, 0, nullptr, nullptr, drop_scale, workspace, workspace_bytes,
+                          stream);
 }
 
 }  // extern "C"

@@ -102,6 +102,7 @@ struct F32Args {
   const int32_t* tok;
   const int32_t* chan;
   int32_t n_tok, channels, q_s, q_c, d, rd, residual;
+  const float* drop_scale;  // [batch] per-image multiplier of delta (drop-path); NULL: none
 };
 
 template <int D, int RD>
@@ -205,6 +206,7 @@ __global__ void __launch_bounds__(kF32Threads) bigemm_fwd_f32_kernel(F32Args a) 
 #pragma unroll
     for (int j = 0; j < kG; ++j) acc = fmaf(am[j], s_pu[j][c], acc);
     const int64_t off = row * a.channels + ch;
+    if (a.drop_scale) acc *= a.drop_scale[b];  // block.py:99-107: delta * keep_mask / keep_probability
     a.out[off] = a.residual ? a.x[off] + acc : acc;
   }
 }
@@ -229,8 +231,8 @@ int rms_scale_f32(const float* x, float* scale, int64_t rows, int32_t channels, 
 
 int launch_fwd_f32(const float* x, float* out, const float* row_scale, const float* packed, const int32_t* tok,
                    const int32_t* chan, int32_t batch, int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c,
-                   int32_t d, int32_t rd, int32_t residual, hipStream_t stream) {
-  F32Args a{x, out, row_scale, packed, tok, chan, n_tok, channels, q_s, q_c, d, rd, residual};
+                   int32_t d, int32_t rd, int32_t residual, const float* drop_scale, hipStream_t stream) {
+  F32Args a{x, out, row_scale, packed, tok, chan, n_tok, channels, q_s, q_c, d, rd, residual, drop_scale};
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(batch) * q_s * q_c));
   if (d == 64 && rd == 128)
     hipLaunchKernelGGL((bigemm_fwd_f32_kernel<64, 128>), grid, dim3(kF32Threads), 0, stream, a);

@@ -50,6 +50,7 @@ struct ResidentLds {
   static constexpr int LDC = C + 8;  // tile row stride (elements)
   uint16_t tile[kNBuf][kPairRows * LDC];
   float rsc[kNBuf][kPairRows];
+  float dsc[kNBuf][2];      // drop-path scale of the pair's two token groups (DROP)
   u32x4 xch[QC][2][4][64];  // partial W (f32x16 per lane as 4 quarters) by group and writer half
   u32x4 head[3][64];        // token-operand rows A_u, A_v, A_o
 };
@@ -118,8 +119,9 @@ __device__ __forceinline__ u32x4 load_row_vec(const uint16_t* x, int32_t id, int
 }
 
 // The persistent loop of one wave: channel group g, expanded-dimension half HF.  OM: rows are
-// stored at the output-row table's positions instead of their input positions.
-template <class Ty, int QC, int HF, bool OM>
+// stored at the output-row table's positions instead of their input positions.  DROP: the
+// rounded delta of each image is multiplied by a.drop_scale[image] before the residual.
+template <class Ty, int QC, int HF, bool OM, bool DROP>
 __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds<QC>& sh, int g, int n_iter) {
   constexpr int C = QC * kD;
   constexpr int LDC = ResidentLds<QC>::LDC;
@@ -158,6 +160,9 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
   int32_t ids_cur[NI], ids_prev[NI];
   int32_t tok_n[NI], tout_n[NI], img_n[NI];
   u32x4 xr[NI];
+  // DROP: drop-path scale of the rows of pair it (loaded with the rows, one pair ahead).
+  float ds_cur[NI];
+  auto drop_of = [&](int32_t img) { return a.drop_scale[img < a.batch ? img : a.batch - 1]; };
   // pos: the pair whose table entries are read next; the grid stride in groups is 2 n_wg.
   const int32_t step_b = static_cast<int32_t>(2 * n_wg / a.q_s);
   const int32_t step_s = static_cast<int32_t>(2 * n_wg - static_cast<int64_t>(step_b) * a.q_s);
@@ -169,6 +174,7 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
     const int32_t in = row_id(a, tok_n[j], img_n[j]);
     ids_cur[j] = out_id<OM>(a, in, tout_n[j], img_n[j]);
     xr[j] = load_row_vec<C>(a.x, in, vcol);
+    ds_cur[j] = DROP ? drop_of(img_n[j]) : 1.0f;
   }
   if (n_iter > 1) {
     pair_advance(pos, step_b, step_s, a.q_s);
@@ -195,6 +201,7 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
         if (lane % LPR == LPR - 1) sh.rsc[buf][r] = rms_scale<Ty>(acc / static_cast<float>(C), a.eps);
       }
       *reinterpret_cast<u32x4*>(&tl[r * LDC + vcol]) = xr[j];
+      if (DROP && lane % LPR == 0 && r % kG == 0) sh.dsc[buf][r / kG] = ds_cur[j];
     }
     __syncthreads();
 
@@ -206,6 +213,7 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
       const int32_t in = row_id(a, tok_n[j], img_n[j]);
       ids_next[j] = out_id<OM>(a, in, tout_n[j], img_n[j]);
       xr[j] = load_row_vec<C>(a.x, in, vcol);
+      if (DROP) ds_cur[j] = drop_of(img_n[j]);  // pair it + 1 (this pair's were written in (1))
     }
     if (it + 2 < n_iter) {
       pair_advance(pos, step_b, step_s, a.q_s);
@@ -272,10 +280,11 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
     pair_output<Ty, 1>(Wh, sh.head[2][lane], lane, dl);
     mfma_drain();
     auto dst = [&](int i) { return &tl[pair_token_row(i, hh) * LDC + col[HF]]; };
+    const float s0 = DROP ? sh.dsc[buf][0] : 1.0f, s1 = DROP ? sh.dsc[buf][1] : 1.0f;
     if (a.residual)
-      pair_store_block<Ty, true>(dl[0], xk[HF], dst);
+      pair_store_block<Ty, true, DROP>(dl[0], xk[HF], dst, s0, s1);
     else
-      pair_store_block<Ty, false>(dl[0], xk[HF], dst);
+      pair_store_block<Ty, false, DROP>(dl[0], xk[HF], dst, s0, s1);
   }
 
   // Rows of the last pair (ids_prev was rotated to it by the last iteration).
@@ -290,7 +299,7 @@ __device__ __forceinline__ void resident_wave(const ResidentArgs& a, ResidentLds
   }
 }
 
-template <class Ty, int QC, bool OM>
+template <class Ty, int QC, bool OM, bool DROP>
 __global__ void __attribute__((amdgpu_flat_work_group_size(128 * QC, 128 * QC), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_resident_kernel(ResidentArgs a) {
   __shared__ __attribute__((aligned(16))) ResidentLds<QC> sh;
@@ -303,9 +312,9 @@ bigemm_fwd_resident_kernel(ResidentArgs a) {
     sh.head[f][lane] = reinterpret_cast<const u32x4*>(a.packed + f * kFragElems)[lane];
   __syncthreads();
   if (wave & 1)
-    resident_wave<Ty, QC, 1, OM>(a, sh, wave >> 1, n_iter);
+    resident_wave<Ty, QC, 1, OM, DROP>(a, sh, wave >> 1, n_iter);
   else
-    resident_wave<Ty, QC, 0, OM>(a, sh, wave >> 1, n_iter);
+    resident_wave<Ty, QC, 0, OM, DROP>(a, sh, wave >> 1, n_iter);
 }
 
 template <class Ty, int QC>
@@ -314,11 +323,15 @@ int launch_qc(const ResidentArgs& a, hipStream_t stream) {
   const int64_t slots = static_cast<int64_t>(device_cus()) * (4 / QC);
   const int64_t grid = a.n_pairs < slots ? a.n_pairs : slots;
   if (grid <= 0) return OW_OK;
+  if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   if (a.out_tok)
-    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, true>), dim3(static_cast<unsigned>(grid)), dim3(128 * QC),
-                       0, stream, a);
+    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, true, false>), dim3(static_cast<unsigned>(grid)),
+                       dim3(128 * QC), 0, stream, a);
+  else if (a.drop_scale)
+    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, false, true>), dim3(static_cast<unsigned>(grid)),
+                       dim3(128 * QC), 0, stream, a);
   else
-    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, false>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((bigemm_fwd_resident_kernel<Ty, QC, false, false>), dim3(static_cast<unsigned>(grid)),
                        dim3(128 * QC), 0, stream, a);
   return hip_status(hipGetLastError(), "bigemm_fwd_resident_kernel launch");
 }

@@ -356,12 +356,21 @@ __device__ __forceinline__ void pair_chunk_f8(const u32x2 (&Pu)[KS], const u32x2
 // Output of one 32-channel block of a pair: dl (lane = channel, register i = token kord(i)) is
 // rounded to Ty; with RESIDUAL, x (the lane's token-side operands xk[0], xk[1], same tokens in
 // the same order) is added and the sum rounded again, the reference's two rounding points
-// (omniweave/models/block.py:87-108).  dst(i) is the element address of register i.
-template <class Ty, bool RESIDUAL, class Dst>
-__device__ __forceinline__ void pair_store_block(const f32x16& dl, const u32x4 (&xk)[2], Dst dst) {
+// (omniweave/models/block.py:87-108).  dst(i) is the element address of register i.  With
+// SCALE, the rounded delta of token group 0 (registers 0..7) is multiplied by s0, that of group
+// 1 by s1, and rounded again before the residual: the per-sample drop-path of training
+// (block.py:99-107), where the scale is keep_mask * (1 / keep_probability) of the group's
+// image and the reference's delta * keep_mask / keep_probability rounds once per product.
+template <class Ty, bool RESIDUAL, bool SCALE = false, class Dst>
+__device__ __forceinline__ void pair_store_block(const f32x16& dl, const u32x4 (&xk)[2], Dst dst, float s0 = 1.0f,
+                                                 float s1 = 1.0f) {
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
     uint32_t v = Ty::pack2(dl[i], dl[i + 1]);
+    if constexpr (SCALE) {
+      const float s = i < 8 ? s0 : s1;
+      v = Ty::pack2(Ty::to_f32(lo16(v)) * s, Ty::to_f32(hi16(v)) * s);
+    }
     if constexpr (RESIDUAL) {
       const uint32_t xp = xk[i >> 3][(i & 7) >> 1];
       v = Ty::pack2(Ty::to_f32(lo16(xp)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(xp)) + Ty::to_f32(hi16(v)));
@@ -419,6 +428,7 @@ struct ResidentArgs {
   int32_t norm;     // fuse the RMSNorm prologue
   int32_t residual; // write x + delta instead of delta
   float eps;
+  const float* drop_scale;  // [batch] per-image multiplier of the rounded delta; NULL: none
 };
 
 bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);
@@ -432,7 +442,7 @@ int pack_weights_f32(const void* a_u, const void* a_v, const void* a_o, const vo
 int rms_scale_f32(const float* x, float* scale, int64_t rows, int32_t channels, float eps, hipStream_t stream);
 int launch_fwd_f32(const float* x, float* out, const float* row_scale, const float* packed, const int32_t* tok,
                    const int32_t* chan, int32_t batch, int32_t n_tok, int32_t channels, int32_t q_s, int32_t q_c,
-                   int32_t d, int32_t rd, int32_t residual, hipStream_t stream);
+                   int32_t d, int32_t rd, int32_t residual, const float* drop_scale, hipStream_t stream);
 
 // fp32 backward building blocks (bigemm_bwd_f32.hip).
 int bwd_gather_f32(const float* x, const float* dy, const float* rscale, const int32_t* tok, const int32_t* chan,

@@ -27,7 +27,8 @@ import torch
 from torch import Tensor
 
 from omniwave_amd import _native
-from omniwave_amd.routing import RoutePlan, build_route_plan, device_tables, s2d_rows_table
+from omniwave_amd.routing import (RoutePlan, build_route_plan, device_tables, native_plan, plan_key, plan_tiles,
+                                  s2d_rows_table)
 
 SPATIAL_TILE = 16
 CHANNEL_TILES = (64, 128)
@@ -148,7 +149,7 @@ def _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, compute_d
                      fp8: bool = False):
     srcs = (a_u, a_v, a_o, b_u, b_v, b_o, gamma) + ((norm_weight,) if norm_weight is not None else ())
     versions = tuple(_version(t) for t in srcs)
-    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype, plan.key(), fp8)
+    key = tuple((t.data_ptr(), t.dtype, tuple(t.shape)) for t in srcs) + (compute_dtype, plan_key(plan), fp8)
     entry = _PACK_CACHE.get(key)
     if (entry is not None and None not in versions and entry.versions == versions
             and all(r() is t for r, t in zip(entry.refs, srcs))):
@@ -173,9 +174,13 @@ def clear_pack_cache() -> None:
 # Custom op
 
 
-def _plan_desc(plan: RoutePlan) -> list[int]:
-    return [plan.height, plan.width, plan.channels, plan.spatial_tile, plan.channel_tile,
-            _native.OW_ROUTE[plan.route], plan.radix_level]
+def _plan_desc(plan) -> list[int]:
+    """The custom ops' plan argument: build_route_plan's arguments as integers, read from the
+    plan's fields (this package's RoutePlan or the reference's, omniweave/models/routing.py:17-33)."""
+    h, w, c, g, d, route, level = plan_key(plan)
+    if route not in _native.OW_ROUTE:
+        raise ValueError(f"unknown route type: {route!r}")
+    return [h, w, c, g, d, _native.OW_ROUTE[route], level]
 
 
 def _plan_from_desc(desc: list[int]) -> RoutePlan:
@@ -197,9 +202,11 @@ def bigemm_fwd(
     plan_desc: list[int],
     flags: int,
     eps: float,
+    drop_scale: Tensor | None,
 ) -> Tensor:
     """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC; flag
-    OW_FUSE_FP8 selects the fp8 channel side."""
+    OW_FUSE_FP8 selects the fp8 channel side.  ``drop_scale`` ([B] fp32 or None): per-image
+    multiplier of the rounded delta, the drop-path of training (``ow_bigemm_fwd_drop``)."""
     plan = _plan_from_desc(plan_desc)
     x = x.contiguous()
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
@@ -210,30 +217,38 @@ def bigemm_fwd(
                               fp8)
     tok, ch = device_tables(plan, x.device)
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
-    native_plan = plan.native()
+    oplan = native_plan(plan)
     lib = _native.lib()
-    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), x.shape[0], flags)
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(oplan), x.shape[0], flags)
     workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
+    common = (x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(), tok.data_ptr(), ch.data_ptr(),
+              ctypes.byref(oplan), x.shape[0], b_u.shape[2], _DTYPE_CODE[x.dtype], flags)
     with torch.cuda.device(x.device):
-        _native.check(
-            lib.ow_bigemm_fwd(
-                x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
-                tok.data_ptr(), ch.data_ptr(), ctypes.byref(native_plan), x.shape[0], b_u.shape[2],
-                _DTYPE_CODE[x.dtype], flags, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
-            ),
-            "ow_bigemm_fwd",
-        )
+        if drop_scale is None:
+            _native.check(lib.ow_bigemm_fwd(*common, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device)),
+                          "ow_bigemm_fwd")
+        else:
+            scale = _drop_scale_arg(drop_scale, x)
+            _native.check(lib.ow_bigemm_fwd_drop(*common, scale.data_ptr(), workspace.data_ptr(), ws_bytes,
+                                                 _stream_ptr(x.device)), "ow_bigemm_fwd_drop")
     return out
 
 
+def _drop_scale_arg(drop_scale: Tensor, x: Tensor) -> Tensor:
+    if drop_scale.shape != (x.shape[0],) or drop_scale.device != x.device:
+        raise ValueError(f"drop_scale must be [{x.shape[0]}] on {x.device}, got {tuple(drop_scale.shape)} on "
+                         f"{drop_scale.device}")
+    return drop_scale.to(torch.float32).contiguous()
+
+
 @bigemm_fwd.register_fake
-def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps):
+def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
 def _bigemm_fwd_setup_context(ctx, inputs, output):
-    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps = inputs
-    ctx.save_for_backward(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o)
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale = inputs
+    ctx.save_for_backward(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale)
     ctx.plan_desc, ctx.flags, ctx.eps = list(plan_desc), int(flags), float(eps)
 
 
@@ -242,11 +257,11 @@ def _bigemm_fwd_backward(ctx, grad):
 
     if ctx.flags & _native.OW_FUSE_FP8:
         raise NotImplementedError("the fp8 BiGEMM variant is inference-only (no backward)")
-    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o = ctx.saved_tensors
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale = ctx.saved_tensors
     grads = bigemm_backward(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o,
-                            _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps)
+                            _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps, drop_scale=drop_scale)
     grads = tuple(g if need else None for g, need in zip(grads, ctx.needs_input_grad))
-    return grads + (None, None, None)
+    return grads + (None, None, None, None)
 
 
 bigemm_fwd.register_autograd(_bigemm_fwd_backward, setup_context=_bigemm_fwd_setup_context)
@@ -261,21 +276,39 @@ def _require(x, plan, b_u) -> None:
 def bigemm_delta_hip(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma) -> Tensor:
     """delta for pre-normalised x (omniweave/ops/reference.py:120-173 semantics)."""
     _require(x, plan, b_u)
-    return bigemm_fwd(x, None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), 0, 0.0)
+    return bigemm_fwd(x, None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), 0, 0.0, None)
 
 
 def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, eps: float = 1e-6,
-                     residual: bool = True, fp8: bool = False) -> Tensor:
-    """RMSNorm(x) -> BiGEMM -> (+ x) fused (omniweave/models/block.py:83-108, no drop-path).
+                     residual: bool = True, fp8: bool = False, drop_scale: Tensor | None = None) -> Tensor:
+    """RMSNorm(x) -> BiGEMM -> (+ x) fused (omniweave/models/block.py:83-108).
 
-    ``fp8=True`` runs the channel-side products on e4m3fn MFMAs (inference only; bf16 / fp16
-    activations).
+    ``drop_scale`` ([B] float32 on x's device, or None): the per-sample drop-path of training
+    (block.py:99-107), ``keep_mask / keep_probability`` per image, applied to the rounded delta
+    inside the kernel, with a matching backward (see ``drop_path_scale``).  ``fp8=True`` runs
+    the channel-side products on e4m3fn MFMAs (inference only; bf16 / fp16 activations).
     """
     _require(x, plan, b_u)
     if fp8 and x.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError(f"hip backend not supported: the fp8 variant takes bf16 or fp16 activations, not {x.dtype}")
     flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0) | (_native.OW_FUSE_FP8 if fp8 else 0)
-    return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps))
+    return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps),
+                      drop_scale)
+
+
+def drop_path_scale(batch: int, drop_path_rate: float, dtype: torch.dtype, device) -> Tensor:
+    """Per-image drop-path factors for ``bigemm_block_hip(..., drop_scale=...)``.
+
+    Draws the keep mask exactly as the reference does (omniweave/models/block.py:100-106: a
+    ``[B, 1, 1, 1]`` tensor of the activation dtype, ``bernoulli_(keep_probability)``), so the
+    random stream is consumed identically, and returns ``keep_mask * (1 / keep_probability)``
+    in float32 ([B]): the reference's ``delta * keep_mask / keep_probability`` on the GPU
+    multiplies by that fp32 reciprocal.
+    """
+    keep = 1.0 - drop_path_rate
+    mask = torch.empty((batch, 1, 1, 1), dtype=dtype, device=device).bernoulli_(keep)
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(keep, dtype=torch.float32)
+    return mask.reshape(batch).to(torch.float32) * inv.to(device)
 
 
 # ---------------------------------------------------------------------------------------
@@ -311,15 +344,15 @@ def bigemm_fwd_s2d(
     tok, ch = device_tables(plan, x.device)
     rows = s2d_rows_table(plan, factor, x.device)
     out = torch.empty((b, h // factor, w // factor, c * factor * factor), dtype=x.dtype, device=x.device)
-    native_plan = plan.native()
+    oplan = native_plan(plan)
     lib = _native.lib()
-    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), b, flags)
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(oplan), b, flags)
     workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
         _native.check(
             lib.ow_bigemm_fwd_rows(
                 x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
-                tok.data_ptr(), ch.data_ptr(), rows.data_ptr(), ctypes.byref(native_plan), b, b_u.shape[2],
+                tok.data_ptr(), ch.data_ptr(), rows.data_ptr(), ctypes.byref(oplan), b, b_u.shape[2],
                 _DTYPE_CODE[x.dtype], flags, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),
             ),
             "ow_bigemm_fwd_rows",
@@ -375,7 +408,7 @@ def bigemm_fwd_chain(
     fp8 = bool(flags & _native.OW_FUSE_FP8)
     packed = _cached_operands(norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, x.dtype, plan, fp8)
     tok, ch = device_tables(plan, x.device)
-    q_c = ch.numel() // plan.channel_tile
+    q_c = ch.numel() // plan_tiles(plan)[1]
     if factor > 0:
         if h % factor or w % factor:
             raise ValueError(f"height {h} and width {w} must be divisible by factor {factor}")
@@ -393,16 +426,16 @@ def bigemm_fwd_chain(
                              f"{tuple(stats_in.shape)}")
         stats_in = stats_in.contiguous()
         parts = stats_in.shape[1]
-    native_plan = plan.native()
+    oplan = native_plan(plan)
     lib = _native.lib()
-    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(native_plan), b, flags)
+    ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(oplan), b, flags)
     workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
     written = ctypes.c_int32(0)
     with torch.cuda.device(x.device):
         _native.check(
             lib.ow_bigemm_fwd_chain(
                 x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(),
-                tok.data_ptr(), ch.data_ptr(), rows, ctypes.byref(native_plan), b, b_u.shape[2],
+                tok.data_ptr(), ch.data_ptr(), rows, ctypes.byref(oplan), b, b_u.shape[2],
                 _DTYPE_CODE[x.dtype], flags, None if stats_in is None else stats_in.data_ptr(), parts,
                 stats.data_ptr() if stats.numel() else None, ctypes.byref(written),
                 workspace.data_ptr(), ws_bytes, _stream_ptr(x.device),

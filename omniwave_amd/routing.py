@@ -24,7 +24,12 @@ SHIFT = 2   # omniweave/models/routing.py:72
 
 @dataclass(frozen=True)
 class RoutePlan:
-    """Immutable routing specification for one block (omniweave/models/routing.py:17-33)."""
+    """Immutable routing specification for one block (omniweave/models/routing.py:17-33).
+
+    Exactly the reference's fields.  Everything this package derives from a plan goes through
+    the free functions below (``plan_tiles``, ``plan_key``, ``native_plan``), which read only
+    these fields, so the reference's own ``RoutePlan`` objects are accepted wherever a plan is.
+    """
 
     token_indices: torch.Tensor    # [Q_s, g] int64, pad index = N
     channel_indices: torch.Tensor  # [Q_c, d] int64, pad index = C
@@ -36,22 +41,26 @@ class RoutePlan:
     route: str
     radix_level: int
 
-    @property
-    def spatial_tile(self) -> int:
-        return int(self.token_indices.shape[1])
 
-    @property
-    def channel_tile(self) -> int:
-        return int(self.channel_indices.shape[1])
+def plan_tiles(plan) -> tuple[int, int]:
+    """(g, d): the spatial and channel tile of any plan with the reference's fields."""
+    return int(plan.token_indices.shape[1]), int(plan.channel_indices.shape[1])
 
-    def key(self) -> tuple:
-        """Hashable descriptor (the tensors make the dataclass itself unsuitable as a key)."""
-        return (self.height, self.width, self.channels, self.spatial_tile, self.channel_tile,
-                self.route, self.radix_level)
 
-    def native(self) -> _native.OwPlan:
-        return _native.make_plan(self.height, self.width, self.channels, self.spatial_tile,
-                                 self.channel_tile, self.route, self.radix_level, WINDOW, SHIFT)
+def plan_key(plan) -> tuple:
+    """Hashable descriptor of a plan (its tensors make the dataclass itself unsuitable as a
+    key): the arguments of build_route_plan, which determine the tables."""
+    g, d = plan_tiles(plan)
+    return (int(plan.height), int(plan.width), int(plan.channels), g, d, str(plan.route), int(plan.radix_level))
+
+
+def native_plan(plan) -> _native.OwPlan:
+    """The C-ABI descriptor (OwPlan) of a plan."""
+    g, d = plan_tiles(plan)
+    if plan.route not in _native.OW_ROUTE:
+        raise ValueError(f"unknown route type: {plan.route!r}")
+    return _native.make_plan(int(plan.height), int(plan.width), int(plan.channels), g, d, plan.route,
+                             int(plan.radix_level), WINDOW, SHIFT)
 
 
 def _route_tables(height, width, channels, spatial_tile, channel_tile, route, radix_level):
@@ -119,10 +128,10 @@ def build_stage_schedule(depth: int) -> list[tuple[str, int]]:
 _DEVICE_TABLES: dict[tuple, tuple[torch.Tensor, torch.Tensor]] = {}
 
 
-def device_tables(plan: RoutePlan, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+def device_tables(plan, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
     """int32 token/channel tables of ``plan`` resident on ``device`` (uploaded once)."""
     dev = torch.device(device)
-    key = plan.key() + (dev.type, dev.index)
+    key = plan_key(plan) + (dev.type, dev.index)
     hit = _DEVICE_TABLES.get(key)
     if hit is None:
         tok = plan.token_indices.reshape(-1).to(torch.int32).to(dev)
@@ -135,19 +144,19 @@ def device_tables(plan: RoutePlan, device: torch.device) -> tuple[torch.Tensor, 
 _S2D_ROWS: dict[tuple, torch.Tensor] = {}
 
 
-def s2d_rows_table(plan: RoutePlan, factor: int, device: torch.device) -> torch.Tensor:
+def s2d_rows_table(plan, factor: int, device: torch.device) -> torch.Tensor:
     """int32 ``[Q_s * g]`` output-row table on ``device`` (``ow_route_s2d_rows``): the row each
     token slot occupies in ``space_to_depth(out, factor)`` viewed as ``[H*W, C]`` rows per image
     (omniweave/models/backbone.py:14-27); pad slots hold H*W."""
     dev = torch.device(device)
-    key = plan.key() + (int(factor), dev.type, dev.index)
+    key = plan_key(plan) + (int(factor), dev.type, dev.index)
     hit = _S2D_ROWS.get(key)
     if hit is None:
         lib = _native.lib()
         tok = np.ascontiguousarray(plan.token_indices.reshape(-1).numpy(), dtype=np.int32)
         rows = np.empty_like(tok)
         ptr = _native._c_int32_p
-        native = plan.native()
+        native = native_plan(plan)
         _native.check(lib.ow_route_s2d_rows(_native.ctypes.byref(native), int(factor), tok.ctypes.data_as(ptr),
                                             rows.ctypes.data_as(ptr)), "ow_route_s2d_rows")
         hit = torch.from_numpy(rows).to(dev)

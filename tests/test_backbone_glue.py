@@ -14,7 +14,7 @@ import omniwave_amd
 from omniwave_amd import _native
 from omniwave_amd.backbone import space_to_depth_nhwc
 from omniwave_amd.hip import stem_is_supported
-from omniwave_amd.routing import s2d_rows_table
+from omniwave_amd.routing import native_plan, s2d_rows_table
 from oracle.backbone import space_to_depth_loops, space_to_depth_nhwc as oracle_s2d, stem_reference
 
 
@@ -73,7 +73,7 @@ def test_s2d_rows_rejects_indivisible_sizes() -> None:
     plan = omniwave_amd.build_route_plan(7, 7, 128, 16, 64, "local", 0)
     tok = np.ascontiguousarray(plan.token_indices.reshape(-1).numpy(), dtype=np.int32)
     out = np.empty_like(tok)
-    native = plan.native()
+    native = native_plan(plan)
     rc = _native.lib().ow_route_s2d_rows(ctypes.byref(native), 2, tok.ctypes.data_as(_native._c_int32_p),
                                          out.ctypes.data_as(_native._c_int32_p))
     assert rc != 0

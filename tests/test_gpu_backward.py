@@ -55,7 +55,7 @@ def make_case(b, h, w, c, d, route, level, dtype, seed=0, rd=None):
 
 def oracle_grads(x, plan, params, dy, fused: bool, residual: bool):
     """fp32 CPU autograd of the oracle block (fused) or delta (not fused)."""
-    oplan = oracle_plan(plan.height, plan.width, plan.channels, plan.spatial_tile, plan.channel_tile,
+    oplan = oracle_plan(plan.height, plan.width, plan.channels, 16, int(plan.channel_indices.shape[1]),
                         plan.route, plan.radix_level)
     xs = x.float().clone().requires_grad_(True)
     ps = {k: v.clone().requires_grad_(True) for k, v in params.items()}

@@ -64,7 +64,7 @@ def rounded(params, dtype):
 
 def oracle_delta(x, plan, params, dtype):
     p = rounded(params, dtype)
-    oplan = oracle_plan(plan.height, plan.width, plan.channels, plan.spatial_tile, plan.channel_tile,
+    oplan = oracle_plan(plan.height, plan.width, plan.channels, 16, int(plan.channel_indices.shape[1]),
                         plan.route, plan.radix_level)
     return bigemm_delta_reference(x=x.float(), plan=oplan, **p)
 

@@ -64,7 +64,7 @@ def emulate_fp8_delta(x, plan, p):
     """The fp8 kernel's arithmetic on the CPU: delta [B,H,W,C] fp32 (rounded as the kernel)."""
     dt = x.dtype
     c = plan.channels
-    oplan = oracle_plan(plan.height, plan.width, c, 16, plan.channel_tile, plan.route, plan.radix_level)
+    oplan = oracle_plan(plan.height, plan.width, c, 16, int(plan.channel_indices.shape[1]), plan.route, plan.radix_level)
     var = x.float().square().mean(dim=-1, keepdim=True)
     r = torch.rsqrt(var.to(dt) + 1e-6).float()
     tiles, mask = pack_tiles(x.float(), oplan)                     # [B, Q_s, Q_c, g, d]

@@ -72,7 +72,10 @@ def test_fwd_rejects_bad_arguments_without_touching_the_gpu() -> None:
     P = ctypes.c_void_p(16)
     NB = lib.ow_packed_weight_bytes(4, 128, 256, bf16)
     out = ctypes.c_void_p(32)
-    assert fwd(P, out, NB, plan, flags=_native.OW_FUSE_NORM) == 1 and b"workspace" in lib.ow_last_error()
+    # An unaligned x takes element access, whose RMSNorm statistics come from a pass into the
+    # workspace: without one the call is refused before any launch.
+    x_unaligned = ctypes.c_void_p(18)
+    assert fwd(x_unaligned, out, NB, plan, flags=_native.OW_FUSE_NORM) == 1 and b"workspace" in lib.ow_last_error()
     assert lib.ow_fwd_workspace_bytes(ctypes.byref(plan), 3, _native.OW_FUSE_NORM) == 3 * 196 * 4
     assert lib.ow_fwd_workspace_bytes(ctypes.byref(plan), 3, 0) == 0
     bad = _native.make_plan(14, 14, 512, 8, 128, "local", 0)
@@ -92,9 +95,10 @@ def test_fwd_chain_rejects_bad_arguments_without_touching_the_gpu() -> None:
     NB = lib.ow_packed_weight_bytes(4, 128, 256, bf16)
     written = ctypes.c_int32(7)
 
-    def chain(dtype=bf16, flags=_native.OW_FUSE_NORM, stats_in=None, parts=0, w=ctypes.byref(written)):
-        return lib.ow_bigemm_fwd_chain(P, out, 1e-6, P, NB, P, P, None, ctypes.byref(plan), 1, 256, dtype, flags,
-                                       stats_in, parts, None, w, None, 0, None)
+    def chain(dtype=bf16, flags=_native.OW_FUSE_NORM, stats_in=None, parts=0, w=ctypes.byref(written), x=P,
+              stats_out=None):
+        return lib.ow_bigemm_fwd_chain(x, out, 1e-6, P, NB, P, P, None, ctypes.byref(plan), 1, 256, dtype, flags,
+                                       stats_in, parts, stats_out, w, None, 0, None)
 
     assert chain(w=None) == 1 and b"stats_written" in lib.ow_last_error()
     assert chain(dtype=f32) == 2 and written.value == 0
@@ -102,7 +106,13 @@ def test_fwd_chain_rejects_bad_arguments_without_touching_the_gpu() -> None:
     assert chain(stats_in=P, parts=65) == 1 and b"stats_in_parts" in lib.ow_last_error()
     assert chain(stats_in=P, parts=4, flags=0) == 1 and b"OW_FUSE_NORM" in lib.ow_last_error()
     written.value = 7
-    assert chain() == 1 and b"workspace" in lib.ow_last_error() and written.value == 0
+    # Unaligned x: element access, RMSNorm statistics from a workspace pass; none is given.
+    assert chain(x=ctypes.c_void_p(18)) == 1 and b"workspace" in lib.ow_last_error() and written.value == 0
+    # stats_in ([196, 4] floats) and stats_out ([196, 4]) must not share memory.
+    base = 1 << 20
+    for s_in, s_out in ((base, base), (base, base + 4 * 196 * 4 - 4), (base + 4, base)):
+        assert chain(stats_in=ctypes.c_void_p(s_in), parts=4, stats_out=ctypes.c_void_p(s_out)) == 1
+        assert b"overlap" in lib.ow_last_error()
 
 
 def test_hip_is_supported_reasons_on_cpu() -> None:
