@@ -234,6 +234,24 @@ int ow_bigemm_fwd_drop(const void* x, void* out, float eps,
                        void* stream);
 
 /*
+ * ow_bigemm_fwd without a workspace argument.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops with
+ * a fixed footprint, harnesses that forbid hipMalloc).  The RMSNorm row scales that
+ * ow_bigemm_fwd keeps in its workspace (see ow_fwd_workspace_bytes) go to a scratch array in
+ * the library's device memory instead: 1,048,576 fp32 rows (4 MiB), held on each GPU the
+ * library runs on until the process ends.  A launch that would need more rows (batch * H * W)
+ * is rejected with OW_ERR_UNSUPPORTED before any device work.  The call allocates nothing; the
+ * first call on a device looks up the array's address there (hipGetSymbolAddress).  All calls
+ * on one GPU share its array, so calls that overlap on one GPU (concurrent streams, threads)
+ * race; calls ordered on one stream do not.  Results equal ow_bigemm_fwd's bit for bit.
+ */
+int ow_bigemm_fwd_noalloc(const void* x, void* out, float eps,
+                          const void* packed, size_t packed_bytes,
+                          const int32_t* token_index, const int32_t* channel_index,
+                          const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype,
+                          int32_t flags, void* stream);
+
+/*
  * Backbone stem as one gather-GEMM (omniweave/models/backbone.py:121,173-176): image
  * [batch, 3, height, width] (NCHW) -> space_to_depth(4) -> x W^T with weight [n_out, 48]
  * (nn.Linear(48, n_out, bias=False), input order (row offset, column offset, channel)) ->

@@ -139,9 +139,7 @@ constexpr int kNormPartials = 3;
 //                 levels >= 1, omniweave/models/routing.py:107-121): every 16-byte vector of
 //                 a row holds 8/n consecutive tile columns of the group
 //   kModeElement  anything else (padded groups, unaligned or ragged rows): element access
-constexpr int kModeContig = 0;
-constexpr int kModeStrided = 1;
-constexpr int kModeElement = 2;
+// (kModeContig, kModeStrided, kModeElement: ow_device.h)
 constexpr int kBatch = 16;  // global loads kept in flight per thread by the gather / scatter loops
 
 // The M = 8/n elements of a strided channel group held by one 16-byte row vector (element
@@ -970,6 +968,44 @@ int dispatch_fwd(const FwdArgs& a, int d, int rd, hipStream_t s) {
 }  // namespace
 }  // namespace ow
 
+namespace ow {
+
+// Kernel and channel-group access of a bf16 / f16 launch (routing.py:107-121: identity channel
+// order at level 0 or with one group; at levels >= 1 group qc is the channels congruent to
+// (qc + level) mod q_c).
+FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c, int32_t dtype, int32_t flags) {
+  const int32_t c = plan->channels, d = plan->channel_tile;
+  FwdPath p{};
+  p.resident = dtype != OW_DTYPE_F32 && !(flags & OW_FUSE_FP8) && resident_supported(d, 2 * d, c, q_c) &&
+               aligned16(x) && aligned16(out);
+  const bool vec_ok = (c % 8 == 0) && aligned16(x) && aligned16(out);
+  const bool identity = plan->radix_level == 0 || q_c <= 1;
+  p.mode = kModeElement;
+  if (vec_ok && identity && c % d == 0)
+    p.mode = kModeContig;
+  else if (vec_ok && !identity && c == q_c * d && (q_c == 2 || q_c == 4 || q_c == 8))
+    p.mode = kModeStrided;
+  return p;
+}
+
+// The RMSNorm row scales of a launch come from one of four places (kNorm*); only kNormBuffer
+// (and the fp32 kernel with OW_FUSE_NORM) uses the workspace, for batch * H * W floats.
+bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype,
+                            int32_t flags, bool stats_in) {
+  if (!(flags & OW_FUSE_NORM)) return false;
+  if (dtype == OW_DTYPE_F32) return true;
+  int32_t q_s = 0, q_c = 0;
+  if (ow_plan_dims(plan, &q_s, &q_c) != OW_OK) return false;
+  const FwdPath p = fwd_path(x, out, plan, q_c, dtype, flags);
+  if (p.resident && rd == 2 * plan->channel_tile) return false;
+  if (p.mode == kModeElement) return true;
+  if (stats_in) return false;
+  const int32_t c = plan->channels, j = c / 128;
+  return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));
+}
+
+}  // namespace ow
+
 extern "C" {
 
 size_t ow_packed_weight_bytes(int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype) {
@@ -1092,19 +1128,6 @@ int ow_rms_scale(const void* x, float* scale, int64_t rows, int32_t channels, fl
   return OW_OK;
 }
 
-// The RMSNorm row scales of a launch come from one of four places (kNorm*); only kNormBuffer
-// (and the fp32 kernel with OW_FUSE_NORM) uses the workspace, for batch * H * W floats.
-// Returns true when the launch needs it.
-static bool fwd_needs_scale_buffer(bool fp32, bool norm, bool resident, int32_t mode, bool stats_in, int32_t c) {
-  if (!norm) return false;
-  if (fp32) return true;
-  if (resident) return false;
-  if (mode == ow::kModeElement) return true;
-  if (stats_in) return false;
-  const int32_t j = c / 128;
-  return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));
-}
-
 static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
                             const int32_t* token_index, const int32_t* channel_index, const int32_t* out_rows,
                             const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
@@ -1141,20 +1164,12 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   OW_CHECK_ARG(static_cast<int64_t>(batch) * n < (int64_t(1) << 31), "batch * H * W must be < 2^31");
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  // Kernel and channel-group access (routing.py:107-121): identity order at level 0 or with one
-  // group; at levels >= 1 group qc is the channels congruent to (qc + level) mod q_c.
   const bool fp32 = dtype == OW_DTYPE_F32;
-  const bool resident = !fp32 && !fp8 && ow::resident_supported(d, rd, c, q_c) && ow::aligned16(x) &&
-                        ow::aligned16(out);
-  const bool vec_ok = (c % 8 == 0) && ow::aligned16(x) && ow::aligned16(out);
-  const bool identity = plan->radix_level == 0 || q_c <= 1;
-  int32_t mode = ow::kModeElement;
-  if (vec_ok && identity && c % d == 0)
-    mode = ow::kModeContig;
-  else if (vec_ok && !identity && c == q_c * d && (q_c == 2 || q_c == 4 || q_c == 8))
-    mode = ow::kModeStrided;
+  const ow::FwdPath path = ow::fwd_path(x, out, plan, q_c, dtype, flags);
+  const bool resident = path.resident && rd == 2 * d;
+  const int32_t mode = path.mode;
   float* scale = nullptr;
-  if (fwd_needs_scale_buffer(fp32, norm, resident, mode, stats_in != nullptr, c)) {
+  if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr)) {
     const size_t need = ow_fwd_workspace_bytes(plan, batch, flags);
     OW_CHECK_ARG(workspace && workspace_bytes >= need, "workspace holds %zu bytes; %zu needed", workspace_bytes,
                  need);

@@ -432,6 +432,20 @@ struct ResidentArgs {
 };
 
 bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);
+
+// Dispatch of a forward launch (bigemm_fwd.hip): the resident kernel (given rd = 2 d), or the
+// streamed kernel's channel-group access mode; and whether the launch needs the batch * H * W
+// fp32 RMSNorm row-scale buffer (statistics from a separate pass).
+constexpr int kModeContig = 0;
+constexpr int kModeStrided = 1;
+constexpr int kModeElement = 2;
+struct FwdPath {
+  bool resident;
+  int32_t mode;
+};
+FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c, int32_t dtype, int32_t flags);
+bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype,
+                            int32_t flags, bool stats_in);
 int launch_fwd_resident(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
 
 // fp32 path (bigemm_fwd_f32.hip): operand packing, RMSNorm row scales and the forward.
