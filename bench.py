@@ -355,16 +355,23 @@ def fp8_section(model_batch: int, steps: int, dev) -> dict:
     del inputs
     torch.manual_seed(0)
     model = omniwave_amd.create_model("omniweave_t").to(device=dev, dtype=torch.bfloat16).eval()
-    omniwave_amd.enable_fp8(model)
     gen = torch.Generator().manual_seed(0)
     xi = torch.randn(model_batch, 3, 224, 224, generator=gen).to(device=dev, dtype=torch.bfloat16)
+    models = {}
     with torch.inference_mode():
-        ms = _graph_ms(lambda: model(xi), 1, steps)
+        for label, min_tile in (("fp8_d128", 128), ("fp8_all", 64), ("bf16", 10 ** 9)):
+            omniwave_amd.enable_fp8(model, min_channel_tile=min_tile)
+            ms = _graph_ms(lambda: model(xi), 1, steps)
+            models[label] = {"images_per_s": round(model_batch / (ms * 1e-3), 1), "ms_per_batch": round(ms, 3)}
+    omniwave_amd.enable_fp8(model, enabled=False)
     return {
-        "workload": f"fused block fp8 channel side, {name} shifted0; omniweave_t fp8 at [{model_batch},3,224,224]",
+        "workload": f"fused block fp8 channel side (V' on the K=64 e4m3 MFMA), {name} shifted0; omniweave_t at "
+                    f"[{model_batch},3,224,224] with fp8 on the d=128 blocks (fp8_d128, the default), on every "
+                    "block (fp8_all), and none (bf16), same process",
         "stage3_sweep": sweep,
-        "model_images_per_s": round(model_batch / (ms * 1e-3), 1),
-        "model_ms_per_batch": round(ms, 3),
+        "model_images_per_s": models["fp8_d128"]["images_per_s"],
+        "model_ms_per_batch": models["fp8_d128"]["ms_per_batch"],
+        "model": models,
     }
 
 

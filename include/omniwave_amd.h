@@ -118,12 +118,15 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o,
 
 /*
  * fp8 inference variant (no counterpart in the reference, which has no fp8 path): the
- * channel-side products U' = P B_u'' and V' = P B_v'' run on e4m3fn MFMAs with fp32
- * accumulation; the token side, the gate, Z B_o and A_o W stay in the activation dtype.
- * Per-tensor scales: B_u'' and B_v'' by their absmax over all channel groups; P by the static
- * bound ||A||_inf sqrt(C) that the RMSNorm'd rows obey (hence OW_FUSE_NORM).  Packed layout:
- * the token-side head (act_dtype), 16 scale floats, then per (q, 32-row chunk) the fp8
- * B_u'' / B_v'' fragments and the act_dtype B_o fragments.  Arguments as ow_pack_weights;
+ * channel-side product V' = P B_v'' runs on the K = 64 e4m3 MFMA with fp32 accumulation; the
+ * token side, U' = P B_u'', the gate, Z B_o and A_o W stay in the activation dtype (each
+ * e4m3-quantised operand adds ~2.6% rel-L2 to delta; quantising U' as well would put delta
+ * past 5e-2 of fp32).  Per-tensor scales: B_v'' by its absmax over all channel groups; P_v by
+ * the static bound ||A_v||_inf sqrt(C) that the RMSNorm'd rows obey (hence OW_FUSE_NORM), its
+ * multiplier folded into the token operand; V''s dequantisation folded into the packed B_o.
+ * Packed layout: the token-side head (act_dtype), 16 scale floats, then per (q, 32-row chunk)
+ * in 1 KB units the act_dtype B_u'' fragments, the fp8 B_v'' K64 fragments (2 KB each) and the
+ * act_dtype B_o fragments, padded to a multiple of 4 units.  Arguments as ow_pack_weights;
  * `packed` holds ow_packed_weight_bytes_fp8(q_c, d, rd) bytes.
  */
 size_t ow_packed_weight_bytes_fp8(int32_t q_c, int32_t d, int32_t rd);

@@ -147,10 +147,16 @@ class OmniWeaveBlock(nn.Module):
         return x + delta
 
 
-def enable_fp8(model: nn.Module, enabled: bool = True) -> nn.Module:
-    """Switch every OmniWeaveBlock of ``model`` to the fp8-e4m3 channel side (inference with
-    bf16 / fp16 activations on the hip backend) or back; returns ``model``."""
+def enable_fp8(model: nn.Module, enabled: bool = True, min_channel_tile: int = 128) -> nn.Module:
+    """Switch the OmniWeaveBlocks of ``model`` whose channel tile is at least
+    ``min_channel_tile`` to the fp8-e4m3 channel side (inference with bf16 / fp16 activations on
+    the hip backend), or every block back (``enabled=False``); returns ``model``.
+
+    The default leaves d = 64 blocks (OmniWeave-T's stages 1-2) in bf16: their resident-weight
+    kernel is bound by VALU work, which fp8 MFMAs do not reduce, and the fp8 variant of those
+    shapes runs on the slower streamed kernel.  ``min_channel_tile=64`` switches every block.
+    """
     for module in model.modules():
         if isinstance(module, OmniWeaveBlock):
-            module.fp8 = enabled
+            module.fp8 = enabled and int(module.b_u.shape[1]) >= min_channel_tile
     return model

@@ -204,8 +204,11 @@ bigemm_fwd_kernel(FwdArgs a) {
   constexpr int FR_U = KS;         // B_u'^T fragments per chunk (B_v'^T the same)
   constexpr int FR_O = 2 * MB;     // B_o^T fragments per chunk (MB blocks x 2 K steps)
   constexpr int FR_CH = 2 * FR_U + FR_O;
-  // 1 KB copy units per chunk: 2 KS fp8 fragments of 512 bytes + FR_O Ty fragments with F8.
-  constexpr int CH_UNITS = F8 ? FR_U + FR_O : FR_CH;
+  // 1 KB copy units per chunk (fp8: KS Ty B_u'^T, KS / 4 two-unit fp8 B_v'^T and FR_O Ty B_o
+  // fragments, padded to whole copy rounds).
+  constexpr int CH_UNITS = F8 ? f8_chunk_units(D) : FR_CH;
+  constexpr int F8_BV = FR_U;               // fp8: first unit of the B_v'^T K64 fragments
+  constexpr int F8_BO = FR_U + 2 * (D / 64);  // fp8: first unit of the B_o fragments
   constexpr int CH_ELEMS = CH_UNITS * kFragElems;
   constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, in 16-bit elements
   static_assert(TPW % 2 == 0, "token groups come in pairs");
@@ -445,10 +448,13 @@ bigemm_fwd_kernel(FwdArgs a) {
   int col[KS / 2];
 #pragma unroll
   for (int cb = 0; cb < KS / 2; ++cb) col[cb] = 32 * cb + l32;
-  using POp = std::conditional_t<F8, u32x2, u32x4>;  // P^T operand: fp8 or Ty K steps
-  POp Pu[NP][KS], Pv[NP][KS];
+  // P^T operands: Ty K steps; with F8, P_v as fp8 K64 operands (KS / 4 of them).
+  constexpr int KV = F8 ? KS / 4 : KS;
+  using VOp = std::conditional_t<F8, u32x8, u32x4>;
+  u32x4 Pu[NP][KS];
+  VOp Pv[NP][KV];
   u32x4 xk[NP][KS / 2][2];  // the lane's x values, kept for the residual
-  const float* f8s = reinterpret_cast<const float*>(a.packed + kHeadElems);  // fp8 scales
+  const float qv = F8 ? reinterpret_cast<const float*>(a.packed + kHeadElems)[kF8QuantPv] : 1.0f;  // fp8 scales
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int row0 = (wave * TPW + 2 * p) * kG;
@@ -456,11 +462,10 @@ bigemm_fwd_kernel(FwdArgs a) {
     if (a.norm != kNormNone) {  // lane's slots j are tokens 16 tg + kord(j, hh) of its group tg
       const float* r8 = &rsc[row0 + 16 * ((lane >> 4) & 1) + 4 * hh];
       bu = scale8<Ty>(fAu, r8);
-      bv = scale8<Ty>(fAv, r8);
+      bv = F8 ? scale8m<Ty>(fAv, r8, qv) : scale8<Ty>(fAv, r8);  // fp8: P_v comes out quantised
     }
     if constexpr (F8)
-      pair_token_side_f8<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, f8s[kF8QuantPu], f8s[kF8QuantPv], Pu[p],
-                                 Pv[p], xk[p]);
+      pair_token_side_f8<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, Pu[p], Pv[p], xk[p]);
     else
       pair_token_side<Ty, KS>(xs + row0 * LDX, LDX, col, bu, bv, lane, Pu[p], Pv[p], xk[p]);
   }
@@ -480,12 +485,12 @@ bigemm_fwd_kernel(FwdArgs a) {
       U = f32x16{};
       V = f32x16{};
       if constexpr (F8) {
-        const u32x2* c8 = reinterpret_cast<const u32x2*>(chunk_buf(ec));
+        const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
+        const u32x8* c8 = reinterpret_cast<const u32x8*>(chunk_buf(ec) + F8_BV * kFragElems);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          U = mma32_f8(c8[ks * (kF8FragBytes / 8) + lane], Pu[0][ks], U);
-          V = mma32_f8(c8[(FR_U + ks) * (kF8FragBytes / 8) + lane], Pv[0][ks], V);
-        }
+        for (int ks = 0; ks < KS; ++ks) U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[0][ks], U);
+#pragma unroll
+        for (int s = 0; s < KV; ++s) V = mma32x64_f8(c8[s * (kF8K64Bytes / 32) + lane], Pv[0][s], V);
       } else {
         const u32x4* cf = reinterpret_cast<const u32x4*>(chunk_buf(ec));
 #pragma unroll
@@ -495,13 +500,10 @@ bigemm_fwd_kernel(FwdArgs a) {
         }
       }
     };
-    // Gate and W += Z B_o of chunk ec.  The fp8 dequantisation factors are read once, before
-    // the loop: a global load inside it would make the waits for the chunk copies (which count
-    // all outstanding vector-memory operations) wait for the copy of chunk ec + 2 as well.
-    const float du = F8 ? f8s[kF8DeqU] : 1.0f, dv = F8 ? f8s[kF8DeqV] : 1.0f;
+    // Gate and W += Z B_o of chunk ec (fp8: the packed B_o carries V''s dequantisation).
     auto gate_w = [&](int ec, const f32x16& U, const f32x16& V) {
       const uint16_t* cw = chunk_buf(ec);
-      const u32x4* co = reinterpret_cast<const u32x4*>(F8 ? cw + FR_U * kFragElems : cw + 2 * FR_U * kFragElems);
+      const u32x4* co = reinterpret_cast<const u32x4*>(F8 ? cw + F8_BO * kFragElems : cw + 2 * FR_U * kFragElems);
       u32x4 Z[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s)
@@ -509,8 +511,7 @@ bigemm_fwd_kernel(FwdArgs a) {
         for (int q = 0; q < 4; ++q) {
           const float u0 = U[8 * s + 2 * q], u1 = U[8 * s + 2 * q + 1];
           const float v0 = V[8 * s + 2 * q], v1 = V[8 * s + 2 * q + 1];
-          Z[s][q] = F8 ? Ty::pack2(silu_gate(u0 * du, v0 * dv), silu_gate(u1 * du, v1 * dv))
-                       : Ty::pack2(silu_gate(u0, v0), silu_gate(u1, v1));
+          Z[s][q] = Ty::pack2(silu_gate(u0, v0), silu_gate(u1, v1));
         }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -554,14 +555,13 @@ bigemm_fwd_kernel(FwdArgs a) {
     const uint16_t* cw = chunk_buf(ec);
     const u32x4* cf = reinterpret_cast<const u32x4*>(cw);
     if constexpr (F8) {
-      const u32x2* c8 = reinterpret_cast<const u32x2*>(cw);
-      const u32x4* co = reinterpret_cast<const u32x4*>(cw + FR_U * kFragElems);
-      auto fu = [&](int ks) { return c8[ks * (kF8FragBytes / 8) + lane]; };
-      auto fv = [&](int ks) { return c8[(FR_U + ks) * (kF8FragBytes / 8) + lane]; };
+      const u32x8* c8 = reinterpret_cast<const u32x8*>(cw + F8_BV * kFragElems);
+      const u32x4* co = reinterpret_cast<const u32x4*>(cw + F8_BO * kFragElems);
+      auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
+      auto fv = [&](int s) { return c8[s * (kF8K64Bytes / 32) + lane]; };
       auto fo = [&](int mb, int s) { return co[(2 * mb + s) * (kFragElems / 8) + lane]; };
-      const float du = f8s[kF8DeqU], dv = f8s[kF8DeqV];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, du, dv, W[p]);
+      for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
     } else {
       auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
       auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
@@ -776,8 +776,8 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
 }
 
 // fp8 channel side: per-tensor scales, in three launches (f8_zero, f8_amax, f8_finalize).
-// f8_amax: absmax of the folded B_u'' / B_v'' over all channel groups, 8 values per thread,
-// wave maxima combined with atomic max on the (non-negative) float bits.
+// f8_amax: absmax of the folded B_v'' over all channel groups, 8 values per thread, wave
+// maxima combined with atomic max on the (non-negative) float bits.
 __global__ void __launch_bounds__(64) f8_zero_kernel(float* scales) {
   if (threadIdx.x < kF8ScaleFloats) scales[threadIdx.x] = 0.0f;
 }
@@ -785,7 +785,7 @@ __global__ void __launch_bounds__(64) f8_zero_kernel(float* scales) {
 __global__ void __launch_bounds__(256) f8_amax_kernel(PackArgs p, float* scales) {
   const int n = p.q_c * p.d * p.rd;
   const int i0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-  float mu = 0.0f, mv = 0.0f;
+  float mv = 0.0f;
   for (int i = i0; i < i0 + 8 && i < n; ++i) {
     const int qc = i / p.rd;  // q * d + c
     float w = 1.0f;
@@ -793,53 +793,37 @@ __global__ void __launch_bounds__(256) f8_amax_kernel(PackArgs p, float* scales)
       const int gc = p.chan[qc];
       w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
     }
-    mu = fmaxf(mu, fabsf(load_f32(p.b_u, i, p.wdtype) * w * kNegLog2e));
     mv = fmaxf(mv, fabsf(load_f32(p.b_v, i, p.wdtype) * w * kNegLn2));
   }
-  for (int m = 32; m > 0; m >>= 1) {
-    mu = fmaxf(mu, __shfl_xor(mu, m));
-    mv = fmaxf(mv, __shfl_xor(mv, m));
-  }
-  if ((threadIdx.x & 63) == 0) {
-    atomicMax(reinterpret_cast<unsigned int*>(scales + kF8AmaxBu), __float_as_uint(mu));
-    atomicMax(reinterpret_cast<unsigned int*>(scales + kF8AmaxBv), __float_as_uint(mv));
-  }
+  for (int m = 32; m > 0; m >>= 1) mv = fmaxf(mv, __shfl_xor(mv, m));
+  if ((threadIdx.x & 63) == 0) atomicMax(reinterpret_cast<unsigned int*>(scales + kF8AmaxBv), __float_as_uint(mv));
 }
 
-// The P operand is quantised with the static bound |P| <= ||A||_inf sqrt(C) (1.02): the
-// RMSNorm'd rows satisfy |x_c r| <= sqrt(C), the 2% cover the Ty rounding of r and of the A
-// operand.  One wave: lane i < 16 sums |row i| of the Ty-rounded A_u / A_v.
+// P_v is quantised with the static bound |P_v| <= ||A_v||_inf sqrt(C) (1.02): the RMSNorm'd
+// rows satisfy |x_c r| <= sqrt(C), the 2% cover the Ty rounding of r and of the token operand.
+// One wave: lane i < 16 sums |row i| of the Ty-rounded A_v.  V' = V'_q s_b / q_v.
 template <class Ty>
 __global__ void __launch_bounds__(64) f8_finalize_kernel(PackArgs p, float* scales) {
   const int lane = threadIdx.x;
-  float su = 0.0f, sv = 0.0f;
-  if (lane < kG) {
-    for (int j = 0; j < kG; ++j) {
-      su += fabsf(Ty::to_f32(Ty::from_f32(load_f32(p.a_u, lane * kG + j, p.wdtype))));
-      sv += fabsf(Ty::to_f32(Ty::from_f32(load_f32(p.a_v, lane * kG + j, p.wdtype))));
-    }
-  }
-  for (int m = 32; m > 0; m >>= 1) {
-    su = fmaxf(su, __shfl_xor(su, m));
-    sv = fmaxf(sv, __shfl_xor(sv, m));
-  }
+  float sv = 0.0f;
+  if (lane < kG)
+    for (int j = 0; j < kG; ++j) sv += fabsf(Ty::to_f32(Ty::from_f32(load_f32(p.a_v, lane * kG + j, p.wdtype))));
+  for (int m = 32; m > 0; m >>= 1) sv = fmaxf(sv, __shfl_xor(sv, m));
   if (lane == 0) {
-    const float au = scales[kF8AmaxBu], av = scales[kF8AmaxBv];
+    const float av = scales[kF8AmaxBv];
     const float root_c = sqrtf(static_cast<float>(p.channels)) * 1.02f;
-    const float qu = su > 0.0f ? kF8Max / (su * root_c) : 1.0f;
     const float qv = sv > 0.0f ? kF8Max / (sv * root_c) : 1.0f;
-    const float sbu = au > 0.0f ? au / kF8Max : 1.0f;
     const float sbv = av > 0.0f ? av / kF8Max : 1.0f;
-    scales[kF8DeqU] = sbu / qu;
     scales[kF8DeqV] = sbv / qv;
-    scales[kF8QuantPu] = qu;
     scales[kF8QuantPv] = qv;
   }
 }
 
-// fp8 packing, one thread per packed value: the Ty head, then per (q, ec) the e4m3fn
-// B_u'^T / B_v'^T fragments (value / s_b, s_b = absmax / 448) and the Ty B_o fragments, with
-// the lane / slot order of pack_kernel.
+// fp8 packing, one thread per 16-bit unit of the packed buffer: the Ty head, then per (q, ec)
+// the Ty B_u'^T fragments (pack_kernel's order), the e4m3fn B_v'^T K64 fragments (value / s_b,
+// s_b = absmax / 448; lane (e, hh) byte j = B_v''[64 s + 32 (j / 16) + 8 ((j % 16) / 4) + 4 hh
+// + j % 4][32 ec + e], two bytes per thread) and the Ty B_o fragments times V''s
+// dequantisation factor, then the chunk's padding (zero).
 template <class Ty>
 __global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* scales) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -855,36 +839,50 @@ __global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* s
     reinterpret_cast<uint16_t*>(base)[idx] = Ty::from_f32(val);
     return;
   }
-  const int ks_n = p.d / 16, mb_n = p.d / 32, nch = p.rd / 32;
-  const int64_t ch_units = static_cast<int64_t>(2 * ks_n + 2 * mb_n) * kFragElems;
-  const int64_t ch_bytes = static_cast<int64_t>(2 * ks_n) * kF8FragBytes + static_cast<int64_t>(2 * mb_n) * 2 * kFragElems;
+  const int ks_n = p.d / 16, nk64 = p.d / 64, nch = p.rd / 32;
+  const int64_t ch_units16 = static_cast<int64_t>(f8_chunk_units(p.d)) * kFragElems;  // 16-bit units per chunk
   int64_t rem = idx - kHeadElems;
-  const int q = static_cast<int>(rem / (nch * ch_units));
-  rem -= static_cast<int64_t>(q) * nch * ch_units;
-  const int ec = static_cast<int>(rem / ch_units);
-  rem -= static_cast<int64_t>(ec) * ch_units;
-  const int fr = static_cast<int>(rem / kFragElems);
+  const int q = static_cast<int>(rem / (nch * ch_units16));
+  rem -= static_cast<int64_t>(q) * nch * ch_units16;
+  const int ec = static_cast<int>(rem / ch_units16);
+  rem -= static_cast<int64_t>(ec) * ch_units16;
+  uint16_t* chunk = reinterpret_cast<uint16_t*>(base + kF8HeadBytes) + (static_cast<int64_t>(q) * nch + ec) * ch_units16;
+  const int fr = static_cast<int>(rem / kFragElems);  // 1 KB unit of the chunk
   const int e = static_cast<int>(rem % kFragElems);
-  const int lane = e / 8, j = e % 8;
-  const int l32 = lane & 31, hh = lane >> 5;
-  uint8_t* chunk = base + kF8HeadBytes + (static_cast<int64_t>(q) * nch + ec) * ch_bytes;
-  if (fr < 2 * ks_n) {
-    const bool is_u = fr < ks_n;
-    const int ks = fr % ks_n;
-    const int col = 32 * ec + l32;
-    const int c = 16 * ks + 8 * (j / 4) + 4 * hh + (j % 4);
-    const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + col;
-    float w = 1.0f;
-    if (p.chan) {
-      const int gc = p.chan[q * p.d + c];
-      w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
-    }
-    const float val = load_f32(is_u ? p.b_u : p.b_v, src, p.wdtype) * w * (is_u ? kNegLog2e : kNegLn2);
-    const float amax = scales[is_u ? kF8AmaxBu : kF8AmaxBv];
+  auto norm_w = [&](int c) {
+    if (!p.chan) return 1.0f;
+    const int gc = p.chan[q * p.d + c];
+    return (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
+  };
+  float out = 0.0f;
+  if (fr < ks_n) {  // Ty B_u'^T
+    const int lane = e / 8, j = e % 8;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int c = 16 * fr + 8 * (j / 4) + 4 * hh + (j % 4);
+    const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + 32 * ec + l32;
+    out = load_f32(p.b_u, src, p.wdtype) * norm_w(c) * kNegLog2e;
+  } else if (fr < ks_n + 2 * nk64) {  // fp8 B_v'^T: bytes 2 e, 2 e + 1 of the K64 fragments
+    const int64_t byte = static_cast<int64_t>(fr - ks_n) * 2 * kFragElems + 2 * e;
+    const int s = static_cast<int>(byte / kF8K64Bytes);
+    const int in = static_cast<int>(byte % kF8K64Bytes);
+    const int lane = in / 32, j = in % 32;  // j even
+    const int l32 = lane & 31, hh = lane >> 5;
+    const float amax = scales[kF8AmaxBv];
     const float mul = amax > 0.0f ? kF8Max / amax : 1.0f;
-    chunk[static_cast<int64_t>(fr) * kF8FragBytes + e] = static_cast<uint8_t>(cvt_fp8x2<false>(val * mul, 0.0f, 0u));
-  } else {
-    const int f = fr - 2 * ks_n;
+    float v2[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int jj = j + t;
+      const int c = 64 * s + 32 * (jj / 16) + 8 * ((jj % 16) / 4) + 4 * hh + (jj % 4);
+      const int64_t src = (static_cast<int64_t>(q) * p.d + c) * p.rd + 32 * ec + l32;
+      v2[t] = load_f32(p.b_v, src, p.wdtype) * norm_w(c) * kNegLn2 * mul;
+    }
+    chunk[static_cast<int64_t>(fr) * kFragElems + e] = static_cast<uint16_t>(cvt_fp8x2<false>(v2[0], v2[1], 0u));
+    return;
+  } else if (fr < ks_n + 2 * nk64 + 2 * (p.d / 32)) {  // Ty B_o x dequantisation of V'
+    const int f = fr - ks_n - 2 * nk64;
+    const int lane = e / 8, j = e % 8;
+    const int l32 = lane & 31, hh = lane >> 5;
     const int mb = f / 2, s = f % 2;
     const int c = 32 * mb + l32;
     const int ee = 32 * ec + 16 * s + 8 * (j / 4) + 4 * hh + (j % 4);
@@ -894,9 +892,9 @@ __global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* s
       const int gc = p.chan[q * p.d + c];
       w = (gc >= 0 && gc < p.channels) ? (p.gamma ? p.gamma[gc] : 1.0f) : 0.0f;
     }
-    uint16_t* ob = reinterpret_cast<uint16_t*>(chunk + static_cast<int64_t>(2 * ks_n) * kF8FragBytes);
-    ob[static_cast<int64_t>(f) * kFragElems + e] = Ty::from_f32(load_f32(p.b_o, src, p.wdtype) * w);
+    out = load_f32(p.b_o, src, p.wdtype) * w * scales[kF8DeqV];
   }
+  chunk[static_cast<int64_t>(fr) * kFragElems + e] = Ty::from_f32(out);
 }
 
 int64_t packed_elems(int32_t q_c, int32_t d, int32_t rd) {
@@ -1057,7 +1055,8 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const voi
 
 size_t ow_packed_weight_bytes_fp8(int32_t q_c, int32_t d, int32_t rd) {
   if (q_c < 1 || d < 32 || rd < 32 || d % 32 || rd % 32) return 0;
-  return static_cast<size_t>(ow::kF8HeadBytes) + static_cast<size_t>(q_c) * (rd / 32) * 128 * static_cast<size_t>(d);
+  return static_cast<size_t>(ow::kF8HeadBytes) +
+         static_cast<size_t>(q_c) * (rd / 32) * static_cast<size_t>(ow::f8_chunk_units(d)) * 1024;
 }
 
 int ow_pack_weights_fp8(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,
@@ -1074,8 +1073,11 @@ int ow_pack_weights_fp8(const void* a_u, const void* a_v, const void* a_o, const
   OW_CHECK_SUPPORTED(act_dtype == OW_DTYPE_BF16 || act_dtype == OW_DTYPE_F16, "unsupported activation dtype %d",
                      act_dtype);
   OW_CHECK_ARG(ow::aligned16(packed), "packed weights must be 16-byte aligned");
+  // One thread per 16-bit unit of the head and of the chunks (the scale floats between them are
+  // written by f8_zero / f8_amax / f8_finalize).
+  const int64_t units = ow::kHeadElems + static_cast<int64_t>(q_c) * (rd / 32) * ow::f8_chunk_units(d) * ow::kFragElems;
   ow::PackArgs p{a_u, a_v, a_o, b_u, b_v, b_o, norm_weight, gamma, channel_index, packed,
-                 weight_dtype, q_c, d, rd, channels, ow::packed_elems(q_c, d, rd)};
+                 weight_dtype, q_c, d, rd, channels, units};
   float* scales = reinterpret_cast<float*>(static_cast<uint8_t*>(packed) + ow::kHeadElems * 2);
   const unsigned blocks = static_cast<unsigned>((p.total + 255) / 256);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -266,16 +266,33 @@ __device__ __forceinline__ void pair_chunk(const u32x4 (&Pu)[KS], const u32x4 (&
 }
 
 // ---- fp8 (OCP e4m3fn) channel side ----------------------------------------------------------
+// Only V' = P_v B_v'' runs on fp8: with e4m3's 3-bit mantissa every quantised operand adds
+// ~2.6% rel-L2 and the four of U' and V' together put delta ~5.4% from fp32, past the 5e-2
+// gate, while one side alone stays near 3.8%.  V' uses the double-rate K = 64 MFMA
+// (v_mfma_f32_32x32x64_f8f6f4): per 32-row chunk of the expanded dimension, d / 64 products
+// instead of d / 16.
+//
 // Byte layout of an fp8 packed buffer: the Ty token-side head (kHeadElems elements), then
-// kF8ScaleFloats floats of scales, then per (q, 32-row chunk ec) KS fp8 B_u'^T fragments, KS
-// fp8 B_v'^T fragments (512 bytes each, 8 bytes per lane) and 2 MB Ty B_o fragments (1 KB).
-constexpr int kF8FragBytes = 512;
+// kF8ScaleFloats floats of scales, then per (q, 32-row chunk ec), in 1 KB units: KS Ty B_u'^T
+// fragments (as the Ty layout), d / 64 fp8 B_v'^T K64 fragments (2 KB: 64 lanes x 32 bytes)
+// and 2 MB Ty B_o fragments, the chunk padded to a multiple of 4 units (whole copy rounds of
+// 4 waves).  The dequantisation factor of V' is folded into the packed B_o (Z is linear in
+// V'), the quantisation multiplier of P_v into the token operand A_v diag(r).
+constexpr int kF8K64Bytes = 2048;
 constexpr int kF8ScaleFloats = 16;
 constexpr int kF8HeadBytes = kHeadElems * 2 + kF8ScaleFloats * 4;
-// Scale slots: dequantisation factors of the U' / V' accumulators and the P quantisation
-// multipliers (448 / bound of |P|); the raw B''-absmax slots are the packer's.
-constexpr int kF8DeqU = 0, kF8DeqV = 1, kF8QuantPu = 2, kF8QuantPv = 3, kF8AmaxBu = 4, kF8AmaxBv = 5;
+// Scale slots: V' dequantisation (folded into B_o by the packer), P_v quantisation multiplier
+// (448 / bound of |P_v|), absmax of the folded B_v''.
+constexpr int kF8DeqV = 0, kF8QuantPv = 1, kF8AmaxBv = 2;
 constexpr float kF8Max = 448.0f;
+
+// 1 KB units of one fp8 chunk for channel tile d.
+__host__ __device__ constexpr int f8_chunk_units(int d) {
+  return ((d / 16 + 2 * (d / 64) + 2 * (d / 32)) + 3) / 4 * 4;
+}
+
+typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // Two floats -> two e4m3fn bytes (round to nearest even) in the low (HI = false) or high half
 // of `old`.
@@ -284,26 +301,43 @@ __device__ __forceinline__ uint32_t cvt_fp8x2(float a, float b, uint32_t old) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), HI));
 }
 
-// Accumulator registers 8s..8s+7 times `mul` as a packed fp8 K step (slot order as pack_kstep).
-__device__ __forceinline__ u32x2 pack_kstep_f8(const f32x16& acc, int s, float mul) {
-  uint32_t lo = cvt_fp8x2<false>(acc[8 * s + 0] * mul, acc[8 * s + 1] * mul, 0u);
-  lo = cvt_fp8x2<true>(acc[8 * s + 2] * mul, acc[8 * s + 3] * mul, lo);
-  uint32_t hi = cvt_fp8x2<false>(acc[8 * s + 4] * mul, acc[8 * s + 5] * mul, 0u);
-  hi = cvt_fp8x2<true>(acc[8 * s + 6] * mul, acc[8 * s + 7] * mul, hi);
-  return u32x2{lo, hi};
+// K64 fp8 operand from the P^T accumulators of two 32-channel blocks (b0: channels 0..31 of the
+// K step, b1: 32..63): slot j < 16 is register j of b0, slot j >= 16 register j - 16 of b1, so
+// lane (t, hh) slot j holds channel 32 (j / 16) + 8 ((j % 16) / 4) + 4 hh + j % 4 of token t.
+__device__ __forceinline__ u32x8 pack_k64_f8(const f32x16& b0, const f32x16& b1) {
+  u32x8 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] = cvt_fp8x2<true>(b0[4 * q + 2], b0[4 * q + 3], cvt_fp8x2<false>(b0[4 * q], b0[4 * q + 1], 0u));
+    v[4 + q] = cvt_fp8x2<true>(b1[4 * q + 2], b1[4 * q + 3], cvt_fp8x2<false>(b1[4 * q], b1[4 * q + 1], 0u));
+  }
+  return v;
 }
 
-__device__ __forceinline__ f32x16 mma32_f8(u32x2 a, u32x2 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
-                                                    0, 0);
+// 32x32x64 e4m3 x e4m3 -> fp32 (no block scales).
+__device__ __forceinline__ f32x16 mma32x64_f8(u32x8 a, u32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(__builtin_bit_cast(i32x8, a), __builtin_bit_cast(i32x8, b), c,
+                                                          0, 0, 0, 0, 0, 0);
 }
 
-// Token side of a pair with fp8 outputs: as pair_token_side, the P^T accumulators multiplied by
-// qu / qv and rounded to e4m3fn.
+// Token-operand row scaled by the RMSNorm scales times m (see scale8).
+template <class Ty>
+__device__ __forceinline__ u32x4 scale8m(u32x4 a, const float* r, float m) {
+  u32x4 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k0 = 8 * (q >> 1) + 2 * (q & 1);
+    v[q] = Ty::pack2(Ty::to_f32(lo16(a[q])) * (r[k0] * m), Ty::to_f32(hi16(a[q])) * (r[k0 + 1] * m));
+  }
+  return v;
+}
+
+// Token side of a pair for the fp8 variant: P_u as Ty K steps (pair_token_side), P_v (whose
+// token operand bv already carries the quantisation multiplier) as fp8 K64 operands.
 template <class Ty, int KS>
 __device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, const int (&col)[KS / 2], u32x4 bu,
-                                                   u32x4 bv, int lane, float qu, float qv, u32x2 (&Pu)[KS],
-                                                   u32x2 (&Pv)[KS], u32x4 (&xk)[KS / 2][2]) {
+                                                   u32x4 bv, int lane, u32x4 (&Pu)[KS], u32x8 (&Pv)[KS / 4],
+                                                   u32x4 (&xk)[KS / 2][2]) {
   const int hh = lane >> 5;
   const bool g0 = (lane & 16) == 0;
   const u32x4 bu0 = keep_if(g0, bu), bu1 = keep_if(!g0, bu);
@@ -314,6 +348,7 @@ __device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, c
     xk[cb][0] = column8(tl + (4 * hh) * ld + col[cb], ld);
     xk[cb][1] = column8(tl + (16 + 4 * hh) * ld + col[cb], ld);
   }
+  f32x16 pv_prev = zero;
 #pragma unroll
   for (int cb = 0; cb < KS / 2; ++cb) {
     const u32x4 x0 = xk[cb][0], x1 = xk[cb][1];
@@ -322,31 +357,32 @@ __device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, c
     pu = Ty::mma32(x1, bu1, pu);
     pv = Ty::mma32(x1, bv1, pv);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      Pu[2 * cb + s] = pack_kstep_f8(pu, s, qu);
-      Pv[2 * cb + s] = pack_kstep_f8(pv, s, qv);
-    }
+    for (int s = 0; s < 2; ++s) Pu[2 * cb + s] = pack_kstep<Ty>(pu, s);
+    if (cb & 1)
+      Pv[cb / 2] = pack_k64_f8(pv_prev, pv);
+    else
+      pv_prev = pv;
   }
 }
 
-// pair_chunk with fp8 U'/V' products: fu(ks), fv(ks) return fp8 fragments (u32x2), the
-// accumulators are dequantised by du / dv before the gate; the Z B_o product stays in Ty.
+// pair_chunk for the fp8 variant: U' on Ty MFMAs, V' on K64 fp8 MFMAs (fv(s) returns the
+// chunk's fp8 B_v'^T K64 fragment s), the gate and Z B_o as pair_chunk (the packed B_o carries
+// V''s dequantisation factor).
 template <class Ty, int KS, int MB, class FU, class FV, class FO>
-__device__ __forceinline__ void pair_chunk_f8(const u32x2 (&Pu)[KS], const u32x2 (&Pv)[KS], FU fu, FV fv, FO fo,
-                                              float du, float dv, f32x16 (&W)[MB]) {
+__device__ __forceinline__ void pair_chunk_f8(const u32x4 (&Pu)[KS], const u32x8 (&Pv)[KS / 4], FU fu, FV fv, FO fo,
+                                              f32x16 (&W)[MB]) {
   f32x16 U = {}, V = {};
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    U = mma32_f8(fu(ks), Pu[ks], U);
-    V = mma32_f8(fv(ks), Pv[ks], V);
-  }
+  for (int ks = 0; ks < KS; ++ks) U = Ty::mma32(fu(ks), Pu[ks], U);
+#pragma unroll
+  for (int s = 0; s < KS / 4; ++s) V = mma32x64_f8(fv(s), Pv[s], V);
   u32x4 Z[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q] * du, V[8 * s + 2 * q] * dv),
-                          silu_gate(U[8 * s + 2 * q + 1] * du, V[8 * s + 2 * q + 1] * dv));
+      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
+                          silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll

@@ -118,7 +118,7 @@ def test_model_fused_glue_matches_forward_features(fp8) -> None:
                 blk.gamma.fill_(1.0)
     model = model.to(device=DEV, dtype=torch.bfloat16)
     if fp8:
-        omniwave_amd.enable_fp8(model)
+        omniwave_amd.enable_fp8(model, min_channel_tile=64)
     x = torch.randn(2, 3, 224, 224, generator=torch.Generator().manual_seed(1)).to(DEV, torch.bfloat16)
     with torch.no_grad():
         got = model(x)
