@@ -1205,7 +1205,8 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
     r.eps = eps;
     r.drop_scale = drop_scale;
-    const int rc = ow::launch_fwd_resident(r, dtype, s);
+    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level) ? ow::launch_fwd_wave(r, dtype, s)
+                                                                          : ow::launch_fwd_resident(r, dtype, s);
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }

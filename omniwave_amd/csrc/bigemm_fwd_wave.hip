@@ -1,0 +1,350 @@
+// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2} (the
+// 56x56x128 stage of OmniWeave-T), one (pair, channel group) unit per wave at a time.
+//
+// Same math and operand packing as the other forward kernels (reference
+// omniweave/ops/reference.py:147-171; operand scheme in ow_device.h).  Organisation:
+//   * a workgroup owns one channel group g: its 48 KB of packed weights (4 chunks of the
+//     expanded dimension) are copied to LDS once and read from there by all four waves;
+//   * each wave processes whole units: the 32 tokens of a pair of token groups against all
+//     128 expanded rows of group g, so the token side is computed once per unit and no partial
+//     sums cross waves — no workgroup barrier after the weight copy;
+//   * the q_c workgroups of a team (logical ids q_c m .. q_c m + q_c - 1, one per channel group,
+//     placed on one XCD) walk the same pairs; each wave reads its pair's whole rows (the
+//     RMSNorm statistics need all C channels) one pair ahead into registers, in the 32x32x16
+//     operand layout (lane = token, 8 channels per 16-byte piece), sums the squares with
+//     v_dot2_f32 and writes only its group's columns to its own LDS tile; the other group's
+//     wave reads the same rows, which its XCD's L2 serves;
+//   * rows come from the token table; group g is channels 64 g .. 64 g + 63, which is the
+//     plan's channel order at radix level 0 or with one group (omniweave/models/routing.py:
+//     107-121; the interleaved groups of the other plans take the resident kernel);
+//   * the residual round(x + round(delta)) is written into the tile, which the wave then stores
+//     as whole 16-byte row pieces.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ow_device.h"
+
+namespace ow {
+namespace {
+
+constexpr int kD = 64;
+constexpr int kRD = 128;
+constexpr int kKS = kD / 16;                  // 16-deep K steps over a channel group
+constexpr int kMB = kD / 32;                  // 32-channel blocks of the group
+constexpr int kNCH = kRD / 32;                // 32-row chunks of the expanded dimension
+constexpr int kFrCh = 2 * kKS + 2 * kMB;      // fragments per chunk (B_u'^T, B_v'^T, B_o)
+constexpr int kGroupFrags = kNCH * kFrCh;     // 48 fragments = 48 KB per channel group
+constexpr int kLdt = kD + 8;                  // tile row stride (elements)
+constexpr int kWavesWg = 4;
+
+struct WaveLds {
+  u32x4 w[kGroupFrags][64];        // the group's packed weights
+  uint16_t tile[kWavesWg][32 * kLdt];  // per wave: the pair's rows, group columns
+  float rsc[kWavesWg][32];         // per wave: RMSNorm scale of each token of the pair
+  int32_t rows[kWavesWg][32];      // per wave: output row of each token (-1: not stored)
+};
+
+// Logical workgroup id such that ids q_c m .. q_c m + q_c - 1 run on one XCD (workgroups are
+// dispatched round-robin over the 8 XCDs).
+__device__ __forceinline__ int wave_xcd_remap(int bid, int nwg) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+}
+
+// Buffer descriptor of a tensor (raw, no stride): loads past num_records return zero and
+// stores there are dropped, so pad rows need no branches; the launcher keeps tensors below
+// 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a byte offset past every buffer
+
+// Position of a pair's first token group 2 pair = b q_s + s (image b, group s of the image),
+// advanced along the wave's pair sequence with additions only.
+struct PairPos {
+  int32_t b, s;
+};
+
+__device__ __forceinline__ void pos_advance(PairPos& pos, int32_t step_b, int32_t step_s, int32_t q_s) {
+  pos.b += step_b;
+  pos.s += step_s;
+  if (pos.s >= q_s) {
+    pos.s -= q_s;
+    ++pos.b;
+  }
+}
+
+// Token-table entries of this lane's token (lane % 32) for the pair at `pos`: only loads here;
+// the values are examined a pair later (unit_row), so the loads are not waited on meanwhile.
+struct TokEntry {
+  int32_t tk, to, b;
+};
+
+template <bool OM>
+__device__ __forceinline__ TokEntry tok_entry(const ResidentArgs& a, PairPos pos, bool live, int l32) {
+  // The pair's second token group (lanes 16..31) is the next group; selects, no branch.
+  const int32_t s1 = pos.s + 1;
+  const bool wrap = s1 == a.q_s;
+  const int32_t s = l32 >= 16 ? (wrap ? 0 : s1) : pos.s;
+  const int32_t b = (l32 >= 16 && wrap) ? pos.b + 1 : pos.b;
+  TokEntry e;
+  e.b = live ? b : a.batch;
+  e.tk = a.tok[s * kG + (l32 & 15)];  // s < q_s: in bounds for every pair
+  e.to = OM ? a.out_tok[s * kG + (l32 & 15)] : 0;
+  return e;
+}
+
+// Input row of the entry's token (-1: pad token or past the end), and its output row.
+template <bool OM>
+__device__ __forceinline__ void unit_row(const ResidentArgs& a, const TokEntry& e, int32_t& in, int32_t& out) {
+  // Bitwise conditions and selects: a branch here would make the compiler wait for every
+  // outstanding memory operation before reading e.tk.
+  const bool ok = (e.b < a.batch) & (e.tk >= 0) & (e.tk < a.n_tok);
+  const int32_t base = e.b * a.n_tok;
+  in = ok ? base + e.tk : -1;
+  out = in;
+  if (OM) out = (ok & (e.to >= 0) & (e.to < a.n_tok)) ? base + e.to : -1;
+}
+
+// The 16-byte pieces 2 ks + hh (channels 16 ks + 8 hh ..) of this lane's token row, ks < C / 16;
+// zeros for row -1.
+template <int NV>
+__device__ __forceinline__ void load_pieces(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh,
+                                            u32x4 (&v)[NV]) {
+  const uint32_t base = row >= 0 ? static_cast<uint32_t>(row) * static_cast<uint32_t>(channels * 2) + 16u * hh
+                                 : kOutOfRange;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * k, 0, 0);
+}
+
+template <class Ty, int QC, bool OM, bool DROP>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
+  constexpr int C = QC * kD;
+  constexpr int NV = C / 16;  // row pieces per lane
+  __shared__ __attribute__((aligned(16))) WaveLds sh;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int lid = wave_xcd_remap(blockIdx.x, gridDim.x);
+  const int g = lid % QC;
+  const int team = lid / QC;
+  const int n_team = gridDim.x / QC;
+  const int64_t stride = static_cast<int64_t>(n_team) * kWavesWg;
+  const int64_t first = static_cast<int64_t>(team) * kWavesWg + wave;
+
+  // The group's weights into LDS (1 KB per wave and copy), the token operands into registers.
+  {
+    const uint16_t* src = a.packed + kHeadElems + static_cast<size_t>(g) * kGroupFrags * kFragElems;
+    for (int f = wave; f < kGroupFrags; f += kWavesWg)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(f) * kFragElems + lane * 8),
+          (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
+  }
+  const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
+  const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
+  const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (first >= n_pairs) return;  // after the only workgroup barrier
+
+  uint16_t* tile = sh.tile[wave];
+  float* rsc = sh.rsc[wave];
+  int32_t* rows = sh.rows[wave];
+  int col[kMB];
+#pragma unroll
+  for (int cb = 0; cb < kMB; ++cb) col[cb] = 32 * cb + l32;
+  const uint32_t bytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * C * 2);
+  const __amdgpu_buffer_rsrc_t rx = tensor_rsrc(a.x, bytes), ro = tensor_rsrc(a.out, bytes);
+
+  // The wave's pairs are first, first + stride, ...  `pos` is the position of the pair whose
+  // table entries are read next (two pairs ahead of the one computed).
+  const int32_t step_b = static_cast<int32_t>(2 * stride / a.q_s);
+  const int32_t step_s = static_cast<int32_t>(2 * stride - static_cast<int64_t>(step_b) * a.q_s);
+  PairPos pos{static_cast<int32_t>(2 * first / a.q_s), 0};
+  pos.s = static_cast<int32_t>(2 * first - static_cast<int64_t>(pos.b) * a.q_s);
+  int64_t pos_pair = first;
+  auto next_entry = [&]() {
+    const TokEntry e = tok_entry<OM>(a, pos, pos_pair < n_pairs, l32);
+    pos_advance(pos, step_b, step_s, a.q_s);
+    pos_pair += stride;
+    return e;
+  };
+
+  // One unit: pair p from xc (this lane's pieces, loaded a unit ago), output row out_c of this
+  // lane's token.  `ent` holds the table entries of the next pair (read a unit ago): once xc
+  // is in the tile, the next pair's pieces are loaded into xc, and ent takes the entries of
+  // the pair after that.
+  auto unit = [&](int64_t p, u32x4 (&xc)[NV], TokEntry& ent, int32_t& out_c) {
+    int32_t in_n, out_n;
+    unit_row<OM>(a, ent, in_n, out_n);
+
+    // RMSNorm scale of this lane's token: its half of the row here, the other half in lane
+    // l ^ 32.
+    float acc = 0.0f;
+    if (a.norm) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(xc[k][e], acc);
+      acc += __shfl_xor(acc, 32);
+    }
+    // The group's columns into the tile; the row scale (0 for pad tokens) and output row.
+    if (QC == 1 || g == 0) {  // g is uniform: a scalar branch, no dynamic register indexing
+#pragma unroll
+      for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[(QC - 1) * 4 + k];
+    }
+    if (hh == 0) {
+      rsc[l32] = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
+      rows[l32] = out_c;
+    }
+    load_pieces<NV>(rx, in_n, C, hh, xc);  // the next pair, a unit ahead of its use
+    ent = next_entry();
+    wave_lds_sync();
+
+    // Token side.  Lane slots j of the token operand are tokens 16 tg + kord(j, hh) of its
+    // group tg: two runs of four scales.
+    u32x4 bu = fAu, bv = fAv;
+    if (a.norm) {
+      const float* r8 = &rsc[16 * ((lane >> 4) & 1) + 4 * hh];
+      bu = scale8<Ty>(fAu, r8);
+      bv = scale8<Ty>(fAv, r8);
+    }
+    u32x4 Pu[kKS], Pv[kKS], xk[kMB][2];
+    pair_token_side<Ty, kKS>(tile, kLdt, col, bu, bv, lane, Pu, Pv, xk);
+
+    // Channel side: the four chunks of the expanded dimension, weights from LDS.  The U'/V'
+    // fragments of chunk e + 1 are read while chunk e's gate runs, so the MFMAs do not wait on
+    // LDS latency one fragment at a time.
+    f32x16 W[kMB] = {};
+    u32x4 fr[2 * kKS];
+    auto read_uv = [&](int e) {
+#pragma unroll
+      for (int f = 0; f < 2 * kKS; ++f) fr[f] = sh.w[e * kFrCh + f][lane];
+    };
+    read_uv(0);
+#pragma unroll
+    for (int e = 0; e < kNCH; ++e) {
+      f32x16 U = {}, V = {};
+#pragma unroll
+      for (int ks = 0; ks < kKS; ++ks) {
+        U = Ty::mma32(fr[ks], Pu[ks], U);
+        V = Ty::mma32(fr[kKS + ks], Pv[ks], V);
+      }
+      u32x4 fo[2 * kMB];
+#pragma unroll
+      for (int f = 0; f < 2 * kMB; ++f) fo[f] = sh.w[e * kFrCh + 2 * kKS + f][lane];
+      if (e + 1 < kNCH) read_uv(e + 1);
+      u32x4 Z[2];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          Z[s2][q] = Ty::pack2(silu_gate(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q]),
+                               silu_gate(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1]));
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], fo[2 * mb + s2], W[mb]);
+    }
+
+    // delta = A_o W, rounded, plus x (and the drop-path scale), into the tile in place: the
+    // token side has read it.
+    f32x16 dl[kMB];
+    mfma_drain();
+    pair_output<Ty, kMB>(W, fAo, lane, dl);
+    mfma_drain();
+    float s0 = 1.0f, s1 = 1.0f;
+    if constexpr (DROP) {
+      const int64_t tg0 = 2 * p;
+      const int64_t b0 = tg0 / a.q_s, b1 = (tg0 + 1) / a.q_s;
+      s0 = a.drop_scale[b0 < a.batch ? b0 : a.batch - 1];
+      s1 = a.drop_scale[b1 < a.batch ? b1 : a.batch - 1];
+    }
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+      auto dst = [&](int i) { return &tile[pair_token_row(i, hh) * kLdt + 32 * mb + l32]; };
+      if (a.residual)
+        pair_store_block<Ty, true, DROP>(dl[mb], xk[mb], dst, s0, s1);
+      else
+        pair_store_block<Ty, false, DROP>(dl[mb], xk[mb], dst, s0, s1);
+    }
+    wave_lds_sync();
+
+    // The tile's rows to memory: 32 rows x 8 pieces of the group's columns, 4 per lane; pad
+    // rows go past the buffer.
+    u32x4 ov[4];
+    int32_t orow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = (lane >> 3) + 8 * j;
+      orow[j] = rows[r];
+      ov[j] = *reinterpret_cast<const u32x4*>(&tile[r * kLdt + (lane & 7) * 8]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t rb = orow[j] >= 0 ? static_cast<uint32_t>(orow[j]) * static_cast<uint32_t>(C * 2) : kOutOfRange;
+      __builtin_amdgcn_raw_buffer_store_b128(ov[j], ro, rb + 2u * (kD * g + (lane & 7) * 8), 0, 0);
+    }
+    // The next unit overwrites the tile and the row table: every lane's reads above are done.
+    wave_lds_sync();
+    out_c = out_n;
+  };
+
+  u32x4 x[NV];
+  TokEntry ent = next_entry();
+  int32_t in0, out_c;
+  unit_row<OM>(a, ent, in0, out_c);
+  load_pieces<NV>(rx, in0, C, hh, x);
+  ent = next_entry();
+#pragma unroll 1
+  for (int64_t p = first; p < n_pairs; p += stride) unit(p, x, ent, out_c);
+}
+
+template <class Ty, int QC>
+int launch_qc(const ResidentArgs& a, hipStream_t stream) {
+  // Two workgroups of four waves per CU (~67 KB of LDS each); whole teams of QC workgroups.
+  const int32_t n_pairs = a.n_pairs;
+  int64_t grid = static_cast<int64_t>(device_cus()) * 2;
+  const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWavesWg - 1) / kWavesWg;
+  if (grid / QC > teams_needed) grid = teams_needed * QC;
+  grid -= grid % QC;
+  if (grid <= 0) return OW_OK;
+  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
+  if (a.out_tok)
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false>), g, b, 0, stream, a, n_pairs);
+  else if (a.drop_scale)
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, true>), g, b, 0, stream, a, n_pairs);
+  else
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, false>), g, b, 0, stream, a, n_pairs);
+  return hip_status(hipGetLastError(), "bigemm_fwd_wave_kernel launch");
+}
+
+template <class Ty>
+int launch_ty(const ResidentArgs& a, hipStream_t stream) {
+  switch (a.q_c) {
+    case 1: return launch_qc<Ty, 1>(a, stream);
+    case 2: return launch_qc<Ty, 2>(a, stream);
+    default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 2} (got %d)", a.q_c);
+  }
+}
+
+}  // namespace
+
+bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level) {
+  return d == kD && rd == kRD && (q_c == 1 || (q_c == 2 && radix_level == 0)) && channels == q_c * kD;
+}
+
+int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream) {
+  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, stream);
+  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, stream);
+  return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+}
+
+}  // namespace ow
