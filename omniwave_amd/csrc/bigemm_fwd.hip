@@ -165,6 +165,13 @@ __device__ __forceinline__ StridedPack<M> strided_pack(const u32x4& v, int res) 
   }
 }
 
+// round(x + v) on two packed values (low and high halves): the residual of the block output,
+// x the input and v the rounded delta.
+template <class Ty>
+__device__ __forceinline__ uint32_t add_residual2(uint32_t x, uint32_t v) {
+  return Ty::pack2(Ty::to_f32(lo16(x)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(x)) + Ty::to_f32(hi16(v)));
+}
+
 // Maps the hardware workgroup id to a logical id so that the q_c workgroups of one row chunk
 // run on the same XCD (workgroups are dispatched round-robin over the 8 XCDs): their gathers
 // and scatters touch the same cache lines of x and out, which then meet in one L2.
@@ -174,13 +181,55 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
 }
 
-// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane).
-__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, int lane) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + lane * 8),
-                                   (__attribute__((address_space(3))) void*)(dst), 16, 0, 0);
+// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane, LDS
+// address M0 + 16 lane).  Issued as inline assembly so that the compiler does not track it: for
+// the builtin it waits for every outstanding LDS DMA before the next LDS read, which would
+// serialise each weight chunk's copy with the reads of the chunk before it.  The kernel waits
+// for the copies itself (wait_vmcnt / wait_lds_dma) before the barrier that publishes a chunk,
+// and nothing else in the kernel uses M0.
+// src and dst are wave-uniform (scalar base address, M0); the lane's byte offset lane16 = 16 lane
+// is the only vector operand.
+__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, uint32_t lane16) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)dst)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane16), "s"(src), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
 }
 
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// ds_read_b128 at byte offset OFF from addr, issued as inline assembly: the compiler neither
+// moves it next to its use nor waits for it, so several reads stay in flight.  Under the d = 128
+// kernel's register pressure the compiler otherwise keeps a single fragment register and waits
+// for every read right before its MFMA.  The value is used only after lds_wait<N>(v), N = the
+// number of LDS reads issued after this one: LDS returns in order, so LDS or scalar-memory
+// operations of the compiler issued in between can only make that wait stricter.
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read_async(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // Waits until at most N vector-memory operations of this wave are outstanding.
 template <int N>
@@ -248,10 +297,15 @@ bigemm_fwd_kernel(FwdArgs a) {
       return (ec & 1) ? xs : wb;
     }
   };
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto issue_chunk = [&](int ec) {
     const uint16_t* src = wsrc + static_cast<size_t>(ec) * CH_ELEMS;
     uint16_t* dst = chunk_buf(ec);
-    for (int f = wave; f < CH_UNITS; f += kWaves) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane);
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+      const int f = wave_u + i * kWaves;
+      copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, 16u * lane);
+    }
   };
   issue_chunk(0);
 
@@ -479,7 +533,102 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) W[p][mb][i] = 0.0f;
 
-  if constexpr (PIPE) {
+  if constexpr (PIPE && !F8) {
+    // One step issues chunk ec + 1's U'/V' products and chunk ec's W += Z B_o, their weight
+    // fragments read DEPTH ahead (lds_read_async), and computes one gate value of chunk ec per
+    // U'/V' product, so the gate's VALU work runs while the products execute.
+    constexpr int DEPTH = 4;
+    const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
+    auto stream = [&](auto nu_tag, auto no_tag, uint32_t bn, uint32_t bo, f32x16& Un, f32x16& Vn,
+                      const f32x16& Uc, const f32x16& Vc) {
+      constexpr int NU = decltype(nu_tag)::value;  // U'/V' fragments of chunk ec + 1 (0 or 2 KS)
+      constexpr int NO = decltype(no_tag)::value;  // B_o fragments of chunk ec (0 or FR_O)
+      constexpr int NF = NU + NO;
+      static_assert(NO == 0 || NU == 0 || NU == 16, "one gate value per U'/V' product");
+      auto read = [&](auto ic) -> u32x4 {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i < NU)
+          return lds_read_async<((i & 1) ? FR_U + i / 2 : i / 2) * kFragElems * 2>(bn);
+        else
+          return lds_read_async<(i - NU) * kFragElems * 2>(bo);
+      };
+      u32x4 fr[DEPTH];
+      static_for<0, DEPTH>([&](auto ic) {
+        if constexpr (decltype(ic)::value < NF) fr[decltype(ic)::value] = read(ic);
+      });
+      // Gate values k = 8 s + 2 q + h of chunk ec -> Z[s] word q, half h.
+      u32x4 Z[2];
+      float zl = 0.0f;
+      auto gate = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const float z = silu_gate(Uc[k], Vc[k]);
+        if constexpr (k % 2 == 0)
+          zl = z;
+        else
+          Z[k / 8][(k % 8) / 2] = Ty::pack2(zl, z);
+      };
+      if constexpr (NO > 0 && NU == 0) static_for<0, 16>(gate);
+      if constexpr (NU > 0) {
+        Un = f32x16{};
+        Vn = f32x16{};
+      }
+      static_for<0, NF>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int after = NF - 1 - i < DEPTH - 1 ? NF - 1 - i : DEPTH - 1;
+        lds_wait<after>(fr[i % DEPTH]);
+        if constexpr (i < NU) {
+          if constexpr (i % 2 == 0)
+            Un = Ty::mma32(fr[i % DEPTH], Pu[0][i / 2], Un);
+          else
+            Vn = Ty::mma32(fr[i % DEPTH], Pv[0][i / 2], Vn);
+        } else {
+          constexpr int j = i - NU;
+          W[0][j / 2] = Ty::mma32(Z[j % 2], fr[i % DEPTH], W[0][j / 2]);
+        }
+        if constexpr (i + DEPTH < NF) fr[i % DEPTH] = read(std::integral_constant<int, i + DEPTH>{});
+        if constexpr (NO > 0 && i < NU) gate(ic);
+      });
+      if constexpr (NU > 0 && NO > 0 && NCH >= 8) {  // (rd = 128 spills with the hint)
+        // Interleave: each U'/V' product followed by about one gate value's VALU work.
+        static_for<0, NU>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // VALU, transcendental
+        });
+      }
+    };
+    using Nu = std::integral_constant<int, 2 * KS>;
+    using No = std::integral_constant<int, FR_O>;
+    using Zero = std::integral_constant<int, 0>;
+    auto base = [&](int ec) { return lds_addr(chunk_buf(ec)) + lane16; };
+    // Step ec: wait for chunk ec + 1 (at ec = 0 chunk 2 may still be in flight: nothing else is
+    // outstanding during the loop, so the count is exact); the barrier also means every wave is
+    // done with chunk ec - 1, whose buffer then takes chunk ec + 2.
+    auto step = [&](int ec, f32x16& Uc, f32x16& Vc, f32x16& Un, f32x16& Vn) {
+      const uint32_t bo = base(ec) + 2u * FR_U * kFragElems * 2u;
+      if (ec + 1 < NCH) {
+        if (ec == 0 && NCH > 2)
+          wait_vmcnt<DPW>();
+        else
+          wait_lds_dma();
+        __syncthreads();
+        if (ec >= 1 && ec + 2 < NCH) issue_chunk(ec + 2);
+        stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+      } else {
+        stream(Zero{}, No{}, 0u, bo, Un, Vn, Uc, Vc);
+      }
+    };
+    wait_lds_dma();
+    __syncthreads();
+    if (NCH > 1) issue_chunk(1);
+    if (NCH > 2) issue_chunk(2);
+    f32x16 Ua, Va, Ub, Vb;
+    stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
+#pragma unroll
+    for (int ec = 0; ec < NCH; ec += 2) {
+      step(ec, Ua, Va, Ub, Vb);
+      step(ec + 1, Ub, Vb, Ua, Va);
+    }
+  } else if constexpr (PIPE) {
     // U'/V' of chunk ec (fp8: e4m3 fragments and P operands, dequantised in the gate).
     auto uv = [&](int ec, f32x16& U, f32x16& V) {
       U = f32x16{};
@@ -587,24 +736,21 @@ bigemm_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       auto dst = [&](int i) { return &st[pair_token_row(i, hh) * LDX + 32 * mb + l32]; };
-      if (a.drop_scale) {
-        if (a.residual)
-          pair_store_block<Ty, true, true>(dl[mb], xk[p][mb], dst, s0, s1);
-        else
-          pair_store_block<Ty, false, true>(dl[mb], xk[p][mb], dst, s0, s1);
-      } else if (a.residual) {
-        pair_store_block<Ty, true>(dl[mb], xk[p][mb], dst);
-      } else {
+      // The residual is added in the store loop below, from x in memory: keeping the lane's
+      // x values in registers through the chunk loop would cost 32 VGPRs there.
+      if (a.drop_scale)
+        pair_store_block<Ty, false, true>(dl[mb], xk[p][mb], dst, s0, s1);
+      else
         pair_store_block<Ty, false>(dl[mb], xk[p][mb], dst);
-      }
     }
   }
   __syncthreads();
 
   // The finished tile to memory.  Each wave stores rows [32 wave, 32 wave + 32) of the tile;
-  // the output-row ids and the tile data of a batch of rows are read from LDS first, then the
-  // stores are issued without waiting in between (an LDS round trip per store would leave
-  // the loop latency-bound).
+  // the output-row ids and the tile data of a batch of rows are read from LDS first (and, with
+  // the residual, the same elements of x from memory), then the stores are issued without
+  // waiting in between (an LDS round trip per store would leave the loop latency-bound).  The
+  // residual is round(x + tile value), the tile holding the rounded (drop-path scaled) delta.
   if (a.mode == kModeContig || a.mode == kModeStrided) {
     constexpr int WR = ROWS / kWaves;  // rows per wave
     static_assert(WR == 32, "32 rows per wave");
@@ -627,13 +773,41 @@ bigemm_fwd_kernel(FwdArgs a) {
       for (int k0 = 0; k0 < NIT; k0 += KB) {
         int32_t ids[KB];
         Elt val[KB][VPL];
+        u32x4 xv[KB][VPL];
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
           const int r = wave * WR + rsub + RPI * (k0 + k);
           ids[k] = rowout[r];
+          const int32_t in = rowid[r];  // >= 0 wherever the output row is
 #pragma unroll
-          for (int q = 0; q < VPL; ++q)
+          for (int q = 0; q < VPL; ++q) {
             val[k][q] = *reinterpret_cast<const Elt*>(&xs[r * LDX + (sub + q * LPR) * M]);
+            xv[k][q] = u32x4{0u, 0u, 0u, 0u};
+            if (a.residual && in >= 0)
+              xv[k][q] = *reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(in) * a.channels +
+                                                          (M == 8 ? col0 : 0) + (sub + q * LPR) * 8);
+          }
+        }
+        if (a.residual) {
+#pragma unroll
+          for (int k = 0; k < KB; ++k)
+#pragma unroll
+            for (int q = 0; q < VPL; ++q) {
+              if constexpr (M == 8) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) val[k][q][e] = add_residual2<Ty>(xv[k][q][e], val[k][q][e]);
+              } else {
+                const StridedPack<M> xe = strided_pack<M>(xv[k][q], strided_res);
+                if constexpr (M == 4) {
+                  val[k][q].x = add_residual2<Ty>(xe.x, val[k][q].x);
+                  val[k][q].y = add_residual2<Ty>(xe.y, val[k][q].y);
+                } else if constexpr (M == 2) {
+                  val[k][q] = add_residual2<Ty>(xe, val[k][q]);
+                } else {
+                  val[k][q] = lo16(add_residual2<Ty>(xe, val[k][q]));
+                }
+              }
+            }
         }
         if constexpr (M == 8) {
           // Sum of squares of the stored values of each row's group columns: the next block's
@@ -686,7 +860,11 @@ bigemm_fwd_kernel(FwdArgs a) {
       const int r = i / D, k = i % D;
       const int64_t id = rowout[r];
       const int c = chx[k];
-      if (id >= 0 && c >= 0) a.out[id * a.channels + c] = xs[r * LDX + k];
+      if (id >= 0 && c >= 0) {
+        uint16_t v = xs[r * LDX + k];
+        if (a.residual) v = lo16(add_residual2<Ty>(a.x[static_cast<int64_t>(rowid[r]) * a.channels + c], v));
+        a.out[id * a.channels + c] = v;
+      }
     }
   }
 }
