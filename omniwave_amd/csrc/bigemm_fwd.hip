@@ -128,10 +128,7 @@ struct FwdArgs {
 //   kNormPartials row_scale holds `parts` partial sums of squares per row, written by the
 //                previous block's launch (stats_out); the tile load reads only the group's
 //                columns
-constexpr int kNormNone = 0;
-constexpr int kNormBuffer = 1;
-constexpr int kNormInline = 2;
-constexpr int kNormPartials = 3;
+// (kNormNone, kNormBuffer, kNormInline, kNormPartials: ow_device.h)
 
 // Channel-group access modes.
 //   kModeContig   group qc is columns [qc*d, qc*d + d): 16-byte row vectors (radix level 0)
@@ -165,12 +162,6 @@ __device__ __forceinline__ StridedPack<M> strided_pack(const u32x4& v, int res) 
   }
 }
 
-// round(x + v) on two packed values (low and high halves): the residual of the block output,
-// x the input and v the rounded delta.
-template <class Ty>
-__device__ __forceinline__ uint32_t add_residual2(uint32_t x, uint32_t v) {
-  return Ty::pack2(Ty::to_f32(lo16(x)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(x)) + Ty::to_f32(hi16(v)));
-}
 
 // Maps the hardware workgroup id to a logical id so that the q_c workgroups of one row chunk
 // run on the same XCD (workgroups are dispatched round-robin over the 8 XCDs): their gathers
@@ -181,62 +172,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
 }
 
-// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane, LDS
-// address M0 + 16 lane).  Issued as inline assembly so that the compiler does not track it: for
-// the builtin it waits for every outstanding LDS DMA before the next LDS read, which would
-// serialise each weight chunk's copy with the reads of the chunk before it.  The kernel waits
-// for the copies itself (wait_vmcnt / wait_lds_dma) before the barrier that publishes a chunk,
-// and nothing else in the kernel uses M0.
-// src and dst are wave-uniform (scalar base address, M0); the lane's byte offset lane16 = 16 lane
-// is the only vector operand.
-__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, uint32_t lane16) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)dst)));
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane16), "s"(src), "s"(lds)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
 
-__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// LDS byte address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
-
-// ds_read_b128 at byte offset OFF from addr, issued as inline assembly: the compiler neither
-// moves it next to its use nor waits for it, so several reads stay in flight.  Under the d = 128
-// kernel's register pressure the compiler otherwise keeps a single fragment register and waits
-// for every read right before its MFMA.  The value is used only after lds_wait<N>(v), N = the
-// number of LDS reads issued after this one: LDS returns in order, so LDS or scalar-memory
-// operations of the compiler issued in between can only make that wait stricter.
-template <int OFF>
-__device__ __forceinline__ u32x4 lds_read_async(uint32_t addr) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void lds_wait(u32x4& v) {
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
-}
-
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
-// Waits until at most N vector-memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 // One workgroup: 4 waves x TPW token groups (TPW/2 pairs of 16 tokens per wave) x one channel
 // group q_c.

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "ow_common.h"
 
@@ -125,6 +126,74 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ uint16_t lo16(uint32_t v) { return static_cast<uint16_t>(v & 0xffffu); }
 __device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16_t>(v >> 16); }
+
+// round(x + v) on two packed values (low and high halves): the residual of the block output,
+// x the input and v the rounded delta.
+template <class Ty>
+__device__ __forceinline__ uint32_t add_residual2(uint32_t x, uint32_t v) {
+  return Ty::pack2(Ty::to_f32(lo16(x)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(x)) + Ty::to_f32(hi16(v)));
+}
+
+// Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane, LDS
+// address M0 + 16 lane).  Issued as inline assembly so that the compiler does not track it: for
+// the builtin it waits for every outstanding LDS DMA before the next LDS read, which would
+// serialise each weight chunk's copy with the reads of the chunk before it.  The kernel waits
+// for the copies itself (wait_vmcnt / wait_lds_dma) before the barrier that publishes a chunk,
+// and nothing else in the kernel uses M0.
+// src and dst are wave-uniform (scalar base address, M0); the lane's byte offset lane16 = 16 lane
+// is the only vector operand.
+// lds: LDS byte address of the destination.
+__device__ __forceinline__ void copy_frag_to_lds_at(const uint16_t* src, uint32_t lds, uint32_t lane16) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane16), "s"(src), "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+__device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* dst, uint32_t lane16) {
+  copy_frag_to_lds_at(src, static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint16_t*)dst)),
+                      lane16);
+}
+
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Waits until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// ds_read_b128 at byte offset OFF from addr, issued as inline assembly: the compiler neither
+// moves it next to its use nor waits for it, so several reads stay in flight.  Under the d = 128
+// kernel's register pressure the compiler otherwise keeps a single fragment register and waits
+// for every read right before its MFMA.  The value is used only after lds_wait<N>(v), N = the
+// number of LDS reads issued after this one: LDS returns in order, so LDS or scalar-memory
+// operations of the compiler issued in between can only make that wait stricter.
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read_async(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // ---------------------------------------------------------------------------------------
 // One 32-token pair (token groups 0 and 1 of 16 tokens) of a channel group, all on 32x32x16
@@ -483,6 +552,13 @@ FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c
 bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype,
                             int32_t flags, bool stats_in);
 int launch_fwd_resident(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
+// Where the RMSNorm row scales of a streamed launch come from (bigemm_fwd.hip, FwdArgs).
+constexpr int kNormNone = 0;
+constexpr int kNormBuffer = 1;
+constexpr int kNormInline = 2;
+constexpr int kNormPartials = 3;
+
+
 // One (pair, channel group) unit per wave, the group's weights in LDS (bigemm_fwd_wave.hip):
 // d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2}, channel groups in channel order.
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level);
