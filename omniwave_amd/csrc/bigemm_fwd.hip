@@ -1100,10 +1100,23 @@ FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c
   return p;
 }
 
+// d = 128, rd = 256 launches with contiguous channel groups and 16-byte aligned rows (bf16 /
+// f16, not fp8) take the persistent kernel.
+bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype, int32_t flags,
+                      int32_t batch) {
+  if ((dtype != OW_DTYPE_BF16 && dtype != OW_DTYPE_F16) || (flags & OW_FUSE_FP8)) return false;
+  int32_t q_s = 0, q_c = 0;
+  if (ow_plan_dims(plan, &q_s, &q_c) != OW_OK) return false;
+  const FwdPath p = fwd_path(x, out, plan, q_c, dtype, flags);
+  if (p.resident || p.mode != kModeContig) return false;
+  const int64_t elems = static_cast<int64_t>(batch) * plan->height * plan->width * plan->channels;
+  return persist_supported(plan->channel_tile, rd, plan->channels, q_c, elems);
+}
+
 // The RMSNorm row scales of a launch come from one of four places (kNorm*); only kNormBuffer
 // (and the fp32 kernel with OW_FUSE_NORM) uses the workspace, for batch * H * W floats.
 bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype,
-                            int32_t flags, bool stats_in) {
+                            int32_t flags, bool stats_in, int32_t batch) {
   if (!(flags & OW_FUSE_NORM)) return false;
   if (dtype == OW_DTYPE_F32) return true;
   int32_t q_s = 0, q_c = 0;
@@ -1112,6 +1125,8 @@ bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, 
   if (p.resident && rd == 2 * plan->channel_tile) return false;
   if (p.mode == kModeElement) return true;
   if (stats_in) return false;
+  // The persistent kernel reads no whole rows: its scales come from the statistics pass.
+  if (fwd_uses_persist(x, out, plan, rd, dtype, flags, batch)) return true;
   const int32_t c = plan->channels, j = c / 128;
   return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));
 }
@@ -1285,7 +1300,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   const bool resident = path.resident && rd == 2 * d;
   const int32_t mode = path.mode;
   float* scale = nullptr;
-  if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr)) {
+  if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr, batch)) {
     const size_t need = ow_fwd_workspace_bytes(plan, batch, flags);
     OW_CHECK_ARG(workspace && workspace_bytes >= need, "workspace holds %zu bytes; %zu needed", workspace_bytes,
                  need);
@@ -1321,6 +1336,40 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.drop_scale = drop_scale;
     const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level) ? ow::launch_fwd_wave(r, dtype, s)
                                                                           : ow::launch_fwd_resident(r, dtype, s);
+    if (rc == OW_OK) ow::clear_error();
+    return rc;
+  }
+  if (ow::fwd_uses_persist(x, out, plan, rd, dtype, flags, batch)) {
+    ow::PersistArgs p{};
+    p.x = static_cast<const uint16_t*>(x);
+    p.out = static_cast<uint16_t*>(out);
+    p.packed = static_cast<const uint16_t*>(packed);
+    p.tok = token_index;
+    p.out_tok = out_rows;
+    p.batch = batch;
+    p.n_tok = n;
+    p.channels = c;
+    p.q_s = q_s;
+    p.q_c = q_c;
+    p.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
+    p.eps = eps;
+    p.drop_scale = drop_scale;
+    p.norm = ow::kNormNone;
+    if (norm) {
+      if (scale) {
+        p.norm = ow::kNormBuffer;
+        p.row_scale = scale;
+      } else {
+        p.norm = ow::kNormPartials;
+        p.row_scale = stats_in;
+        p.parts = stats_in_parts;
+      }
+    }
+    if (stats_out && !out_rows) {
+      p.stats_out = stats_out;
+      if (stats_written) *stats_written = 1;
+    }
+    const int rc = ow::launch_fwd_persist(p, dtype, s);
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }

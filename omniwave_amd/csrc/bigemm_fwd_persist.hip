@@ -1,0 +1,440 @@
+// Persistent BiGEMM forward for d = 128, rd = 256 with contiguous channel groups (radix level 0,
+// or one group) and 16-byte aligned rows: the 14x14x512 and 7x7x1024 stages of OmniWeave-T.
+//
+// Same math and operand packing as bigemm_fwd.hip (reference omniweave/ops/reference.py:147-171;
+// operand scheme in ow_device.h).  Organisation:
+//   * one workgroup of eight waves per CU (145 KB of LDS), persistent over units of 256 token
+//     rows (16 token groups: one 32-token pair per wave) x one channel group; unit u is row chunk
+//     u / q_c, channel group u % q_c, and workgroup b takes units b, b + grid, ...  With the grid
+//     a multiple of 8 every unit of a workgroup runs on that workgroup's XCD (workgroups are
+//     dispatched round-robin over the 8 XCDs), so an XCD sees the weights of only 8 / q_c
+//     channel groups in its L2 (one at q_c = 8);
+//   * the eight waves share one stream of weight chunks (24 KB per 32-row chunk of the expanded
+//     dimension, three LDS buffers, copied global -> LDS with global_load_lds), with the chunk
+//     loop of bigemm_fwd.hip: chunk ec + 1's U'/V' products issued with chunk ec's gate values
+//     between them, then chunk ec's W += Z B_o;
+//   * the x tile is copied straight into LDS (buffer_load ... lds; pad tokens read as zero): each
+//     wave loads, and later reads, only its own 32 rows, so the tile needs no workgroup
+//     barrier.  A wave's rows of the next unit are requested as soon as its output phase has
+//     read the current rows for the residual, and land while the stores and the next unit's
+//     first chunk copy are in flight;
+//   * the RMSNorm row scales come from a statistics buffer (a separate pass) or from the
+//     previous block's per-group sums of squares (chained statistics): the tile holds only the
+//     unit's own channel group;
+//   * the output: delta = A_o W, rounded (and scaled by the drop-path factor), is staged per
+//     wave in the chunk buffers that the loop no longer reads, and stored as 16-byte row pieces
+//     with the residual round(x + delta), x from the tile.
+// Tile layout: row r holds its 128 channels, 16-byte piece p at slot p ^ (4 ((r >> 2) & 1)), so
+// the two lane halves of a token-side column read (rows 4 apart) hit different LDS banks.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "ow_device.h"
+
+namespace ow {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kRD = 256;
+constexpr int kKS = kD / 16;             // 16-deep K steps over the channel group
+constexpr int kMB = kD / 32;             // 32-channel output blocks
+constexpr int kNCH = kRD / 32;           // 32-row chunks of the expanded dimension
+constexpr int kFrU = kKS;                // B_u'^T fragments per chunk (B_v'^T the same)
+constexpr int kFrO = 2 * kMB;            // B_o fragments per chunk
+constexpr int kFrCh = 2 * kFrU + kFrO;   // 24 fragments = 24 KB per chunk
+constexpr int kChElems = kFrCh * kFragElems;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 32 * kWaves;       // 256 rows per unit
+constexpr int kGroups = kRows / kG;      // 16 token groups per unit
+constexpr int kDpw = kFrCh / kWaves;     // chunk-copy fragments per wave
+constexpr int kTileOps = 32 * kD * 2 / 1024;  // 1 KB tile copies per wave (8)
+constexpr int kLdo = kD + 8;             // output staging row stride (elements)
+static_assert(kFrCh % kWaves == 0, "chunk copies split evenly over the waves");
+
+struct PersistLds {
+  uint16_t x[kRows * kD];              // the unit's tile, 64 KB
+  uint16_t w[3][kChElems];             // weight chunk buffers, after the chunk loop the output staging
+  int32_t rowid[2][kRows];             // per unit (double-buffered): input row, -1 for pad rows
+  int32_t rowout[2][kRows];            // output row, -1: not stored
+  float rsc[2][kRows];                 // RMSNorm scale of each row
+  float dsc[2][kGroups];               // drop-path scale of each token group
+};
+static_assert(32 * kLdo * 2 * kWaves <= 3 * kChElems * 2, "output staging fits in the chunk buffers");
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t persist_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOffOut = 0x80000000u;  // a byte offset past every buffer (the launcher keeps
+                                           // x below 2 GiB)
+
+// 16 bytes per lane from x (byte offset voff, kOffOut: zeros) to LDS byte address lds + 16 lane,
+// untracked by the compiler (no compiler wait before later LDS reads); the kernel waits with
+// wait_vmcnt.
+__device__ __forceinline__ void tile_copy(__amdgpu_buffer_rsrc_t rx, uint32_t voff, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rx),
+               "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// A wave-uniform pointer the compiler may not prove uniform (the scalar operand of a copy).
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Token-table entries of one row of a unit (loads only: consumed by meta_write a phase later).
+struct TokLoad {
+  int32_t t, to, b;
+  float ds;
+};
+
+template <class Ty>
+__global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units) {
+  __shared__ __attribute__((aligned(16))) PersistLds sh;
+  // lane and wave are re-read opaquely at the top of every unit (see the loop): the compiler
+  // would otherwise compute hundreds of per-lane addresses once, before the loop, and keep them
+  // live (spilled) through it.
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int hh = lane >> 5, l32 = lane & 31;
+  uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
+  const uint32_t xbytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
+  const __amdgpu_buffer_rsrc_t rx = persist_rsrc(a.x, xbytes);
+  const int64_t n_groups = static_cast<int64_t>(a.batch) * a.q_s;
+
+  // Row l < 32 of this wave in unit u (lanes < 32): the token-table loads of meta_write.
+  auto meta_load = [&](int32_t u) {
+    TokLoad e{-1, -1, -1, 1.0f};
+    if (lane < 32) {
+      const int64_t tg = static_cast<int64_t>(u / a.q_c) * kGroups + 2 * wave + (lane >> 4);
+      if (tg < n_groups) {
+        e.b = static_cast<int32_t>(tg / a.q_s);
+        const int32_t sg = static_cast<int32_t>(tg - static_cast<int64_t>(e.b) * a.q_s);
+        e.t = a.tok[sg * kG + (lane & 15)];
+        if (a.out_tok) e.to = a.out_tok[sg * kG + (lane & 15)];
+        if (a.drop_scale) e.ds = a.drop_scale[e.b];
+      }
+    }
+    return e;
+  };
+  // Input / output rows and drop-path scales of this wave's rows, slot s; returns the lane's
+  // input row (-1: pad token or past the batch).
+  auto meta_write = [&](const TokLoad& e, int s) {
+    int32_t id = -1, od = -1;
+    if (lane < 32) {
+      if (e.b >= 0 && e.t >= 0 && e.t < a.n_tok) {
+        id = e.b * a.n_tok + e.t;
+        od = id;
+        if (a.out_tok) od = (e.to >= 0 && e.to < a.n_tok) ? e.b * a.n_tok + e.to : -1;
+      }
+      sh.rowid[s][32 * wave + lane] = id;
+      sh.rowout[s][32 * wave + lane] = od;
+      if ((lane & 15) == 0) sh.dsc[s][2 * wave + (lane >> 4)] = e.ds;
+    }
+    wave_lds_sync();
+    return id;
+  };
+  // kNormBuffer: the row's scale; kNormPartials: the sum of its partial sums of squares.
+  auto stats_load = [&](int32_t id) {
+    float v = 0.0f;
+    if (lane < 32 && id >= 0) {
+      if (a.norm == kNormBuffer) {
+        v = a.row_scale[id];
+      } else if (a.norm == kNormPartials) {
+        for (int q = 0; q < a.parts; ++q) v += a.row_scale[static_cast<int64_t>(id) * a.parts + q];
+      }
+    }
+    return v;
+  };
+  auto stats_write = [&](float v, int32_t id, int s) {
+    if (lane < 32) {
+      float r = 1.0f;
+      if (id >= 0 && a.norm == kNormBuffer) r = v;
+      if (id >= 0 && a.norm == kNormPartials) r = rms_scale<Ty>(v / static_cast<float>(a.channels), a.eps);
+      sh.rsc[s][32 * wave + lane] = r;
+    }
+  };
+  // This wave's 32 tile rows of unit u (slot s): copy k covers rows 4k .. 4k + 3, lane -> row
+  // 4k + lane / 16, slot lane % 16, which holds the row's piece (lane % 16) ^ (4 (k & 1)).
+  auto issue_tile = [&](int32_t u, int s) {
+    const uint32_t col0 = static_cast<uint32_t>((u % a.q_c) * kD * 2);
+#pragma unroll
+    for (int k = 0; k < kTileOps; ++k) {
+      const int r = 32 * wave + 4 * k + (lane >> 4);
+      const int32_t id = sh.rowid[s][r];
+      const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ (4 * (k & 1)));
+      const uint32_t voff = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) + col0 + 16u * piece
+                                    : kOffOut;
+      tile_copy(rx, voff, lds_addr(&sh.x[(32 * wave_u + 4 * k) * kD]));
+    }
+  };
+  auto issue_chunk = [&](int32_t u, int ec) {
+    const uint16_t* src =
+        uniform_ptr(a.packed + kHeadElems + (static_cast<size_t>(u % a.q_c) * kNCH + ec) * kChElems);
+    uint16_t* dst = sh.w[ec % 3];
+#pragma unroll
+    for (int i = 0; i < kDpw; ++i) {
+      const int f = wave_u + i * kWaves;
+      copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane16);
+    }
+  };
+
+  int32_t u = blockIdx.x;
+  if (u >= n_units) return;
+  int s = 0;
+  {
+    const int32_t id = meta_write(meta_load(u), 0);
+    issue_tile(u, 0);
+    issue_chunk(u, 0);
+    stats_write(stats_load(id), id, 0);
+    wave_lds_sync();
+    wait_vmcnt<kDpw>();  // this wave's tile rows; chunk 0 may still be in flight
+  }
+
+#pragma unroll 1
+  for (; u < n_units; u += gridDim.x, s ^= 1) {
+    asm volatile("" : "+v"(lane), "+v"(wave));
+    hh = lane >> 5;
+    l32 = lane & 31;
+    lane16 = 16u * static_cast<uint32_t>(lane);
+    const int32_t un = u + static_cast<int32_t>(gridDim.x);
+    const bool has_next = un < n_units;
+    const int qc = u % a.q_c;
+    TokLoad en{-1, -1, -1, 1.0f};
+    if (has_next) en = meta_load(un);  // consumed after the token side
+
+    // Token side of this wave's pair (rows 32 wave .. + 31 of the tile).
+    u32x4 Pu[kKS], Pv[kKS], xk[kKS / 2][2];
+    {
+      // The token operands are read per unit (L2 hits) rather than kept live through the loop.
+      const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
+      const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
+      int col[kKS / 2];  // tile column of channel 32 cb + l32 for this lane half's rows
+#pragma unroll
+      for (int cb = 0; cb < kKS / 2; ++cb) col[cb] = (32 * cb + l32) ^ (32 * hh);
+      u32x4 bu = fAu, bv = fAv;
+      if (a.norm != kNormNone) {
+        const float* r8 = &sh.rsc[s][32 * wave + 16 * ((lane >> 4) & 1) + 4 * hh];
+        bu = scale8<Ty>(fAu, r8);
+        bv = scale8<Ty>(fAv, r8);
+      }
+      pair_token_side<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
+    }
+    int32_t id_next = -1;
+    if (has_next) id_next = meta_write(en, s ^ 1);
+
+    // Chunk 0 has landed for every wave; chunks 1 and 2 go out, then the next unit's statistics
+    // input (consumed at the end of this unit; younger than the copies, so the chunk waits below
+    // stay exact).
+    wait_lds_dma();
+    __syncthreads();
+    issue_chunk(u, 1);
+    issue_chunk(u, 2);
+    float snext = 0.0f;
+    if (has_next) snext = stats_load(id_next);
+
+    f32x16 W[kMB];
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) W[mb][i] = 0.0f;
+
+    // Chunk loop (as bigemm_fwd.hip's pipelined loop): one step issues chunk ec + 1's U'/V'
+    // products and chunk ec's W += Z B_o, their fragments read DEPTH ahead, with one gate value
+    // of chunk ec computed after each U'/V' product.
+    constexpr int DEPTH = 4;
+    auto stream = [&](auto nu_tag, auto no_tag, uint32_t bn, uint32_t bo, f32x16& Un, f32x16& Vn,
+                      const f32x16& Uc, const f32x16& Vc) {
+      constexpr int NU = decltype(nu_tag)::value;  // U'/V' fragments of chunk ec + 1 (0 or 2 KS)
+      constexpr int NO = decltype(no_tag)::value;  // B_o fragments of chunk ec (0 or kFrO)
+      constexpr int NF = NU + NO;
+      static_assert(NO == 0 || NU == 0 || NU == 16, "one gate value per U'/V' product");
+      auto read = [&](auto ic) -> u32x4 {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i < NU)
+          return lds_read_async<((i & 1) ? kFrU + i / 2 : i / 2) * kFragElems * 2>(bn);
+        else
+          return lds_read_async<(i - NU) * kFragElems * 2>(bo);
+      };
+      u32x4 fr[DEPTH];
+      static_for<0, DEPTH>([&](auto ic) {
+        if constexpr (decltype(ic)::value < NF) fr[decltype(ic)::value] = read(ic);
+      });
+      u32x4 Z[2];
+      float zl = 0.0f;
+      auto gate = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const float z = silu_gate(Uc[k], Vc[k]);
+        if constexpr (k % 2 == 0)
+          zl = z;
+        else
+          Z[k / 8][(k % 8) / 2] = Ty::pack2(zl, z);
+      };
+      if constexpr (NO > 0 && NU == 0) static_for<0, 16>(gate);
+      if constexpr (NU > 0) {
+        Un = f32x16{};
+        Vn = f32x16{};
+      }
+      static_for<0, NF>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int after = NF - 1 - i < DEPTH - 1 ? NF - 1 - i : DEPTH - 1;
+        lds_wait<after>(fr[i % DEPTH]);
+        if constexpr (i < NU) {
+          if constexpr (i % 2 == 0)
+            Un = Ty::mma32(fr[i % DEPTH], Pu[i / 2], Un);
+          else
+            Vn = Ty::mma32(fr[i % DEPTH], Pv[i / 2], Vn);
+        } else {
+          constexpr int j = i - NU;
+          W[j / 2] = Ty::mma32(Z[j % 2], fr[i % DEPTH], W[j / 2]);
+        }
+        if constexpr (i + DEPTH < NF) fr[i % DEPTH] = read(std::integral_constant<int, i + DEPTH>{});
+        if constexpr (NO > 0 && i < NU) gate(ic);
+      });
+      if constexpr (NU > 0 && NO > 0) {
+        static_for<0, NU>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // VALU, transcendental
+        });
+      }
+    };
+    using Nu = std::integral_constant<int, 2 * kKS>;
+    using No = std::integral_constant<int, kFrO>;
+    using Zero = std::integral_constant<int, 0>;
+    auto base = [&](int ec) { return lds_addr(sh.w[ec % 3]) + lane16; };
+    // Step ec waits for chunk ec + 1 (issued at step ec - 1, or before the loop for ec <= 1: at
+    // ec = 0 chunk 2, issued after it, may still be in flight); the barrier also means every
+    // wave is done with chunk ec - 1, whose buffer takes chunk ec + 2.
+    auto step = [&](int ec, f32x16& Uc, f32x16& Vc, f32x16& Un, f32x16& Vn) {
+      const uint32_t bo = base(ec) + 2u * kFrU * kFragElems * 2u;
+      if (ec + 1 < kNCH) {
+        if (ec == 0)
+          wait_vmcnt<kDpw>();
+        else
+          wait_lds_dma();
+        __syncthreads();
+        if (ec >= 1 && ec + 2 < kNCH) issue_chunk(u, ec + 2);
+        stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+      } else {
+        stream(Zero{}, No{}, 0u, bo, Un, Vn, Uc, Vc);
+      }
+    };
+    f32x16 Ua, Va, Ub = {}, Vb = {};
+    stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
+#pragma unroll
+    for (int ec = 0; ec < kNCH; ec += 2) {
+      step(ec, Ua, Va, Ub, Vb);
+      step(ec + 1, Ub, Vb, Ua, Va);
+    }
+
+    // Output.  Past the barrier every wave is done with the chunk buffers: each stages its 32
+    // rows of rounded delta (times the drop-path scale) there; the residual's x elements are
+    // this unit's tile rows, read from LDS before the next unit's tile rows replace them.
+    mfma_drain();
+    __syncthreads();
+    const int piece = lane & 15;
+    const int64_t colq = static_cast<int64_t>(qc) * kD;
+    const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
+    f32x16 dl[kMB];
+    pair_output<Ty, kMB>(W, fAo, lane, dl);
+    mfma_drain();
+    uint16_t* st = &sh.w[0][0] + wave * 32 * kLdo;
+    const float s0 = sh.dsc[s][2 * wave], s1 = sh.dsc[s][2 * wave + 1];
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        uint32_t v = Ty::pack2(dl[mb][i], dl[mb][i + 1]);
+        if (a.drop_scale) {
+          const float sc = i < 8 ? s0 : s1;
+          v = Ty::pack2(Ty::to_f32(lo16(v)) * sc, Ty::to_f32(hi16(v)) * sc);
+        }
+        const int r0 = pair_token_row(i, hh);
+        st[r0 * kLdo + 32 * mb + l32] = lo16(v);
+        st[(r0 + 1) * kLdo + 32 * mb + l32] = hi16(v);
+      }
+    // Pass k covers piece lane % 16 of rows lane / 16 + 4 k of the wave (tile slot of the piece:
+    // piece ^ 4 (k & 1)).
+    u32x4 xv[8], val[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int rr = (lane >> 4) + 4 * k;
+      xv[k] = *reinterpret_cast<const u32x4*>(&sh.x[(32 * wave + rr) * kD + ((piece ^ (4 * (k & 1))) * 8)]);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) val[k] = *reinterpret_cast<const u32x4*>(&st[((lane >> 4) + 4 * k) * kLdo + piece * 8]);
+    // The tile reads are complete (their values are in registers): the next unit's rows go out.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (has_next) issue_tile(un, s ^ 1);
+    const __amdgpu_buffer_rsrc_t ro = persist_rsrc(a.out, xbytes);
+    const __amdgpu_buffer_rsrc_t rs =
+        persist_rsrc(a.stats_out, static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.q_c * 4));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int rr = (lane >> 4) + 4 * k;
+      const int32_t id = sh.rowout[s][32 * wave + rr];
+      u32x4 v = val[k];
+      if (a.residual) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = add_residual2<Ty>(xv[k][e], v[e]);
+      }
+      if (a.stats_out) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(v[e], acc);
+        acc = group_sum<16>(acc);
+        const uint32_t so = (piece == 15 && id >= 0) ? (static_cast<uint32_t>(id) * a.q_c + qc) * 4u : kOffOut;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc), rs, so, 0, 0);
+      }
+      const uint32_t oo = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) +
+                                        static_cast<uint32_t>(colq * 2) + 16u * piece
+                                  : kOffOut;
+      __builtin_amdgcn_raw_buffer_store_b128(v, ro, oo, 0, 0);
+    }
+    if (has_next) {
+      stats_write(snext, id_next, s ^ 1);
+      wave_lds_sync();
+      __syncthreads();  // every wave is done with its staging rows, which chunk 0 overwrites
+      issue_chunk(un, 0);
+      wait_vmcnt<kDpw>();  // the next unit's tile rows (and this unit's stores); chunk 0 may be in flight
+    }
+  }
+}
+
+}  // namespace
+
+bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems) {
+  return d == kD && rd == kRD && channels == q_c * kD && x_elems * 2 < (int64_t(1) << 31);
+}
+
+int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) {
+  const int64_t chunks = (static_cast<int64_t>(a.batch) * a.q_s + kGroups - 1) / kGroups;
+  const int64_t units = chunks * a.q_c;
+  if (units == 0) return OW_OK;
+  if (units > 0x7fffffff) return fail(OW_ERR_UNSUPPORTED, "grid too large (%lld units)", (long long)units);
+  // One workgroup per CU, a multiple of 8 (whole XCD rounds) when there are enough units.
+  int64_t grid = device_cus();
+  if (grid > units) grid = units;
+  if (grid >= 8) grid -= grid % 8;
+  const dim3 g(static_cast<unsigned>(grid));
+  if (a.norm == kNormInline) return fail(OW_ERR_INVALID, "the persistent forward takes precomputed row statistics");
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL(bigemm_fwd_persist_kernel<BF16>, g, dim3(kThreads), 0, stream, a, static_cast<int32_t>(units));
+  else if (dtype == OW_DTYPE_F16)
+    hipLaunchKernelGGL(bigemm_fwd_persist_kernel<F16>, g, dim3(kThreads), 0, stream, a, static_cast<int32_t>(units));
+  else
+    return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  return hip_status(hipGetLastError(), "bigemm_fwd_persist_kernel launch");
+}
+
+}  // namespace ow

@@ -218,40 +218,72 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     u32x4 Pu[kKS], Pv[kKS], xk[kMB][2];
     pair_token_side<Ty, kKS>(tile, kLdt, col, bu, bv, lane, Pu, Pv, xk);
 
-    // Channel side: the four chunks of the expanded dimension, weights from LDS.  The U'/V'
-    // fragments of chunk e + 1 are read while chunk e's gate runs, so the MFMAs do not wait on
-    // LDS latency one fragment at a time.
+    // Channel side over the four chunks of the expanded dimension, software-pipelined: step e
+    // issues chunk e + 1's U'/V' products with two of chunk e's gate values after each of them
+    // (the gate's VALU work runs while the products execute), then chunk e's W += Z B_o
+    // products.  The weight fragments come from LDS DEPTH reads ahead of their MFMAs
+    // (lds_read_async: no compiler wait per read; lds_wait before each use).
     f32x16 W[kMB] = {};
-    u32x4 fr[2 * kKS];
-    auto read_uv = [&](int e) {
-#pragma unroll
-      for (int f = 0; f < 2 * kKS; ++f) fr[f] = sh.w[e * kFrCh + f][lane];
-    };
-    read_uv(0);
-#pragma unroll
-    for (int e = 0; e < kNCH; ++e) {
-      f32x16 U = {}, V = {};
-#pragma unroll
-      for (int ks = 0; ks < kKS; ++ks) {
-        U = Ty::mma32(fr[ks], Pu[ks], U);
-        V = Ty::mma32(fr[kKS + ks], Pv[ks], V);
-      }
-      u32x4 fo[2 * kMB];
-#pragma unroll
-      for (int f = 0; f < 2 * kMB; ++f) fo[f] = sh.w[e * kFrCh + 2 * kKS + f][lane];
-      if (e + 1 < kNCH) read_uv(e + 1);
+    const uint32_t wbase = lds_addr(&sh.w[0][lane]);
+    constexpr int DEPTH = 4;
+    auto step = [&](auto e_tag, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
+      constexpr int E = decltype(e_tag)::value;      // chunk of the gate and B_o products; -1: none
+      constexpr int NU = E + 1 < kNCH ? 2 * kKS : 0;  // U'/V' products of chunk E + 1 (U, V alternate)
+      constexpr int NO = E >= 0 ? 2 * kMB : 0;        // B_o products of chunk E
+      constexpr int NF = NU + NO;
+      static_assert(NU == 0 || NO == 0 || 2 * NU == 16, "two gate values per U'/V' product");
+      auto read = [&](auto ic) -> u32x4 {
+        constexpr int i = decltype(ic)::value;
+        constexpr int f = i < NU ? (E + 1) * kFrCh + ((i & 1) ? kKS + i / 2 : i / 2) : E * kFrCh + 2 * kKS + (i - NU);
+        return lds_read_async<f * kFragElems * 2>(wbase);
+      };
+      u32x4 fr[DEPTH];
+      static_for<0, DEPTH>([&](auto ic) {
+        if constexpr (decltype(ic)::value < NF) fr[decltype(ic)::value] = read(ic);
+      });
+      // Gate values k = 8 s + 2 q + h of chunk E -> Z[s] word q, half h.
       u32x4 Z[2];
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          Z[s2][q] = Ty::pack2(silu_gate(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q]),
-                               silu_gate(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1]));
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], fo[2 * mb + s2], W[mb]);
-    }
+      float zl = 0.0f;
+      auto gate = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const float z = silu_gate(Uc[k], Vc[k]);
+        if constexpr (k % 2 == 0)
+          zl = z;
+        else
+          Z[k / 8][(k % 8) / 2] = Ty::pack2(zl, z);
+      };
+      if constexpr (NO > 0 && NU == 0) static_for<0, 16>(gate);
+      if constexpr (NU > 0) {
+        Un = f32x16{};
+        Vn = f32x16{};
+      }
+      static_for<0, NF>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int after = NF - 1 - i < DEPTH - 1 ? NF - 1 - i : DEPTH - 1;
+        lds_wait<after>(fr[i % DEPTH]);
+        if constexpr (i < NU) {
+          if constexpr (i % 2 == 0)
+            Un = Ty::mma32(fr[i % DEPTH], Pu[i / 2], Un);
+          else
+            Vn = Ty::mma32(fr[i % DEPTH], Pv[i / 2], Vn);
+        } else {
+          constexpr int j = i - NU;
+          W[j / 2] = Ty::mma32(Z[j % 2], fr[i % DEPTH], W[j / 2]);
+        }
+        if constexpr (i + DEPTH < NF) fr[i % DEPTH] = read(std::integral_constant<int, i + DEPTH>{});
+        if constexpr (NO > 0 && i < NU) {
+          gate(std::integral_constant<int, 2 * i>{});
+          gate(std::integral_constant<int, 2 * i + 1>{});
+        }
+      });
+    };
+    f32x16 Ua, Va, Ub = {}, Vb = {};
+    step(std::integral_constant<int, -1>{}, Ua, Va, Ub, Vb);
+    step(std::integral_constant<int, 0>{}, Ub, Vb, Ua, Va);
+    step(std::integral_constant<int, 1>{}, Ua, Va, Ub, Vb);
+    step(std::integral_constant<int, 2>{}, Ub, Vb, Ua, Va);
+    step(std::integral_constant<int, 3>{}, Ua, Va, Ub, Vb);
+    static_assert(kNCH == 4, "four chunks: the step sequence above");
 
     // delta = A_o W, rounded, plus x (and the drop-path scale), into the tile in place: the
     // token side has read it.

@@ -57,7 +57,7 @@ int ow_bigemm_fwd_noalloc(const void* x, void* out, float eps, const void* packe
   // Rejected before any device call when the launch would need more row scales than the array
   // holds.
   const int64_t rows = static_cast<int64_t>(batch) * plan->height * plan->width;
-  const bool needs = ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, false);
+  const bool needs = ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, false, batch);
   OW_CHECK_SUPPORTED(!needs || rows <= ow::kScratchRows,
                      "batch * H * W = %lld rows of RMSNorm scales exceed the %lld rows of the library's scratch",
                      (long long)rows, (long long)ow::kScratchRows);

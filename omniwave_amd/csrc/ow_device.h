@@ -550,7 +550,7 @@ struct FwdPath {
 };
 FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c, int32_t dtype, int32_t flags);
 bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype,
-                            int32_t flags, bool stats_in);
+                            int32_t flags, bool stats_in, int32_t batch);
 int launch_fwd_resident(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
 // Where the RMSNorm row scales of a streamed launch come from (bigemm_fwd.hip, FwdArgs).
 constexpr int kNormNone = 0;
@@ -558,6 +558,31 @@ constexpr int kNormBuffer = 1;
 constexpr int kNormInline = 2;
 constexpr int kNormPartials = 3;
 
+
+// Persistent d = 128 forward (bigemm_fwd_persist.hip): one eight-wave workgroup per CU over
+// units of 256 rows x one contiguous channel group, the next unit's tile copied into LDS during
+// the current unit's output phase.  RMSNorm scales from a statistics buffer or the previous
+// block's per-group sums (norm: kNormNone, kNormBuffer or kNormPartials).
+struct PersistArgs {
+  const uint16_t* x;
+  uint16_t* out;
+  const uint16_t* packed;
+  const int32_t* tok;       // [q_s * 16]
+  const int32_t* out_tok;   // [q_s * 16] output row of each token slot; NULL: the token table
+  const float* row_scale;   // kNormBuffer: [batch * n_tok] scales; kNormPartials: [batch * n_tok, parts] sums
+  float* stats_out;         // NULL, or [batch * n_tok, q_c]: sum of squares of each stored row's group columns
+  const float* drop_scale;  // NULL, or [batch]: per-image multiplier of the rounded delta
+  int32_t batch, n_tok, channels, q_s, q_c;
+  int32_t norm;
+  int32_t parts;
+  float eps;
+  int32_t residual;
+};
+bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
+int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream);
+// Whether a bf16 / f16 launch takes the persistent kernel.
+bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype, int32_t flags,
+                      int32_t batch);
 
 // One (pair, channel group) unit per wave, the group's weights in LDS (bigemm_fwd_wave.hip):
 // d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2}, channel groups in channel order.
