@@ -82,6 +82,37 @@ __global__ void __launch_bounds__(kThreads) rms_rows_kernel(RmsArgs a) {
   }
 }
 
+// C = 128 J (J in {1, 2, 4, 8}): 16 lanes per row, lane l16 reads vectors l16 + 16 j of its row,
+// 4 rows per wave instruction, NP passes per wave (16 loads in flight per lane), sums over the
+// 16 lanes with DPP.
+template <class Ty, int J>
+__global__ void __launch_bounds__(kThreads) rms_rows16_kernel(RmsArgs a) {
+  constexpr int NP = J < 16 ? 16 / J : 1;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * (4 * NP);
+  u32x4 v[NP][J];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t row = base + 4 * p + (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      v[p][j] = u32x4{0u, 0u, 0u, 0u};
+      if (row < a.rows) v[p][j] = *reinterpret_cast<const u32x4*>(a.x + row * a.channels + ((lane & 15) + 16 * j) * 8);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(v[p][j][e], acc);
+    acc = group_sum<16>(acc);
+    const int64_t row = base + 4 * p + (lane >> 4);
+    if ((lane & 15) == 15 && row < a.rows) a.scale[row] = rms_scale<Ty>(acc / static_cast<float>(a.channels), a.eps);
+  }
+}
+
 // Any C: one wave per row, element loads.
 template <class Ty>
 __global__ void __launch_bounds__(kThreads) rms_rows_generic_kernel(RmsArgs a) {
@@ -1020,6 +1051,20 @@ template <class Ty>
 int launch_rms(const RmsArgs& a, hipStream_t s) {
   const int vprw = a.channels % 8 == 0 ? a.channels / 8 : 0;
   const unsigned blocks8 = static_cast<unsigned>((a.rows + kWaves * 8 - 1) / (kWaves * 8));
+  auto rows16 = [&](auto j_tag) {
+    constexpr int J = decltype(j_tag)::value;
+    constexpr int RW = 4 * (J < 16 ? 16 / J : 1);  // rows per wave
+    const unsigned blocks = static_cast<unsigned>((a.rows + kWaves * RW - 1) / (kWaves * RW));
+    hipLaunchKernelGGL((rms_rows16_kernel<Ty, J>), dim3(blocks), dim3(kThreads), 0, s, a);
+    return hip_status(hipGetLastError(), "rms_rows16_kernel launch");
+  };
+  switch (vprw) {
+    case 16: return rows16(std::integral_constant<int, 1>{});
+    case 32: return rows16(std::integral_constant<int, 2>{});
+    case 64: return rows16(std::integral_constant<int, 4>{});
+    case 128: return rows16(std::integral_constant<int, 8>{});
+    default: break;
+  }
   switch (vprw) {
     case 8: hipLaunchKernelGGL((rms_rows_kernel<Ty, 8>), dim3(blocks8), dim3(kThreads), 0, s, a); break;
     case 16: hipLaunchKernelGGL((rms_rows_kernel<Ty, 16>), dim3(blocks8), dim3(kThreads), 0, s, a); break;

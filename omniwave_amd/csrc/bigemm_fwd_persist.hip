@@ -52,6 +52,7 @@ constexpr int kGroups = kRows / kG;      // 16 token groups per unit
 constexpr int kDpw = kFrCh / kWaves;     // chunk-copy fragments per wave
 constexpr int kTileOps = 32 * kD * 2 / 1024;  // 1 KB tile copies per wave (8)
 constexpr int kLdo = kD + 8;             // output staging row stride (elements)
+constexpr int kTokLds = 512;             // token-table entries kept in LDS (q_s <= 32)
 static_assert(kFrCh % kWaves == 0, "chunk copies split evenly over the waves");
 
 struct PersistLds {
@@ -61,6 +62,9 @@ struct PersistLds {
   int32_t rowout[2][kRows];            // output row, -1: not stored
   float rsc[2][kRows];                 // RMSNorm scale of each row
   float dsc[2][kGroups];               // drop-path scale of each token group
+  u32x4 tok_ops[3][64];                // token-side operand rows (A_u, A_v, A_o), read per unit
+  int32_t tok[kTokLds];                // the token table when it has at most kTokLds entries
+  int32_t out_tok[kTokLds];            // the output-row table (same bound)
 };
 static_assert(32 * kLdo * 2 * kWaves <= 3 * kChElems * 2, "output staging fits in the chunk buffers");
 
@@ -110,6 +114,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   const uint32_t xbytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
   const __amdgpu_buffer_rsrc_t rx = persist_rsrc(a.x, xbytes);
   const int64_t n_groups = static_cast<int64_t>(a.batch) * a.q_s;
+  const bool tok_lds = a.q_s * kG <= kTokLds;  // token tables copied to LDS at the start
 
   // Row l < 32 of this wave in unit u (lanes < 32): the token-table loads of meta_write.
   auto meta_load = [&](int32_t u) {
@@ -119,8 +124,14 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       if (tg < n_groups) {
         e.b = static_cast<int32_t>(tg / a.q_s);
         const int32_t sg = static_cast<int32_t>(tg - static_cast<int64_t>(e.b) * a.q_s);
-        e.t = a.tok[sg * kG + (lane & 15)];
-        if (a.out_tok) e.to = a.out_tok[sg * kG + (lane & 15)];
+        const int ti = sg * kG + (lane & 15);
+        if (tok_lds) {
+          e.t = sh.tok[ti];
+          if (a.out_tok) e.to = sh.out_tok[ti];
+        } else {
+          e.t = a.tok[ti];
+          if (a.out_tok) e.to = a.out_tok[ti];
+        }
         if (a.drop_scale) e.ds = a.drop_scale[e.b];
       }
     }
@@ -191,6 +202,14 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   int32_t u = blockIdx.x;
   if (u >= n_units) return;
   int s = 0;
+  if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
+  if (tok_lds) {
+    for (int i = threadIdx.x; i < a.q_s * kG; i += kThreads) {
+      sh.tok[i] = a.tok[i];
+      if (a.out_tok) sh.out_tok[i] = a.out_tok[i];
+    }
+  }
+  __syncthreads();
   {
     const int32_t id = meta_write(meta_load(u), 0);
     issue_tile(u, 0);
@@ -215,9 +234,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // Token side of this wave's pair (rows 32 wave .. + 31 of the tile).
     u32x4 Pu[kKS], Pv[kKS], xk[kKS / 2][2];
     {
-      // The token operands are read per unit (L2 hits) rather than kept live through the loop.
-      const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
-      const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
+      // The token operands are read per unit from LDS rather than kept live through the loop.
+      const u32x4 fAu = sh.tok_ops[0][lane];
+      const u32x4 fAv = sh.tok_ops[1][lane];
       int col[kKS / 2];  // tile column of channel 32 cb + l32 for this lane half's rows
 #pragma unroll
       for (int cb = 0; cb < kKS / 2; ++cb) col[cb] = (32 * cb + l32) ^ (32 * hh);
@@ -343,7 +362,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     __syncthreads();
     const int piece = lane & 15;
     const int64_t colq = static_cast<int64_t>(qc) * kD;
-    const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
+    const u32x4 fAo = sh.tok_ops[2][lane];
     f32x16 dl[kMB];
     pair_output<Ty, kMB>(W, fAo, lane, dl);
     mfma_drain();
@@ -406,7 +425,12 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       wave_lds_sync();
       __syncthreads();  // every wave is done with its staging rows, which chunk 0 overwrites
       issue_chunk(un, 0);
-      wait_vmcnt<kDpw>();  // the next unit's tile rows (and this unit's stores); chunk 0 may be in flight
+      // The next unit's tile rows have landed once at most this unit's stores (8 row pieces, 8
+      // statistics values) and chunk 0's copies, all issued after them, are outstanding.
+      if (a.stats_out)
+        wait_vmcnt<kDpw + 16>();
+      else
+        wait_vmcnt<kDpw + 8>();
     }
   }
 }
