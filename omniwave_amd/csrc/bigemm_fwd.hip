@@ -1146,10 +1146,10 @@ FwdPath fwd_path(const void* x, const void* out, const OwPlan* plan, int32_t q_c
 }
 
 // d = 128, rd = 256 launches with contiguous channel groups and 16-byte aligned rows (bf16 /
-// f16, not fp8) take the persistent kernel.
+// f16, also with the fp8 channel side) take the persistent kernel.
 bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype, int32_t flags,
                       int32_t batch) {
-  if ((dtype != OW_DTYPE_BF16 && dtype != OW_DTYPE_F16) || (flags & OW_FUSE_FP8)) return false;
+  if (dtype != OW_DTYPE_BF16 && dtype != OW_DTYPE_F16) return false;
   int32_t q_s = 0, q_c = 0;
   if (ow_plan_dims(plan, &q_s, &q_c) != OW_OK) return false;
   const FwdPath p = fwd_path(x, out, plan, q_c, dtype, flags);
@@ -1399,6 +1399,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     p.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
     p.eps = eps;
     p.drop_scale = drop_scale;
+    p.fp8 = fp8 ? 1 : 0;
     p.norm = ow::kNormNone;
     if (norm) {
       if (scale) {

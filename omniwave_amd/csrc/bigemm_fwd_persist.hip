@@ -49,11 +49,9 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRows = 32 * kWaves;       // 256 rows per unit
 constexpr int kGroups = kRows / kG;      // 16 token groups per unit
-constexpr int kDpw = kFrCh / kWaves;     // chunk-copy fragments per wave
 constexpr int kTileOps = 32 * kD * 2 / 1024;  // 1 KB tile copies per wave (8)
 constexpr int kLdo = kD + 8;             // output staging row stride (elements)
 constexpr int kTokLds = 512;             // token-table entries kept in LDS (q_s <= 32)
-static_assert(kFrCh % kWaves == 0, "chunk copies split evenly over the waves");
 
 struct PersistLds {
   uint16_t x[kRows * kD];              // the unit's tile, 64 KB
@@ -101,8 +99,16 @@ struct TokLoad {
   float ds;
 };
 
-template <class Ty>
+// F8: V' = P_v B_v'' on the K = 64 e4m3 MFMA (ow_device.h, fp8 channel side); a chunk is then
+// f8_chunk_units(128) = 20 copy units, which waves 0-3 copy three of and waves 4-7 two of.
+template <class Ty, bool F8>
 __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units) {
+  constexpr int CHU = F8 ? f8_chunk_units(kD) : kFrCh;      // 1 KB copy units per chunk
+  constexpr int CH_ELEMS = CHU * kFragElems;
+  constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, 16-bit elements
+  constexpr int F8_BV = kFrU;                                // fp8: first unit of B_v'^T (K = 64)
+  constexpr int F8_BO = kFrU + 2 * (kD / 64);                // fp8: first unit of B_o
+  static_assert(CHU <= kFrCh && CHU > 2 * kWaves, "two or three copy units per wave");
   __shared__ __attribute__((aligned(16))) PersistLds sh;
   // lane and wave are re-read opaquely at the top of every unit (see the loop): the compiler
   // would otherwise compute hundreds of per-lane addresses once, before the loop, and keep them
@@ -189,15 +195,24 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     }
   };
   auto issue_chunk = [&](int32_t u, int ec) {
-    const uint16_t* src =
-        uniform_ptr(a.packed + kHeadElems + (static_cast<size_t>(u % a.q_c) * kNCH + ec) * kChElems);
+    const uint16_t* src = uniform_ptr(a.packed + HEAD + (static_cast<size_t>(u % a.q_c) * kNCH + ec) * CH_ELEMS);
     uint16_t* dst = sh.w[ec % 3];
 #pragma unroll
-    for (int i = 0; i < kDpw; ++i) {
+    for (int i = 0; i < 3; ++i) {
       const int f = wave_u + i * kWaves;
-      copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane16);
+      if (f < CHU) copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane16);
     }
   };
+  // Waits until at most this wave's copies of one chunk plus E younger operations are
+  // outstanding.
+  auto wait_chunk = [&](auto e_tag) {
+    constexpr int E = decltype(e_tag)::value;
+    if (F8 && wave_u >= CHU - 2 * kWaves)
+      wait_vmcnt<2 + E>();
+    else
+      wait_vmcnt<3 + E>();
+  };
+  using E0 = std::integral_constant<int, 0>;
 
   int32_t u = blockIdx.x;
   if (u >= n_units) return;
@@ -216,7 +231,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     issue_chunk(u, 0);
     stats_write(stats_load(id), id, 0);
     wave_lds_sync();
-    wait_vmcnt<kDpw>();  // this wave's tile rows; chunk 0 may still be in flight
+    wait_chunk(E0{});  // this wave's tile rows; chunk 0 may still be in flight
   }
 
 #pragma unroll 1
@@ -232,7 +247,10 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     if (has_next) en = meta_load(un);  // consumed after the token side
 
     // Token side of this wave's pair (rows 32 wave .. + 31 of the tile).
-    u32x4 Pu[kKS], Pv[kKS], xk[kKS / 2][2];
+    constexpr int KV = F8 ? kKS / 4 : kKS;
+    using VOp = std::conditional_t<F8, u32x8, u32x4>;
+    u32x4 Pu[kKS], xk[kKS / 2][2];
+    VOp Pv[KV];
     {
       // The token operands are read per unit from LDS rather than kept live through the loop.
       const u32x4 fAu = sh.tok_ops[0][lane];
@@ -244,9 +262,17 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       if (a.norm != kNormNone) {
         const float* r8 = &sh.rsc[s][32 * wave + 16 * ((lane >> 4) & 1) + 4 * hh];
         bu = scale8<Ty>(fAu, r8);
-        bv = scale8<Ty>(fAv, r8);
+        if constexpr (F8) {  // P_v comes out quantised: the multiplier is in the token operand
+          const float qv = reinterpret_cast<const float*>(a.packed + kHeadElems)[kF8QuantPv];
+          bv = scale8m<Ty>(fAv, r8, qv);
+        } else {
+          bv = scale8<Ty>(fAv, r8);
+        }
       }
-      pair_token_side<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
+      if constexpr (F8)
+        pair_token_side_f8<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
+      else
+        pair_token_side<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
     }
     int32_t id_next = -1;
     if (has_next) id_next = meta_write(en, s ^ 1);
@@ -310,7 +336,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         if constexpr (i < NU) {
           if constexpr (i % 2 == 0)
             Un = Ty::mma32(fr[i % DEPTH], Pu[i / 2], Un);
-          else
+          else if constexpr (!F8)  // (stream runs only without F8)
             Vn = Ty::mma32(fr[i % DEPTH], Pv[i / 2], Vn);
         } else {
           constexpr int j = i - NU;
@@ -333,22 +359,84 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // Step ec waits for chunk ec + 1 (issued at step ec - 1, or before the loop for ec <= 1: at
     // ec = 0 chunk 2, issued after it, may still be in flight); the barrier also means every
     // wave is done with chunk ec - 1, whose buffer takes chunk ec + 2.
+    // fp8: chunk ec + 1's U' (bf16 / f16) and V' (K = 64 e4m3) products, then chunk ec's gate and
+    // W += Z B_o (the packed B_o carries V''s dequantisation).
+    auto uv8 = [&](int ec, f32x16& U, f32x16& V) {
+      U = f32x16{};
+      V = f32x16{};
+      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
+      const u32x8* c8 = reinterpret_cast<const u32x8*>(sh.w[ec % 3] + F8_BV * kFragElems);
+#pragma unroll
+      for (int ks = 0; ks < kKS; ++ks) U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], U);
+#pragma unroll
+      for (int q = 0; q < KV; ++q) {
+        if constexpr (F8) V = mma32x64_f8(c8[q * (kF8K64Bytes / 32) + lane], Pv[q], V);
+      }
+    };
+    auto gate_w8 = [&](int ec, const f32x16& U, const f32x16& V) {
+      const u32x4* co = reinterpret_cast<const u32x4*>(sh.w[ec % 3] + F8_BO * kFragElems);
+      u32x4 Z[2];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          Z[s2][q] = Ty::pack2(silu_gate(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q]),
+                               silu_gate(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1]));
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], co[(2 * mb + s2) * (kFragElems / 8) + lane], W[mb]);
+    };
+    // fp8 step: chunk en's U' products with two of chunk ec's gate values after each, chunk en's
+    // V' products, then chunk ec's W += Z B_o.
+    auto step8 = [&](int en, int ec, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
+      Un = f32x16{};
+      Vn = f32x16{};
+      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[en % 3]);
+      const u32x8* c8 = reinterpret_cast<const u32x8*>(sh.w[en % 3] + F8_BV * kFragElems);
+      const u32x4* co = reinterpret_cast<const u32x4*>(sh.w[ec % 3] + F8_BO * kFragElems);
+      u32x4 Z[2];
+#pragma unroll
+      for (int ks = 0; ks < kKS; ++ks) {
+        Un = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], Un);
+        const int k = 2 * ks;
+        Z[k / 8][(k % 8) / 2] = Ty::pack2(silu_gate(Uc[k], Vc[k]), silu_gate(Uc[k + 1], Vc[k + 1]));
+      }
+#pragma unroll
+      for (int q = 0; q < KV; ++q) {
+        if constexpr (F8) Vn = mma32x64_f8(c8[q * (kF8K64Bytes / 32) + lane], Pv[q], Vn);
+      }
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], co[(2 * mb + s2) * (kFragElems / 8) + lane], W[mb]);
+    };
     auto step = [&](int ec, f32x16& Uc, f32x16& Vc, f32x16& Un, f32x16& Vn) {
       const uint32_t bo = base(ec) + 2u * kFrU * kFragElems * 2u;
       if (ec + 1 < kNCH) {
         if (ec == 0)
-          wait_vmcnt<kDpw>();
+          wait_chunk(E0{});
         else
           wait_lds_dma();
         __syncthreads();
         if (ec >= 1 && ec + 2 < kNCH) issue_chunk(u, ec + 2);
-        stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+        if constexpr (F8) {
+          step8(ec + 1, ec, Un, Vn, Uc, Vc);
+        } else {
+          stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+        }
       } else {
-        stream(Zero{}, No{}, 0u, bo, Un, Vn, Uc, Vc);
+        if constexpr (F8)
+          gate_w8(ec, Uc, Vc);
+        else
+          stream(Zero{}, No{}, 0u, bo, Un, Vn, Uc, Vc);
       }
     };
     f32x16 Ua, Va, Ub = {}, Vb = {};
-    stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
+    if constexpr (F8)
+      uv8(0, Ua, Va);
+    else
+      stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
 #pragma unroll
     for (int ec = 0; ec < kNCH; ec += 2) {
       step(ec, Ua, Va, Ub, Vb);
@@ -428,9 +516,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       // The next unit's tile rows have landed once at most this unit's stores (8 row pieces, 8
       // statistics values) and chunk 0's copies, all issued after them, are outstanding.
       if (a.stats_out)
-        wait_vmcnt<kDpw + 16>();
+        wait_chunk(std::integral_constant<int, 16>{});
       else
-        wait_vmcnt<kDpw + 8>();
+        wait_chunk(std::integral_constant<int, 8>{});
     }
   }
 }
@@ -452,10 +540,16 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
   if (grid >= 8) grid -= grid % 8;
   const dim3 g(static_cast<unsigned>(grid));
   if (a.norm == kNormInline) return fail(OW_ERR_INVALID, "the persistent forward takes precomputed row statistics");
-  if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL(bigemm_fwd_persist_kernel<BF16>, g, dim3(kThreads), 0, stream, a, static_cast<int32_t>(units));
+  if (a.fp8 && a.norm == kNormNone) return fail(OW_ERR_INVALID, "the fp8 channel side needs the fused RMSNorm");
+  const int32_t n = static_cast<int32_t>(units);
+  if (dtype == OW_DTYPE_BF16 && a.fp8)
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<BF16, true>), g, dim3(kThreads), 0, stream, a, n);
+  else if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<BF16, false>), g, dim3(kThreads), 0, stream, a, n);
+  else if (dtype == OW_DTYPE_F16 && a.fp8)
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<F16, true>), g, dim3(kThreads), 0, stream, a, n);
   else if (dtype == OW_DTYPE_F16)
-    hipLaunchKernelGGL(bigemm_fwd_persist_kernel<F16>, g, dim3(kThreads), 0, stream, a, static_cast<int32_t>(units));
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<F16, false>), g, dim3(kThreads), 0, stream, a, n);
   else
     return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   return hip_status(hipGetLastError(), "bigemm_fwd_persist_kernel launch");

@@ -577,6 +577,7 @@ struct PersistArgs {
   int32_t parts;
   float eps;
   int32_t residual;
+  int32_t fp8;              // V' on the e4m3 MFMA (fp8 packed weights)
 };
 bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
 int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream);
