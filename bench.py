@@ -57,14 +57,22 @@ def case_work(batch, h, w, c, d, rd=None, elem=2):
     return flops, nbytes
 
 
-def kernel_of(c: int, d: int, rd: int | None = None) -> str:
-    """HIP kernel that carries a fused launch (the dispatch rule of ow_bigemm_fwd for aligned
-    inputs): the persistent resident-weight kernel for d=64/rd=128 with C = q_c*64, q_c <= 4,
-    otherwise the streamed tile kernel (after the RMSNorm statistics kernel)."""
+def kernel_of(c: int, d: int, level: int = 0, rd: int | None = None) -> str:
+    """HIP kernel(s) that carry a fused bf16 launch with 16-byte aligned rows (the dispatch rule of
+    ow_bigemm_fwd): d=64/rd=128 with C = q_c*64 runs the one-unit-per-wave kernel when the channel
+    groups are contiguous and q_c <= 2, else the resident-weight kernel (q_c <= 4); d=128/rd=256
+    with contiguous groups runs the RMSNorm statistics kernel, then the persistent kernel; the rest
+    runs the streamed tile kernel."""
     rd = rd or 2 * d
     q_c = math.ceil(c / d)
-    if d == 64 and rd == 128 and q_c in (1, 2, 4) and c == q_c * 64:
-        return "bigemm_fwd_resident_kernel"
+    contiguous = level == 0 or q_c == 1
+    if d == 64 and rd == 128 and c == q_c * 64:
+        if q_c in (1, 2) and contiguous:
+            return "bigemm_fwd_wave_kernel"
+        if q_c in (1, 2, 4):
+            return "bigemm_fwd_resident_kernel"
+    if d == 128 and rd == 256 and c == q_c * 128 and contiguous:
+        return "rms_rows16_kernel+bigemm_fwd_persist_kernel"
     return "bigemm_fwd_kernel"
 
 
@@ -618,7 +626,7 @@ def main() -> int:
             fn = (lambda x=x, nw=nw, plan=plan, p=p: bigemm_block_hip(x, nw, plan, **p))
             flops, nbytes = case_work(args.batch, h, w, c, d)
             cases.append(dict(name=f"{name}_{route}{level}", stage=name, d=d, fn=fn, flops=flops, bytes=nbytes,
-                              kernel=kernel_of(c, d)))
+                              kernel=kernel_of(c, d, level)))
 
     if args.profile_launches > 0:
         return profile_mode(cases, args.profile_launches, args.calibrate_copy_mib, dev)
