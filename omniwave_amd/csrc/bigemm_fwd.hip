@@ -170,30 +170,6 @@ struct FwdArgs {
 // (kModeContig, kModeStrided, kModeElement: ow_device.h)
 constexpr int kBatch = 16;  // global loads kept in flight per thread by the gather / scatter loops
 
-// The M = 8/n elements of a strided channel group held by one 16-byte row vector (element
-// index res + t n for t < M, res < n the group's first channel), packed in order: M = 4 and
-// M = 2 as 16-bit halves of two / one word, M = 1 in the low half.  res is wave-uniform, so
-// the word choices are uniform selects and each pair of halves is one v_perm_b32 (result
-// bytes 0-1 from the low operand, 2-3 from the high one).
-template <int M>
-using StridedPack = std::conditional_t<M == 4, u32x2, uint32_t>;
-
-template <int M>
-__device__ __forceinline__ StridedPack<M> strided_pack(const u32x4& v, int res) {
-  const uint32_t sel = (res & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
-  if constexpr (M == 4) {  // n = 2: halves (res & 1) of words 0..3
-    return u32x2{__builtin_amdgcn_perm(v[1], v[0], sel), __builtin_amdgcn_perm(v[3], v[2], sel)};
-  } else if constexpr (M == 2) {  // n = 4: words res / 2 and res / 2 + 2
-    const bool w1 = (res & 2) != 0;
-    return __builtin_amdgcn_perm(w1 ? v[3] : v[2], w1 ? v[1] : v[0], sel);
-  } else {  // n = 8: word res / 2
-    const int w = res >> 1;
-    const uint32_t word = w == 0 ? v[0] : w == 1 ? v[1] : w == 2 ? v[2] : v[3];
-    return (res & 1) ? word >> 16 : word;
-  }
-}
-
-
 // Maps the hardware workgroup id to a logical id so that the q_c workgroups of one row chunk
 // run on the same XCD (workgroups are dispatched round-robin over the 8 XCDs): their gathers
 // and scatters touch the same cache lines of x and out, which then meet in one L2.
@@ -476,6 +452,7 @@ bigemm_fwd_kernel(FwdArgs a) {
   VOp Pv[NP][KV];
   u32x4 xk[NP][KS / 2][2];  // the lane's x values, kept for the residual
   const float qv = F8 ? reinterpret_cast<const float*>(a.packed + kHeadElems)[kF8QuantPv] : 1.0f;  // fp8 scales
+  const float deq8 = F8 ? f8_deq(a.packed) : 1.0f;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int row0 = (wave * TPW + 2 * p) * kG;
@@ -627,7 +604,7 @@ bigemm_fwd_kernel(FwdArgs a) {
         for (int q = 0; q < 4; ++q) {
           const float u0 = U[8 * s + 2 * q], u1 = U[8 * s + 2 * q + 1];
           const float v0 = V[8 * s + 2 * q], v1 = V[8 * s + 2 * q + 1];
-          Z[s][q] = Ty::pack2(silu_gate(u0, v0), silu_gate(u1, v1));
+          Z[s][q] = Ty::pack2(f8_gate<Ty>(u0, v0, deq8), f8_gate<Ty>(u1, v1, deq8));
         }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -677,7 +654,7 @@ bigemm_fwd_kernel(FwdArgs a) {
       auto fv = [&](int s) { return c8[s * (kF8K64Bytes / 32) + lane]; };
       auto fo = [&](int mb, int s) { return co[(2 * mb + s) * (kFragElems / 8) + lane]; };
 #pragma unroll
-      for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p]);
+      for (int p = 0; p < NP; ++p) pair_chunk_f8<Ty, KS, MB>(Pu[p], Pv[p], fu, fv, fo, W[p], deq8);
     } else {
       auto fu = [&](int ks) { return cf[ks * (kFragElems / 8) + lane]; };
       auto fv = [&](int ks) { return cf[(FR_U + ks) * (kFragElems / 8) + lane]; };
@@ -1037,7 +1014,9 @@ __global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* s
       const int gc = p.chan[q * p.d + c];
       w = (gc >= 0 && gc < p.channels) ? (p.gamma ? p.gamma[gc] : 1.0f) : 0.0f;
     }
-    out = load_f32(p.b_o, src, p.wdtype) * w * scales[kF8DeqV];
+    // V''s dequantisation folded into B_o with bf16 activations; f16 applies it in the gate
+    // (f8_gate: Z in the quantised scale would overflow f16).
+    out = load_f32(p.b_o, src, p.wdtype) * w * (std::is_same_v<Ty, F16> ? 1.0f : scales[kF8DeqV]);
   }
   chunk[static_cast<int64_t>(fr) * kFragElems + e] = Ty::from_f32(out);
 }
@@ -1153,7 +1132,7 @@ bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_
   int32_t q_s = 0, q_c = 0;
   if (ow_plan_dims(plan, &q_s, &q_c) != OW_OK) return false;
   const FwdPath p = fwd_path(x, out, plan, q_c, dtype, flags);
-  if (p.resident || p.mode != kModeContig) return false;
+  if (p.resident || (p.mode != kModeContig && p.mode != kModeStrided)) return false;
   const int64_t elems = static_cast<int64_t>(batch) * plan->height * plan->width * plan->channels;
   return persist_supported(plan->channel_tile, rd, plan->channels, q_c, elems);
 }
@@ -1400,6 +1379,8 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     p.eps = eps;
     p.drop_scale = drop_scale;
     p.fp8 = fp8 ? 1 : 0;
+    p.chan = channel_index;
+    p.stride = mode == ow::kModeStrided ? q_c : 1;
     p.norm = ow::kNormNone;
     if (norm) {
       if (scale) {

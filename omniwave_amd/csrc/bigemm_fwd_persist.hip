@@ -93,6 +93,43 @@ __device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
   return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Strided channel groups (radix levels >= 1: group qc is channels res + t NS, t < 128, NS = q_c):
+// a 16-byte piece of a row holds M = 8 / NS columns of every group, so the tile comes through
+// registers.  strided_fetch loads a wave's whole rows, NS pieces per lane and row (16 lanes per
+// row, 4 rows per pass, passes p0 .. p0 + NP - 1); strided_write keeps the group's columns
+// (strided_pack) at the tile's swizzled positions.
+template <int NS, int NP>
+__device__ __forceinline__ void strided_fetch(__amdgpu_buffer_rsrc_t rx, const int32_t* rowid, int channels, int lane,
+                                              int p0, u32x4 (&v)[NP][NS]) {
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int32_t id = rowid[4 * (p0 + p) + (lane >> 4)];
+    const uint32_t off =
+        id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(channels * 2) + 16u * (lane & 15) : kOffOut;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) v[p][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 256u * j, 0, 0);
+  }
+}
+template <int NS, int NP>
+__device__ __forceinline__ void strided_write(uint16_t* xw, int lane, int res, int p0, const u32x4 (&v)[NP][NS]) {
+  constexpr int M = 8 / NS;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int r = 4 * (p0 + p) + (lane >> 4);  // row of the wave; swizzle bit (r >> 2) & 1 = (p0 + p) & 1
+    const int sw = 32 * ((p0 + p) & 1);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int c0 = M * ((lane & 15) + 16 * j);
+      const StridedPack<M> e = strided_pack<M>(v[p][j], res);
+      uint16_t* dst = xw + r * kD + (c0 ^ sw);
+      if constexpr (M == 1)
+        *dst = static_cast<uint16_t>(e);
+      else
+        *reinterpret_cast<StridedPack<M>*>(dst) = e;
+    }
+  }
+}
+
 // Token-table entries of one row of a unit (loads only: consumed by meta_write a phase later).
 struct TokLoad {
   int32_t t, to, b;
@@ -101,8 +138,11 @@ struct TokLoad {
 
 // F8: V' = P_v B_v'' on the K = 64 e4m3 MFMA (ow_device.h, fp8 channel side); a chunk is then
 // f8_chunk_units(128) = 20 copy units, which waves 0-3 copy three of and waves 4-7 two of.
-template <class Ty, bool F8>
+// NS: 1 for contiguous channel groups (tile rows by DMA), else the channel stride of the
+// strided groups (q_c = NS; tile rows through registers, output by 2-byte stores).
+template <class Ty, bool F8, int NS>
 __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units) {
+  constexpr int SNP = NS == 8 ? 4 : 8;  // strided fetch: passes per batch (at most 32 pieces per lane)
   constexpr int CHU = F8 ? f8_chunk_units(kD) : kFrCh;      // 1 KB copy units per chunk
   constexpr int CH_ELEMS = CHU * kFragElems;
   constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, 16-bit elements
@@ -214,8 +254,30 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   };
   using E0 = std::integral_constant<int, 0>;
 
+  // Strided groups: the q_c units of a row chunk (consecutive logical ids) run on one XCD, so the
+  // 2-byte stores of their interleaved columns meet in one L2.
   int32_t u = blockIdx.x;
+  if constexpr (NS > 1) {
+    const int nwg = gridDim.x, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int per = nwg >> 3, rem = nwg & 7;
+    u = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+  }
   if (u >= n_units) return;
+  // First channel of a group, mod NS (the group's residue) for unit u.
+  auto group_res = [&](int32_t uu) { return NS > 1 ? (a.chan[(uu % a.q_c) * kD] & (NS - 1)) : 0; };
+  // Strided tile of unit uu, slot ss: every batch fetched and written now (the first unit).
+  auto strided_tile = [&](int32_t uu, int ss) {
+    if constexpr (NS > 1) {
+      const int res = group_res(uu);
+#pragma unroll
+      for (int p0 = 0; p0 < 8; p0 += SNP) {
+        u32x4 v[SNP][NS];
+        strided_fetch<NS, SNP>(rx, &sh.rowid[ss][32 * wave], a.channels, lane, p0, v);
+        strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, res, p0, v);
+      }
+      wave_lds_sync();
+    }
+  };
   int s = 0;
   if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
   if (tok_lds) {
@@ -227,8 +289,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   __syncthreads();
   {
     const int32_t id = meta_write(meta_load(u), 0);
-    issue_tile(u, 0);
+    if constexpr (NS == 1) issue_tile(u, 0);
     issue_chunk(u, 0);
+    strided_tile(u, 0);
     stats_write(stats_load(id), id, 0);
     wave_lds_sync();
     wait_chunk(E0{});  // this wave's tile rows; chunk 0 may still be in flight
@@ -360,7 +423,8 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // ec = 0 chunk 2, issued after it, may still be in flight); the barrier also means every
     // wave is done with chunk ec - 1, whose buffer takes chunk ec + 2.
     // fp8: chunk ec + 1's U' (bf16 / f16) and V' (K = 64 e4m3) products, then chunk ec's gate and
-    // W += Z B_o (the packed B_o carries V''s dequantisation).
+    // W += Z B_o (V''s dequantisation: f8_gate).
+    const float deq8 = F8 ? f8_deq(a.packed) : 1.0f;
     auto uv8 = [&](int ec, f32x16& U, f32x16& V) {
       U = f32x16{};
       V = f32x16{};
@@ -380,8 +444,8 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          Z[s2][q] = Ty::pack2(silu_gate(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q]),
-                               silu_gate(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1]));
+          Z[s2][q] = Ty::pack2(f8_gate<Ty>(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q], deq8),
+                               f8_gate<Ty>(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1], deq8));
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
@@ -400,7 +464,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       for (int ks = 0; ks < kKS; ++ks) {
         Un = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], Un);
         const int k = 2 * ks;
-        Z[k / 8][(k % 8) / 2] = Ty::pack2(silu_gate(Uc[k], Vc[k]), silu_gate(Uc[k + 1], Vc[k + 1]));
+        Z[k / 8][(k % 8) / 2] = Ty::pack2(f8_gate<Ty>(Uc[k], Vc[k], deq8), f8_gate<Ty>(Uc[k + 1], Vc[k + 1], deq8));
       }
 #pragma unroll
       for (int q = 0; q < KV; ++q) {
@@ -480,9 +544,13 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     wave_lds_sync();
 #pragma unroll
     for (int k = 0; k < 8; ++k) val[k] = *reinterpret_cast<const u32x4*>(&st[((lane >> 4) + 4 * k) * kLdo + piece * 8]);
-    // The tile reads are complete (their values are in registers): the next unit's rows go out.
+    // The tile reads are complete (their values are in registers): the next unit's rows go out
+    // (strided groups: fetched through registers after the stores).
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (has_next) issue_tile(un, s ^ 1);
+    if constexpr (NS == 1) {
+      if (has_next) issue_tile(un, s ^ 1);
+    }
+    const int res_u = group_res(u);
     const __amdgpu_buffer_rsrc_t ro = persist_rsrc(a.out, xbytes);
     const __amdgpu_buffer_rsrc_t rs =
         persist_rsrc(a.stats_out, static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.q_c * 4));
@@ -503,10 +571,36 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         const uint32_t so = (piece == 15 && id >= 0) ? (static_cast<uint32_t>(id) * a.q_c + qc) * 4u : kOffOut;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc), rs, so, 0, 0);
       }
-      const uint32_t oo = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) +
-                                        static_cast<uint32_t>(colq * 2) + 16u * piece
-                                  : kOffOut;
-      __builtin_amdgcn_raw_buffer_store_b128(v, ro, oo, 0, 0);
+      if constexpr (NS == 1) {
+        const uint32_t oo = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) +
+                                          static_cast<uint32_t>(colq * 2) + 16u * piece
+                                    : kOffOut;
+        __builtin_amdgcn_raw_buffer_store_b128(v, ro, oo, 0, 0);
+      } else {
+        *reinterpret_cast<u32x4*>(&st[((lane >> 4) + 4 * k) * kLdo + piece * 8]) = v;  // final values
+      }
+    }
+    if constexpr (NS > 1) {
+      // Strided groups: tile column t is channel res + t NS of the row; lane l stores column
+      // 64 h + l of one row per instruction, so the lanes writing one 128-byte line of out come
+      // together in one request (2-byte elements: the other groups' columns lie in between).
+      wave_lds_sync();
+#pragma unroll 4
+      for (int rr = 0; rr < 32; ++rr) {
+        const int32_t id = sh.rowout[s][32 * wave + rr];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int t = 64 * h + lane;
+          const uint16_t v = st[rr * kLdo + t];
+          const uint32_t ob = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) +
+                                            2u * static_cast<uint32_t>(res_u + t * NS)
+                                      : kOffOut;
+          __builtin_amdgcn_raw_buffer_store_b16(v, ro, ob, 0, 0);
+        }
+      }
+    }
+    if constexpr (NS > 1) {
+      if (has_next) strided_tile(un, s ^ 1);
     }
     if (has_next) {
       stats_write(snext, id_next, s ^ 1);
@@ -514,11 +608,14 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       __syncthreads();  // every wave is done with its staging rows, which chunk 0 overwrites
       issue_chunk(un, 0);
       // The next unit's tile rows have landed once at most this unit's stores (8 row pieces, 8
-      // statistics values) and chunk 0's copies, all issued after them, are outstanding.
-      if (a.stats_out)
-        wait_chunk(std::integral_constant<int, 16>{});
-      else
-        wait_chunk(std::integral_constant<int, 8>{});
+      // statistics values) and chunk 0's copies, all issued after them, are outstanding
+      // (strided groups: the rows were written by this wave).
+      if constexpr (NS == 1) {
+        if (a.stats_out)
+          wait_chunk(std::integral_constant<int, 16>{});
+        else
+          wait_chunk(std::integral_constant<int, 8>{});
+      }
     }
   }
 }
@@ -527,6 +624,27 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
 
 bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems) {
   return d == kD && rd == kRD && channels == q_c * kD && x_elems * 2 < (int64_t(1) << 31);
+}
+
+template <class Ty>
+void launch_stride(const PersistArgs& a, dim3 g, int32_t n, hipStream_t stream) {
+  auto go = [&](auto f8_tag, auto ns_tag) {
+    constexpr bool F8 = decltype(f8_tag)::value;
+    constexpr int NS = decltype(ns_tag)::value;
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<Ty, F8, NS>), g, dim3(kThreads), 0, stream, a, n);
+  };
+  auto by_ns = [&](auto f8_tag) {
+    switch (a.stride) {
+      case 2: go(f8_tag, std::integral_constant<int, 2>{}); break;
+      case 4: go(f8_tag, std::integral_constant<int, 4>{}); break;
+      case 8: go(f8_tag, std::integral_constant<int, 8>{}); break;
+      default: go(f8_tag, std::integral_constant<int, 1>{}); break;
+    }
+  };
+  if (a.fp8)
+    by_ns(std::true_type{});
+  else
+    by_ns(std::false_type{});
 }
 
 int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) {
@@ -542,16 +660,14 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
   if (a.norm == kNormInline) return fail(OW_ERR_INVALID, "the persistent forward takes precomputed row statistics");
   if (a.fp8 && a.norm == kNormNone) return fail(OW_ERR_INVALID, "the fp8 channel side needs the fused RMSNorm");
   const int32_t n = static_cast<int32_t>(units);
-  if (dtype == OW_DTYPE_BF16 && a.fp8)
-    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<BF16, true>), g, dim3(kThreads), 0, stream, a, n);
-  else if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<BF16, false>), g, dim3(kThreads), 0, stream, a, n);
-  else if (dtype == OW_DTYPE_F16 && a.fp8)
-    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<F16, true>), g, dim3(kThreads), 0, stream, a, n);
-  else if (dtype == OW_DTYPE_F16)
-    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<F16, false>), g, dim3(kThreads), 0, stream, a, n);
+  if (dtype != OW_DTYPE_BF16 && dtype != OW_DTYPE_F16) return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  if (a.stride != 1 && a.stride != 2 && a.stride != 4 && a.stride != 8)
+    return fail(OW_ERR_UNSUPPORTED, "persistent forward: channel stride %d", a.stride);
+  if (a.stride != 1 && a.stride != a.q_c) return fail(OW_ERR_INVALID, "strided groups need stride == q_c");
+  if (dtype == OW_DTYPE_BF16)
+    launch_stride<BF16>(a, g, n, stream);
   else
-    return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+    launch_stride<F16>(a, g, n, stream);
   return hip_status(hipGetLastError(), "bigemm_fwd_persist_kernel launch");
 }
 

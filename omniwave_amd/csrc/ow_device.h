@@ -195,6 +195,29 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// The M = 8/n elements of a strided channel group held by one 16-byte row vector (element
+// index res + t n for t < M, res < n the group's first channel), packed in order: M = 4 and
+// M = 2 as 16-bit halves of two / one word, M = 1 in the low half.  res is wave-uniform, so
+// the word choices are uniform selects and each pair of halves is one v_perm_b32 (result
+// bytes 0-1 from the low operand, 2-3 from the high one).
+template <int M>
+using StridedPack = std::conditional_t<M == 4, u32x2, uint32_t>;
+
+template <int M>
+__device__ __forceinline__ StridedPack<M> strided_pack(const u32x4& v, int res) {
+  const uint32_t sel = (res & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+  if constexpr (M == 4) {  // n = 2: halves (res & 1) of words 0..3
+    return u32x2{__builtin_amdgcn_perm(v[1], v[0], sel), __builtin_amdgcn_perm(v[3], v[2], sel)};
+  } else if constexpr (M == 2) {  // n = 4: words res / 2 and res / 2 + 2
+    const bool w1 = (res & 2) != 0;
+    return __builtin_amdgcn_perm(w1 ? v[3] : v[2], w1 ? v[1] : v[0], sel);
+  } else {  // n = 8: word res / 2
+    const int w = res >> 1;
+    const uint32_t word = w == 0 ? v[0] : w == 1 ? v[1] : w == 2 ? v[2] : v[3];
+    return (res & 1) ? word >> 16 : word;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // One 32-token pair (token groups 0 and 1 of 16 tokens) of a channel group, all on 32x32x16
 // MFMAs.  Token-side products use the block-diagonal 32x32 token matrix: K step g covers the
@@ -355,6 +378,22 @@ constexpr int kF8HeadBytes = kHeadElems * 2 + kF8ScaleFloats * 4;
 constexpr int kF8DeqV = 0, kF8QuantPv = 1, kF8AmaxBv = 2;
 constexpr float kF8Max = 448.0f;
 
+// Gate of the fp8 channel side from U' and the quantised V' (ow_pack_weights_fp8): with bf16
+// activations V''s dequantisation factor is folded into the packed B_o (Z = SiLU(U) V stays in
+// the quantised scale, far inside bf16 range); with f16 activations that Z would overflow f16
+// (|V'| reaches 1e4 - 1e5), so the factor deq is applied here and the packed B_o carries none.
+template <class Ty>
+__device__ __forceinline__ float f8_gate(float up, float vq, float deq) {
+  if constexpr (std::is_same_v<Ty, F16>)
+    return silu_gate(up, vq * deq);
+  else
+    return silu_gate(up, vq);
+}
+// V''s dequantisation factor from an fp8 packed buffer (its scale slots follow the head).
+__device__ __forceinline__ float f8_deq(const uint16_t* packed) {
+  return reinterpret_cast<const float*>(packed + kHeadElems)[kF8DeqV];
+}
+
 // 1 KB units of one fp8 chunk for channel tile d.
 __host__ __device__ constexpr int f8_chunk_units(int d) {
   return ((d / 16 + 2 * (d / 64) + 2 * (d / 32)) + 3) / 4 * 4;
@@ -435,11 +474,10 @@ __device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, c
 }
 
 // pair_chunk for the fp8 variant: U' on Ty MFMAs, V' on K64 fp8 MFMAs (fv(s) returns the
-// chunk's fp8 B_v'^T K64 fragment s), the gate and Z B_o as pair_chunk (the packed B_o carries
-// V''s dequantisation factor).
+// chunk's fp8 B_v'^T K64 fragment s), the gate (f8_gate) and Z B_o as pair_chunk.
 template <class Ty, int KS, int MB, class FU, class FV, class FO>
 __device__ __forceinline__ void pair_chunk_f8(const u32x4 (&Pu)[KS], const u32x8 (&Pv)[KS / 4], FU fu, FV fv, FO fo,
-                                              f32x16 (&W)[MB]) {
+                                              f32x16 (&W)[MB], float deq) {
   f32x16 U = {}, V = {};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) U = Ty::mma32(fu(ks), Pu[ks], U);
@@ -450,8 +488,8 @@ __device__ __forceinline__ void pair_chunk_f8(const u32x4 (&Pu)[KS], const u32x8
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      Z[s][q] = Ty::pack2(silu_gate(U[8 * s + 2 * q], V[8 * s + 2 * q]),
-                          silu_gate(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1]));
+      Z[s][q] = Ty::pack2(f8_gate<Ty>(U[8 * s + 2 * q], V[8 * s + 2 * q], deq),
+                          f8_gate<Ty>(U[8 * s + 2 * q + 1], V[8 * s + 2 * q + 1], deq));
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -578,6 +616,8 @@ struct PersistArgs {
   float eps;
   int32_t residual;
   int32_t fp8;              // V' on the e4m3 MFMA (fp8 packed weights)
+  const int32_t* chan;      // [q_c * 128] channel table (strided groups: the first entry of a group)
+  int32_t stride;           // 1: contiguous groups; 2, 4, 8: strided groups (= q_c)
 };
 bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
 int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream);

@@ -9,7 +9,8 @@ Checks per case:
 * against an emulation of the kernel's quantised arithmetic on the CPU (P_v's quantisation
   multiplier folded into the token operand A_v diag(r) before its rounding to the activation
   dtype, e4m3fn rounding of P_v and of B_v'' / s_b, fp32 accumulation, V''s dequantisation
-  folded into the packed B_o, activation-dtype rounding of P_u, Z, W and delta): rel-L2 <= 1e-2
+  folded into the packed B_o with bf16 activations and applied in the gate with f16 ones (Z in
+  the quantised scale would overflow f16), activation-dtype rounding of P_u, Z, W and delta): rel-L2 <= 1e-2
   on delta, so the kernel computes what it is designed to compute (the slack covers e4m3
   rounding flips from the fp32 summation order);
 * against the fp32 oracle: rel-L2 <= 5e-2 on delta itself (LayerScale 1, so delta is not
@@ -44,11 +45,11 @@ def announce(msg: str) -> None:
     print(f"\n[gpu-case] {msg}", file=sys.stderr, flush=True)
 
 
-def make_case(b, h, w, c, d, route, level, seed):
+def make_case(b, h, w, c, d, route, level, seed, dtype=torch.bfloat16):
     gen = torch.Generator().manual_seed(seed)
     plan = omniwave_amd.build_route_plan(h, w, c, 16, d, route, level)
     q_c, rd = plan.channel_indices.shape[0], 2 * d
-    x = torch.randn(b, h, w, c, generator=gen).to(torch.bfloat16)
+    x = torch.randn(b, h, w, c, generator=gen).to(dtype)
     p = dict(
         a_u=torch.randn(16, 16, generator=gen) / 4, a_v=torch.randn(16, 16, generator=gen) / 4,
         a_o=torch.randn(16, 16, generator=gen) / 4,
@@ -92,8 +93,12 @@ def emulate_fp8_delta(x, plan, p):
     pv = q8(ar_v @ tiles)
     u = torch.einsum("bsqik,qke->bsqie", pu, bu)
     v = torch.einsum("bsqik,qke->bsqie", pv, bv_q)
-    z = (u * v / (1.0 + torch.exp2(u))).to(dt).float()
-    bo = (p["b_o"] * gm[:, None, :] * dv).to(dt).float()
+    if dt == torch.float16:  # dequantisation in the gate, none in the packed B_o
+        z = (u * (v * dv) / (1.0 + torch.exp2(u))).to(dt).float()
+        bo = (p["b_o"] * gm[:, None, :]).to(dt).float()
+    else:
+        z = (u * v / (1.0 + torch.exp2(u))).to(dt).float()
+        bo = (p["b_o"] * gm[:, None, :] * dv).to(dt).float()
     wt = torch.einsum("bsqie,qek->bsqik", z, bo).to(dt).float()
     delta = torch.einsum("ij,bsqjk->bsqik", a_o, wt).to(dt).float() * mask.float()
     return unpack_tiles(delta, oplan, x.shape[0])
@@ -125,6 +130,29 @@ def test_fp8_block_matches_emulation_and_oracle(stage, route, level) -> None:
     assert e_out <= 5e-2
     # Residual epilogue: out = round(x + round(delta)).
     assert torch.equal(out, (x.float() + delta.float()).to(torch.bfloat16))
+
+
+F16_ROUTES = [("local", 0), ("radix", 1)]
+
+
+@pytest.mark.parametrize("route,level", F16_ROUTES, ids=[f"{r}{l}" for r, l in F16_ROUTES])
+@pytest.mark.parametrize("stage", list(STAGES))
+def test_fp8_block_f16_activations(stage, route, level) -> None:
+    """f16 activations: V''s dequantisation is applied in the gate (the bf16 arrangement, folded
+    into B_o, overflows f16 in Z); finite outputs, emulation and oracle parity as for bf16."""
+    h, w, c, d = STAGES[stage]
+    announce(f"fp8 block f16 stage={stage} route={route}{level} B=2")
+    plan, x, p = make_case(2, h, w, c, d, route, level, seed=7, dtype=torch.float16)
+    delta = run_fp8(x, plan, p, residual=False)
+    out = run_fp8(x, plan, p, residual=True)
+    assert torch.isfinite(delta).all() and torch.isfinite(out).all()
+    emu = emulate_fp8_delta(x, plan, p)
+    ref_delta = block_reference(x.float(), oracle_plan(h, w, c, 16, d, route, level), p, residual=False)
+    e_emu, e_delta = rel_l2(delta, emu), rel_l2(delta, ref_delta)
+    print(f"fp8 f16 {stage} {route}{level}: delta vs emulation {e_emu:.2e}, delta vs fp32 {e_delta:.2e}", flush=True)
+    assert e_emu <= 1e-2
+    assert e_delta <= 5e-2
+    assert torch.equal(out, (x.float() + delta.float()).to(torch.float16))
 
 
 @pytest.mark.parametrize("min_tile", [128, 64], ids=["d128", "all"])
