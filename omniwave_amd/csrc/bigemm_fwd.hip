@@ -1358,8 +1358,9 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.residual = (flags & OW_FUSE_RESIDUAL) ? 1 : 0;
     r.eps = eps;
     r.drop_scale = drop_scale;
-    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level) ? ow::launch_fwd_wave(r, dtype, s)
-                                                                          : ow::launch_fwd_resident(r, dtype, s);
+    const int64_t x_elems = static_cast<int64_t>(batch) * n * c;
+    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems) ? ow::launch_fwd_wave(r, dtype, s)
+                                                                                   : ow::launch_fwd_resident(r, dtype, s);
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }

@@ -6,9 +6,9 @@
 //   * one workgroup of eight waves per CU (145 KB of LDS), persistent over units of 256 token
 //     rows (16 token groups: one 32-token pair per wave) x one channel group; unit u is row chunk
 //     u / q_c, channel group u % q_c, and workgroup b takes units b, b + grid, ...  With the grid
-//     a multiple of 8 every unit of a workgroup runs on that workgroup's XCD (workgroups are
-//     dispatched round-robin over the 8 XCDs), so an XCD sees the weights of only 8 / q_c
-//     channel groups in its L2 (one at q_c = 8);
+//     a multiple of 8 (and q_c dividing 8) all units of workgroup b are of channel group b % q_c,
+//     and so are all units of its XCD (workgroups are dispatched round-robin over the 8 XCDs):
+//     an XCD's L2 holds the weights of one channel group;
 //   * the eight waves share one stream of weight chunks (24 KB per 32-row chunk of the expanded
 //     dimension, three LDS buffers, copied global -> LDS with global_load_lds), with the chunk
 //     loop of bigemm_fwd.hip: chunk ec + 1's U'/V' products issued with chunk ec's gate values
@@ -652,10 +652,13 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
   const int64_t units = chunks * a.q_c;
   if (units == 0) return OW_OK;
   if (units > 0x7fffffff) return fail(OW_ERR_UNSUPPORTED, "grid too large (%lld units)", (long long)units);
-  // One workgroup per CU, a multiple of 8 (whole XCD rounds) when there are enough units.
+  // One workgroup per CU; with more units than CUs a multiple of 8 (whole XCD rounds), so that
+  // every unit of a workgroup belongs to one channel group; with fewer, one unit per workgroup.
   int64_t grid = device_cus();
-  if (grid > units) grid = units;
-  if (grid >= 8) grid -= grid % 8;
+  if (grid >= units)
+    grid = units;
+  else if (grid >= 8)
+    grid -= grid % 8;
   const dim3 g(static_cast<unsigned>(grid));
   if (a.norm == kNormInline) return fail(OW_ERR_INVALID, "the persistent forward takes precomputed row statistics");
   if (a.fp8 && a.norm == kNormNone) return fail(OW_ERR_INVALID, "the fp8 channel side needs the fused RMSNorm");

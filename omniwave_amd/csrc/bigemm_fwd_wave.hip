@@ -369,8 +369,10 @@ int launch_ty(const ResidentArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level) {
-  return d == kD && rd == kRD && (q_c == 1 || (q_c == 2 && radix_level == 0)) && channels == q_c * kD;
+bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems) {
+  // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.
+  return d == kD && rd == kRD && (q_c == 1 || (q_c == 2 && radix_level == 0)) && channels == q_c * kD &&
+         x_elems * 2 < (int64_t(1) << 31);
 }
 
 int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream) {
