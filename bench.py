@@ -61,8 +61,9 @@ def kernel_of(c: int, d: int, level: int = 0, rd: int | None = None) -> str:
     """HIP kernel(s) that carry a fused bf16 launch with 16-byte aligned rows (the dispatch rule of
     ow_bigemm_fwd): d=64/rd=128 with C = q_c*64 runs the one-unit-per-wave kernel when the channel
     groups are contiguous and q_c <= 2, else the resident-weight kernel (q_c <= 4); d=128/rd=256
-    with contiguous groups, or strided groups with q_c in {2, 4, 8}, runs the RMSNorm statistics
-    kernel, then the persistent kernel; the rest runs the streamed tile kernel."""
+    with contiguous groups runs the RMSNorm statistics kernel, then the persistent kernel, and with
+    strided groups (q_c in {2, 4, 8}) the persistent kernel alone (it reads whole rows and forms
+    the statistics itself); the rest runs the streamed tile kernel."""
     rd = rd or 2 * d
     q_c = math.ceil(c / d)
     contiguous = level == 0 or q_c == 1
@@ -71,8 +72,10 @@ def kernel_of(c: int, d: int, level: int = 0, rd: int | None = None) -> str:
             return "bigemm_fwd_wave_kernel"
         if q_c in (1, 2, 4):
             return "bigemm_fwd_resident_kernel"
-    if d == 128 and rd == 256 and c == q_c * 128 and (contiguous or q_c in (2, 4, 8)):
+    if d == 128 and rd == 256 and c == q_c * 128 and contiguous:
         return "rms_rows16_kernel+bigemm_fwd_persist_kernel"
+    if d == 128 and rd == 256 and c == q_c * 128 and q_c in (2, 4, 8):
+        return "bigemm_fwd_persist_kernel"
     return "bigemm_fwd_kernel"
 
 

@@ -1149,8 +1149,9 @@ bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, 
   if (p.resident && rd == 2 * plan->channel_tile) return false;
   if (p.mode == kModeElement) return true;
   if (stats_in) return false;
-  // The persistent kernel reads no whole rows: its scales come from the statistics pass.
-  if (fwd_uses_persist(x, out, plan, rd, dtype, flags, batch)) return true;
+  // The persistent kernel reads whole rows only for strided groups (and forms their scales);
+  // with contiguous groups its scales come from the statistics pass.
+  if (fwd_uses_persist(x, out, plan, rd, dtype, flags, batch)) return p.mode != kModeStrided;
   const int32_t c = plan->channels, j = c / 128;
   return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));
 }
@@ -1387,10 +1388,12 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
       if (scale) {
         p.norm = ow::kNormBuffer;
         p.row_scale = scale;
-      } else {
+      } else if (stats_in) {
         p.norm = ow::kNormPartials;
         p.row_scale = stats_in;
         p.parts = stats_in_parts;
+      } else {
+        p.norm = ow::kNormInline;  // strided groups: scales from the whole-row tile fetch
       }
     }
     if (stats_out && !out_rows) {

@@ -1,5 +1,6 @@
 // Persistent BiGEMM forward for d = 128, rd = 256 with contiguous channel groups (radix level 0,
-// or one group) and 16-byte aligned rows: the 14x14x512 and 7x7x1024 stages of OmniWeave-T.
+// or one group) or the strided groups of radix levels >= 1 (q_c in {2, 4, 8}), and 16-byte
+// aligned rows: the 14x14x512 and 7x7x1024 stages of OmniWeave-T.
 //
 // Same math and operand packing as bigemm_fwd.hip (reference omniweave/ops/reference.py:147-171;
 // operand scheme in ow_device.h).  Organisation:
@@ -20,7 +21,8 @@
 //     first chunk copy are in flight;
 //   * the RMSNorm row scales come from a statistics buffer (a separate pass) or from the
 //     previous block's per-group sums of squares (chained statistics): the tile holds only the
-//     unit's own channel group;
+//     unit's own channel group; strided groups read whole rows anyway and form the scales from
+//     them when neither is given;
 //   * the output: delta = A_o W, rounded (and scaled by the drop-path factor), is staged per
 //     wave in the chunk buffers that the loop no longer reads, and stored as 16-byte row pieces
 //     with the residual round(x + delta), x from the tile.
@@ -213,7 +215,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     return v;
   };
   auto stats_write = [&](float v, int32_t id, int s) {
-    if (lane < 32) {
+    if (lane < 32 && a.norm != kNormInline) {  // kNormInline: strided_tile writes the scales
       float r = 1.0f;
       if (id >= 0 && a.norm == kNormBuffer) r = v;
       if (id >= 0 && a.norm == kNormPartials) r = rms_scale<Ty>(v / static_cast<float>(a.channels), a.eps);
@@ -265,7 +267,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   if (u >= n_units) return;
   // First channel of a group, mod NS (the group's residue) for unit u.
   auto group_res = [&](int32_t uu) { return NS > 1 ? (a.chan[(uu % a.q_c) * kD] & (NS - 1)) : 0; };
-  // Strided tile of unit uu, slot ss: every batch fetched and written now (the first unit).
+  // Strided tile of unit uu, slot ss: every batch fetched and written now.  The fetch holds whole
+  // rows (16 lanes per row), so with kNormInline the rows' RMSNorm scales are formed here: sum of
+  // squares over the 16 lanes (DPP), the total in lane 15 of the row.
   auto strided_tile = [&](int32_t uu, int ss) {
     if constexpr (NS > 1) {
       const int res = group_res(uu);
@@ -274,6 +278,22 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         u32x4 v[SNP][NS];
         strided_fetch<NS, SNP>(rx, &sh.rowid[ss][32 * wave], a.channels, lane, p0, v);
         strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, res, p0, v);
+        if (a.norm == kNormInline) {
+#pragma unroll
+          for (int p = 0; p < SNP; ++p) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(v[p][j][e], acc);
+            acc = group_sum<16>(acc);
+            if ((lane & 15) == 15) {
+              const int r = 32 * wave + 4 * (p0 + p) + (lane >> 4);
+              sh.rsc[ss][r] =
+                  sh.rowid[ss][r] >= 0 ? rms_scale<Ty>(acc / static_cast<float>(a.channels), a.eps) : 1.0f;
+            }
+          }
+        }
       }
       wave_lds_sync();
     }
@@ -318,9 +338,11 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       // The token operands are read per unit from LDS rather than kept live through the loop.
       const u32x4 fAu = sh.tok_ops[0][lane];
       const u32x4 fAv = sh.tok_ops[1][lane];
-      int col[kKS / 2];  // tile column of channel 32 cb + l32 for this lane half's rows
-#pragma unroll
-      for (int cb = 0; cb < kKS / 2; ++cb) col[cb] = (32 * cb + l32) ^ (32 * hh);
+      // X^T operands by transposed reads; channel c of tile row r sits at c ^ (32 ((r >> 2) & 1)).
+      const uint32_t xb = lds_addr(sh.x) + 2u * static_cast<uint32_t>(32 * kD * wave);
+      pair_xt_tr<kKS>(
+          [&](int r, int c) { return xb + 2u * static_cast<uint32_t>(r * kD + (c ^ (32 * ((r >> 2) & 1)))); }, lane,
+          xk);
       u32x4 bu = fAu, bv = fAv;
       if (a.norm != kNormNone) {
         const float* r8 = &sh.rsc[s][32 * wave + 16 * ((lane >> 4) & 1) + 4 * hh];
@@ -333,9 +355,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         }
       }
       if constexpr (F8)
-        pair_token_side_f8<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
+        pair_token_side_f8_mma<Ty, kKS>(xk, bu, bv, lane, Pu, Pv);
       else
-        pair_token_side<Ty, kKS>(sh.x + 32 * wave * kD, kD, col, bu, bv, lane, Pu, Pv, xk);
+        pair_token_side_mma<Ty, kKS>(xk, bu, bv, lane, Pu, Pv);
     }
     int32_t id_next = -1;
     if (has_next) id_next = meta_write(en, s ^ 1);
@@ -515,23 +537,24 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     const int piece = lane & 15;
     const int64_t colq = static_cast<int64_t>(qc) * kD;
     const u32x4 fAo = sh.tok_ops[2][lane];
+    // delta^T: lane l32 = the wave's row l32, registers 4 q .. 4 q + 3 = channels 32 mb + 8 q +
+    // 4 hh .. + 3, staged as 8-byte row pieces.
     f32x16 dl[kMB];
-    pair_output<Ty, kMB>(W, fAo, lane, dl);
+    pair_output_t<Ty, kMB>(W, fAo, lane, dl);
     mfma_drain();
     uint16_t* st = &sh.w[0][0] + wave * 32 * kLdo;
-    const float s0 = sh.dsc[s][2 * wave], s1 = sh.dsc[s][2 * wave + 1];
+    const float sc = sh.dsc[s][2 * wave + ((lane >> 4) & 1)];
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        uint32_t v = Ty::pack2(dl[mb][i], dl[mb][i + 1]);
+      for (int q = 0; q < 4; ++q) {
+        uint32_t v0 = Ty::pack2(dl[mb][4 * q], dl[mb][4 * q + 1]);
+        uint32_t v1 = Ty::pack2(dl[mb][4 * q + 2], dl[mb][4 * q + 3]);
         if (a.drop_scale) {
-          const float sc = i < 8 ? s0 : s1;
-          v = Ty::pack2(Ty::to_f32(lo16(v)) * sc, Ty::to_f32(hi16(v)) * sc);
+          v0 = Ty::pack2(Ty::to_f32(lo16(v0)) * sc, Ty::to_f32(hi16(v0)) * sc);
+          v1 = Ty::pack2(Ty::to_f32(lo16(v1)) * sc, Ty::to_f32(hi16(v1)) * sc);
         }
-        const int r0 = pair_token_row(i, hh);
-        st[r0 * kLdo + 32 * mb + l32] = lo16(v);
-        st[(r0 + 1) * kLdo + 32 * mb + l32] = hi16(v);
+        *reinterpret_cast<u32x2*>(&st[l32 * kLdo + 32 * mb + 8 * q + 4 * hh]) = u32x2{v0, v1};
       }
     // Pass k covers piece lane % 16 of rows lane / 16 + 4 k of the wave (tile slot of the piece:
     // piece ^ 4 (k & 1)).
@@ -660,7 +683,8 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
   else if (grid >= 8)
     grid -= grid % 8;
   const dim3 g(static_cast<unsigned>(grid));
-  if (a.norm == kNormInline) return fail(OW_ERR_INVALID, "the persistent forward takes precomputed row statistics");
+  if (a.norm == kNormInline && a.stride == 1)
+    return fail(OW_ERR_INVALID, "the persistent forward with contiguous groups takes precomputed row statistics");
   if (a.fp8 && a.norm == kNormNone) return fail(OW_ERR_INVALID, "the fp8 channel side needs the fused RMSNorm");
   const int32_t n = static_cast<int32_t>(units);
   if (dtype != OW_DTYPE_BF16 && dtype != OW_DTYPE_F16) return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);

@@ -305,6 +305,55 @@ __device__ __forceinline__ u32x4 pack_kstep(const f32x16& acc, int s) {
 // (already r-scaled) token-operand rows, used for the K step of the lane's own group.  The X^T
 // operands read are returned in xk[cb][g] (the residual of the lane's output elements).
 template <class Ty, int KS>
+__device__ __forceinline__ void pair_token_side_mma(const u32x4 (&xk)[KS / 2][2], u32x4 bu, u32x4 bv, int lane,
+                                                    u32x4 (&Pu)[KS], u32x4 (&Pv)[KS]) {
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 bu0 = keep_if(g0, bu), bu1 = keep_if(!g0, bu);
+  const u32x4 bv0 = keep_if(g0, bv), bv1 = keep_if(!g0, bv);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const u32x4 x0 = xk[cb][0], x1 = xk[cb][1];
+    f32x16 pu = Ty::mma32(x0, bu0, zero);
+    f32x16 pv = Ty::mma32(x0, bv0, zero);
+    pu = Ty::mma32(x1, bu1, pu);
+    pv = Ty::mma32(x1, bv1, pv);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Pu[2 * cb + s] = pack_kstep<Ty>(pu, s);
+      Pv[2 * cb + s] = pack_kstep<Ty>(pv, s);
+    }
+  }
+}
+
+// X^T operands of a pair (as pair_token_side reads them) by transposed LDS reads
+// (ds_read_b64_tr_b16): in each group of 16 lanes, lane L reads the 8 bytes of row r0 + L / 4 at
+// channel c0 + 4 (L % 4), and lane i of the group then holds channel c0 + i of rows r0 .. r0 + 3
+// (element k = row r0 + k).  Lane (l32, hh) needs rows 16 g + 4 hh + 0..3 and 16 g + 8 + 4 hh +
+// 0..3 of channel 32 cb + l32: two reads per operand instead of eight 16-bit reads.  at(r, c)
+// is the LDS byte address of pair row r, channel c (4 consecutive channels must be adjacent).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t addr) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_s16x4*>(static_cast<uintptr_t>(addr)));
+  return __builtin_bit_cast(u32x2, v);
+}
+template <int KS, class At>
+__device__ __forceinline__ void pair_xt_tr(At at, int lane, u32x4 (&xk)[KS / 2][2]) {
+  const int hh = lane >> 5, l16 = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const int c = 32 * cb + 16 * half + 4 * (l16 & 3);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int r = 16 * g + 4 * hh + (l16 >> 2);
+      const u32x2 a = lds_read_tr16(at(r, c)), b = lds_read_tr16(at(r + 8, c));
+      xk[cb][g] = u32x4{a[0], a[1], b[0], b[1]};
+    }
+  }
+}
+
+template <class Ty, int KS>
 __device__ __forceinline__ void pair_token_side(const uint16_t* tl, int ld, const int (&col)[KS / 2], u32x4 bu,
                                                 u32x4 bv, int lane, u32x4 (&Pu)[KS], u32x4 (&Pv)[KS],
                                                 u32x4 (&xk)[KS / 2][2]) {
@@ -473,6 +522,31 @@ __device__ __forceinline__ void pair_token_side_f8(const uint16_t* tl, int ld, c
   }
 }
 
+// pair_token_side_f8 from X^T operands already read (pair_xt_tr).
+template <class Ty, int KS>
+__device__ __forceinline__ void pair_token_side_f8_mma(const u32x4 (&xk)[KS / 2][2], u32x4 bu, u32x4 bv, int lane,
+                                                       u32x4 (&Pu)[KS], u32x8 (&Pv)[KS / 4]) {
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 bu0 = keep_if(g0, bu), bu1 = keep_if(!g0, bu);
+  const u32x4 bv0 = keep_if(g0, bv), bv1 = keep_if(!g0, bv);
+  const f32x16 zero = {};
+  f32x16 pv_prev = zero;
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const u32x4 x0 = xk[cb][0], x1 = xk[cb][1];
+    f32x16 pu = Ty::mma32(x0, bu0, zero);
+    f32x16 pv = Ty::mma32(x0, bv0, zero);
+    pu = Ty::mma32(x1, bu1, pu);
+    pv = Ty::mma32(x1, bv1, pv);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) Pu[2 * cb + s] = pack_kstep<Ty>(pu, s);
+    if (cb & 1)
+      Pv[cb / 2] = pack_k64_f8(pv_prev, pv);
+    else
+      pv_prev = pv;
+  }
+}
+
 // pair_chunk for the fp8 variant: U' on Ty MFMAs, V' on K64 fp8 MFMAs (fv(s) returns the
 // chunk's fp8 B_v'^T K64 fragment s), the gate (f8_gate) and Z B_o as pair_chunk.
 template <class Ty, int KS, int MB, class FU, class FV, class FO>
@@ -533,6 +607,21 @@ __device__ __forceinline__ void pair_output(const f32x16 (&W)[MB], u32x4 ao, int
   for (int mb = 0; mb < MB; ++mb) {
     dl[mb] = Ty::mma32(ao0, pack_kstep<Ty>(W[mb], 0), zero);
     dl[mb] = Ty::mma32(ao1, pack_kstep<Ty>(W[mb], 1), dl[mb]);
+  }
+}
+
+// delta^T[mb] = W[mb]^T A_o^T for the pair (the same products as pair_output with the operands
+// swapped): lane l32 = token l32 of the pair, register i = channel 32 mb + kord(i, hh), so a
+// lane holds four runs of four consecutive channels of its token's row.
+template <class Ty, int MB>
+__device__ __forceinline__ void pair_output_t(const f32x16 (&W)[MB], u32x4 ao, int lane, f32x16 (&dl)[MB]) {
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 ao0 = keep_if(g0, ao), ao1 = keep_if(!g0, ao);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 0), ao0, zero);
+    dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 1), ao1, dl[mb]);
   }
 }
 
@@ -600,7 +689,8 @@ constexpr int kNormPartials = 3;
 // Persistent d = 128 forward (bigemm_fwd_persist.hip): one eight-wave workgroup per CU over
 // units of 256 rows x one contiguous channel group, the next unit's tile copied into LDS during
 // the current unit's output phase.  RMSNorm scales from a statistics buffer or the previous
-// block's per-group sums (norm: kNormNone, kNormBuffer or kNormPartials).
+// block's per-group sums (norm: kNormNone, kNormBuffer or kNormPartials), or for strided groups
+// from the whole rows the tile fetch reads (kNormInline).
 struct PersistArgs {
   const uint16_t* x;
   uint16_t* out;
