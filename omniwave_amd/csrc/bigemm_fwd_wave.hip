@@ -152,9 +152,6 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   uint16_t* tile = sh.tile[wave];
   float* rsc = sh.rsc[wave];
   int32_t* rows = sh.rows[wave];
-  int col[kMB];
-#pragma unroll
-  for (int cb = 0; cb < kMB; ++cb) col[cb] = 32 * cb + l32;
   const uint32_t bytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * C * 2);
   const __amdgpu_buffer_rsrc_t rx = tensor_rsrc(a.x, bytes), ro = tensor_rsrc(a.out, bytes);
 
@@ -215,8 +212,13 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       bu = scale8<Ty>(fAu, r8);
       bv = scale8<Ty>(fAv, r8);
     }
-    u32x4 Pu[kKS], Pv[kKS], xk[kMB][2];
-    pair_token_side<Ty, kKS>(tile, kLdt, col, bu, bv, lane, Pu, Pv, xk);
+    u32x4 Pu[kKS], Pv[kKS];
+    {
+      u32x4 xk[kKS / 2][2];  // X^T operands by transposed reads
+      const uint32_t tb = lds_addr(tile);
+      pair_xt_tr<kKS>([&](int r, int c) { return tb + 2u * static_cast<uint32_t>(r * kLdt + c); }, lane, xk);
+      pair_token_side_mma<Ty, kKS>(xk, bu, bv, lane, Pu, Pv);
+    }
 
     // Channel side over the four chunks of the expanded dimension, software-pipelined: step e
     // issues chunk e + 1's U'/V' products with two of chunk e's gate values after each of them
@@ -285,26 +287,25 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     step(std::integral_constant<int, 3>{}, Ua, Va, Ub, Vb);
     static_assert(kNCH == 4, "four chunks: the step sequence above");
 
-    // delta = A_o W, rounded, plus x (and the drop-path scale), into the tile in place: the
-    // token side has read it.
+    // delta^T = W^T A_o^T (lane = token row), rounded, plus x (and the drop-path scale), into
+    // the tile in place as 8-byte pieces: the token side has read it.
     f32x16 dl[kMB];
     mfma_drain();
-    pair_output<Ty, kMB>(W, fAo, lane, dl);
+    pair_output_t<Ty, kMB>(W, fAo, lane, dl);
     mfma_drain();
-    float s0 = 1.0f, s1 = 1.0f;
+    float sc = 1.0f;
     if constexpr (DROP) {
-      const int64_t tg0 = 2 * p;
-      const int64_t b0 = tg0 / a.q_s, b1 = (tg0 + 1) / a.q_s;
-      s0 = a.drop_scale[b0 < a.batch ? b0 : a.batch - 1];
-      s1 = a.drop_scale[b1 < a.batch ? b1 : a.batch - 1];
+      const int64_t tg = 2 * p + ((lane >> 4) & 1);  // the lane's token group
+      const int64_t b = tg / a.q_s;
+      sc = a.drop_scale[b < a.batch ? b : a.batch - 1];
     }
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
-      auto dst = [&](int i) { return &tile[pair_token_row(i, hh) * kLdt + 32 * mb + l32]; };
+      auto at = [&](int q) { return &tile[l32 * kLdt + 32 * mb + 8 * q + 4 * hh]; };
       if (a.residual)
-        pair_store_block<Ty, true, DROP>(dl[mb], xk[mb], dst, s0, s1);
+        pair_store_block_t<Ty, true, DROP>(dl[mb], at, sc);
       else
-        pair_store_block<Ty, false, DROP>(dl[mb], xk[mb], dst, s0, s1);
+        pair_store_block_t<Ty, false, DROP>(dl[mb], at, sc);
     }
     wave_lds_sync();
 

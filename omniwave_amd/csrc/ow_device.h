@@ -597,6 +597,31 @@ __device__ __forceinline__ void pair_store_block(const f32x16& dl, const u32x4 (
   }
 }
 
+// Output of one 32-channel block of a pair from delta^T (pair_output_t: lane l32 = token row,
+// registers 4 q .. 4 q + 3 = channels 8 q + 4 hh .. + 3 of the block), in place in an LDS row
+// tile that holds x: rounded to Ty (with SCALE times the drop-path scale s of the lane's token
+// and rounded again, as pair_store_block), with RESIDUAL plus x read from the same positions,
+// written back as 8-byte pieces.  at(q) is the LDS element pointer of the lane's run q.
+template <class Ty, bool RESIDUAL, bool SCALE = false, class At>
+__device__ __forceinline__ void pair_store_block_t(const f32x16& dl, At at, float s = 1.0f) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t v0 = Ty::pack2(dl[4 * q], dl[4 * q + 1]);
+    uint32_t v1 = Ty::pack2(dl[4 * q + 2], dl[4 * q + 3]);
+    if constexpr (SCALE) {
+      v0 = Ty::pack2(Ty::to_f32(lo16(v0)) * s, Ty::to_f32(hi16(v0)) * s);
+      v1 = Ty::pack2(Ty::to_f32(lo16(v1)) * s, Ty::to_f32(hi16(v1)) * s);
+    }
+    u32x2* p = reinterpret_cast<u32x2*>(at(q));
+    if constexpr (RESIDUAL) {
+      const u32x2 x = *p;
+      v0 = add_residual2<Ty>(x[0], v0);
+      v1 = add_residual2<Ty>(x[1], v1);
+    }
+    *p = u32x2{v0, v1};
+  }
+}
+
 // delta[mb] = A_o W[mb] for the pair; ao is the lane's A_o operand row (K step of its group).
 template <class Ty, int MB>
 __device__ __forceinline__ void pair_output(const f32x16 (&W)[MB], u32x4 ao, int lane, f32x16 (&dl)[MB]) {
