@@ -1,5 +1,6 @@
-// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2} (the
-// 56x56x128 stage of OmniWeave-T), one (pair, channel group) unit per wave at a time.
+// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4} and
+// contiguous channel groups (the 56x56x128 and 28x28x256 stages of OmniWeave-T), one (pair,
+// channel group) unit per wave at a time.
 //
 // Same math and operand packing as the other forward kernels (reference
 // omniweave/ops/reference.py:147-171; operand scheme in ow_device.h).  Organisation:
@@ -40,6 +41,7 @@ constexpr int kWavesWg = 4;
 
 struct WaveLds {
   u32x4 w[kGroupFrags][64];        // the group's packed weights
+  u32x4 tok_ops[3][64];            // token-side operand rows A_u, A_v, A_o (read per unit)
   uint16_t tile[kWavesWg][32 * kLdt];  // per wave: the pair's rows, group columns
   float rsc[kWavesWg][32];         // per wave: RMSNorm scale of each token of the pair
   int32_t rows[kWavesWg][32];      // per wave: output row of each token (-1: not stored)
@@ -119,11 +121,26 @@ __device__ __forceinline__ void load_pieces(__amdgpu_buffer_rsrc_t rx, int32_t r
   for (int k = 0; k < NV; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * k, 0, 0);
 }
 
+// Pieces 2 (k0 + k) + hh, k < 4, of this lane's token row (one channel group of a d = 64 row):
+// one batch of the streamed row read.
+__device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh, int k0,
+                                           u32x4 (&v)[4]) {
+  const uint32_t base = row >= 0 ? static_cast<uint32_t>(row) * static_cast<uint32_t>(channels * 2) + 16u * hh
+                                 : kOutOfRange;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * (k0 + k), 0, 0);
+}
+
 template <class Ty, int QC, bool OM, bool DROP>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr int C = QC * kD;
   constexpr int NV = C / 16;  // row pieces per lane
+  // q_c = 4: the next pair's rows are streamed in four batches (one channel group each) during
+  // the chunk loop, reduced to this lane's sum of squares and its group's pieces, instead of
+  // being held whole (64 registers) for a unit.
+  constexpr bool STREAM = QC == 4;
+  constexpr int NX = STREAM ? 4 : NV;  // pieces carried from one unit to the next
   __shared__ __attribute__((aligned(16))) WaveLds sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -142,9 +159,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
           (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(f) * kFragElems + lane * 8),
           (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
   }
-  const u32x4 fAu = reinterpret_cast<const u32x4*>(a.packed)[lane];
-  const u32x4 fAv = reinterpret_cast<const u32x4*>(a.packed + kFragElems)[lane];
-  const u32x4 fAo = reinterpret_cast<const u32x4*>(a.packed + 2 * kFragElems)[lane];
+  if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (first >= n_pairs) return;  // after the only workgroup barrier
@@ -173,39 +188,53 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   // lane's token.  `ent` holds the table entries of the next pair (read a unit ago): once xc
   // is in the tile, the next pair's pieces are loaded into xc, and ent takes the entries of
   // the pair after that.
-  auto unit = [&](int64_t p, u32x4 (&xc)[NV], TokEntry& ent, int32_t& out_c) {
+  auto unit = [&](int64_t p, u32x4 (&xc)[NX], float& ssq, TokEntry& ent, int32_t& out_c) {
     int32_t in_n, out_n;
     unit_row<OM>(a, ent, in_n, out_n);
 
-    // RMSNorm scale of this lane's token: its half of the row here, the other half in lane
-    // l ^ 32.
+    // RMSNorm scale of this lane's token: its half of the row here (streamed: summed as the
+    // batches arrived), the other half in lane l ^ 32.
     float acc = 0.0f;
     if (a.norm) {
+      if constexpr (STREAM) {
+        acc = ssq;
+      } else {
 #pragma unroll
-      for (int k = 0; k < NV; ++k)
+        for (int k = 0; k < NV; ++k)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(xc[k][e], acc);
+          for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(xc[k][e], acc);
+      }
       acc += __shfl_xor(acc, 32);
     }
     // The group's columns into the tile; the row scale (0 for pad tokens) and output row.
-    if (QC == 1 || g == 0) {  // g is uniform: a scalar branch, no dynamic register indexing
+    if constexpr (STREAM || QC == 1) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
     } else {
+      const int k0 = g == 0 ? 0 : 4;  // g is uniform: a scalar select, no dynamic register indexing
+      if (k0 == 0) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[(QC - 1) * 4 + k];
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[4 + k];
+      }
     }
     if (hh == 0) {
       rsc[l32] = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
       rows[l32] = out_c;
     }
-    load_pieces<NV>(rx, in_n, C, hh, xc);  // the next pair, a unit ahead of its use
+    if constexpr (STREAM)
+      ssq = 0.0f;  // the next pair's batches are read during the chunk loop
+    else
+      load_pieces<NV>(rx, in_n, C, hh, xc);  // the next pair, a unit ahead of its use
     ent = next_entry();
     wave_lds_sync();
 
     // Token side.  Lane slots j of the token operand are tokens 16 tg + kord(j, hh) of its
     // group tg: two runs of four scales.
+    // The token operands are read per unit from LDS rather than kept live through the loop.
+    const u32x4 fAu = sh.tok_ops[0][lane], fAv = sh.tok_ops[1][lane];
     u32x4 bu = fAu, bv = fAv;
     if (a.norm) {
       const float* r8 = &rsc[16 * ((lane >> 4) & 1) + 4 * hh];
@@ -228,8 +257,27 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     f32x16 W[kMB] = {};
     const uint32_t wbase = lds_addr(&sh.w[0][lane]);
     constexpr int DEPTH = 4;
+    u32x4 vb[4];  // streamed batch in flight
     auto step = [&](auto e_tag, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
       constexpr int E = decltype(e_tag)::value;      // chunk of the gate and B_o products; -1: none
+      if constexpr (STREAM) {
+        // Step E + 1 takes in batch E (channel group E of the next pair's rows, read a step ago)
+        // and reads batch E + 1.
+        constexpr int T = E + 1;
+        if constexpr (T >= 1) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ssq = Ty::dot2sq(vb[k][e], ssq);
+          if (T - 1 == g) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xc[k] = vb[k];
+          }
+        }
+        // (the reads after the batch is consumed: one batch of registers in flight)
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (T < QC) load_batch(rx, in_n, C, hh, 4 * T, vb);
+      }
       constexpr int NU = E + 1 < kNCH ? 2 * kKS : 0;  // U'/V' products of chunk E + 1 (U, V alternate)
       constexpr int NO = E >= 0 ? 2 * kMB : 0;        // B_o products of chunk E
       constexpr int NF = NU + NO;
@@ -291,7 +339,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     // the tile in place as 8-byte pieces: the token side has read it.
     f32x16 dl[kMB];
     mfma_drain();
-    pair_output_t<Ty, kMB>(W, fAo, lane, dl);
+    pair_output_t<Ty, kMB>(W, sh.tok_ops[2][lane], lane, dl);
     mfma_drain();
     float sc = 1.0f;
     if constexpr (DROP) {
@@ -329,14 +377,31 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     out_c = out_n;
   };
 
-  u32x4 x[NV];
+  u32x4 x[NX];
+  float ssq = 0.0f;
   TokEntry ent = next_entry();
   int32_t in0, out_c;
   unit_row<OM>(a, ent, in0, out_c);
-  load_pieces<NV>(rx, in0, C, hh, x);
+  if constexpr (STREAM) {
+#pragma unroll
+    for (int t = 0; t < QC; ++t) {
+      u32x4 v[4];
+      load_batch(rx, in0, C, hh, 4 * t, v);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssq = Ty::dot2sq(v[k][e], ssq);
+      if (t == g) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = v[k];
+      }
+    }
+  } else {
+    load_pieces<NV>(rx, in0, C, hh, x);
+  }
   ent = next_entry();
 #pragma unroll 1
-  for (int64_t p = first; p < n_pairs; p += stride) unit(p, x, ent, out_c);
+  for (int64_t p = first; p < n_pairs; p += stride) unit(p, x, ssq, ent, out_c);
 }
 
 template <class Ty, int QC>
@@ -364,7 +429,8 @@ int launch_ty(const ResidentArgs& a, hipStream_t stream) {
   switch (a.q_c) {
     case 1: return launch_qc<Ty, 1>(a, stream);
     case 2: return launch_qc<Ty, 2>(a, stream);
-    default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 2} (got %d)", a.q_c);
+    case 4: return launch_qc<Ty, 4>(a, stream);
+    default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 2, 4} (got %d)", a.q_c);
   }
 }
 
@@ -372,7 +438,7 @@ int launch_ty(const ResidentArgs& a, hipStream_t stream) {
 
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems) {
   // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.
-  return d == kD && rd == kRD && (q_c == 1 || (q_c == 2 && radix_level == 0)) && channels == q_c * kD &&
+  return d == kD && rd == kRD && (q_c == 1 || ((q_c == 2 || q_c == 4) && radix_level == 0)) && channels == q_c * kD &&
          x_elems * 2 < (int64_t(1) << 31);
 }
 
