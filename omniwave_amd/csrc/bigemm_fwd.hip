@@ -1150,7 +1150,8 @@ bool fwd_needs_scale_buffer(const void* x, const void* out, const OwPlan* plan, 
   if (p.mode == kModeElement) return true;
   if (stats_in) return false;
   // The persistent kernel reads whole rows only for strided groups (and forms their scales);
-  // with contiguous groups its scales come from the statistics pass.
+  // with contiguous groups its scales come from the statistics pass (measured: cheaper than
+  // whole-row tile fetches through registers at 14x14x512 and 7x7x1024).
   if (fwd_uses_persist(x, out, plan, rd, dtype, flags, batch)) return p.mode != kModeStrided;
   const int32_t c = plan->channels, j = c / 128;
   return !(c % 128 == 0 && (j == 1 || j == 2 || j == 4 || j == 8));

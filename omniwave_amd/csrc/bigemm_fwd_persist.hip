@@ -141,10 +141,12 @@ struct TokLoad {
 // F8: V' = P_v B_v'' on the K = 64 e4m3 MFMA (ow_device.h, fp8 channel side); a chunk is then
 // f8_chunk_units(128) = 20 copy units, which waves 0-3 copy three of and waves 4-7 two of.
 // NS: 1 for contiguous channel groups (tile rows by DMA), else the channel stride of the
-// strided groups (q_c = NS; tile rows through registers, output by 2-byte stores).
+// strided groups (q_c = NS; whole rows through registers, QW = NS pieces per lane and row, which
+// also give the RMSNorm scales; output by 2-byte stores).
 template <class Ty, bool F8, int NS>
 __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units) {
-  constexpr int SNP = NS == 8 ? 4 : 8;  // strided fetch: passes per batch (at most 32 pieces per lane)
+  constexpr int QW = NS > 1 ? NS : 0;  // register-tile fetch width (0: DMA tile)
+  constexpr int SNP = QW == 8 ? 1 : 2;  // register tiles: passes (4 rows each) per batch
   constexpr int CHU = F8 ? f8_chunk_units(kD) : kFrCh;      // 1 KB copy units per chunk
   constexpr int CH_ELEMS = CHU * kFragElems;
   constexpr int HEAD = F8 ? kF8HeadBytes / 2 : kHeadElems;  // packed head, 16-bit elements
@@ -256,10 +258,10 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   };
   using E0 = std::integral_constant<int, 0>;
 
-  // Strided groups: the q_c units of a row chunk (consecutive logical ids) run on one XCD, so the
-  // 2-byte stores of their interleaved columns meet in one L2.
+  // Strided groups: the q_c units of a row chunk (consecutive logical ids) run on one XCD, so
+  // their whole-row reads and the 2-byte stores of their interleaved columns meet in one L2.
   int32_t u = blockIdx.x;
-  if constexpr (NS > 1) {
+  if constexpr (QW > 0) {
     const int nwg = gridDim.x, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int per = nwg >> 3, rem = nwg & 7;
     u = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
@@ -267,23 +269,23 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   if (u >= n_units) return;
   // First channel of a group, mod NS (the group's residue) for unit u.
   auto group_res = [&](int32_t uu) { return NS > 1 ? (a.chan[(uu % a.q_c) * kD] & (NS - 1)) : 0; };
-  // Strided tile of unit uu, slot ss: every batch fetched and written now.  The fetch holds whole
-  // rows (16 lanes per row), so with kNormInline the rows' RMSNorm scales are formed here: sum of
-  // squares over the 16 lanes (DPP), the total in lane 15 of the row.
-  auto strided_tile = [&](int32_t uu, int ss) {
-    if constexpr (NS > 1) {
-      const int res = group_res(uu);
-#pragma unroll
-      for (int p0 = 0; p0 < 8; p0 += SNP) {
-        u32x4 v[SNP][NS];
-        strided_fetch<NS, SNP>(rx, &sh.rowid[ss][32 * wave], a.channels, lane, p0, v);
-        strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, res, p0, v);
-        if (a.norm == kNormInline) {
+  // Register tiles (QW > 0), one batch of passes p0 .. p0 + SNP - 1: tile_fetch issues the loads
+  // of whole rows (16 lanes per row), tile_put writes the group's columns to the tile and, with
+  // kNormInline, the rows' RMSNorm scales: sum of squares over the 16 lanes (DPP), the total in
+  // lane 15 of the row.
+  using TileBatch = u32x4[SNP][QW > 0 ? QW : 1];
+  auto tile_fetch = [&](int ss, int p0, TileBatch& v) {
+    if constexpr (QW > 0) strided_fetch<NS, SNP>(rx, &sh.rowid[ss][32 * wave], a.channels, lane, p0, v);
+  };
+  auto tile_put = [&](int32_t uu, int ss, int p0, const TileBatch& v) {
+    if constexpr (QW > 0) {
+      strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, group_res(uu), p0, v);
+      if (a.norm == kNormInline) {
 #pragma unroll
           for (int p = 0; p < SNP; ++p) {
             float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < NS; ++j)
+            for (int j = 0; j < QW; ++j)
 #pragma unroll
               for (int e = 0; e < 4; ++e) acc = Ty::dot2sq(v[p][j][e], acc);
             acc = group_sum<16>(acc);
@@ -293,7 +295,21 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
                   sh.rowid[ss][r] >= 0 ? rms_scale<Ty>(acc / static_cast<float>(a.channels), a.eps) : 1.0f;
             }
           }
-        }
+      }
+    }
+  };
+  // The whole register tile of unit uu, slot ss (after the unit's stores; batch 0 already
+  // requested into va): each batch's loads go out before the previous batch is put (two batches
+  // of registers in flight).
+  auto strided_tile = [&](int32_t uu, int ss, TileBatch& va) {
+    if constexpr (QW > 0) {
+      TileBatch vb;
+#pragma unroll
+      for (int p0 = 0; p0 < 8; p0 += 2 * SNP) {
+        tile_fetch(ss, p0 + SNP, vb);
+        tile_put(uu, ss, p0, va);
+        if (p0 + 2 * SNP < 8) tile_fetch(ss, p0 + 2 * SNP, va);
+        tile_put(uu, ss, p0 + SNP, vb);
       }
       wave_lds_sync();
     }
@@ -309,9 +325,11 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   __syncthreads();
   {
     const int32_t id = meta_write(meta_load(u), 0);
-    if constexpr (NS == 1) issue_tile(u, 0);
+    if constexpr (QW == 0) issue_tile(u, 0);
     issue_chunk(u, 0);
-    strided_tile(u, 0);
+    TileBatch va0;
+    tile_fetch(0, 0, va0);
+    strided_tile(u, 0, va0);
     stats_write(stats_load(id), id, 0);
     wave_lds_sync();
     wait_chunk(E0{});  // this wave's tile rows; chunk 0 may still be in flight
@@ -570,7 +588,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // The tile reads are complete (their values are in registers): the next unit's rows go out
     // (strided groups: fetched through registers after the stores).
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if constexpr (NS == 1) {
+    if constexpr (QW == 0) {
       if (has_next) issue_tile(un, s ^ 1);
     }
     const int res_u = group_res(u);
@@ -622,8 +640,12 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         }
       }
     }
-    if constexpr (NS > 1) {
-      if (has_next) strided_tile(un, s ^ 1);
+    if constexpr (QW > 0) {
+      if (has_next) {
+        TileBatch vpre;
+        tile_fetch(s ^ 1, 0, vpre);
+        strided_tile(un, s ^ 1, vpre);
+      }
     }
     if (has_next) {
       stats_write(snext, id_next, s ^ 1);
@@ -633,7 +655,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       // The next unit's tile rows have landed once at most this unit's stores (8 row pieces, 8
       // statistics values) and chunk 0's copies, all issued after them, are outstanding
       // (strided groups: the rows were written by this wave).
-      if constexpr (NS == 1) {
+      if constexpr (QW == 0) {
         if (a.stats_out)
           wait_chunk(std::integral_constant<int, 16>{});
         else
