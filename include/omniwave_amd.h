@@ -325,9 +325,10 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
 int ow_bwd_rmsnorm(const void* x, const void* g, const float* rscale, const void* dout, void* dx,
                    int64_t rows, int32_t channels, int32_t residual, int32_t dtype, void* stream);
 
-/* Packed weights of the fused d = 64 backward (rd 128 or 256): per channel group and 32-row
- * chunk, the folded B_u'', B_v'', B_o'' as the forward's and transposed 32x32x16 MFMA operands
- * (24 fragments of 1 KB); ow_bwd_packed_bytes gives the size. */
+/* Packed weights of the fused backward (d 64 or 128, rd 128 or 256): per channel group and
+ * 32-row chunk, the folded B_u'', B_v'', B_o'' as the forward's and transposed 32x32x16 MFMA
+ * operands (3 d / 16 + 6 d / 32 fragments of 1 KB: 24 at d = 64, 48 at d = 128);
+ * ow_bwd_packed_bytes gives the size. */
 size_t ow_bwd_packed_bytes(int32_t q_c, int32_t d, int32_t rd);
 int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype,
                         const float* norm_weight, const float* gamma, const int32_t* channel_index,
@@ -349,6 +350,18 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
                  const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
                  void* dv, void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d,
                  int32_t rd, int32_t dtype, void* stream);
+
+/* The d = 128 backward's token side and first channel-side products in one kernel (replaces
+ * ow_tile_mix x3, the U'/V'/dZ GEMMs and ow_bwd_gate of the composed backward; the reference's
+ * fp32 autograd recompute, omniweave/ops/triton.py:256-292): from the routed tiles X' and dY
+ * ([q_c][slots][128], ow_bwd_gather) and the fp32 [16][16] token matrices, per 32-slot pair
+ * P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw, [q_c][slots][128]) and per
+ * 32-row chunk of the expanded dimension U'^T, V'^T, dZ^T and the gate backward, stored as z,
+ * du, dv ([q_c][slots][rd]).  packed from ow_pack_bwd_weights with d = 128; slots % 16 == 0,
+ * bf16 / f16, every buffer 16-byte aligned and below 2 GiB. */
+int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                   const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                   void* dv, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
 
 /* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
  * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and

@@ -201,18 +201,37 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                               bv.data_ptr(), bv_t.data_ptr(), bo.data_ptr(), bo_t.data_ptr(), stream),
                           "ow_fold_weights")
             au_t, av_t, ao_t = (a.t().contiguous() for a in (au, av, ao))
-            # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
-            pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
-            pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
-            dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
-            # Channel side: batched GEMMs + the gate kernel.
-            u = torch.bmm(pu, bu)
-            v = torch.bmm(pv, bv)
-            dz = torch.bmm(dw, bo_t)
-            z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
-            _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
-                                          dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
-            del u, v, dz
+            if d == 128 and dtype != torch.float32:
+                # One kernel: token side P_u, P_v, dW', then U', V', dZ per 32-row chunk and the
+                # gate backward (Z, dU', dV').
+                nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
+                wpk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+                _native.check(lib.ow_pack_bwd_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                                      nw.data_ptr() if nw is not None else None, gm.data_ptr(),
+                                                      ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
+                                                      stream), "ow_pack_bwd_weights")
+                pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
+                pv, dw = torch.empty_like(pu), torch.empty_like(pu)
+                z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
+                du, dv = torch.empty_like(z), torch.empty_like(z)
+                _native.check(lib.ow_bwd_channel(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                                 ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
+                                                 dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(), slots,
+                                                 q_c, d, rd, code, stream), "ow_bwd_channel")
+                del wpk
+            else:
+                # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
+                pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
+                pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
+                dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
+                # Channel side: batched GEMMs + the gate kernel.
+                u = torch.bmm(pu, bu)
+                v = torch.bmm(pv, bv)
+                dz = torch.bmm(dw, bo_t)
+                z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
+                _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(),
+                                              du.data_ptr(), dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
+                del u, v, dz
             wp = torch.bmm(z, bo)
             dpu = torch.bmm(du, bu_t)
             dpv = torch.bmm(dv, bv_t)

@@ -481,20 +481,22 @@ __global__ void __launch_bounds__(256) tile_outer_kernel(const uint16_t* in1, co
   for (int i = 0; i < 4; ++i) partial[((4 * h + i) * 16 + l16) * n_waves + wave] = acc[i];
 }
 
-// ---- Fused channel side of the backward, d = 64 -----------------------------------------
-// Packed backward weights, per (group q, 32-row chunk ec of the expanded dimension), 24
-// fragments of 64 lanes x 8 (the 32x32x16 operand layouts of the forward; kord(j, hh) =
-// 8(j/4) + 4hh + j%4):
-//   [0, 4)   B_u''^T  A operand: lane -> row e = 32 ec + l32, slot j -> channel 16 ks + kord
-//   [4, 8)   B_v''^T  A operand (same)
-//   [8, 12)  B_o''    A operand: lane -> row e, slot j -> channel 16 ks + kord
-//   [12, 16) B_o''    B operand (mb, s): lane -> channel 32 mb + l32, slot j -> e = 32 ec + 16 s + kord
-//   [16, 20) B_u''^T  B operand (mb, s): lane -> channel, slot j -> e (same order)
-//   [20, 24) B_v''^T  B operand (mb, s)
+// ---- Fused channel side of the backward -----------------------------------------------
+// Packed backward weights, per (group q, 32-row chunk ec of the expanded dimension), 3 KS + 6 MB
+// fragments of 64 lanes x 8 (KS = d / 16, MB = d / 32; the 32x32x16 operand layouts of the
+// forward; kord(j, hh) = 8(j/4) + 4hh + j%4):
+//   [0, KS)          B_u''^T  A operand: lane -> row e = 32 ec + l32, slot j -> channel 16 ks + kord
+//   [KS, 2 KS)       B_v''^T  A operand (same)
+//   [2 KS, 3 KS)     B_o''    A operand: lane -> row e, slot j -> channel 16 ks + kord
+//   then 2 MB each:  B_o''    B operand (mb, s): lane -> channel 32 mb + l32, slot j -> e = 32 ec + 16 s + kord
+//                    B_u''^T  B operand (mb, s): lane -> channel, slot j -> e (same order)
+//                    B_v''^T  B operand (mb, s)
+// (d = 64: 24 fragments per chunk; d = 128: 48, the first 24 of which the d = 128 channel kernel reads.)
 constexpr int kBwdD = 64;
 constexpr int kBwdKS = kBwdD / 16;
 constexpr int kBwdMB = kBwdD / 32;
 constexpr int kBwdFr = 3 * kBwdKS + 6 * kBwdMB;  // 24 fragments per chunk
+__host__ __device__ constexpr int bwd_frags(int d) { return 3 * (d / 16) + 6 * (d / 32); }
 
 struct BwdPackArgs {
   const void* b_u;
@@ -506,6 +508,7 @@ struct BwdPackArgs {
   uint16_t* packed;
   int32_t wdtype, q_c, rd, channels;
   int64_t total;
+  int32_t d;
 };
 
 template <class Ty>
@@ -513,7 +516,8 @@ __global__ void __launch_bounds__(256) pack_bwd_kernel(BwdPackArgs p) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= p.total) return;
   const int nch = p.rd / 32;
-  const int64_t per_chunk = static_cast<int64_t>(kBwdFr) * kFragElems;
+  const int ks_n = p.d / 16, mb_n = p.d / 32;
+  const int64_t per_chunk = static_cast<int64_t>(bwd_frags(p.d)) * kFragElems;
   const int q = static_cast<int>(idx / (nch * per_chunk));
   int64_t rem = idx - static_cast<int64_t>(q) * nch * per_chunk;
   const int ec = static_cast<int>(rem / per_chunk);
@@ -524,27 +528,27 @@ __global__ void __launch_bounds__(256) pack_bwd_kernel(BwdPackArgs p) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int kord = 8 * (j / 4) + 4 * hh + (j % 4);
   int c, e, mat;  // mat: 0 = B_u, 1 = B_v, 2 = B_o
-  if (fr < 3 * kBwdKS) {
-    mat = fr / kBwdKS;
+  if (fr < 3 * ks_n) {
+    mat = fr / ks_n;
     e = 32 * ec + l32;
-    c = 16 * (fr % kBwdKS) + kord;
+    c = 16 * (fr % ks_n) + kord;
   } else {
-    const int f = fr - 3 * kBwdKS;
-    const int m = f / (2 * kBwdMB);  // 0: B_o, 1: B_u, 2: B_v
+    const int f = fr - 3 * ks_n;
+    const int m = f / (2 * mb_n);  // 0: B_o, 1: B_u, 2: B_v
     mat = m == 0 ? 2 : m - 1;
-    const int mb = (f % (2 * kBwdMB)) / 2, sh = f % 2;
+    const int mb = (f % (2 * mb_n)) / 2, sh = f % 2;
     c = 32 * mb + l32;
     e = 32 * ec + 16 * sh + kord;
   }
-  const int32_t ch = p.chan[q * kBwdD + c];
+  const int32_t ch = p.chan[q * p.d + c];
   const bool ok = ch >= 0 && ch < p.channels;
   float val;
   if (mat == 2) {
     const float gm = ok ? (p.gamma ? p.gamma[ch] : 1.0f) : 0.0f;
-    val = load_any(p.b_o, (static_cast<int64_t>(q) * p.rd + e) * kBwdD + c, p.wdtype) * gm;
+    val = load_any(p.b_o, (static_cast<int64_t>(q) * p.rd + e) * p.d + c, p.wdtype) * gm;
   } else {
     const float w = ok ? (p.norm_w ? p.norm_w[ch] : 1.0f) : 0.0f;
-    val = load_any(mat == 0 ? p.b_u : p.b_v, (static_cast<int64_t>(q) * kBwdD + c) * p.rd + e, p.wdtype) * w *
+    val = load_any(mat == 0 ? p.b_u : p.b_v, (static_cast<int64_t>(q) * p.d + c) * p.rd + e, p.wdtype) * w *
           (mat == 0 ? kNegLog2e : kNegLn2);
   }
   p.packed[idx] = Ty::from_f32(val);
@@ -931,6 +935,214 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
   return OW_OK;
 }
 
+// ---- Channel side of the backward, d = 128: token side, U'/V'/dZ and the gate -------------
+// Eight waves per workgroup, one workgroup per CU, persistent over units of 256 slots x one
+// channel group (unit u: group u % q_c, slots 256 (u / q_c) + 32 wave .. for wave `wave`):
+//   * P_u = A_u X', P_v = A_v X' from the wave's 32 X' rows, then dW' = A_o^T dY from its 32 dY
+//     rows: the forward's block-diagonal token-side products (32x32x16 MFMAs), the X^T operands
+//     by transposed LDS reads of the rows, which buffer_load ... lds copies into the wave's
+//     swizzled tile (piece p of row r at slot p ^ 4 ((r >> 2) & 1)); P_u, P_v, dW' are stored;
+//   * per 32-row chunk ec of the expanded dimension: U'^T = B_u''^T P_u^T, V'^T, dZ^T = B_o''
+//     dW'^T (the chunk's 24 A-operand fragments of ow_pack_bwd_weights, shared by the eight
+//     waves through three LDS buffers), the gate backward (as bwd_gate_kernel), and Z, dU', dV'
+//     stored slot-major.
+// The products that consume them (W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T, the
+// slot reductions for dB and the token-matrix gradients) run after it.  Stores and copies are
+// counted in vmcnt in issue order (explicit waits below).
+constexpr int kB2D = 128;
+constexpr int kB2KS = kB2D / 16;       // K steps over the channel group
+constexpr int kB2FrA = 3 * kB2KS;      // A-operand fragments per chunk (24 KB)
+constexpr int kB2Waves = 8;
+constexpr int kB2Rows = 32 * kB2Waves;  // slots per unit
+
+struct BwdChanArgs {
+  const uint16_t* xt;   // [q_c][slots][128] X' tiles
+  const uint16_t* dyt;  // [q_c][slots][128] dY tiles
+  const float* a_u;     // [16][16] token matrices, fp32
+  const float* a_v;
+  const float* a_o;
+  const uint16_t* packed;  // ow_pack_bwd_weights, d = 128
+  uint16_t* pu;            // [q_c][slots][128]
+  uint16_t* pv;
+  uint16_t* dw;
+  uint16_t* z;  // [q_c][slots][rd]
+  uint16_t* du;
+  uint16_t* dv;
+  int64_t slots;
+  int32_t q_c;
+};
+
+struct BwdChanLds {
+  uint16_t x[kB2Waves][32 * kB2D];     // per wave: its 32 rows (X', then dY)
+  uint16_t w[3][kB2FrA * kFragElems];  // chunk buffers
+  u32x4 tok[3][64];                    // A_u, A_v, A_o^T token-operand rows
+};
+
+// out = the token-side product of one operand f (pair_token_side_mma for a single product).
+template <class Ty, int KS>
+__device__ __forceinline__ void token_side_one(const u32x4 (&xk)[KS / 2][2], u32x4 f, int lane, u32x4 (&out)[KS]) {
+  const bool g0 = (lane & 16) == 0;
+  const u32x4 f0 = keep_if(g0, f), f1 = keep_if(!g0, f);
+  const f32x16 zero = {};
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    f32x16 acc = Ty::mma32(xk[cb][0], f0, zero);
+    acc = Ty::mma32(xk[cb][1], f1, acc);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) out[2 * cb + s2] = pack_kstep<Ty>(acc, s2);
+  }
+}
+
+template <class Ty, int RD>
+__global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32_t n_units) {
+  constexpr int NCH = RD / 32;
+  constexpr int CH = kB2FrA * kFragElems;                  // one chunk buffer (elements)
+  constexpr int PACK_CH = bwd_frags(kB2D) * kFragElems;   // packed chunk stride (both operand halves)
+  __shared__ __attribute__((aligned(16))) BwdChanLds sh;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = lane >> 5, l32 = lane & 31;
+  const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
+  const int64_t rows = a.slots * a.q_c;
+  const uint32_t tbytes = static_cast<uint32_t>(rows * kB2D * 2), ebytes = static_cast<uint32_t>(rows * RD * 2);
+  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(a.xt, tbytes), rdy = buffer_rsrc(a.dyt, tbytes);
+  const __amdgpu_buffer_rsrc_t rpu = buffer_rsrc(a.pu, tbytes), rpv = buffer_rsrc(a.pv, tbytes),
+                               rdw = buffer_rsrc(a.dw, tbytes);
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(a.z, ebytes), rdu = buffer_rsrc(a.du, ebytes),
+                               rdv = buffer_rsrc(a.dv, ebytes);
+  if (wave == 0) {
+    sh.tok[0][lane] = token_frag<Ty, false>(a.a_u, lane);
+    sh.tok[1][lane] = token_frag<Ty, false>(a.a_v, lane);
+  } else if (wave == 1) {
+    sh.tok[2][lane] = token_frag<Ty, true>(a.a_o, lane);
+  }
+  const uint32_t xlds = lds_addr(sh.x[wave]);
+
+  for (int32_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int q = u % a.q_c;
+    const int64_t slot0 = static_cast<int64_t>(u / a.q_c) * kB2Rows + 32 * wave;
+    const int64_t row0 = static_cast<int64_t>(q) * a.slots + slot0;
+    // Copy k: rows 4k .. 4k + 3 of the wave; lane -> row 4k + lane / 16, LDS slot lane % 16,
+    // which holds the row's piece (lane % 16) ^ 4 (k & 1); rows past the slots read as zero.
+    auto copy_tile = [&](__amdgpu_buffer_rsrc_t r) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int rr = 4 * k + (lane >> 4);
+        const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ (4 * (k & 1)));
+        const uint32_t voff = slot0 + rr < a.slots
+                                  ? static_cast<uint32_t>(row0 + rr) * static_cast<uint32_t>(kB2D * 2) + 16u * piece
+                                  : kOffOut;
+        tile_copy(r, voff, xlds + static_cast<uint32_t>(4 * k * kB2D * 2));
+      }
+    };
+    auto issue_chunk = [&](int ec) {
+      const uint16_t* src = uniform_ptr(a.packed + (static_cast<size_t>(q) * NCH + ec) * PACK_CH);
+      uint16_t* dst = sh.w[ec % 3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int f = wave + i * kB2Waves;
+        copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane16);
+      }
+    };
+    auto at = [&](int r, int c) {
+      return xlds + 2u * static_cast<uint32_t>(r * kB2D + (c ^ (32 * ((r >> 2) & 1))));
+    };
+    // Lane (slot l32, hh) of K-step operand ks holds channels 16 ks + 4 hh + (0..3, 8..11).
+    const int64_t my_row = row0 + l32;
+    const bool my_ok = slot0 + l32 < a.slots;
+    auto store_ops = [&](__amdgpu_buffer_rsrc_t r, const u32x4 (&v)[kB2KS]) {
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) {
+        const uint32_t o = my_ok ? static_cast<uint32_t>(my_row * kB2D + 16 * ks + 4 * hh) * 2u : kOffOut;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{v[ks][0], v[ks][1]}, r, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{v[ks][2], v[ks][3]}, r, my_ok ? o + 16u : kOffOut, 0, 0);
+      }
+    };
+
+    __syncthreads();  // the previous unit is done with the chunk buffers; tok is written
+    copy_tile(rxt);    // 8 operations
+    issue_chunk(0);    // 3
+    issue_chunk(1);    // 3
+    wait_vmcnt<6>();   // the X' rows (the chunk copies may be in flight)
+    wave_lds_sync();
+    u32x4 xk[kB2KS / 2][2];
+    pair_xt_tr<kB2KS>(at, lane, xk);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile is read: the dY rows replace it
+    copy_tile(rdy);  // 8
+    u32x4 Pu[kB2KS], Pv[kB2KS], Dw[kB2KS];
+    pair_token_side_mma<Ty, kB2KS>(xk, sh.tok[0][lane], sh.tok[1][lane], lane, Pu, Pv);
+    store_ops(rpu, Pu);  // 16
+    store_ops(rpv, Pv);  // 16
+    wait_vmcnt<32>();    // the dY rows (and with them both chunk copies); the stores may be in flight
+    wave_lds_sync();
+    pair_xt_tr<kB2KS>(at, lane, xk);
+    token_side_one<Ty, kB2KS>(xk, sh.tok[2][lane], lane, Dw);
+    store_ops(rdw, Dw);  // 16
+
+    // Chunk loop.  Step ec: [wait for chunk ec] [barrier] [copies of chunk ec + 2: 3] [products,
+    // gate] [stores: 12].  Chunk ec >= 2 was copied at step ec - 2, and 12 + 3 + 12 operations
+    // (12 + 12 without a copy at step ec - 1) were issued after it; chunks 0 and 1 landed before
+    // the dY rows.
+#pragma unroll 1
+    for (int ec = 0; ec < NCH; ++ec) {
+      if (ec >= 2) {
+        if (ec + 1 < NCH)
+          wait_vmcnt<27>();
+        else
+          wait_vmcnt<24>();
+      }
+      __syncthreads();  // chunk ec is in LDS for every wave; every wave is done with chunk ec - 1
+      if (ec + 2 < NCH) issue_chunk(ec + 2);
+      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
+      f32x16 U = {}, V = {}, G = {};
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) {
+        U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], U);
+        V = Ty::mma32(cf[(kB2KS + ks) * (kFragElems / 8) + lane], Pv[ks], V);
+        G = Ty::mma32(cf[(2 * kB2KS + ks) * (kFragElems / 8) + lane], Dw[ks], G);
+      }
+      mfma_drain();
+      f32x16 Z, DU, DV;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float up = U[i], vp = V[i], g = G[i];
+        const float sg = gate_sigmoid(up);
+        Z[i] = up * vp * sg;
+        DU[i] = g * vp * sg * (1.0f - kLn2 * up * (1.0f - sg));
+        DV[i] = g * up * sg;
+      }
+      // Registers 4b .. 4b + 3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32.
+      auto store_chunk = [&](__amdgpu_buffer_rsrc_t r, const f32x16& m) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t o =
+              my_ok ? static_cast<uint32_t>(my_row * RD + 32 * ec + 8 * b + 4 * hh) * 2u : kOffOut;
+          __builtin_amdgcn_raw_buffer_store_b64(
+              u32x2{Ty::pack2(m[4 * b], m[4 * b + 1]), Ty::pack2(m[4 * b + 2], m[4 * b + 3])}, r, o, 0, 0);
+        }
+      };
+      store_chunk(rz, Z);
+      store_chunk(rdu, DU);
+      store_chunk(rdv, DV);
+    }
+  }
+}
+
+template <int RD>
+int launch_bwd_chan_rd(const BwdChanArgs& a, int32_t n_units, int32_t dtype, hipStream_t s) {
+  int64_t grid = device_cus();
+  if (grid >= n_units)
+    grid = n_units;
+  else if (grid >= 8)
+    grid -= grid % 8;
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL((bwd_chan_d128_kernel<BF16, RD>), g, dim3(512), 0, s, a, n_units);
+  else
+    hipLaunchKernelGGL((bwd_chan_d128_kernel<F16, RD>), g, dim3(512), 0, s, a, n_units);
+  return hip_status(hipGetLastError(), "bwd_chan_d128_kernel launch");
+}
+
 unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 // out[b][i] = round(x[b][i] * scale[b]): the upstream gradient of the delta branch under
@@ -1274,22 +1486,23 @@ int ow_tile_outer(const void* in1, const void* in2, float* partial, int32_t n_wa
 }
 
 size_t ow_bwd_packed_bytes(int32_t q_c, int32_t d, int32_t rd) {
-  if (q_c < 1 || d != ow::kBwdD || (rd != 128 && rd != 256)) return 0;
-  return static_cast<size_t>(q_c) * (rd / 32) * ow::kBwdFr * ow::kFragElems * 2;
+  if (q_c < 1 || (d != 64 && d != 128) || (rd != 128 && rd != 256)) return 0;
+  return static_cast<size_t>(q_c) * (rd / 32) * ow::bwd_frags(d) * ow::kFragElems * 2;
 }
 
 int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype, const float* norm_weight,
                         const float* gamma, const int32_t* channel_index, int32_t channels, int32_t q_c, int32_t d,
                         int32_t rd, int32_t compute_dtype, void* packed, void* stream) {
   OW_CHECK_ARG(b_u && b_v && b_o && channel_index && packed, "tensor pointer is NULL");
-  OW_CHECK_SUPPORTED(d == ow::kBwdD && (rd == 128 || rd == 256), "fused backward needs d = 64, rd in {128, 256}");
+  OW_CHECK_SUPPORTED((d == 64 || d == 128) && (rd == 128 || rd == 256),
+                     "packed backward weights need d in {64, 128}, rd in {128, 256}");
   OW_CHECK_ARG(q_c >= 1 && channels >= 1, "bad shape q_c=%d C=%d", q_c, channels);
   OW_CHECK_ARG(weight_dtype >= OW_DTYPE_F32 && weight_dtype <= OW_DTYPE_F16, "unknown weight dtype %d", weight_dtype);
   OW_CHECK_SUPPORTED(compute_dtype == OW_DTYPE_BF16 || compute_dtype == OW_DTYPE_F16, "unsupported compute dtype %d",
                      compute_dtype);
   const int64_t total = static_cast<int64_t>(ow_bwd_packed_bytes(q_c, d, rd) / 2);
   ow::BwdPackArgs p{b_u, b_v, b_o, norm_weight, gamma, channel_index, static_cast<uint16_t*>(packed),
-                    weight_dtype, q_c, rd, channels, total};
+                    weight_dtype, q_c, rd, channels, total, d};
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (compute_dtype == OW_DTYPE_BF16)
     hipLaunchKernelGGL(ow::pack_bwd_kernel<ow::BF16>, dim3(ow::blocks_for(total)), dim3(256), 0, s, p);
@@ -1337,6 +1550,39 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
                      mu(dxt), partial, slots, slots / 32, 0, q_c};
   a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
   return ow::launch_bwd_fused<false>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
+}
+
+int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                   const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
+                   int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+  OW_CHECK_SUPPORTED(d == ow::kB2D && (rd == 128 || rd == 256), "backward channel kernel needs d = 128, rd in {128, 256}");
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 16 == 0, "bad shape q_c=%d slots=%lld (multiple of 16)", q_c,
+               (long long)slots);
+  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
+               packed_bytes);
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31), "tiles of %lld slots exceed 2 GiB",
+               (long long)slots);
+  OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && z && du && dv, "tensor pointer is NULL");
+  for (const void* p : {xt, dyt, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
+                        static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
+                        static_cast<const void*>(dv)})
+    OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
+  const ow::BwdChanArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
+                          slots, q_c};
+  const int64_t units = static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows);
+  OW_CHECK_ARG(units < (int64_t(1) << 31), "too many units");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rc = rd == 256 ? ow::launch_bwd_chan_rd<256>(a, static_cast<int32_t>(units), dtype, s)
+                           : ow::launch_bwd_chan_rd<128>(a, static_cast<int32_t>(units), dtype, s);
+  if (rc == OW_OK) ow::clear_error();
+  return rc;
 }
 
 int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,

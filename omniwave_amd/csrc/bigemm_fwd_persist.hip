@@ -68,33 +68,6 @@ struct PersistLds {
 };
 static_assert(32 * kLdo * 2 * kWaves <= 3 * kChElems * 2, "output staging fits in the chunk buffers");
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t persist_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-constexpr uint32_t kOffOut = 0x80000000u;  // a byte offset past every buffer (the launcher keeps
-                                           // x below 2 GiB)
-
-// 16 bytes per lane from x (byte offset voff, kOffOut: zeros) to LDS byte address lds + 16 lane,
-// untracked by the compiler (no compiler wait before later LDS reads); the kernel waits with
-// wait_vmcnt.
-__device__ __forceinline__ void tile_copy(__amdgpu_buffer_rsrc_t rx, uint32_t voff, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rx),
-               "s"(lds)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
-// A wave-uniform pointer the compiler may not prove uniform (the scalar operand of a copy).
-__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
 // Strided channel groups (radix levels >= 1: group qc is channels res + t NS, t < 128, NS = q_c):
 // a 16-byte piece of a row holds M = 8 / NS columns of every group, so the tile comes through
 // registers.  strided_fetch loads a wave's whole rows, NS pieces per lane and row (16 lanes per
@@ -162,7 +135,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   int hh = lane >> 5, l32 = lane & 31;
   uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
   const uint32_t xbytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
-  const __amdgpu_buffer_rsrc_t rx = persist_rsrc(a.x, xbytes);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, xbytes);
   const int64_t n_groups = static_cast<int64_t>(a.batch) * a.q_s;
   const bool tok_lds = a.q_s * kG <= kTokLds;  // token tables copied to LDS at the start
 
@@ -592,9 +565,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       if (has_next) issue_tile(un, s ^ 1);
     }
     const int res_u = group_res(u);
-    const __amdgpu_buffer_rsrc_t ro = persist_rsrc(a.out, xbytes);
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(a.out, xbytes);
     const __amdgpu_buffer_rsrc_t rs =
-        persist_rsrc(a.stats_out, static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.q_c * 4));
+        buffer_rsrc(a.stats_out, static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.q_c * 4));
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int rr = (lane >> 4) + 4 * k;

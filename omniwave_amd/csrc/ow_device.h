@@ -156,6 +156,34 @@ __device__ __forceinline__ void copy_frag_to_lds(const uint16_t* src, uint16_t* 
                       lane16);
 }
 
+// Raw buffer resource over `bytes` bytes at p (no stride): loads past the end return zero and
+// stores there are dropped, so pad rows need no branches (callers keep buffers below 2 GiB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOffOut = 0x80000000u;  // a byte offset past every buffer below 2 GiB
+
+// 16 bytes per lane from a buffer (byte offset voff, kOffOut: zeros) to LDS byte address
+// lds + 16 lane (lds wave-uniform), untracked by the compiler (no compiler wait before later LDS
+// reads); the kernel waits with wait_vmcnt.
+__device__ __forceinline__ void tile_copy(__amdgpu_buffer_rsrc_t rx, uint32_t voff, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rx),
+               "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// A wave-uniform pointer the compiler may not prove uniform (the scalar operand of a copy).
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Waits until at most N vector-memory operations of this wave are outstanding.
