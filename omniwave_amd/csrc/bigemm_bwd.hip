@@ -954,6 +954,8 @@ constexpr int kB2KS = kB2D / 16;       // K steps over the channel group
 constexpr int kB2FrA = 3 * kB2KS;      // A-operand fragments per chunk (24 KB)
 constexpr int kB2Waves = 8;
 constexpr int kB2Rows = 32 * kB2Waves;  // slots per unit
+constexpr int kB2St = 40;               // staging row stride (elements) of the chunk outputs
+static_assert(3 * 32 * kB2St <= 32 * kB2D, "the chunk outputs' staging fits in a wave's tile");
 
 struct BwdChanArgs {
   const uint16_t* xt;   // [q_c][slots][128] X' tiles
@@ -1080,16 +1082,16 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
     store_ops(rdw, Dw);  // 16
 
     // Chunk loop.  Step ec: [wait for chunk ec] [barrier] [copies of chunk ec + 2: 3] [products,
-    // gate] [stores: 12].  Chunk ec >= 2 was copied at step ec - 2, and 12 + 3 + 12 operations
-    // (12 + 12 without a copy at step ec - 1) were issued after it; chunks 0 and 1 landed before
+    // gate] [stores: 6].  Chunk ec >= 2 was copied at step ec - 2, and 6 + 3 + 6 operations
+    // (6 + 6 without a copy at step ec - 1) were issued after it; chunks 0 and 1 landed before
     // the dY rows.
 #pragma unroll 1
     for (int ec = 0; ec < NCH; ++ec) {
       if (ec >= 2) {
         if (ec + 1 < NCH)
-          wait_vmcnt<27>();
+          wait_vmcnt<15>();
         else
-          wait_vmcnt<24>();
+          wait_vmcnt<12>();
       }
       __syncthreads();  // chunk ec is in LDS for every wave; every wave is done with chunk ec - 1
       if (ec + 2 < NCH) issue_chunk(ec + 2);
@@ -1111,19 +1113,32 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
         DU[i] = g * vp * sg * (1.0f - kLn2 * up * (1.0f - sg));
         DV[i] = g * up * sg;
       }
-      // Registers 4b .. 4b + 3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32.
-      auto store_chunk = [&](__amdgpu_buffer_rsrc_t r, const f32x16& m) {
+      // Registers 4b .. 4b + 3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32: staged
+      // per wave as [32 slots][32 rows] (row stride kB2St) in the wave's tile, which the chunk
+      // loop does not read, then stored as 64-byte row pieces (four lanes per slot).
+      uint16_t* stg = sh.x[wave];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t o =
-              my_ok ? static_cast<uint32_t>(my_row * RD + 32 * ec + 8 * b + 4 * hh) * 2u : kOffOut;
-          __builtin_amdgcn_raw_buffer_store_b64(
-              u32x2{Ty::pack2(m[4 * b], m[4 * b + 1]), Ty::pack2(m[4 * b + 2], m[4 * b + 3])}, r, o, 0, 0);
+      for (int t = 0; t < 3; ++t) {
+        const f32x16& m = t == 0 ? Z : t == 1 ? DU : DV;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          *reinterpret_cast<u32x2*>(&stg[t * 32 * kB2St + l32 * kB2St + 8 * b + 4 * hh]) =
+              u32x2{Ty::pack2(m[4 * b], m[4 * b + 1]), Ty::pack2(m[4 * b + 2], m[4 * b + 3])};
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const __amdgpu_buffer_rsrc_t r = t == 0 ? rz : t == 1 ? rdu : rdv;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int sl = 16 * h + (lane >> 2), part = lane & 3;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[t * 32 * kB2St + sl * kB2St + 8 * part]);
+          const uint32_t o = slot0 + sl < a.slots
+                                 ? static_cast<uint32_t>((row0 + sl) * RD + 32 * ec + 8 * part) * 2u
+                                 : kOffOut;
+          __builtin_amdgcn_raw_buffer_store_b128(v, r, o, 0, 0);
         }
-      };
-      store_chunk(rz, Z);
-      store_chunk(rdu, DU);
-      store_chunk(rdv, DV);
+      }
     }
   }
 }
