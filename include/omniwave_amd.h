@@ -363,6 +363,19 @@ int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const floa
                    const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
                    void* dv, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
 
+/* The rest of the d = 128 backward's channel side in one kernel (replaces the W'/dP GEMMs,
+ * ow_tile_outer x3 and the dX' ow_tile_mix): from z, du, dv of ow_bwd_channel and the tiles X',
+ * dY, per 32-slot pair dP_u = dU' B_u''^T, dP_v = dV' B_v''^T, dX' = A_u^T dP_u + A_v^T dP_v
+ * (stored to dxt, [q_c][slots][128]), W' = Z B_o'' and the token-matrix gradients dA_u = sum
+ * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
+ * partial[w][3][256] (w < n_partial = ow_bwd_channel_partials(slots, q_c); element 16 t + k),
+ * which the caller sums over w.  Shapes and alignment as ow_bwd_channel. */
+int64_t ow_bwd_channel_partials(int64_t slots, int32_t q_c);
+int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* du, const void* dv,
+                    const float* a_u, const float* a_v, const void* packed, size_t packed_bytes, void* dxt,
+                    float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
+                    int32_t dtype, void* stream);
+
 /* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
  * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and
  * ow_bwd_scatter around it as well): X' = x r and dY rows are read from x, dy ([rows][C],

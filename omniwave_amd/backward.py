@@ -9,7 +9,9 @@ accumulation, entirely on the HIP stream of the gradient:
   ``ow_bwd_params``, ``ow_fold_weights``);
 * for d = 64 one fused MFMA kernel (``ow_bwd_fused``) does the token side (P_u, P_v, dW'), the
   channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u, dP_v), dX' and the token-matrix
-  gradients (per-workgroup partials); otherwise the 16x16 token-side products are
+  gradients (per-workgroup partials); for d = 128 two kernels share that work
+  (``ow_bwd_channel``: token side, U', V', dZ and the gate; ``ow_bwd_channel2``: dP_u, dP_v,
+  dX', W' and the token-matrix gradients); otherwise (fp32) the 16x16 token-side products are
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
   ``ow_bwd_gate``;
@@ -189,6 +191,37 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             d_bv = _slot_reduce(pv, dv)
             d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
             del z, du, dv, pu, pv, dw
+        elif d == 128 and dtype != torch.float32:
+            # Two kernels over 256-slot units: (1) token side P_u, P_v, dW', then U', V', dZ per
+            # 32-row chunk and the gate backward (Z, dU', dV'); (2) dP_u, dP_v, dX', W' and the
+            # token-matrix gradients (per-workgroup partials).
+            nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
+            wpk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _native.check(lib.ow_pack_bwd_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
+                                                  nw.data_ptr() if nw is not None else None, gm.data_ptr(),
+                                                  ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
+                                                  stream), "ow_pack_bwd_weights")
+            pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
+            pv, dw = torch.empty_like(pu), torch.empty_like(pu)
+            z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
+            du, dv = torch.empty_like(z), torch.empty_like(z)
+            _native.check(lib.ow_bwd_channel(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                             ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
+                                             dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(), slots,
+                                             q_c, d, rd, code, stream), "ow_bwd_channel")
+            n_part = lib.ow_bwd_channel_partials(slots, q_c)
+            partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
+            dxt = torch.empty_like(xt)
+            _native.check(lib.ow_bwd_channel2(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                              dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
+                                              dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
+                                              stream), "ow_bwd_channel2")
+            g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
+            g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
+            d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
+            d_bv = _slot_reduce(pv, dv)
+            d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
+            del wpk, z, du, dv, pu, pv, dw, xt, dyt
         else:
             # Folded weights in the compute dtype, plain and transposed (both contiguous).
             bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
@@ -201,37 +234,18 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                               bv.data_ptr(), bv_t.data_ptr(), bo.data_ptr(), bo_t.data_ptr(), stream),
                           "ow_fold_weights")
             au_t, av_t, ao_t = (a.t().contiguous() for a in (au, av, ao))
-            if d == 128 and dtype != torch.float32:
-                # One kernel: token side P_u, P_v, dW', then U', V', dZ per 32-row chunk and the
-                # gate backward (Z, dU', dV').
-                nbytes = lib.ow_bwd_packed_bytes(q_c, d, rd)
-                wpk = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-                _native.check(lib.ow_pack_bwd_weights(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
-                                                      nw.data_ptr() if nw is not None else None, gm.data_ptr(),
-                                                      ch.data_ptr(), plan.channels, q_c, d, rd, code, wpk.data_ptr(),
-                                                      stream), "ow_pack_bwd_weights")
-                pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
-                pv, dw = torch.empty_like(pu), torch.empty_like(pu)
-                z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
-                du, dv = torch.empty_like(z), torch.empty_like(z)
-                _native.check(lib.ow_bwd_channel(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
-                                                 ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
-                                                 dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(), slots,
-                                                 q_c, d, rd, code, stream), "ow_bwd_channel")
-                del wpk
-            else:
-                # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
-                pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
-                pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
-                dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
-                # Channel side: batched GEMMs + the gate kernel.
-                u = torch.bmm(pu, bu)
-                v = torch.bmm(pv, bv)
-                dz = torch.bmm(dw, bo_t)
-                z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
-                _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(),
-                                              du.data_ptr(), dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
-                del u, v, dz
+            # Token side: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (per 16-slot tile).
+            pu = _tile_mix(lib, xt, au, None, None, d, code, stream)
+            pv = _tile_mix(lib, xt, av, None, None, d, code, stream)
+            dw = _tile_mix(lib, dyt, ao_t, None, None, d, code, stream)
+            # Channel side: batched GEMMs + the gate kernel.
+            u = torch.bmm(pu, bu)
+            v = torch.bmm(pv, bv)
+            dz = torch.bmm(dw, bo_t)
+            z, du, dv = torch.empty_like(u), torch.empty_like(u), torch.empty_like(u)
+            _native.check(lib.ow_bwd_gate(u.data_ptr(), v.data_ptr(), dz.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                          dv.data_ptr(), u.numel(), code, stream), "ow_bwd_gate")
+            del u, v, dz
             wp = torch.bmm(z, bo)
             dpu = torch.bmm(du, bu_t)
             dpv = torch.bmm(dv, bv_t)

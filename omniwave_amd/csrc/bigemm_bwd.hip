@@ -1143,14 +1143,271 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
   }
 }
 
+// ---- Channel side of the backward, d = 128, second part --------------------------------------
+// Same units as bwd_chan_d128_kernel.  Per 32-slot pair (one per wave):
+//   * pass 1 over the chunks of the expanded dimension: dP_u^T... as accumulators DPu[mb] +=
+//     dU' B_u''^T, DPv[mb] += dV' B_v''^T (lane = channel 32 mb + l32, register i = slot
+//     kord(i, hh)), the pair's dU', dV' chunk rows copied to the wave's LDS region and the
+//     chunk's B-operand fragments shared by the eight waves (three LDS buffers);
+//   * dX'^T = dP_u^T A_u + dP_v^T A_v with the operands swapped (lane = slot, registers =
+//     channels), stored as 8-byte row pieces;
+//   * dA_u += dP_u X'^T, dA_v += dP_v X'^T per 16-slot tile on 16x16x16 MFMAs over the channels:
+//     dP rows by transposed LDS reads of dP staged channel-major, X' rows from memory;
+//   * pass 2: W'[mb] += Z B_o'' from the Z chunk rows, then dA_o += dY W'^T the same way.
+// The token-matrix gradients leave as per-workgroup fp32 partials (waves added in a fixed order).
+struct BwdChan2Args {
+  const uint16_t* xt;   // [q_c][slots][128]
+  const uint16_t* dyt;
+  const uint16_t* z;    // [q_c][slots][rd]
+  const uint16_t* du;
+  const uint16_t* dv;
+  const float* a_u;     // [16][16] fp32
+  const float* a_v;
+  const uint16_t* packed;  // ow_pack_bwd_weights, d = 128
+  uint16_t* dxt;           // [q_c][slots][128]
+  float* partial;          // [gridDim][3][256]
+  int64_t slots;
+  int32_t q_c;
+};
+
+constexpr int kB2FrB = 16;  // B-operand fragments of pass 1 per chunk (B_u''^T, B_v''^T)
+
+struct BwdChan2Lds {
+  uint16_t r[kB2Waves][32 * kB2D];      // per wave: operand chunk rows, then staged dP / W' (8 KB)
+  uint16_t w[3][kB2FrB * kFragElems];   // chunk buffers
+  u32x4 tok[2][64];                     // A_u^T, A_v^T token-operand rows
+  float red[kB2Waves][3][256];          // per-wave dA sums
+};
+
+template <class Ty, int RD>
+__global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int32_t n_units) {
+  constexpr int NCH = RD / 32;
+  constexpr int MB = kB2D / 32;                            // 4 output blocks of 32 channels
+  constexpr int PACK_CH = bwd_frags(kB2D) * kFragElems;   // packed chunk stride
+  constexpr int OFF_BO = kB2FrA * kFragElems;              // B_o'' B operand within a packed chunk
+  constexpr int OFF_BU = OFF_BO + 2 * MB * kFragElems;     // B_u''^T B operand (B_v''^T follows)
+  __shared__ __attribute__((aligned(16))) BwdChan2Lds sh;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, h4 = lane >> 4;
+  const bool g0 = (lane & 16) == 0;
+  const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
+  const int64_t rows = a.slots * a.q_c;
+  const uint32_t tbytes = static_cast<uint32_t>(rows * kB2D * 2), ebytes = static_cast<uint32_t>(rows * RD * 2);
+  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(a.xt, tbytes), rdy = buffer_rsrc(a.dyt, tbytes),
+                               rdx = buffer_rsrc(a.dxt, tbytes);
+  const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(a.z, ebytes), rdu = buffer_rsrc(a.du, ebytes),
+                               rdv = buffer_rsrc(a.dv, ebytes);
+  if (wave == 0) {
+    sh.tok[0][lane] = token_frag<Ty, true>(a.a_u, lane);
+    sh.tok[1][lane] = token_frag<Ty, true>(a.a_v, lane);
+  }
+  const uint32_t rlds = lds_addr(sh.r[wave]);
+  f32x4 dA[3] = {};
+
+  for (int32_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int q = u % a.q_c;
+    const int64_t slot0 = static_cast<int64_t>(u / a.q_c) * kB2Rows + 32 * wave;
+    const int64_t row0 = static_cast<int64_t>(q) * a.slots + slot0;
+    const uint16_t* pk = a.packed + static_cast<size_t>(q) * NCH * PACK_CH;
+    // Chunk rows of one [slots][RD] tensor (32 slots x 32 values, 2 KB) into the wave's region
+    // at byte offset `at`: two copies, lane -> slot 16 c + lane / 4, 16 bytes at value 8 (lane % 4).
+    auto copy_rows = [&](__amdgpu_buffer_rsrc_t r, int ec, uint32_t at) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int sl = 16 * c + (lane >> 2);
+        const uint32_t voff =
+            slot0 + sl < a.slots ? static_cast<uint32_t>((row0 + sl) * RD + 32 * ec + 8 * (lane & 3)) * 2u : kOffOut;
+        tile_copy(r, voff, rlds + at + 1024u * c);
+      }
+    };
+    // K-step operand s of a staged chunk (lane (slot l32, hh): values 16 s + 4 hh + 0..3 and + 8).
+    auto row_op = [&](uint32_t at, int s2) {
+      const uint16_t* base = sh.r[wave] + at / 2 + l32 * 32 + 16 * s2 + 4 * hh;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(base), hi = *reinterpret_cast<const u32x2*>(base + 8);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    auto copy_w = [&](int ec, int off, int nfr) {  // nfr / 8 fragments per wave
+      const uint16_t* src = uniform_ptr(pk + static_cast<size_t>(ec) * PACK_CH + off);
+      uint16_t* dst = sh.w[ec % 3];
+      for (int i = 0; i < nfr / kB2Waves; ++i) {
+        const int f = wave + i * kB2Waves;
+        copy_frag_to_lds(src + f * kFragElems, dst + f * kFragElems, lane16);
+      }
+    };
+    // Stage an accumulator set (lane = channel 32 mb + l32, register 4b + k = slot 8b + 4hh + k)
+    // channel-major: region [128 channels][32 slots], bf16.
+    auto stage = [&](const f32x16 (&m)[MB]) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          *reinterpret_cast<u32x2*>(&sh.r[wave][(32 * mb + l32) * 32 + 8 * b + 4 * hh]) =
+              u32x2{Ty::pack2(m[mb][4 * b], m[mb][4 * b + 1]), Ty::pack2(m[mb][4 * b + 2], m[mb][4 * b + 3])};
+      wave_lds_sync();
+    };
+    // Rows 16 g + l16, channels 16 ks + 4 h4 .. + 3 of the staged set, by transposed reads (the
+    // 16x16x16 operand: lane (t = l16, h4)).
+    auto staged_op = [&](int g, int ks) {
+      const uint32_t addr = rlds + 2u * static_cast<uint32_t>((16 * ks + 4 * h4 + (l16 >> 2)) * 32 + 16 * g + 4 * (l16 & 3));
+      return lds_read_tr16(addr);
+    };
+    // Rows 16 g + l16 of a [slots][128] tensor, channels 16 ks + 4 h4 .. + 3 (zero past the slots).
+    auto mem_op = [&](__amdgpu_buffer_rsrc_t r, int g, int ks) {
+      const int sl = 16 * g + l16;
+      const uint32_t o =
+          slot0 + sl < a.slots ? static_cast<uint32_t>((row0 + sl) * kB2D + 16 * ks + 4 * h4) * 2u : kOffOut;
+      return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+    };
+
+    __syncthreads();  // the previous unit is done with every buffer; tok is written
+    // Pass 1.  Step ec: [wait: chunk ec's rows and fragments] [barrier] [rows of ec + 1: 4]
+    // [fragments of ec + 2: 2] [products].  Only the fragments of the next step may be in flight.
+    copy_rows(rdu, 0, 0);
+    copy_rows(rdv, 0, 2048);
+    copy_w(0, OFF_BU, kB2FrB);
+    copy_w(1, OFF_BU, kB2FrB);
+    f32x16 DPu[MB], DPv[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      DPu[mb] = f32x16{};
+      DPv[mb] = f32x16{};
+    }
+#pragma unroll 1
+    for (int ec = 0; ec < NCH; ++ec) {
+      if (ec + 1 < NCH)
+        wait_vmcnt<2>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      const uint32_t cur = 4096u * (ec & 1), nxt = 4096u * ((ec + 1) & 1);
+      if (ec + 1 < NCH) {
+        copy_rows(rdu, ec + 1, nxt);
+        copy_rows(rdv, ec + 1, nxt + 2048);
+      }
+      if (ec + 2 < NCH) copy_w(ec + 2, OFF_BU, kB2FrB);
+      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const u32x4 opu = row_op(cur, s2), opv = row_op(cur + 2048, s2);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          DPu[mb] = Ty::mma32(opu, cf[(2 * mb + s2) * (kFragElems / 8) + lane], DPu[mb]);
+          DPv[mb] = Ty::mma32(opv, cf[(2 * MB + 2 * mb + s2) * (kFragElems / 8) + lane], DPv[mb]);
+        }
+      }
+    }
+    mfma_drain();
+
+    // dX'^T = dP_u^T A_u + dP_v^T A_v: lane = slot l32, registers 4b .. 4b + 3 = channels 32 mb +
+    // 8 b + 4 hh .. + 3.
+    {
+      const u32x4 tu = sh.tok[0][lane], tv = sh.tok[1][lane];
+      const u32x4 tu0 = keep_if(g0, tu), tu1 = keep_if(!g0, tu);
+      const u32x4 tv0 = keep_if(g0, tv), tv1 = keep_if(!g0, tv);
+      const bool ok = slot0 + l32 < a.slots;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        f32x16 dx = Ty::mma32(pack_kstep<Ty>(DPu[mb], 0), tu0, f32x16{});
+        dx = Ty::mma32(pack_kstep<Ty>(DPu[mb], 1), tu1, dx);
+        dx = Ty::mma32(pack_kstep<Ty>(DPv[mb], 0), tv0, dx);
+        dx = Ty::mma32(pack_kstep<Ty>(DPv[mb], 1), tv1, dx);
+        mfma_drain();
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t o = ok ? static_cast<uint32_t>((row0 + l32) * kB2D + 32 * mb + 8 * b + 4 * hh) * 2u : kOffOut;
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{Ty::pack2(dx[4 * b], dx[4 * b + 1]), Ty::pack2(dx[4 * b + 2], dx[4 * b + 3])},
+                                                rdx, o, 0, 0);
+        }
+      }
+    }
+    // dA_u, dA_v.
+    stage(DPu);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) dA[0] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks), dA[0]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage(DPv);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) dA[1] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks), dA[1]);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // nothing in flight before pass 2's copies
+
+    // Pass 2: W'[mb] += Z B_o''; [wait] [barrier] [Z rows of ec + 1: 2] [fragments of ec + 2: 1].
+    __syncthreads();  // every wave is done with pass 1's chunk buffers
+    copy_rows(rz, 0, 0);
+    copy_w(0, OFF_BO, 2 * MB);
+    copy_w(1, OFF_BO, 2 * MB);
+    f32x16 W[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) W[mb] = f32x16{};
+#pragma unroll 1
+    for (int ec = 0; ec < NCH; ++ec) {
+      if (ec + 1 < NCH)
+        wait_vmcnt<1>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      const uint32_t cur = 2048u * (ec & 1), nxt = 2048u * ((ec + 1) & 1);
+      if (ec + 1 < NCH) copy_rows(rz, ec + 1, nxt);
+      if (ec + 2 < NCH) copy_w(ec + 2, OFF_BO, 2 * MB);
+      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const u32x4 opz = row_op(cur, s2);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) W[mb] = Ty::mma32(opz, cf[(2 * mb + s2) * (kFragElems / 8) + lane], W[mb]);
+      }
+    }
+    mfma_drain();
+    // dA_o = dY W'^T: A = dY rows from memory, B = staged W' rows.
+    stage(W);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) dA[2] = Ty::mma16(mem_op(rdy, g, ks), staged_op(g, ks), dA[2]);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  }
+
+  // The workgroup's dA sums, waves added in order.
+  mfma_drain();
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sh.red[wave][m][(4 * h4 + i) * 16 + l16] = dA[m][i];
+  __syncthreads();
+  for (int e = threadIdx.x; e < 3 * 256; e += 512) {
+    const int m = e >> 8, k = e & 255;
+    float v = 0.0f;
+    for (int w = 0; w < kB2Waves; ++w) v += sh.red[w][m][k];
+    a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = v;
+  }
+}
+
+template <int RD>
+int launch_bwd_chan2_rd(const BwdChan2Args& a, int64_t grid, int32_t n_units, int32_t dtype, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD>), g, dim3(512), 0, s, a, n_units);
+  else
+    hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD>), g, dim3(512), 0, s, a, n_units);
+  return hip_status(hipGetLastError(), "bwd_chan2_d128_kernel launch");
+}
+
+// Workgroups of the d = 128 backward kernels for `units` units: one per CU (a multiple of 8
+// with more units than CUs), one per unit otherwise.
+int64_t bwd_chan_grid(int64_t units) {
+  int64_t grid = device_cus();
+  if (grid >= units) return units;
+  if (grid >= 8) grid -= grid % 8;
+  return grid;
+}
+
 template <int RD>
 int launch_bwd_chan_rd(const BwdChanArgs& a, int32_t n_units, int32_t dtype, hipStream_t s) {
-  int64_t grid = device_cus();
-  if (grid >= n_units)
-    grid = n_units;
-  else if (grid >= 8)
-    grid -= grid % 8;
-  const dim3 g(static_cast<unsigned>(grid));
+  const dim3 g(static_cast<unsigned>(bwd_chan_grid(n_units)));
   if (dtype == OW_DTYPE_BF16)
     hipLaunchKernelGGL((bwd_chan_d128_kernel<BF16, RD>), g, dim3(512), 0, s, a, n_units);
   else
@@ -1596,6 +1853,43 @@ int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const floa
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rc = rd == 256 ? ow::launch_bwd_chan_rd<256>(a, static_cast<int32_t>(units), dtype, s)
                            : ow::launch_bwd_chan_rd<128>(a, static_cast<int32_t>(units), dtype, s);
+  if (rc == OW_OK) ow::clear_error();
+  return rc;
+}
+
+int64_t ow_bwd_channel_partials(int64_t slots, int32_t q_c) {
+  if (q_c < 1 || slots <= 0 || slots % 16) return 0;
+  return ow::bwd_chan_grid(static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows));
+}
+
+int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* du, const void* dv, const float* a_u,
+                    const float* a_v, const void* packed, size_t packed_bytes, void* dxt, float* partial,
+                    int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+  OW_CHECK_SUPPORTED(d == ow::kB2D && (rd == 128 || rd == 256), "backward channel kernel needs d = 128, rd in {128, 256}");
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 16 == 0, "bad shape q_c=%d slots=%lld (multiple of 16)", q_c,
+               (long long)slots);
+  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
+               packed_bytes);
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  const int64_t grid = ow_bwd_channel_partials(slots, q_c);
+  OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_channel_partials)",
+               (long long)n_partial, (long long)grid);
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31), "tiles of %lld slots exceed 2 GiB",
+               (long long)slots);
+  OW_CHECK_ARG(xt && dyt && z && du && dv && a_u && a_v && dxt && partial, "tensor pointer is NULL");
+  for (const void* p : {xt, dyt, z, du, dv, packed, static_cast<const void*>(dxt)})
+    OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  const ow::BwdChan2Args a{cu(xt), cu(dyt), cu(z), cu(du), cu(dv), a_u, a_v, cu(packed), static_cast<uint16_t*>(dxt),
+                           partial, slots, q_c};
+  const int64_t units = static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rc = rd == 256 ? ow::launch_bwd_chan2_rd<256>(a, grid, static_cast<int32_t>(units), dtype, s)
+                           : ow::launch_bwd_chan2_rd<128>(a, grid, static_cast<int32_t>(units), dtype, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
 }
