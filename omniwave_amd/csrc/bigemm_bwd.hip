@@ -692,26 +692,50 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     // Token side, X' first, then dY, through the wave's tile [32][kLd] in the second weight
     // buffer.
     uint16_t* tx = wb[1] + wave * 32 * kLd;
+    // Routed rows through buffer loads (pads and rows past the end read as zero): every load of
+    // a tile is issued before any is waited on.
+    const uint32_t nbytes_rows = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
+    const __amdgpu_buffer_rsrc_t rrs =
+        buffer_rsrc(a.rscale, a.rscale ? static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * 4) : 0u);
+    auto row_off = [&](int64_t nr, int64_t c) {
+      return nr >= 0 ? static_cast<uint32_t>((nr * a.channels + cbase + c) * 2) : kOffOut;
+    };
+    auto row_scale = [&](int64_t nr) {
+      return __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rrs, nr >= 0 ? static_cast<uint32_t>(nr * 4) : kOffOut, 0, 0));
+    };
     auto stage_tile = [&](const uint16_t* src, bool scale) {
+      if constexpr (RT) {
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(src, nbytes_rows);
+        uint32_t voff[4], soff[4];
+        u32x4 val[4];
+        float rs[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-        u32x4 val;
-        if constexpr (RT) {
-          val = u32x4{0u, 0u, 0u, 0u};
-          const int64_t nr = nhwc_row(r);
-          if (nr >= 0) {
-            val = *reinterpret_cast<const u32x4*>(src + nr * a.channels + cbase + c8);
-            if (scale && a.rscale) {
-              const float rs = a.rscale[nr];
-#pragma unroll
-              for (int w = 0; w < 4; ++w) val[w] = scale2<Ty>(val[w], rs);
-            }
-          }
-        } else {
-          val = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+        for (int k = 0; k < 4; ++k) {
+          const int64_t nr = nhwc_row((lane + 64 * k) >> 3);
+          voff[k] = row_off(nr, ((lane + 64 * k) & 7) * 8);
+          soff[k] = nr >= 0 ? static_cast<uint32_t>(nr * 4) : kOffOut;
         }
-        *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = val;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          val[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[k], 0, 0);
+          rs[k] = (scale && a.rscale) ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrs, soff[k], 0, 0)) : 1.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+          if (scale && a.rscale) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) val[k][w] = scale2<Ty>(val[k][w], rs[k]);
+          }
+          *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = val[k];
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+          *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+        }
       }
       wave_lds_sync();
     };
@@ -842,7 +866,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     for (int g = 0; g < 2; ++g) {
       if constexpr (RT) {
         orow[g] = nhwc_row(16 * g + l16);
-        oscale[g] = (orow[g] >= 0 && a.rscale) ? a.rscale[orow[g]] : 1.0f;
+        oscale[g] = a.rscale ? row_scale(orow[g]) : 1.0f;
       } else {
         orow[g] = slot0 + 16 * g + l16;
         oscale[g] = 1.0f;
@@ -850,11 +874,9 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     }
     auto other_rows = [&](const uint16_t* tiles, const uint16_t* rows, bool scale, int g, int ks) -> u32x2 {
       if constexpr (RT) {
-        u32x2 v = {0u, 0u};
-        if (orow[g] >= 0) {
-          v = *reinterpret_cast<const u32x2*>(rows + orow[g] * a.channels + cbase + 16 * ks + 4 * h4);
-          if (scale && a.rscale) v = u32x2{scale2<Ty>(v[0], oscale[g]), scale2<Ty>(v[1], oscale[g])};
-        }
+        u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                buffer_rsrc(rows, nbytes_rows), row_off(orow[g], 16 * ks + 4 * h4), 0, 0));
+        if (scale && a.rscale) v = u32x2{scale2<Ty>(v[0], oscale[g]), scale2<Ty>(v[1], oscale[g])};
         return v;
       } else {
         return *reinterpret_cast<const u32x2*>(tiles + orow[g] * kBwdD + 16 * ks + 4 * h4);
@@ -1908,6 +1930,8 @@ int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, cons
   OW_CHECK_SUPPORTED(c == q_c * ow::kBwdD && (plan->radix_level == 0 || q_c == 1),
                      "routed backward needs the identity channel order with C = q_c * 64");
   OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 31), "bad batch %d", batch);
+  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * c * 2 < (int64_t(1) << 31),
+               "x and dy must be below 2 GiB (buffer addressing)");
   OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, d, rd), "packed backward weights hold %zu bytes",
                packed_bytes);
   const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
