@@ -778,7 +778,14 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     // Channel side.
     f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
     for (int ec = 0; ec < NCH; ++ec) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // Chunk ec's copies: chunk 0 landed before the tile loads the compiler waited on; chunk
+      // ec >= 1 was issued at step ec - 1, and only that step's 12 stores (live waves) follow it.
+      if (ec > 0) {
+        if (live)
+          wait_vmcnt<12>();
+        else
+          wait_vmcnt<0>();
+      }
       __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1 (ec = 0: its tiles)
       if (ec + 1 < NCH) issue(ec + 1);
       const u32x4* cf = reinterpret_cast<const u32x4*>(wb[ec & 1]);
@@ -882,44 +889,59 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
         return *reinterpret_cast<const u32x2*>(tiles + orow[g] * kBwdD + 16 * ks + 4 * h4);
       }
     };
-    auto outer = [&](f32x4& acc) {
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int ks = 0; ks < kBwdKS; ++ks) {
-          const u32x2 av = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
-          acc = Ty::mma16(av, other_rows(a.xt, a.x, true, g, ks), acc);
-        }
-      wave_lds_sync();
+    auto staged_row = [&](int g, int ks) {
+      return *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
     };
     f32x4 dA[3] = {};
     if (live) {
+      // X' rows read once (all loads before the products) for both dA_u and dA_v.
+      u32x2 xo[2][kBwdKS];
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) xo[g][ks] = other_rows(a.xt, a.x, true, g, ks);
       put(DPu);
-      outer(dA[0]);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) dA[0] = Ty::mma16(staged_row(g, ks), xo[g][ks], dA[0]);
+      wave_lds_sync();
       put(DPv);
-      outer(dA[1]);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) dA[1] = Ty::mma16(staged_row(g, ks), xo[g][ks], dA[1]);
+      wave_lds_sync();
     }
     // dA_o = dY W'^T: A operand from dY rows, B from the staged W' rows.
     if (live) {
+      u32x2 yo[2][kBwdKS];
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) yo[g][ks] = other_rows(a.dyt, a.dy, false, g, ks);
       put(W);
 #pragma unroll
       for (int g = 0; g < 2; ++g)
 #pragma unroll
-        for (int ks = 0; ks < kBwdKS; ++ks) {
-          const u32x2 bv = *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
-          dA[2] = Ty::mma16(other_rows(a.dyt, a.dy, false, g, ks), bv, dA[2]);
-        }
+        for (int ks = 0; ks < kBwdKS; ++ks) dA[2] = Ty::mma16(yo[g][ks], staged_row(g, ks), dA[2]);
       wave_lds_sync();
       put(DX);
+      if constexpr (RT) {
+        uint32_t goff[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stage + r * kLd + c8);
-        if constexpr (RT) {
-          const int64_t nr = nhwc_row(r);
-          if (nr >= 0) *reinterpret_cast<u32x4*>(a.g + nr * a.channels + cbase + c8) = val;
-        } else {
-          *reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8) = val;
+        for (int k = 0; k < 4; ++k) goff[k] = row_off(nhwc_row((lane + 64 * k) >> 3), ((lane + 64 * k) & 7) * 8);
+        const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.g, nbytes_rows);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+          __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(stage + r * kLd + c8), rg, goff[k], 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+          *reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8) = *reinterpret_cast<const u32x4*>(stage + r * kLd + c8);
         }
       }
     }
