@@ -575,6 +575,7 @@ __device__ __forceinline__ void bwd_copy_frag(const uint16_t* src, uint16_t* dst
 // At the end the four waves' dA sums are added in a fixed order and the workgroup writes
 // partial[blockIdx][3][256] (dA_u, dA_v, dA_o, element 16 t + k).
 constexpr int64_t kBwdFusedGrid = 1024;  // at most 2 workgroups per CU x 2 rounds in flight
+constexpr int kZSt = 40;                 // row stride (elements) of the staged chunk outputs
 
 struct BwdFusedArgs {
   const uint16_t* xt;   // [q_c][slots][64] X' tiles
@@ -638,6 +639,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t wb[2][CH_ELEMS];
   __shared__ __attribute__((aligned(16))) u32x4 tok[5][64];  // A_u, A_v, A_o^T, A_u^T, A_v^T operand rows
   __shared__ float red[4][3][256];
+  __shared__ __attribute__((aligned(16))) uint16_t zst[4][32 * kZSt];  // per wave: one chunk output, staged
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, h4 = lane >> 4;
   const bool g0 = (lane & 16) == 0;
@@ -779,10 +781,10 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
     for (int ec = 0; ec < NCH; ++ec) {
       // Chunk ec's copies: chunk 0 landed before the tile loads the compiler waited on; chunk
-      // ec >= 1 was issued at step ec - 1, and only that step's 12 stores (live waves) follow it.
+      // ec >= 1 was issued at step ec - 1, and only that step's 6 stores (live waves) follow it.
       if (ec > 0) {
         if (live)
-          wait_vmcnt<12>();
+          wait_vmcnt<6>();
         else
           wait_vmcnt<0>();
       }
@@ -815,14 +817,26 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
         dvs[s] = pack_kstep<Ty>(DV, s);
       }
       if (live) {
-        // registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32
-        const int64_t base = row * RD + 32 * ec + 4 * hh;
+        // Registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32: each
+        // tensor staged [32 slots][32 rows] in the wave's buffer, then stored as 64-byte row
+        // pieces (four lanes per slot), 6 stores per chunk.
+        uint16_t* zw = zst[wave];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int s = b >> 1, w = 2 * (b & 1);
-          *reinterpret_cast<u32x2*>(a.z + base + 8 * b) = u32x2{zs[s][w], zs[s][w + 1]};
-          *reinterpret_cast<u32x2*>(a.du + base + 8 * b) = u32x2{dus[s][w], dus[s][w + 1]};
-          *reinterpret_cast<u32x2*>(a.dv + base + 8 * b) = u32x2{dvs[s][w], dvs[s][w + 1]};
+        for (int t = 0; t < 3; ++t) {
+          const u32x4(&pk)[2] = t == 0 ? zs : t == 1 ? dus : dvs;
+          uint16_t* dst = t == 0 ? a.z : t == 1 ? a.du : a.dv;
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            *reinterpret_cast<u32x2*>(&zw[l32 * kZSt + 8 * b + 4 * hh]) =
+                u32x2{pk[b >> 1][2 * (b & 1)], pk[b >> 1][2 * (b & 1) + 1]};
+          wave_lds_sync();
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int sl = 16 * h + (lane >> 2), part = lane & 3;
+            *reinterpret_cast<u32x4*>(dst + (slot0 + sl) * RD + 32 * ec + 8 * part) =
+                *reinterpret_cast<const u32x4*>(&zw[sl * kZSt + 8 * part]);
+          }
+          wave_lds_sync();  // the reads are done before the next tensor is staged
         }
       }
 #pragma unroll
