@@ -765,15 +765,27 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     const f32x16 zero = {};
     const int64_t row = slot0 + l32;  // this lane's slot
     if (live) {
+      // P_u, P_v, dW' through the wave's tile (read completely by the token side; no copy targets
+      // it before the chunk loop's first barrier): lane = slot l32, K-step ks slot j -> channel
+      // 16 ks + kord(j, hh); stored as 128-byte rows, eight lanes per slot.
+      wave_lds_sync();
 #pragma unroll
-      for (int ks = 0; ks < kBwdKS; ++ks) {  // lane = slot l32, slot j -> channel 16 ks + kord(j, hh)
-        const int64_t o = row * kBwdD + 16 * ks + 4 * hh;
-        *reinterpret_cast<u32x2*>(a.pu + o) = u32x2{Pu[ks][0], Pu[ks][1]};
-        *reinterpret_cast<u32x2*>(a.pu + o + 8) = u32x2{Pu[ks][2], Pu[ks][3]};
-        *reinterpret_cast<u32x2*>(a.pv + o) = u32x2{Pv[ks][0], Pv[ks][1]};
-        *reinterpret_cast<u32x2*>(a.pv + o + 8) = u32x2{Pv[ks][2], Pv[ks][3]};
-        *reinterpret_cast<u32x2*>(a.dw + o) = u32x2{Dw[ks][0], Dw[ks][1]};
-        *reinterpret_cast<u32x2*>(a.dw + o + 8) = u32x2{Dw[ks][2], Dw[ks][3]};
+      for (int t = 0; t < 3; ++t) {
+        const u32x4(&pk)[kBwdKS] = t == 0 ? Pu : t == 1 ? Pv : Dw;
+        uint16_t* dst = t == 0 ? a.pu : t == 1 ? a.pv : a.dw;
+#pragma unroll
+        for (int ks = 0; ks < kBwdKS; ++ks) {
+          *reinterpret_cast<u32x2*>(&tx[l32 * kLd + 16 * ks + 4 * hh]) = u32x2{pk[ks][0], pk[ks][1]};
+          *reinterpret_cast<u32x2*>(&tx[l32 * kLd + 16 * ks + 8 + 4 * hh]) = u32x2{pk[ks][2], pk[ks][3]};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int sl = 8 * k + (lane >> 3), part = lane & 7;
+          *reinterpret_cast<u32x4*>(dst + (slot0 + sl) * kBwdD + 8 * part) =
+              *reinterpret_cast<const u32x4*>(&tx[sl * kLd + 8 * part]);
+        }
+        wave_lds_sync();
       }
     }
 
