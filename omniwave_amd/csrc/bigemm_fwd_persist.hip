@@ -435,58 +435,90 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // Step ec waits for chunk ec + 1 (issued at step ec - 1, or before the loop for ec <= 1: at
     // ec = 0 chunk 2, issued after it, may still be in flight); the barrier also means every
     // wave is done with chunk ec - 1, whose buffer takes chunk ec + 2.
-    // fp8: chunk ec + 1's U' (bf16 / f16) and V' (K = 64 e4m3) products, then chunk ec's gate and
-    // W += Z B_o (V''s dequantisation: f8_gate).
+    // fp8: chunk ec + 1's U' (bf16 / f16) and V' (K = 64 e4m3) products, chunk ec's gate (V''s
+    // dequantisation: f8_gate) and W += Z B_o, in stream8.
     const float deq8 = F8 ? f8_deq(a.packed) : 1.0f;
-    auto uv8 = [&](int ec, f32x16& U, f32x16& V) {
-      U = f32x16{};
-      V = f32x16{};
-      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
-      const u32x8* c8 = reinterpret_cast<const u32x8*>(sh.w[ec % 3] + F8_BV * kFragElems);
-#pragma unroll
-      for (int ks = 0; ks < kKS; ++ks) U = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], U);
-#pragma unroll
-      for (int q = 0; q < KV; ++q) {
-        if constexpr (F8) V = mma32x64_f8(c8[q * (kF8K64Bytes / 32) + lane], Pv[q], V);
-      }
-    };
-    auto gate_w8 = [&](int ec, const f32x16& U, const f32x16& V) {
-      const u32x4* co = reinterpret_cast<const u32x4*>(sh.w[ec % 3] + F8_BO * kFragElems);
+    // fp8 step as `stream`: the fragments read DEPTH8 ahead with untracked LDS reads in issue
+    // order -- chunk en's 8 U' fragments, its 2 V' K = 64 fragments (two 16-byte halves each,
+    // 32 bytes per lane), then chunk ec's 8 B_o fragments -- with two of chunk ec's gate values
+    // after each U' product.  A V' fragment's halves are refilled together once both are used.
+    constexpr int DEPTH8 = 4;
+    auto stream8 = [&](auto hu_tag, auto ho_tag, int en, int ec, f32x16& Un, f32x16& Vn, const f32x16& Uc,
+                       const f32x16& Vc) {
+      constexpr bool HU = decltype(hu_tag)::value;  // chunk en's U' / V' products
+      constexpr bool HO = decltype(ho_tag)::value;  // chunk ec's gate and W += Z B_o
+      constexpr int NUR = HU ? kKS + 2 * KV : 0;    // reads of chunk en (8 U', 4 V' halves)
+      constexpr int NF = NUR + (HO ? kFrO : 0);
+      const uint32_t bu = HU ? lds_addr(sh.w[en % 3]) + lane16 : 0u;
+      const uint32_t bv = HU ? lds_addr(sh.w[en % 3] + F8_BV * kFragElems) + 32u * static_cast<uint32_t>(lane) : 0u;
+      const uint32_t bo = HO ? lds_addr(sh.w[ec % 3] + F8_BO * kFragElems) + lane16 : 0u;
+      auto read = [&](auto ic) -> u32x4 {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i < kKS && HU)
+          return lds_read_async<i * kFragElems * 2>(bu);
+        else if constexpr (i < NUR)
+          return lds_read_async<((i - kKS) / 2) * kF8K64Bytes + 16 * ((i - kKS) % 2)>(bv);
+        else
+          return lds_read_async<(i - NUR) * kFragElems * 2>(bo);
+      };
+      u32x4 fr[DEPTH8];
+      static_for<0, DEPTH8>([&](auto ic) {
+        if constexpr (decltype(ic)::value < NF) fr[decltype(ic)::value] = read(ic);
+      });
       u32x4 Z[2];
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          Z[s2][q] = Ty::pack2(f8_gate<Ty>(U[8 * s2 + 2 * q], V[8 * s2 + 2 * q], deq8),
-                               f8_gate<Ty>(U[8 * s2 + 2 * q + 1], V[8 * s2 + 2 * q + 1], deq8));
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], co[(2 * mb + s2) * (kFragElems / 8) + lane], W[mb]);
-    };
-    // fp8 step: chunk en's U' products with two of chunk ec's gate values after each, chunk en's
-    // V' products, then chunk ec's W += Z B_o.
-    auto step8 = [&](int en, int ec, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
-      Un = f32x16{};
-      Vn = f32x16{};
-      const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[en % 3]);
-      const u32x8* c8 = reinterpret_cast<const u32x8*>(sh.w[en % 3] + F8_BV * kFragElems);
-      const u32x4* co = reinterpret_cast<const u32x4*>(sh.w[ec % 3] + F8_BO * kFragElems);
-      u32x4 Z[2];
-#pragma unroll
-      for (int ks = 0; ks < kKS; ++ks) {
-        Un = Ty::mma32(cf[ks * (kFragElems / 8) + lane], Pu[ks], Un);
-        const int k = 2 * ks;
-        Z[k / 8][(k % 8) / 2] = Ty::pack2(f8_gate<Ty>(Uc[k], Vc[k], deq8), f8_gate<Ty>(Uc[k + 1], Vc[k + 1], deq8));
+      if constexpr (HU) {
+        Un = f32x16{};
+        Vn = f32x16{};
       }
+      if constexpr (HO && !HU) {
 #pragma unroll
-      for (int q = 0; q < KV; ++q) {
-        if constexpr (F8) Vn = mma32x64_f8(c8[q * (kF8K64Bytes / 32) + lane], Pv[q], Vn);
+        for (int k = 0; k < 16; k += 2)
+          Z[k / 8][(k % 8) / 2] = Ty::pack2(f8_gate<Ty>(Uc[k], Vc[k], deq8), f8_gate<Ty>(Uc[k + 1], Vc[k + 1], deq8));
       }
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) W[mb] = Ty::mma32(Z[s2], co[(2 * mb + s2) * (kFragElems / 8) + lane], W[mb]);
+      static_for<0, NF>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr bool FH = HU && i >= kKS && i < NUR && ((i - kKS) % 2) == 0;
+        constexpr bool SH = HU && i >= kKS && i < NUR && ((i - kKS) % 2) == 1;
+        // Reads issued after read i when iteration i waits: reads go out in index order, DEPTH8
+        // at the start and one per finished read after (two after a V' second half).
+        constexpr int younger = [] {
+          int n = DEPTH8;
+          for (int m = 0; m < i; ++m) {
+            const bool fh = HU && m >= kKS && m < NUR && ((m - kKS) % 2) == 0;
+            const bool sh2 = HU && m >= kKS && m < NUR && ((m - kKS) % 2) == 1;
+            n += fh ? 0 : (sh2 ? 2 : 1);
+          }
+          n = n < NF ? n : NF;
+          return n - 1 - i;
+        }();
+        constexpr int after = younger < 0 ? 0 : younger;
+        lds_wait<after>(fr[i % DEPTH8]);
+        if constexpr (HU && i < kKS) {
+          Un = Ty::mma32(fr[i % DEPTH8], Pu[i], Un);
+          if constexpr (HO) {
+            constexpr int k = 2 * i;
+            Z[k / 8][(k % 8) / 2] =
+                Ty::pack2(f8_gate<Ty>(Uc[k], Vc[k], deq8), f8_gate<Ty>(Uc[k + 1], Vc[k + 1], deq8));
+          }
+        } else if constexpr (SH) {
+          if constexpr (F8) {
+            const u32x4 lo = fr[(i - 1) % DEPTH8], hi = fr[i % DEPTH8];
+            const u32x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            Vn = mma32x64_f8(v8, Pv[(i - kKS) / 2], Vn);
+          }
+        } else if constexpr (i >= NUR) {
+          constexpr int j = i - NUR;
+          W[j / 2] = Ty::mma32(Z[j % 2], fr[i % DEPTH8], W[j / 2]);
+        }
+        // Refills: a read's slot takes the read DEPTH8 later once it is used (a V' first half
+        // together with its second half).
+        if constexpr (SH) {
+          if constexpr (i - 1 + DEPTH8 < NF) fr[(i - 1) % DEPTH8] = read(std::integral_constant<int, i - 1 + DEPTH8>{});
+          if constexpr (i + DEPTH8 < NF) fr[i % DEPTH8] = read(std::integral_constant<int, i + DEPTH8>{});
+        } else if constexpr (!FH) {
+          if constexpr (i + DEPTH8 < NF) fr[i % DEPTH8] = read(std::integral_constant<int, i + DEPTH8>{});
+        }
+      });
     };
     auto step = [&](int ec, f32x16& Uc, f32x16& Vc, f32x16& Un, f32x16& Vn) {
       const uint32_t bo = base(ec) + 2u * kFrU * kFragElems * 2u;
@@ -498,20 +530,20 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         __syncthreads();
         if (ec >= 1 && ec + 2 < kNCH) issue_chunk(u, ec + 2);
         if constexpr (F8) {
-          step8(ec + 1, ec, Un, Vn, Uc, Vc);
+          stream8(std::true_type{}, std::true_type{}, ec + 1, ec, Un, Vn, Uc, Vc);
         } else {
           stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
         }
       } else {
         if constexpr (F8)
-          gate_w8(ec, Uc, Vc);
+          stream8(std::false_type{}, std::true_type{}, ec, ec, Un, Vn, Uc, Vc);
         else
           stream(Zero{}, No{}, 0u, bo, Un, Vn, Uc, Vc);
       }
     };
     f32x16 Ua, Va, Ub = {}, Vb = {};
     if constexpr (F8)
-      uv8(0, Ua, Va);
+      stream8(std::true_type{}, std::false_type{}, 0, 0, Ua, Va, Ub, Vb);
     else
       stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
 #pragma unroll
