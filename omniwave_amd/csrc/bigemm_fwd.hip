@@ -1361,8 +1361,9 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.eps = eps;
     r.drop_scale = drop_scale;
     const int64_t x_elems = static_cast<int64_t>(batch) * n * c;
-    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems) ? ow::launch_fwd_wave(r, dtype, s)
-                                                                                   : ow::launch_fwd_resident(r, dtype, s);
+    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems)
+                       ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s)
+                       : ow::launch_fwd_resident(r, dtype, s);
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }

@@ -1,6 +1,6 @@
-// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4} and
-// contiguous channel groups (the 56x56x128 and 28x28x256 stages of OmniWeave-T), one (pair,
-// channel group) unit per wave at a time.
+// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4} (the
+// 56x56x128 and 28x28x256 stages of OmniWeave-T), one (pair, channel group) unit per wave at a
+// time.
 //
 // Same math and operand packing as the other forward kernels (reference
 // omniweave/ops/reference.py:147-171; operand scheme in ow_device.h).  Organisation:
@@ -15,11 +15,15 @@
 //     operand layout (lane = token, 8 channels per 16-byte piece), sums the squares with
 //     v_dot2_f32 and writes only its group's columns to its own LDS tile; the other group's
 //     wave reads the same rows, which its XCD's L2 serves;
-//   * rows come from the token table; group g is channels 64 g .. 64 g + 63, which is the
-//     plan's channel order at radix level 0 or with one group (omniweave/models/routing.py:
-//     107-121; the interleaved groups of the other plans take the resident kernel);
+//   * rows come from the token table; group g is channels 64 g .. 64 g + 63 at radix level 0 or
+//     with one group, else (SG, q_c = 2) the channels res + 2 t, t < 64, res = (g + level) mod 2
+//     (omniweave/models/routing.py:107-121): the wave's row pieces go through v_perm_b32 to
+//     its group's elements (strided_pack), in order, so the tile and the math are the same;
 //   * the residual round(x + round(delta)) is written into the tile, which the wave then stores
-//     as whole 16-byte row pieces.
+//     as whole 16-byte row pieces, or (SG) as one full row per 2-byte store instruction (the
+//     other group's wave, on the same XCD, fills the rest of each line in L2).  Those stores
+//     cost ~8 us at 56x56x128 x 128 images over 16-byte ones, and ~11 us at q_c = 4, where the
+//     resident kernel is faster: the interleaved q_c = 4 groups take that kernel.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -131,7 +135,7 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t ro
   for (int k = 0; k < 4; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * (k0 + k), 0, 0);
 }
 
-template <class Ty, int QC, bool OM, bool DROP>
+template <class Ty, int QC, bool OM, bool DROP, bool SG>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr int C = QC * kD;
@@ -141,6 +145,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   // being held whole (64 registers) for a unit.
   constexpr bool STREAM = QC == 4;
   constexpr int NX = STREAM ? 4 : NV;  // pieces carried from one unit to the next
+  static_assert(!SG || QC == 2, "interleaved channel groups: q_c = 2");
   __shared__ __attribute__((aligned(16))) WaveLds sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -150,6 +155,8 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   const int n_team = gridDim.x / QC;
   const int64_t stride = static_cast<int64_t>(n_team) * kWavesWg;
   const int64_t first = static_cast<int64_t>(team) * kWavesWg + wave;
+  // SG: the group's first channel (its residue mod q_c), wave-uniform.
+  const int res = SG ? __builtin_amdgcn_readfirstlane(a.chan[g * kD]) & (QC - 1) : 0;
 
   // The group's weights into LDS (1 KB per wave and copy), the token operands into registers.
   {
@@ -207,7 +214,11 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       acc += __shfl_xor(acc, 32);
     }
     // The group's columns into the tile; the row scale (0 for pad tokens) and output row.
-    if constexpr (STREAM || QC == 1) {
+    if constexpr (SG) {
+      // piece 2 k + hh of the row holds group columns 8 k + 4 hh .. 8 k + 4 hh + 3.
+#pragma unroll
+      for (int k = 0; k < NV; ++k) *reinterpret_cast<u32x2*>(&tile[l32 * kLdt + 8 * k + 4 * hh]) = strided_pack<4>(xc[k], res);
+    } else if constexpr (STREAM || QC == 1) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
     } else {
@@ -358,7 +369,22 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     wave_lds_sync();
 
     // The tile's rows to memory: 32 rows x 8 pieces of the group's columns, 4 per lane; pad
-    // rows go past the buffer.
+    // rows go past the buffer.  SG: one row per instruction, lane l storing group column
+    // 2 (l % 32) + hh (channel res + q_c column) as a 2-byte element.
+    if constexpr (SG) {
+      const int32_t my_row = rows[l32];
+      const uint32_t voff = 2u * static_cast<uint32_t>(res + QC * (2 * l32 + hh));
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(&tile[r * kLdt + 2 * l32]);
+        const int32_t orow = __builtin_amdgcn_readlane(my_row, r);
+        const uint32_t rb = orow >= 0 ? static_cast<uint32_t>(orow) * static_cast<uint32_t>(C * 2) : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(hh ? w >> 16 : w), ro, voff, rb, 0);
+      }
+      wave_lds_sync();
+      out_c = out_n;
+      return;
+    }
     u32x4 ov[4];
     int32_t orow[4];
 #pragma unroll
@@ -404,7 +430,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   for (int64_t p = first; p < n_pairs; p += stride) unit(p, x, ssq, ent, out_c);
 }
 
-template <class Ty, int QC>
+template <class Ty, int QC, bool SG>
 int launch_qc(const ResidentArgs& a, hipStream_t stream) {
   // Two workgroups of four waves per CU (~67 KB of LDS each); whole teams of QC workgroups.
   const int32_t n_pairs = a.n_pairs;
@@ -416,20 +442,20 @@ int launch_qc(const ResidentArgs& a, hipStream_t stream) {
   const dim3 g(static_cast<unsigned>(grid)), b(256);
   if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   if (a.out_tok)
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false, SG>), g, b, 0, stream, a, n_pairs);
   else if (a.drop_scale)
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, true>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, true, SG>), g, b, 0, stream, a, n_pairs);
   else
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, false>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, false, SG>), g, b, 0, stream, a, n_pairs);
   return hip_status(hipGetLastError(), "bigemm_fwd_wave_kernel launch");
 }
 
 template <class Ty>
-int launch_ty(const ResidentArgs& a, hipStream_t stream) {
+int launch_ty(const ResidentArgs& a, bool strided, hipStream_t stream) {
   switch (a.q_c) {
-    case 1: return launch_qc<Ty, 1>(a, stream);
-    case 2: return launch_qc<Ty, 2>(a, stream);
-    case 4: return launch_qc<Ty, 4>(a, stream);
+    case 1: return launch_qc<Ty, 1, false>(a, stream);
+    case 2: return strided ? launch_qc<Ty, 2, true>(a, stream) : launch_qc<Ty, 2, false>(a, stream);
+    case 4: return launch_qc<Ty, 4, false>(a, stream);
     default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 2, 4} (got %d)", a.q_c);
   }
 }
@@ -438,13 +464,14 @@ int launch_ty(const ResidentArgs& a, hipStream_t stream) {
 
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems) {
   // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.
-  return d == kD && rd == kRD && (q_c == 1 || ((q_c == 2 || q_c == 4) && radix_level == 0)) && channels == q_c * kD &&
+  return d == kD && rd == kRD && (q_c == 1 || q_c == 2 || (q_c == 4 && radix_level == 0)) && channels == q_c * kD &&
          x_elems * 2 < (int64_t(1) << 31);
 }
 
-int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream) {
-  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, stream);
-  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, stream);
+int launch_fwd_wave(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream) {
+  const bool strided = radix_level != 0 && a.q_c > 1;  // routing.py:107-121
+  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, strided, stream);
+  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, strided, stream);
   return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
 }
 

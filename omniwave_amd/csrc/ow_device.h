@@ -769,9 +769,10 @@ bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_
                       int32_t batch);
 
 // One (pair, channel group) unit per wave, the group's weights in LDS (bigemm_fwd_wave.hip):
-// d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2, 4}, channel groups in channel order.
+// d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2, 4}; channel groups in channel order at radix
+// level 0, else (q_c = 2) the plan's interleaved groups (channels congruent to g + level mod 2).
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems);
-int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
+int launch_fwd_wave(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream);
 
 // fp32 path (bigemm_fwd_f32.hip): operand packing, RMSNorm row scales and the forward.
 int pack_weights_f32(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,

@@ -105,6 +105,33 @@ def test_fused_block_matches_oracle(stage, route, level, dtype) -> None:
     assert torch.equal(out.cpu(), expected)
 
 
+def test_fused_block_past_2gib_matches_small_batches() -> None:
+    """x of 56x56x128 bf16 rows past 2 GiB (2,676 images): the wave kernel's 32-bit offsets do not
+    reach, so the launch takes the resident kernel.  Images are independent, so the first and
+    last two images of the big batch must match the same images run as a batch of 2 (wave
+    kernel, checked against the oracle above) to bf16 rounding, and the oracle directly."""
+    h, w, c, d = STAGES["s1"]
+    b = 2676
+    assert b * h * w * c * 2 >= 2 ** 31
+    announce(f"fused s1 local bf16 B={b} (x past 2 GiB: resident kernel)")
+    plan, x_small, params, norm_w = make_case(2, h, w, c, d, "local", 0, torch.bfloat16, seed=4)
+    dp = to_dev(params)
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(b, h, w, c, generator=gen, device=DEV, dtype=torch.bfloat16)
+    x[:2] = x_small.to(DEV)
+    out = bigemm_block_hip(x, norm_w.to(DEV), plan, **dp, residual=False)
+    torch.cuda.synchronize()
+    for sl in (slice(0, 2), slice(b - 2, b)):
+        small = bigemm_block_hip(x[sl].contiguous(), norm_w.to(DEV), plan, **dp, residual=False)
+        err = rel_l2(out[sl].cpu(), small.cpu())
+        assert err <= 5e-3, f"images {sl}: rel-L2 {err:.3e} against the same images as a batch of 2"
+    ref = oracle_delta(rmsnorm_reference(x_small, norm_w), plan, params, torch.bfloat16)
+    err = rel_l2(out[:2].cpu(), ref)
+    assert err <= TOL[torch.bfloat16], f"rel-L2 {err:.3e} vs the oracle"
+    del x, out
+    torch.cuda.empty_cache()
+
+
 def test_config1_shape_local_bf16() -> None:
     """x [8,14,14,512] ~ N(0,1), local route, g=16, d=128, A ~ N(0,1/16), B ~ N(0,1/fan_in), seed 0."""
     announce("config1 x[8,14,14,512] local bf16 seed=0")
