@@ -376,6 +376,17 @@ int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* 
                     float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
                     int32_t dtype, void* stream);
 
+/* ow_bwd_channel2 with dX' written through the token table instead of to dxt (replaces
+ * ow_bwd_scatter after it): for plans whose channel order is the identity (radix level 0 or
+ * one channel group) and C = q_c * 128, dX' of slot (image b, token group s, row t) goes to
+ * g[b * H * W + token_index[16 s + t]][128 q ..] (pad slots are not stored; every element of
+ * g [batch * H * W][C] is written once).  slots = batch * q_s * 16; the other arguments as in
+ * ow_bwd_channel2; g 16-byte aligned and below 2 GiB. */
+int ow_bwd_channel2_routed(const void* xt, const void* dyt, const void* z, const void* du, const void* dv,
+                           const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
+                           const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
+                           int64_t n_partial, int32_t rd, int32_t dtype, void* stream);
+
 /* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
  * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and
  * ow_bwd_scatter around it as well): X' = x r and dY rows are read from x, dy ([rows][C],

@@ -11,7 +11,9 @@ accumulation, entirely on the HIP stream of the gradient:
   channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u, dP_v), dX' and the token-matrix
   gradients (per-workgroup partials); for d = 128 two kernels share that work
   (``ow_bwd_channel``: token side, U', V', dZ and the gate; ``ow_bwd_channel2``: dP_u, dP_v,
-  dX', W' and the token-matrix gradients); otherwise (fp32) the 16x16 token-side products are
+  dX', W' and the token-matrix gradients; with the identity channel order
+  ``ow_bwd_channel2_routed`` writes dX' straight to the NHWC gradient, so no scatter pass runs);
+  otherwise (fp32) the 16x16 token-side products are
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
   ``ow_bwd_gate``;
@@ -143,7 +145,10 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
         fused = d == 64 and slots % 32 == 0 and dtype != torch.float32
         # The fused kernel reads x / dy and writes g itself when group q is channels
         # [64 q, 64 q + 64) (routing.py:107-121: radix level 0 or a single group).
-        routed = fused and plan.channels == q_c * d and (plan.radix_level == 0 or q_c == 1)
+        identity = plan.channels == q_c * d and (plan.radix_level == 0 or q_c == 1)
+        routed = fused and identity
+        # d = 128: the second channel kernel writes dX' to g itself under the same condition.
+        scatter = not routed and not (d == 128 and dtype != torch.float32 and identity)
         g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing
         if not routed:
             # Routed tiles of X' = x r and of dY.
@@ -211,11 +216,18 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                              q_c, d, rd, code, stream), "ow_bwd_channel")
             n_part = lib.ow_bwd_channel_partials(slots, q_c)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
-            dxt = torch.empty_like(xt)
-            _native.check(lib.ow_bwd_channel2(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
-                                              dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
-                                              dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
-                                              stream), "ow_bwd_channel2")
+            if scatter:
+                dxt = torch.empty_like(xt)
+                _native.check(lib.ow_bwd_channel2(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                                  dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
+                                                  dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
+                                                  stream), "ow_bwd_channel2")
+            else:
+                _native.check(lib.ow_bwd_channel2_routed(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                                         dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(),
+                                                         nbytes, tok.data_ptr(), ctypes.byref(oplan), batch,
+                                                         g.data_ptr(), partial.data_ptr(), n_part, rd, code, stream),
+                              "ow_bwd_channel2_routed")
             g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
@@ -261,9 +273,9 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             dxt = _tile_mix(lib, dpu, au_t, dpv, av_t, d, code, stream)
             del dpu, dpv, wp, xt, dyt
 
-        # dX' back to NHWC (unless the fused kernel wrote g), then through the RMSNorm (+ the
-        # residual's identity).
-        if not routed:
+        # dX' back to NHWC (unless a kernel wrote g), then through the RMSNorm (+ the residual's
+        # identity).
+        if scatter:
             _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(),
                                              ctypes.byref(oplan), batch, code, g.data_ptr(), stream),
                           "ow_bwd_scatter")

@@ -1238,6 +1238,11 @@ struct BwdChan2Args {
   float* partial;          // [gridDim][3][256]
   int64_t slots;
   int32_t q_c;
+  // Routed dX' (RT): written to g [batch * n_tok][channels] through the token table (group q is
+  // channels 128 q .. 128 q + 127) instead of dxt.
+  const int32_t* tok = nullptr;  // [q_s * 16]
+  uint16_t* g = nullptr;
+  int32_t q_s = 0, n_tok = 0, channels = 0;
 };
 
 constexpr int kB2FrB = 16;  // B-operand fragments of pass 1 per chunk (B_u''^T, B_v''^T)
@@ -1249,7 +1254,7 @@ struct BwdChan2Lds {
   float red[kB2Waves][3][256];          // per-wave dA sums
 };
 
-template <class Ty, int RD>
+template <class Ty, int RD, bool RT>
 __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int32_t n_units) {
   constexpr int NCH = RD / 32;
   constexpr int MB = kB2D / 32;                            // 4 output blocks of 32 channels
@@ -1264,8 +1269,10 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
   const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
   const int64_t rows = a.slots * a.q_c;
   const uint32_t tbytes = static_cast<uint32_t>(rows * kB2D * 2), ebytes = static_cast<uint32_t>(rows * RD * 2);
+  uint32_t gbytes = tbytes;  // RT: batch * n_tok * channels values of g (below 2 GiB: host check)
+  if constexpr (RT) gbytes = static_cast<uint32_t>(a.slots / (16 * a.q_s) * a.n_tok * a.channels * 2);
   const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(a.xt, tbytes), rdy = buffer_rsrc(a.dyt, tbytes),
-                               rdx = buffer_rsrc(a.dxt, tbytes);
+                               rdx = buffer_rsrc(RT ? a.g : a.dxt, gbytes);
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(a.z, ebytes), rdu = buffer_rsrc(a.du, ebytes),
                                rdv = buffer_rsrc(a.dv, ebytes);
   if (wave == 0) {
@@ -1376,6 +1383,20 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
       const u32x4 tu0 = keep_if(g0, tu), tu1 = keep_if(!g0, tu);
       const u32x4 tv0 = keep_if(g0, tv), tv1 = keep_if(!g0, tv);
       const bool ok = slot0 + l32 < a.slots;
+      // Byte offset of the lane's slot row in the output: dxt row, or (RT) the NHWC row of its
+      // token at group q's columns (kOffOut for pad slots: the stores are dropped).
+      uint32_t obase = kOffOut;
+      if constexpr (RT) {
+        if (ok) {
+          const int32_t sl = static_cast<int32_t>(slot0 + l32);  // < batch * q_s * 16 < 2^31
+          const int32_t tg = sl >> 4, b = tg / a.q_s, sg = tg - b * a.q_s;
+          const int32_t tk = a.tok[sg * kG + (sl & 15)];
+          if (tk >= 0 && tk < a.n_tok)
+            obase = static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_tok + tk) * a.channels + kB2D * q) * 2u;
+        }
+      } else if (ok) {
+        obase = static_cast<uint32_t>((row0 + l32) * kB2D) * 2u;
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         f32x16 dx = Ty::mma32(pack_kstep<Ty>(DPu[mb], 0), tu0, f32x16{});
@@ -1385,7 +1406,7 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
         mfma_drain();
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const uint32_t o = ok ? static_cast<uint32_t>((row0 + l32) * kB2D + 32 * mb + 8 * b + 4 * hh) * 2u : kOffOut;
+          const uint32_t o = obase == kOffOut ? kOffOut : obase + 2u * static_cast<uint32_t>(32 * mb + 8 * b + 4 * hh);
           __builtin_amdgcn_raw_buffer_store_b64(u32x2{Ty::pack2(dx[4 * b], dx[4 * b + 1]), Ty::pack2(dx[4 * b + 2], dx[4 * b + 3])},
                                                 rdx, o, 0, 0);
         }
@@ -1459,10 +1480,17 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
 template <int RD>
 int launch_bwd_chan2_rd(const BwdChan2Args& a, int64_t grid, int32_t n_units, int32_t dtype, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
-  if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD>), g, dim3(512), 0, s, a, n_units);
-  else
-    hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD>), g, dim3(512), 0, s, a, n_units);
+  if (dtype == OW_DTYPE_BF16) {
+    if (a.g)
+      hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD, true>), g, dim3(512), 0, s, a, n_units);
+    else
+      hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD, false>), g, dim3(512), 0, s, a, n_units);
+  } else {
+    if (a.g)
+      hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD, true>), g, dim3(512), 0, s, a, n_units);
+    else
+      hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD, false>), g, dim3(512), 0, s, a, n_units);
+  }
   return hip_status(hipGetLastError(), "bwd_chan2_d128_kernel launch");
 }
 
@@ -1932,9 +1960,13 @@ int64_t ow_bwd_channel_partials(int64_t slots, int32_t q_c) {
   return ow::bwd_chan_grid(static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows));
 }
 
-int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* du, const void* dv, const float* a_u,
-                    const float* a_v, const void* packed, size_t packed_bytes, void* dxt, float* partial,
-                    int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+namespace ow {
+namespace {
+// ow_bwd_channel2 and its routed form: r.tok / r.g set (and dxt NULL) for the routed one.
+int bwd_channel2(const void* xt, const void* dyt, const void* z, const void* du, const void* dv, const float* a_u,
+                 const float* a_v, const void* packed, size_t packed_bytes, void* dxt, float* partial, int64_t n_partial,
+                 int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, const BwdChan2Args& r,
+                 void* stream) {
   OW_CHECK_SUPPORTED(d == ow::kB2D && (rd == 128 || rd == 256), "backward channel kernel needs d = 128, rd in {128, 256}");
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
   OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 16 == 0, "bad shape q_c=%d slots=%lld (multiple of 16)", q_c,
@@ -1950,18 +1982,64 @@ int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* 
                (long long)n_partial, (long long)grid);
   OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31), "tiles of %lld slots exceed 2 GiB",
                (long long)slots);
-  OW_CHECK_ARG(xt && dyt && z && du && dv && a_u && a_v && dxt && partial, "tensor pointer is NULL");
-  for (const void* p : {xt, dyt, z, du, dv, packed, static_cast<const void*>(dxt)})
+  OW_CHECK_ARG(xt && dyt && z && du && dv && a_u && a_v && (dxt || r.g) && partial, "tensor pointer is NULL");
+  for (const void* p : {xt, dyt, z, du, dv, packed, r.g ? static_cast<const void*>(r.g) : dxt})
     OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
-  const ow::BwdChan2Args a{cu(xt), cu(dyt), cu(z), cu(du), cu(dv), a_u, a_v, cu(packed), static_cast<uint16_t*>(dxt),
-                           partial, slots, q_c};
+  ow::BwdChan2Args a = r;
+  a.xt = cu(xt);
+  a.dyt = cu(dyt);
+  a.z = cu(z);
+  a.du = cu(du);
+  a.dv = cu(dv);
+  a.a_u = a_u;
+  a.a_v = a_v;
+  a.packed = cu(packed);
+  a.dxt = static_cast<uint16_t*>(dxt);
+  a.partial = partial;
+  a.slots = slots;
+  a.q_c = q_c;
   const int64_t units = static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rc = rd == 256 ? ow::launch_bwd_chan2_rd<256>(a, grid, static_cast<int32_t>(units), dtype, s)
                            : ow::launch_bwd_chan2_rd<128>(a, grid, static_cast<int32_t>(units), dtype, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
+}
+}  // namespace
+}  // namespace ow
+
+int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* du, const void* dv, const float* a_u,
+                    const float* a_v, const void* packed, size_t packed_bytes, void* dxt, float* partial,
+                    int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+  OW_CHECK_ARG(dxt, "tensor pointer is NULL");
+  return ow::bwd_channel2(xt, dyt, z, du, dv, a_u, a_v, packed, packed_bytes, dxt, partial, n_partial, slots, q_c, d,
+                          rd, dtype, ow::BwdChan2Args{}, stream);
+}
+
+int ow_bwd_channel2_routed(const void* xt, const void* dyt, const void* z, const void* du, const void* dv,
+                           const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
+                           const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
+                           int64_t n_partial, int32_t rd, int32_t dtype, void* stream) {
+  int32_t q_s = 0, q_c = 0;
+  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
+  const int32_t d = plan->channel_tile, c = plan->channels;
+  OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
+  OW_CHECK_SUPPORTED(d == ow::kB2D && c == q_c * ow::kB2D && (plan->radix_level == 0 || q_c == 1),
+                     "routed backward needs the identity channel order with C = q_c * 128");
+  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 27), "bad batch %d", batch);
+  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * c * 2 < (int64_t(1) << 31),
+               "g must be below 2 GiB (buffer addressing)");
+  OW_CHECK_ARG(token_index && g, "tensor pointer is NULL");
+  ow::BwdChan2Args r{};
+  r.tok = token_index;
+  r.g = static_cast<uint16_t*>(g);
+  r.q_s = q_s;
+  r.n_tok = plan->height * plan->width;
+  r.channels = c;
+  const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
+  return ow::bwd_channel2(xt, dyt, z, du, dv, a_u, a_v, packed, packed_bytes, nullptr, partial, n_partial, slots, q_c,
+                          d, rd, dtype, r, stream);
 }
 
 int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
