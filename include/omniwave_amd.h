@@ -376,14 +376,23 @@ int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* 
                     float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
                     int32_t dtype, void* stream);
 
-/* ow_bwd_channel2 with dX' written through the token table instead of to dxt (replaces
- * ow_bwd_scatter after it): for plans whose channel order is the identity (radix level 0 or
- * one channel group) and C = q_c * 128, dX' of slot (image b, token group s, row t) goes to
- * g[b * H * W + token_index[16 s + t]][128 q ..] (pad slots are not stored; every element of
- * g [batch * H * W][C] is written once).  slots = batch * q_s * 16; the other arguments as in
- * ow_bwd_channel2; g 16-byte aligned and below 2 GiB. */
-int ow_bwd_channel2_routed(const void* xt, const void* dyt, const void* z, const void* du, const void* dv,
-                           const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
+/* ow_bwd_channel and ow_bwd_channel2 with the routing folded in (replace ow_bwd_gather before
+ * them and ow_bwd_scatter after them), for plans whose channel order is the identity (radix
+ * level 0 or one channel group) and C = q_c * 128.  Slot (image b, token group s, row t) of
+ * group q is row b * H * W + token_index[16 s + t] of x, dy ([batch * H * W][C]) at columns
+ * 128 q ..; pad slots read as zero.  ow_bwd_channel_routed folds the RMSNorm scales (rscale
+ * [batch * H * W], NULL without the norm) into the token matrices (P_u = A_u diag(r) x);
+ * ow_bwd_channel2_routed forms X' = x r rounded to the compute dtype (as ow_bwd_gather) for the
+ * token-matrix gradients and writes dX' to g[b * H * W + token_index[16 s + t]][128 q ..]
+ * (every element of g [batch * H * W][C] once) instead of dxt.  slots = batch * q_s * 16; the
+ * other arguments as in ow_bwd_channel / ow_bwd_channel2; x, dy, g 16-byte aligned and below
+ * 2 GiB. */
+int ow_bwd_channel_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                          const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
+                          const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                          void* dv, int32_t rd, int32_t dtype, void* stream);
+int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, const void* z, const void* du,
+                           const void* dv, const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
                            const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
                            int64_t n_partial, int32_t rd, int32_t dtype, void* stream);
 

@@ -160,9 +160,14 @@ _SIGNATURES = {
         + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
            ctypes.c_void_p],
     ),
+    "ow_bwd_channel_routed": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 5 + [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_size_t] + [ctypes.c_void_p] * 6
+        + [ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
+    ),
     "ow_bwd_channel2_routed": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 8 + [ctypes.c_size_t] + [ctypes.c_void_p] * 2 + [ctypes.c_int32]
+        [ctypes.c_void_p] * 9 + [ctypes.c_size_t] + [ctypes.c_void_p] * 2 + [ctypes.c_int32]
         + [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
     "ow_bwd_fused_routed": (

@@ -11,8 +11,9 @@ accumulation, entirely on the HIP stream of the gradient:
   channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u, dP_v), dX' and the token-matrix
   gradients (per-workgroup partials); for d = 128 two kernels share that work
   (``ow_bwd_channel``: token side, U', V', dZ and the gate; ``ow_bwd_channel2``: dP_u, dP_v,
-  dX', W' and the token-matrix gradients; with the identity channel order
-  ``ow_bwd_channel2_routed`` writes dX' straight to the NHWC gradient, so no scatter pass runs);
+  dX', W' and the token-matrix gradients; with the identity channel order their ``_routed``
+  forms read x / dy and write dX' straight to the NHWC gradient, so neither the gather nor the
+  scatter pass runs);
   otherwise (fp32) the 16x16 token-side products are
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
@@ -143,13 +144,14 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                            stream), "ow_rms_scale")
 
         fused = d == 64 and slots % 32 == 0 and dtype != torch.float32
-        # The fused kernel reads x / dy and writes g itself when group q is channels
-        # [64 q, 64 q + 64) (routing.py:107-121: radix level 0 or a single group).
+        chan128 = d == 128 and dtype != torch.float32
+        # The d = 64 fused kernel and the d = 128 channel kernels read x / dy and write g
+        # themselves when group q is channels [d q, d q + d) (routing.py:107-121: radix level 0
+        # or a single group): no gather and no scatter pass.
         identity = plan.channels == q_c * d and (plan.radix_level == 0 or q_c == 1)
-        routed = fused and identity
-        # d = 128: the second channel kernel writes dX' to g itself under the same condition.
-        scatter = not routed and not (d == 128 and dtype != torch.float32 and identity)
+        routed = (fused or chan128) and identity
         g = torch.empty(n_rows, plan.channels, dtype=dtype, device=dev)  # fully written: no clearing
+        rs_ptr = rscale.data_ptr() if rscale is not None else None
         if not routed:
             # Routed tiles of X' = x r and of dY.
             xt = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
@@ -210,30 +212,37 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             pv, dw = torch.empty_like(pu), torch.empty_like(pu)
             z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
             du, dv = torch.empty_like(z), torch.empty_like(z)
-            _native.check(lib.ow_bwd_channel(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
-                                             ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
-                                             dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(), slots,
-                                             q_c, d, rd, code, stream), "ow_bwd_channel")
             n_part = lib.ow_bwd_channel_partials(slots, q_c)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
-            if scatter:
+            if routed:
+                _native.check(lib.ow_bwd_channel_routed(x.data_ptr(), grad_delta.data_ptr(), rs_ptr, tok.data_ptr(),
+                                                        ctypes.byref(oplan), batch, au.data_ptr(), av.data_ptr(),
+                                                        ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(),
+                                                        pv.data_ptr(), dw.data_ptr(), z.data_ptr(), du.data_ptr(),
+                                                        dv.data_ptr(), rd, code, stream), "ow_bwd_channel_routed")
+                _native.check(lib.ow_bwd_channel2_routed(x.data_ptr(), grad_delta.data_ptr(), rs_ptr, z.data_ptr(),
+                                                         du.data_ptr(), dv.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                                         wpk.data_ptr(), nbytes, tok.data_ptr(), ctypes.byref(oplan),
+                                                         batch, g.data_ptr(), partial.data_ptr(), n_part, rd, code,
+                                                         stream), "ow_bwd_channel2_routed")
+            else:
+                _native.check(lib.ow_bwd_channel(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
+                                                 ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
+                                                 dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(), slots,
+                                                 q_c, d, rd, code, stream), "ow_bwd_channel")
                 dxt = torch.empty_like(xt)
                 _native.check(lib.ow_bwd_channel2(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
                                                   dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
                                                   dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                   stream), "ow_bwd_channel2")
-            else:
-                _native.check(lib.ow_bwd_channel2_routed(xt.data_ptr(), dyt.data_ptr(), z.data_ptr(), du.data_ptr(),
-                                                         dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(),
-                                                         nbytes, tok.data_ptr(), ctypes.byref(oplan), batch,
-                                                         g.data_ptr(), partial.data_ptr(), n_part, rd, code, stream),
-                              "ow_bwd_channel2_routed")
             g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
             d_bv = _slot_reduce(pv, dv)
             d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
-            del wpk, z, du, dv, pu, pv, dw, xt, dyt
+            del wpk, z, du, dv, pu, pv, dw
+            if not routed:
+                del xt, dyt
         else:
             # Folded weights in the compute dtype, plain and transposed (both contiguous).
             bu = torch.empty(q_c, d, rd, dtype=dtype, device=dev)
@@ -275,7 +284,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
 
         # dX' back to NHWC (unless a kernel wrote g), then through the RMSNorm (+ the residual's
         # identity).
-        if scatter:
+        if not routed:
             _native.check(lib.ow_bwd_scatter(dxt.data_ptr(), tok.data_ptr(), ch.data_ptr(),
                                              ctypes.byref(oplan), batch, code, g.data_ptr(), stream),
                           "ow_bwd_scatter")

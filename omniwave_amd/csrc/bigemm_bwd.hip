@@ -1042,12 +1042,31 @@ struct BwdChanArgs {
   uint16_t* dv;
   int64_t slots;
   int32_t q_c;
+  // Routed rows (RT): x, dy [batch * n_tok][channels] read through the token table (group q is
+  // channels 128 q .. 128 q + 127) instead of the xt, dyt tiles; the RMSNorm scales (rscale,
+  // NULL: none) are folded into the token operands, as in the forward (A diag(r) x = A X').
+  const uint16_t* x = nullptr;
+  const uint16_t* dy = nullptr;
+  const float* rscale = nullptr;
+  const int32_t* tok = nullptr;  // [q_s * 16]
+  int32_t q_s = 0, n_tok = 0, channels = 0;
 };
 
+// slot_row in 32-bit arithmetic, -1 also for sl >= slots (slots < 2^31 and batch * n_tok <
+// 2^31: the callers check).
+__device__ __forceinline__ int32_t slot_row32(const int32_t* tok, int64_t sl, int64_t slots, int32_t q_s,
+                                              int32_t n_tok) {
+  if (sl >= slots) return -1;
+  const int32_t s32 = static_cast<int32_t>(sl), tg = s32 >> 4, b = tg / q_s, sg = tg - b * q_s;
+  const int32_t tk = tok[sg * kG + (s32 & 15)];
+  return (tk >= 0 && tk < n_tok) ? b * n_tok + tk : -1;
+}
+
 struct BwdChanLds {
-  uint16_t x[kB2Waves][32 * kB2D];     // per wave: its 32 rows (X', then dY)
+  uint16_t x[kB2Waves][32 * kB2D];     // per wave: its 32 rows (X' or x, then dY)
   uint16_t w[3][kB2FrA * kFragElems];  // chunk buffers
   u32x4 tok[3][64];                    // A_u, A_v, A_o^T token-operand rows
+  float rs[kB2Waves][32];              // RT: per wave, the RMSNorm scale of each slot
 };
 
 // out = the token-side product of one operand f (pair_token_side_mma for a single product).
@@ -1065,7 +1084,7 @@ __device__ __forceinline__ void token_side_one(const u32x4 (&xk)[KS / 2][2], u32
   }
 }
 
-template <class Ty, int RD>
+template <class Ty, int RD, bool RT>
 __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32_t n_units) {
   constexpr int NCH = RD / 32;
   constexpr int CH = kB2FrA * kFragElems;                  // one chunk buffer (elements)
@@ -1077,7 +1096,9 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
   const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
   const int64_t rows = a.slots * a.q_c;
   const uint32_t tbytes = static_cast<uint32_t>(rows * kB2D * 2), ebytes = static_cast<uint32_t>(rows * RD * 2);
-  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(a.xt, tbytes), rdy = buffer_rsrc(a.dyt, tbytes);
+  uint32_t xbytes = tbytes;  // RT: batch * n_tok * channels values of x and dy (below 2 GiB: host check)
+  if constexpr (RT) xbytes = static_cast<uint32_t>(a.slots / (16 * a.q_s) * a.n_tok * a.channels * 2);
+  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(RT ? a.x : a.xt, xbytes), rdy = buffer_rsrc(RT ? a.dy : a.dyt, xbytes);
   const __amdgpu_buffer_rsrc_t rpu = buffer_rsrc(a.pu, tbytes), rpv = buffer_rsrc(a.pv, tbytes),
                                rdw = buffer_rsrc(a.dw, tbytes);
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(a.z, ebytes), rdu = buffer_rsrc(a.du, ebytes),
@@ -1094,6 +1115,12 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
     const int q = u % a.q_c;
     const int64_t slot0 = static_cast<int64_t>(u / a.q_c) * kB2Rows + 32 * wave;
     const int64_t row0 = static_cast<int64_t>(q) * a.slots + slot0;
+    // RT: the NHWC row of slot l32 (-1: pad) and its RMSNorm scale, for the wave's table.
+    int32_t my_grow = -1;
+    if constexpr (RT) {
+      my_grow = slot_row32(a.tok, slot0 + l32, a.slots, a.q_s, a.n_tok);
+      if (hh == 0) sh.rs[wave][l32] = (a.rscale && my_grow >= 0) ? a.rscale[my_grow] : 1.0f;
+    }
     // Copy k: rows 4k .. 4k + 3 of the wave; lane -> row 4k + lane / 16, LDS slot lane % 16,
     // which holds the row's piece (lane % 16) ^ 4 (k & 1); rows past the slots read as zero.
     auto copy_tile = [&](__amdgpu_buffer_rsrc_t r) {
@@ -1101,9 +1128,15 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
       for (int k = 0; k < 8; ++k) {
         const int rr = 4 * k + (lane >> 4);
         const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ (4 * (k & 1)));
-        const uint32_t voff = slot0 + rr < a.slots
-                                  ? static_cast<uint32_t>(row0 + rr) * static_cast<uint32_t>(kB2D * 2) + 16u * piece
-                                  : kOffOut;
+        uint32_t voff;
+        if constexpr (RT) {
+          const int32_t gr = __shfl(my_grow, rr);
+          voff = gr >= 0 ? static_cast<uint32_t>(gr * a.channels + kB2D * q) * 2u + 16u * piece : kOffOut;
+        } else {
+          voff = slot0 + rr < a.slots
+                     ? static_cast<uint32_t>(row0 + rr) * static_cast<uint32_t>(kB2D * 2) + 16u * piece
+                     : kOffOut;
+        }
         tile_copy(r, voff, xlds + static_cast<uint32_t>(4 * k * kB2D * 2));
       }
     };
@@ -1142,7 +1175,17 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile is read: the dY rows replace it
     copy_tile(rdy);  // 8
     u32x4 Pu[kB2KS], Pv[kB2KS], Dw[kB2KS];
-    pair_token_side_mma<Ty, kB2KS>(xk, sh.tok[0][lane], sh.tok[1][lane], lane, Pu, Pv);
+    {
+      u32x4 tu = sh.tok[0][lane], tv = sh.tok[1][lane];
+      if constexpr (RT) {
+        if (a.rscale) {  // A diag(r): the rows are x, not X'
+          const float* r8 = &sh.rs[wave][16 * ((lane >> 4) & 1) + 4 * hh];
+          tu = scale8<Ty>(tu, r8);
+          tv = scale8<Ty>(tv, r8);
+        }
+      }
+      pair_token_side_mma<Ty, kB2KS>(xk, tu, tv, lane, Pu, Pv);
+    }
     store_ops(rpu, Pu);  // 16
     store_ops(rpv, Pv);  // 16
     wait_vmcnt<32>();    // the dY rows (and with them both chunk copies); the stores may be in flight
@@ -1238,8 +1281,12 @@ struct BwdChan2Args {
   float* partial;          // [gridDim][3][256]
   int64_t slots;
   int32_t q_c;
-  // Routed dX' (RT): written to g [batch * n_tok][channels] through the token table (group q is
-  // channels 128 q .. 128 q + 127) instead of dxt.
+  // Routed (RT): X' and dY rows from x (times rscale, NULL: none, rounded as the gather) and dy
+  // [batch * n_tok][channels], and dX' written to g, through the token table (group q is channels
+  // 128 q .. 128 q + 127) instead of the xt, dyt, dxt tiles.
+  const uint16_t* x = nullptr;
+  const uint16_t* dy = nullptr;
+  const float* rscale = nullptr;
   const int32_t* tok = nullptr;  // [q_s * 16]
   uint16_t* g = nullptr;
   int32_t q_s = 0, n_tok = 0, channels = 0;
@@ -1269,9 +1316,9 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
   const uint32_t lane16 = 16u * static_cast<uint32_t>(lane);
   const int64_t rows = a.slots * a.q_c;
   const uint32_t tbytes = static_cast<uint32_t>(rows * kB2D * 2), ebytes = static_cast<uint32_t>(rows * RD * 2);
-  uint32_t gbytes = tbytes;  // RT: batch * n_tok * channels values of g (below 2 GiB: host check)
+  uint32_t gbytes = tbytes;  // RT: batch * n_tok * channels values of x, dy, g (below 2 GiB: host check)
   if constexpr (RT) gbytes = static_cast<uint32_t>(a.slots / (16 * a.q_s) * a.n_tok * a.channels * 2);
-  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(a.xt, tbytes), rdy = buffer_rsrc(a.dyt, tbytes),
+  const __amdgpu_buffer_rsrc_t rxt = buffer_rsrc(RT ? a.x : a.xt, gbytes), rdy = buffer_rsrc(RT ? a.dy : a.dyt, gbytes),
                                rdx = buffer_rsrc(RT ? a.g : a.dxt, gbytes);
   const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(a.z, ebytes), rdu = buffer_rsrc(a.du, ebytes),
                                rdv = buffer_rsrc(a.dv, ebytes);
@@ -1329,12 +1376,31 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
       const uint32_t addr = rlds + 2u * static_cast<uint32_t>((16 * ks + 4 * h4 + (l16 >> 2)) * 32 + 16 * g + 4 * (l16 & 3));
       return lds_read_tr16(addr);
     };
-    // Rows 16 g + l16 of a [slots][128] tensor, channels 16 ks + 4 h4 .. + 3 (zero past the slots).
-    auto mem_op = [&](__amdgpu_buffer_rsrc_t r, int g, int ks) {
-      const int sl = 16 * g + l16;
-      const uint32_t o =
-          slot0 + sl < a.slots ? static_cast<uint32_t>((row0 + sl) * kB2D + 16 * ks + 4 * h4) * 2u : kOffOut;
-      return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+    // RT: the NHWC rows of the lane's slots 16 g + l16 (g < 2) and, for X', their RMSNorm scales.
+    int32_t grow[2] = {-1, -1};
+    float grs[2] = {1.0f, 1.0f};
+    if constexpr (RT) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        grow[g] = slot_row32(a.tok, slot0 + 16 * g + l16, a.slots, a.q_s, a.n_tok);
+        if (a.rscale && grow[g] >= 0) grs[g] = a.rscale[grow[g]];
+      }
+    }
+    // Rows 16 g + l16 of a [slots][128] tensor, channels 16 ks + 4 h4 .. + 3 (zero past the slots);
+    // RT: of x (XS: times the row's scale and rounded, X' as the gather forms it) or dy.
+    auto mem_op = [&](__amdgpu_buffer_rsrc_t r, int g, int ks, bool xs) {
+      uint32_t o;
+      if constexpr (RT)
+        o = grow[g] >= 0 ? static_cast<uint32_t>(grow[g] * a.channels + kB2D * q + 16 * ks + 4 * h4) * 2u : kOffOut;
+      else
+        o = slot0 + 16 * g + l16 < a.slots
+                ? static_cast<uint32_t>((row0 + 16 * g + l16) * kB2D + 16 * ks + 4 * h4) * 2u
+                : kOffOut;
+      u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+      if constexpr (RT) {
+        if (xs && a.rscale) v = u32x2{scale2<Ty>(v[0], grs[g]), scale2<Ty>(v[1], grs[g])};
+      }
+      return v;
     };
 
     __syncthreads();  // the previous unit is done with every buffer; tok is written
@@ -1387,13 +1453,8 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
       // token at group q's columns (kOffOut for pad slots: the stores are dropped).
       uint32_t obase = kOffOut;
       if constexpr (RT) {
-        if (ok) {
-          const int32_t sl = static_cast<int32_t>(slot0 + l32);  // < batch * q_s * 16 < 2^31
-          const int32_t tg = sl >> 4, b = tg / a.q_s, sg = tg - b * a.q_s;
-          const int32_t tk = a.tok[sg * kG + (sl & 15)];
-          if (tk >= 0 && tk < a.n_tok)
-            obase = static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_tok + tk) * a.channels + kB2D * q) * 2u;
-        }
+        const int32_t gr = slot_row32(a.tok, slot0 + l32, a.slots, a.q_s, a.n_tok);
+        if (gr >= 0) obase = static_cast<uint32_t>(gr * a.channels + kB2D * q) * 2u;
       } else if (ok) {
         obase = static_cast<uint32_t>((row0 + l32) * kB2D) * 2u;
       }
@@ -1417,13 +1478,13 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[0] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks), dA[0]);
+      for (int ks = 0; ks < kB2KS; ++ks) dA[0] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks, true), dA[0]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     stage(DPv);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[1] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks), dA[1]);
+      for (int ks = 0; ks < kB2KS; ++ks) dA[1] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks, true), dA[1]);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // nothing in flight before pass 2's copies
 
     // Pass 2: W'[mb] += Z B_o''; [wait] [barrier] [Z rows of ec + 1: 2] [fragments of ec + 2: 1].
@@ -1458,7 +1519,7 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[2] = Ty::mma16(mem_op(rdy, g, ks), staged_op(g, ks), dA[2]);
+      for (int ks = 0; ks < kB2KS; ++ks) dA[2] = Ty::mma16(mem_op(rdy, g, ks, false), staged_op(g, ks), dA[2]);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   }
 
@@ -1481,12 +1542,12 @@ template <int RD>
 int launch_bwd_chan2_rd(const BwdChan2Args& a, int64_t grid, int32_t n_units, int32_t dtype, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
   if (dtype == OW_DTYPE_BF16) {
-    if (a.g)
+    if (a.tok)
       hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD, true>), g, dim3(512), 0, s, a, n_units);
     else
       hipLaunchKernelGGL((bwd_chan2_d128_kernel<BF16, RD, false>), g, dim3(512), 0, s, a, n_units);
   } else {
-    if (a.g)
+    if (a.tok)
       hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD, true>), g, dim3(512), 0, s, a, n_units);
     else
       hipLaunchKernelGGL((bwd_chan2_d128_kernel<F16, RD, false>), g, dim3(512), 0, s, a, n_units);
@@ -1506,10 +1567,17 @@ int64_t bwd_chan_grid(int64_t units) {
 template <int RD>
 int launch_bwd_chan_rd(const BwdChanArgs& a, int32_t n_units, int32_t dtype, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(bwd_chan_grid(n_units)));
-  if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL((bwd_chan_d128_kernel<BF16, RD>), g, dim3(512), 0, s, a, n_units);
-  else
-    hipLaunchKernelGGL((bwd_chan_d128_kernel<F16, RD>), g, dim3(512), 0, s, a, n_units);
+  if (dtype == OW_DTYPE_BF16) {
+    if (a.tok)
+      hipLaunchKernelGGL((bwd_chan_d128_kernel<BF16, RD, true>), g, dim3(512), 0, s, a, n_units);
+    else
+      hipLaunchKernelGGL((bwd_chan_d128_kernel<BF16, RD, false>), g, dim3(512), 0, s, a, n_units);
+  } else {
+    if (a.tok)
+      hipLaunchKernelGGL((bwd_chan_d128_kernel<F16, RD, true>), g, dim3(512), 0, s, a, n_units);
+    else
+      hipLaunchKernelGGL((bwd_chan_d128_kernel<F16, RD, false>), g, dim3(512), 0, s, a, n_units);
+  }
   return hip_status(hipGetLastError(), "bwd_chan_d128_kernel launch");
 }
 
@@ -1922,9 +1990,13 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
   return ow::launch_bwd_fused<false>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
 }
 
-int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
-                   const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
-                   int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+namespace ow {
+namespace {
+// ow_bwd_channel and its routed form (r.tok, r.x, r.dy set; xt, dyt NULL).
+int bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
+                int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, const BwdChanArgs& r,
+                void* stream) {
   OW_CHECK_SUPPORTED(d == ow::kB2D && (rd == 128 || rd == 256), "backward channel kernel needs d = 128, rd in {128, 256}");
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
   OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 16 == 0, "bad shape q_c=%d slots=%lld (multiple of 16)", q_c,
@@ -1937,15 +2009,30 @@ int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const floa
   }
   OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31), "tiles of %lld slots exceed 2 GiB",
                (long long)slots);
-  OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && z && du && dv, "tensor pointer is NULL");
-  for (const void* p : {xt, dyt, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
+  const void* xs = r.tok ? static_cast<const void*>(r.x) : xt;
+  const void* ys = r.tok ? static_cast<const void*>(r.dy) : dyt;
+  OW_CHECK_ARG(xs && ys && a_u && a_v && a_o && pu && pv && dw && z && du && dv, "tensor pointer is NULL");
+  for (const void* p : {xs, ys, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
                         static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
                         static_cast<const void*>(dv)})
     OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
-  const ow::BwdChanArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
-                          slots, q_c};
+  ow::BwdChanArgs a = r;
+  a.xt = cu(xt);
+  a.dyt = cu(dyt);
+  a.a_u = a_u;
+  a.a_v = a_v;
+  a.a_o = a_o;
+  a.packed = cu(packed);
+  a.pu = mu(pu);
+  a.pv = mu(pv);
+  a.dw = mu(dw);
+  a.z = mu(z);
+  a.du = mu(du);
+  a.dv = mu(dv);
+  a.slots = slots;
+  a.q_c = q_c;
   const int64_t units = static_cast<int64_t>(q_c) * ((slots + ow::kB2Rows - 1) / ow::kB2Rows);
   OW_CHECK_ARG(units < (int64_t(1) << 31), "too many units");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1953,6 +2040,57 @@ int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const floa
                            : ow::launch_bwd_chan_rd<128>(a, static_cast<int32_t>(units), dtype, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
+}
+
+// The routing of ow_bwd_channel_routed / ow_bwd_channel2_routed: plan checks and the row
+// arguments (slots = batch * q_s * 16).
+int routed128(const OwPlan* plan, int32_t batch, const void* x, const void* dy, const float* rscale,
+              const int32_t* token_index, int64_t& slots, int32_t& q_c, int32_t& d, const uint16_t*& rx,
+              const uint16_t*& rdy, const float*& rrs, const int32_t*& rtok, int32_t& rq_s, int32_t& rn_tok,
+              int32_t& rc_) {
+  int32_t q_s = 0;
+  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
+  d = plan->channel_tile;
+  const int32_t c = plan->channels;
+  OW_CHECK_SUPPORTED(plan->spatial_tile == kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
+  OW_CHECK_SUPPORTED(d == kB2D && c == q_c * kB2D && (plan->radix_level == 0 || q_c == 1),
+                     "routed backward needs the identity channel order with C = q_c * 128");
+  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 27), "bad batch %d", batch);
+  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * c * 2 < (int64_t(1) << 31),
+               "x, dy and g must be below 2 GiB (buffer addressing)");
+  OW_CHECK_ARG(x && dy && token_index, "tensor pointer is NULL");
+  slots = static_cast<int64_t>(batch) * q_s * kG;
+  rx = static_cast<const uint16_t*>(x);
+  rdy = static_cast<const uint16_t*>(dy);
+  rrs = rscale;
+  rtok = token_index;
+  rq_s = q_s;
+  rn_tok = plan->height * plan->width;
+  rc_ = c;
+  return OW_OK;
+}
+}  // namespace
+}  // namespace ow
+
+int ow_bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
+                   const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
+                   int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
+  return ow::bwd_channel(xt, dyt, a_u, a_v, a_o, packed, packed_bytes, pu, pv, dw, z, du, dv, slots, q_c, d, rd, dtype,
+                         ow::BwdChanArgs{}, stream);
+}
+
+int ow_bwd_channel_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
+                          const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
+                          const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
+                          void* dv, int32_t rd, int32_t dtype, void* stream) {
+  ow::BwdChanArgs r{};
+  int64_t slots = 0;
+  int32_t q_c = 0, d = 0;
+  if (int rc = ow::routed128(plan, batch, x, dy, rscale, token_index, slots, q_c, d, r.x, r.dy, r.rscale, r.tok,
+                             r.q_s, r.n_tok, r.channels))
+    return rc;
+  return ow::bwd_channel(nullptr, nullptr, a_u, a_v, a_o, packed, packed_bytes, pu, pv, dw, z, du, dv, slots, q_c, d,
+                         rd, dtype, r, stream);
 }
 
 int64_t ow_bwd_channel_partials(int64_t slots, int32_t q_c) {
@@ -2017,28 +2155,19 @@ int ow_bwd_channel2(const void* xt, const void* dyt, const void* z, const void* 
                           rd, dtype, ow::BwdChan2Args{}, stream);
 }
 
-int ow_bwd_channel2_routed(const void* xt, const void* dyt, const void* z, const void* du, const void* dv,
-                           const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
+int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, const void* z, const void* du,
+                           const void* dv, const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
                            const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
                            int64_t n_partial, int32_t rd, int32_t dtype, void* stream) {
-  int32_t q_s = 0, q_c = 0;
-  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
-  const int32_t d = plan->channel_tile, c = plan->channels;
-  OW_CHECK_SUPPORTED(plan->spatial_tile == ow::kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
-  OW_CHECK_SUPPORTED(d == ow::kB2D && c == q_c * ow::kB2D && (plan->radix_level == 0 || q_c == 1),
-                     "routed backward needs the identity channel order with C = q_c * 128");
-  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 27), "bad batch %d", batch);
-  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * c * 2 < (int64_t(1) << 31),
-               "g must be below 2 GiB (buffer addressing)");
-  OW_CHECK_ARG(token_index && g, "tensor pointer is NULL");
   ow::BwdChan2Args r{};
-  r.tok = token_index;
+  int64_t slots = 0;
+  int32_t q_c = 0, d = 0;
+  if (int rc = ow::routed128(plan, batch, x, dy, rscale, token_index, slots, q_c, d, r.x, r.dy, r.rscale, r.tok,
+                             r.q_s, r.n_tok, r.channels))
+    return rc;
+  OW_CHECK_ARG(g, "tensor pointer is NULL");
   r.g = static_cast<uint16_t*>(g);
-  r.q_s = q_s;
-  r.n_tok = plan->height * plan->width;
-  r.channels = c;
-  const int64_t slots = static_cast<int64_t>(batch) * q_s * ow::kG;
-  return ow::bwd_channel2(xt, dyt, z, du, dv, a_u, a_v, packed, packed_bytes, nullptr, partial, n_partial, slots, q_c,
+  return ow::bwd_channel2(x, dy, z, du, dv, a_u, a_v, packed, packed_bytes, nullptr, partial, n_partial, slots, q_c,
                           d, rd, dtype, r, stream);
 }
 
