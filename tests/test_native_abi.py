@@ -115,6 +115,50 @@ def test_fwd_chain_rejects_bad_arguments_without_touching_the_gpu() -> None:
         assert b"overlap" in lib.ow_last_error()
 
 
+def test_bwd_channel_entries_reject_bad_arguments_without_touching_the_gpu() -> None:
+    """The d = 128 backward entry points (tiles and routed forms) refuse unsupported plans, bad
+    sizes and NULL or unaligned buffers before any launch."""
+    lib = _native.lib()
+    bf16 = _native.OW_DTYPE_BF16
+    P = ctypes.c_void_p(16)
+    NB = lib.ow_bwd_packed_bytes(4, 128, 256)
+    assert NB == 4 * (256 // 32) * (3 * 128 // 16 + 6 * 128 // 32) * 1024
+    plan = _native.make_plan(14, 14, 512, 16, 128, "shifted", 0)
+    radix = _native.make_plan(14, 14, 512, 16, 128, "radix", 1)
+    d64 = _native.make_plan(28, 28, 256, 16, 64, "local", 0)
+    slots = 2 * 13 * 16
+    n_part = lib.ow_bwd_channel_partials(slots, 4)
+    assert n_part > 0 and lib.ow_bwd_channel_partials(slots + 8, 4) == 0
+
+    def chan(x=P, nb=NB, rd=256, dtype=bf16, s=slots):
+        return lib.ow_bwd_channel(x, P, P, P, P, P, nb, P, P, P, P, P, P, s, 4, 128, rd, dtype, None)
+
+    def chan_routed(p=plan, x=P, nb=NB, batch=2):
+        return lib.ow_bwd_channel_routed(x, P, None, P, ctypes.byref(p), batch, P, P, P, P, nb, P, P, P, P, P, P,
+                                         256, bf16, None)
+
+    def chan2_routed(p=plan, g=P, npart=n_part, batch=2):
+        return lib.ow_bwd_channel2_routed(P, P, None, P, P, P, P, P, P, NB, P, ctypes.byref(p), batch, g, P, npart,
+                                          256, bf16, None)
+
+    assert chan(rd=192) == 2 and b"rd in {128, 256}" in lib.ow_last_error()
+    assert chan(dtype=_native.OW_DTYPE_F32) == 2
+    assert chan(s=slots + 8) == 1 and b"multiple of 16" in lib.ow_last_error()
+    assert chan(nb=NB - 2) == 1 and b"packed backward weights" in lib.ow_last_error()
+    assert chan(x=None) == 1 and b"NULL" in lib.ow_last_error()
+    assert chan(x=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
+    assert chan(s=0) == 0  # empty: nothing launched
+    assert chan_routed(p=radix) == 2 and b"identity channel order" in lib.ow_last_error()
+    assert chan_routed(p=d64) == 2
+    assert chan_routed(x=None) == 1 and b"NULL" in lib.ow_last_error()
+    assert chan_routed(batch=-1) == 1 and b"bad batch" in lib.ow_last_error()
+    assert chan_routed(batch=1 << 22) == 1 and b"2 GiB" in lib.ow_last_error()
+    assert chan2_routed(p=radix) == 2 and b"identity channel order" in lib.ow_last_error()
+    assert chan2_routed(g=None) == 1 and b"NULL" in lib.ow_last_error()
+    assert chan2_routed(npart=n_part + 1) == 1 and b"ow_bwd_channel_partials" in lib.ow_last_error()
+    assert chan2_routed(g=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
+
+
 def test_hip_is_supported_reasons_on_cpu() -> None:
     plan = build_route_plan(14, 14, 512, 16, 128, "local")
     ok, reason = hip_is_supported(torch.randn(1, 14, 14, 512), plan, torch.randn(4, 128, 256))
