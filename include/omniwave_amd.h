@@ -338,9 +338,10 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
 /* The d = 64 backward in one kernel (replaces ow_tile_mix x4, ow_tile_outer x3 and the
  * channel-side GEMMs; the reference's fp32 autograd recompute, omniweave/ops/triton.py:256-292):
  * from the routed tiles X' and dY ([q_c][slots][64], ow_bwd_gather) and the fp32 [16][16] token
- * matrices, per 32-slot pair: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw
- * for the parameter-gradient GEMMs), U'^T, V'^T, dZ^T and the gate backward per 32-row chunk
- * (z, du, dv stored to [q_c][slots][rd]), W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
+ * matrices, per 32-slot pair: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw,
+ * [q_c][slots][64] elements), U'^T, V'^T, dZ^T and the gate backward per 32-row chunk (z, du, dv,
+ * [q_c][slots][rd] elements) -- those six in the fragment order ow_bwd_param_reduce64 reads,
+ * not row-major --, W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
  * dX' = A_u^T dP_u + A_v^T dP_v (stored to dxt), and the token-matrix gradients dA_u = sum
  * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
  * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c); element 16 t + k),
@@ -395,6 +396,20 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
                            const void* dv, const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
                            const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
                            int64_t n_partial, int32_t rd, int32_t dtype, void* stream);
+
+/* Parameter-gradient reduction of the d = 64 backward (replaces the slot-reduction GEMMs over
+ * the intermediates): from pu, pv, dw ([q_c][slots][64]) and z, du, dv ([q_c][slots][rd]) as
+ * ow_bwd_fused / ow_bwd_fused_routed write them (per 32-slot pair, 32x32x16 operand fragments
+ * whose K runs over the pair's slots), per workgroup w the sums over its slots of
+ * dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and dB_o'' = Z^T dW' ([rd][64]) into
+ * partial[w] (fp32, those three in that order, 3 * 64 * rd floats); workgroup w covers channel
+ * group w % q_c, so the caller adds rows w = q, q + q_c, .. for group q
+ * (w < n_partial = ow_bwd_param_reduce64_partials(slots, q_c), a multiple of q_c).
+ * slots % 32 == 0, rd in {128, 256}, bf16 / f16. */
+int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c);
+int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
+                          const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
+                          int32_t dtype, void* stream);
 
 /* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
  * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and

@@ -18,7 +18,8 @@ accumulation, entirely on the HIP stream of the gradient:
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
   ``ow_bwd_gate``;
-* the parameter-gradient reductions over slots are batched GEMMs in both cases.
+* the parameter-gradient reductions over slots: for d = 64 ``ow_bwd_param_reduce64`` over the
+  fused kernel's fragment-ordered intermediates, otherwise batched GEMMs.
 
 Gradients are formed for the folded operands the forward evaluates (B_u'' = -log2(e) w B_u,
 B_v'' = -ln(2) w B_v, B_o'' = B_o diag(gamma), SiLU(U) V = U'V' / (1 + 2^U')) and mapped back
@@ -202,9 +203,16 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                 del xt, dyt
             g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
-            d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
-            d_bv = _slot_reduce(pv, dv)
-            d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
+            # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates.
+            n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c)
+            red = torch.empty(n_red, 3 * d * rd, dtype=torch.float32, device=dev)
+            _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
+                                                    du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,
+                                                    rd, code, stream), "ow_bwd_param_reduce64")
+            g_b3 = red.view(n_red // q_c, q_c, 3 * d * rd).sum(dim=0)
+            d_bu = g_b3[:, :d * rd].reshape(q_c, d, rd).contiguous()
+            d_bv = g_b3[:, d * rd:2 * d * rd].reshape(q_c, d, rd).contiguous()
+            d_bo = g_b3[:, 2 * d * rd:].reshape(q_c, rd, d).contiguous()
             del z, du, dv, pu, pv, dw
         elif d == 128 and dtype != torch.float32:
             # Two kernels over 256-slot units: (1) token side P_u, P_v, dW', then U', V', dZ per

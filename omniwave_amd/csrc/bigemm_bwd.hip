@@ -613,6 +613,32 @@ __device__ __forceinline__ uint32_t scale2(uint32_t v, float r) {
   return Ty::pack2(Ty::to_f32(static_cast<uint16_t>(v & 0xffffu)) * r, Ty::to_f32(static_cast<uint16_t>(v >> 16)) * r);
 }
 
+// The d = 64 backward's per-pair intermediates (P_u, P_v, dW' [.. 64], Z, dU', dV' [.. rd]) are
+// kept in HBM as slot-K fragments: for the 32 slots of a pair and each 32-wide block b of the
+// other dimension (channels or expanded rows), two 32x32x16 operand fragments (K-step g = slots
+// 16 g ..), lane (l32, hh) holding entry 32 b + l32 at slots 16 g + kord(j, hh), j < 8: 1 KB each,
+// at element (pair (2 b + g)) * 512 + 8 lane of the pair's 32 * width elements.  The fused kernel
+// writes them with coalesced 16-byte stores and the parameter-gradient reduction reads them as
+// MFMA operands directly (P^T dU' etc. contract over the slots).
+// Stores fragments of blocks b0 .. b0 + KS / 2 - 1 of a [32 slots][..] tile staged in LDS
+// (at(r, c): byte address of slot r, entry c within those blocks) at pair base dst.
+// One fragment at a time (the reads of pair_xt_tr, each fragment stored before the next is read),
+// so the caller's live registers grow by one fragment only.
+template <int KS, class At>
+__device__ __forceinline__ void pair_frag_store(At at, int lane, uint16_t* dst, int b0) {
+  const int hh = lane >> 5, l16 = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+  for (int cb = 0; cb < KS / 2; ++cb) {
+    const int c = 32 * cb + 16 * half + 4 * (l16 & 3);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int r = 16 * g + 4 * hh + (l16 >> 2);
+      const u32x2 lo = lds_read_tr16(at(r, c)), hi = lds_read_tr16(at(r + 8, c));
+      *reinterpret_cast<u32x4*>(dst + (2 * (b0 + cb) + g) * kFragElems + 8 * lane) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  }
+}
+
 // Token-operand fragment of a 16x16 token matrix (lane (t, hh) slot j = M[t % 16][kord(j, hh)],
 // or the transpose with T), rounded to Ty.
 template <class Ty, bool T>
@@ -767,8 +793,10 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     if (live) {
       // P_u, P_v, dW' through the wave's tile (read completely by the token side; no copy targets
       // it before the chunk loop's first barrier): lane = slot l32, K-step ks slot j -> channel
-      // 16 ks + kord(j, hh); stored as 128-byte rows, eight lanes per slot.
+      // 16 ks + kord(j, hh), staged [32 slots][64 channels] and stored as the pair's slot-K
+      // fragments (pair_frag_store), four 1 KB stores per tensor.
       wave_lds_sync();
+      const uint32_t txa = lds_addr(tx);
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
         const u32x4(&pk)[kBwdKS] = t == 0 ? Pu : t == 1 ? Pv : Dw;
@@ -779,12 +807,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
           *reinterpret_cast<u32x2*>(&tx[l32 * kLd + 16 * ks + 8 + 4 * hh]) = u32x2{pk[ks][2], pk[ks][3]};
         }
         wave_lds_sync();
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int sl = 8 * k + (lane >> 3), part = lane & 7;
-          *reinterpret_cast<u32x4*>(dst + (slot0 + sl) * kBwdD + 8 * part) =
-              *reinterpret_cast<const u32x4*>(&tx[sl * kLd + 8 * part]);
-        }
+        pair_frag_store<kBwdKS>([&](int r, int c) { return txa + 2u * static_cast<uint32_t>(r * kLd + c); }, lane,
+                                dst + slot0 * kBwdD, 0);
         wave_lds_sync();
       }
     }
@@ -830,9 +854,10 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       }
       if (live) {
         // Registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32: each
-        // tensor staged [32 slots][32 rows] in the wave's buffer, then stored as 64-byte row
-        // pieces (four lanes per slot), 6 stores per chunk.
+        // tensor staged [32 slots][32 rows] in the wave's buffer, then stored as the pair's two
+        // slot-K fragments of row block ec (pair_frag_store), 6 stores per chunk.
         uint16_t* zw = zst[wave];
+        const uint32_t zwa = lds_addr(zw);
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
           const u32x4(&pk)[2] = t == 0 ? zs : t == 1 ? dus : dvs;
@@ -842,12 +867,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
             *reinterpret_cast<u32x2*>(&zw[l32 * kZSt + 8 * b + 4 * hh]) =
                 u32x2{pk[b >> 1][2 * (b & 1)], pk[b >> 1][2 * (b & 1) + 1]};
           wave_lds_sync();
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int sl = 16 * h + (lane >> 2), part = lane & 3;
-            *reinterpret_cast<u32x4*>(dst + (slot0 + sl) * RD + 32 * ec + 8 * part) =
-                *reinterpret_cast<const u32x4*>(&zw[sl * kZSt + 8 * part]);
-          }
+          pair_frag_store<2>([&](int r, int c) { return zwa + 2u * static_cast<uint32_t>(r * kZSt + c); }, lane,
+                             dst + slot0 * RD, ec);
           wave_lds_sync();  // the reads are done before the next tensor is staged
         }
       }
@@ -1003,6 +1024,109 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
   if (int rc = hip_status(hipGetLastError(), "bwd_fused_d64_kernel launch")) return rc;
   clear_error();
   return OW_OK;
+}
+
+// ---- Parameter-gradient reduction, d = 64 ------------------------------------------------
+// dB_u'' = sum over slots of P_u^T dU', dB_v'' = P_v^T dV' ([64][rd]), dB_o'' = Z^T dW' ([rd][64])
+// per channel group, from the slot-K fragments of ow_bwd_fused (pair_frag_store): a fragment
+// is a 32x32x16 operand whose K runs over 16 slots, so each pair contributes two K steps and
+// no data moves through LDS.  Workgroup b takes group b % q_c and pairs b / q_c, + G / q_c, ..
+// (G = gridDim.x, a multiple of q_c); its NCH = rd / 32 waves own one block of 32 expanded rows
+// each (wave e: dB_u'', dB_v'' columns 32 e .., dB_o'' rows 32 e ..), accumulate in fp32
+// registers and write the workgroup's sums to partial[b] (dB_u'' [64][rd], dB_v'' [64][rd],
+// dB_o'' [rd][64]), which the caller adds over the workgroups of each group.  The next pair's
+// fragments are loaded while the current pair's 12 MFMAs run.
+struct ParamReduceArgs {
+  const uint16_t* pu;  // fragments, [q_c][pairs][32 * 64]
+  const uint16_t* pv;
+  const uint16_t* dw;
+  const uint16_t* z;   // fragments, [q_c][pairs][32 * rd]
+  const uint16_t* du;
+  const uint16_t* dv;
+  float* partial;      // [gridDim][2 * 64 * rd + rd * 64]
+  int64_t pairs;       // per group
+  int32_t q_c;
+};
+
+template <class Ty, int NCH>
+__global__ void __launch_bounds__(64 * NCH) bwd_param_reduce64_kernel(ParamReduceArgs a) {
+  constexpr int RD = 32 * NCH;
+  const int lane = threadIdx.x & 63;
+  const int e = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's expanded-row block
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int q = blockIdx.x % a.q_c;
+  const int64_t pstep = gridDim.x / a.q_c;
+  struct Frags {
+    u32x4 pu[2][2], pv[2][2], dw[2][2];  // [channel block][K step]
+    u32x4 du[2], dv[2], z[2];            // row block e, [K step]
+  };
+  auto load = [&](int64_t pair, Frags& f) {
+    const int64_t pb = static_cast<int64_t>(q) * a.pairs + pair;
+    const int64_t o64 = pb * 32 * kBwdD + 8 * lane, orr = pb * 32 * RD + 8 * lane;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int64_t o = o64 + (2 * b + g) * kFragElems;
+        f.pu[b][g] = *reinterpret_cast<const u32x4*>(a.pu + o);
+        f.pv[b][g] = *reinterpret_cast<const u32x4*>(a.pv + o);
+        f.dw[b][g] = *reinterpret_cast<const u32x4*>(a.dw + o);
+      }
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int64_t o = orr + (2 * e + g) * kFragElems;
+      f.du[g] = *reinterpret_cast<const u32x4*>(a.du + o);
+      f.dv[g] = *reinterpret_cast<const u32x4*>(a.dv + o);
+      f.z[g] = *reinterpret_cast<const u32x4*>(a.z + o);
+    }
+  };
+  f32x16 U[2] = {}, V[2] = {}, O[2] = {};
+  int64_t pair = blockIdx.x / a.q_c;
+  Frags cur, nxt;
+  if (pair < a.pairs) load(pair, cur);
+  for (; pair < a.pairs; pair += pstep) {
+    if (pair + pstep < a.pairs) load(pair + pstep, nxt);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        U[m] = Ty::mma32(cur.pu[m][g], cur.du[g], U[m]);  // channels 32 m .. x rows 32 e ..
+        V[m] = Ty::mma32(cur.pv[m][g], cur.dv[g], V[m]);
+        O[m] = Ty::mma32(cur.z[g], cur.dw[m][g], O[m]);   // rows 32 e .. x channels 32 m ..
+      }
+    }
+    cur = nxt;
+  }
+  mfma_drain();
+  // Accumulator register i of lane (l32, hh): row kord(i, hh) of the product's first operand,
+  // column l32 of the second.
+  float* out = a.partial + static_cast<int64_t>(blockIdx.x) * (3 * kBwdD * RD);
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 8 * (i >> 2) + 4 * hh + (i & 3);
+      out[(32 * m + r) * RD + 32 * e + l32] = U[m][i];
+      out[kBwdD * RD + (32 * m + r) * RD + 32 * e + l32] = V[m][i];
+      out[2 * kBwdD * RD + (32 * e + r) * kBwdD + 32 * m + l32] = O[m][i];
+    }
+}
+
+int64_t bwd_param_reduce64_grid(int64_t pairs, int32_t q_c) {
+  // Two workgroups per CU, at least one pair each; a multiple of q_c.
+  int64_t per_q = (2 * static_cast<int64_t>(device_cus()) + q_c - 1) / q_c;
+  if (per_q > pairs) per_q = pairs;
+  return per_q * q_c;
+}
+
+template <int NCH>
+int launch_param_reduce64(const ParamReduceArgs& a, int64_t grid, int32_t dtype, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<BF16, NCH>), g, dim3(64 * NCH), 0, s, a);
+  else
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, NCH>), g, dim3(64 * NCH), 0, s, a);
+  return hip_status(hipGetLastError(), "bwd_param_reduce64_kernel launch");
 }
 
 // ---- Channel side of the backward, d = 128: token side, U'/V'/dZ and the gate -------------
@@ -1949,6 +2073,36 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
   if (int rc = ow::hip_status(hipGetLastError(), "pack_bwd_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;
+}
+
+int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c) {
+  if (q_c < 1 || slots <= 0 || slots % 32) return 0;
+  return ow::bwd_param_reduce64_grid(slots / 32, q_c);
+}
+
+int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du, const void* dv,
+                          float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd, int32_t dtype,
+                          void* stream) {
+  OW_CHECK_SUPPORTED(rd == 128 || rd == 256, "parameter reduction needs rd in {128, 256} (got %d)", rd);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 32 == 0, "bad shape q_c=%d slots=%lld (multiple of 32)", q_c,
+               (long long)slots);
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  const int64_t grid = ow_bwd_param_reduce64_partials(slots, q_c);
+  OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_param_reduce64_partials)",
+               (long long)n_partial, (long long)grid);
+  OW_CHECK_ARG(pu && pv && dw && z && du && dv && partial, "tensor pointer is NULL");
+  for (const void* p : {pu, pv, dw, z, du, dv})
+    OW_CHECK_ARG(ow::aligned16(p), "fragment buffers must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  ow::ParamReduceArgs a{cu(pu), cu(pv), cu(dw), cu(z), cu(du), cu(dv), partial, slots / 32, q_c};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rc = rd == 128 ? ow::launch_param_reduce64<4>(a, grid, dtype, s) : ow::launch_param_reduce64<8>(a, grid, dtype, s);
+  if (rc == OW_OK) ow::clear_error();
+  return rc;
 }
 
 // Workgroups (and partial rows) of ow_bwd_fused: every workgroup loops over rounds of four
