@@ -401,12 +401,12 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
  * the intermediates): from pu, pv, dw ([q_c][slots][64]) and z, du, dv ([q_c][slots][rd]) as
  * ow_bwd_fused / ow_bwd_fused_routed write them (per 32-slot pair, 32x32x16 operand fragments
  * whose K runs over the pair's slots), per workgroup w the sums over its slots of
- * dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and dB_o'' = Z^T dW' ([rd][64]) into
- * partial[w] (fp32, those three in that order, 3 * 64 * rd floats); workgroup w covers channel
- * group w % q_c, so the caller adds rows w = q, q + q_c, .. for group q
- * (w < n_partial = ow_bwd_param_reduce64_partials(slots, q_c), a multiple of q_c).
+ * dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and dB_o'' = Z^T dW' ([rd][64]) over
+ * slot ranges into partial rows (fp32, those three in that order, 3 * 64 * rd floats); row w
+ * covers channel group w % q_c, so the caller adds rows w = q, q + q_c, .. for group q
+ * (w < n_partial = ow_bwd_param_reduce64_partials(slots, q_c, rd), a multiple of q_c).
  * slots % 32 == 0, rd in {128, 256}, bf16 / f16. */
-int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c);
+int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c, int32_t rd);
 int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
                           const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
                           int32_t dtype, void* stream);

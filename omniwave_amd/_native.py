@@ -170,7 +170,7 @@ _SIGNATURES = {
         [ctypes.c_void_p] * 9 + [ctypes.c_size_t] + [ctypes.c_void_p] * 2 + [ctypes.c_int32]
         + [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
-    "ow_bwd_param_reduce64_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32]),
+    "ow_bwd_param_reduce64_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
     "ow_bwd_param_reduce64": (
         ctypes.c_int,
         [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,

@@ -204,7 +204,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates.
-            n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c)
+            n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c, rd)
             red = torch.empty(n_red, 3 * d * rd, dtype=torch.float32, device=dev)
             _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
                                                     du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,

@@ -1029,13 +1029,18 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
 // ---- Parameter-gradient reduction, d = 64 ------------------------------------------------
 // dB_u'' = sum over slots of P_u^T dU', dB_v'' = P_v^T dV' ([64][rd]), dB_o'' = Z^T dW' ([rd][64])
 // per channel group, from the slot-K fragments of ow_bwd_fused (pair_frag_store): a fragment
-// is a 32x32x16 operand whose K runs over 16 slots, so each pair contributes two K steps and
-// no data moves through LDS.  Workgroup b takes group b % q_c and pairs b / q_c, + G / q_c, ..
-// (G = gridDim.x, a multiple of q_c); its NCH = rd / 32 waves own one block of 32 expanded rows
-// each (wave e: dB_u'', dB_v'' columns 32 e .., dB_o'' rows 32 e ..), accumulate in fp32
-// registers and write the workgroup's sums to partial[b] (dB_u'' [64][rd], dB_v'' [64][rd],
-// dB_o'' [rd][64]), which the caller adds over the workgroups of each group.  The next pair's
-// fragments are loaded while the current pair's 12 MFMAs run.
+// is a 32x32x16 operand whose K runs over 16 slots, so each pair contributes two K steps.
+// Workgroup b takes group q = b % q_c, row half h = (b / q_c) % H (H = rd / 128) and pairs s,
+// s + S, .. (s = b / (q_c H), S = gridDim.x / (q_c H)).  Per pair it needs 36 fragments: the
+// 12 channel-side ones (P_u, P_v, dW') and 24 row-side ones (dU', dV', Z of its 4 row blocks),
+// copied by its 12 waves (three each, buffer_load ... lds, untracked) into one of kRedStages
+// LDS stages, kRedStages - 1 pairs ahead; one barrier per pair.  Wave w computes product
+// t = w / 4 (0: dB_u'', 1: dB_v'', 2: dB_o'' as its transpose dW'^T Z) for row block
+// e = w % 4 + 4 h and both 32-channel blocks, in fp32 registers.  Every workgroup runs the same
+// number of pairs per range; pairs past the end read as zero (out-of-range offsets) and add
+// nothing.  The sums go to the workgroup's blocks of partial[s q_c + q] (dB_u'' [64][rd],
+// dB_v'' [64][rd], dB_o'' [rd][64]; the H row halves fill disjoint blocks), which the caller
+// adds over s for each group.
 struct ParamReduceArgs {
   const uint16_t* pu;  // fragments, [q_c][pairs][32 * 64]
   const uint16_t* pv;
@@ -1043,89 +1048,110 @@ struct ParamReduceArgs {
   const uint16_t* z;   // fragments, [q_c][pairs][32 * rd]
   const uint16_t* du;
   const uint16_t* dv;
-  float* partial;      // [gridDim][2 * 64 * rd + rd * 64]
+  float* partial;      // [rows][2 * 64 * rd + rd * 64]
   int64_t pairs;       // per group
   int32_t q_c;
 };
+constexpr int kReduceWaves = 12;
+constexpr int kRedFrags = 36;   // fragments per pair and workgroup
+constexpr int kRedStages = 4;
 
 template <class Ty, int NCH>
-__global__ void __launch_bounds__(64 * NCH) bwd_param_reduce64_kernel(ParamReduceArgs a) {
+__global__ void __launch_bounds__(64 * kReduceWaves) bwd_param_reduce64_kernel(ParamReduceArgs a) {
   constexpr int RD = 32 * NCH;
+  constexpr int H = NCH / 4;  // row halves
+  __shared__ __attribute__((aligned(16))) u32x4 st[kRedStages][kRedFrags][64];
   const int lane = threadIdx.x & 63;
-  const int e = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's expanded-row block
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
-  const int q = blockIdx.x % a.q_c;
-  const int64_t pstep = gridDim.x / a.q_c;
-  struct Frags {
-    u32x4 pu[2][2], pv[2][2], dw[2][2];  // [channel block][K step]
-    u32x4 du[2], dv[2], z[2];            // row block e, [K step]
-  };
-  auto load = [&](int64_t pair, Frags& f) {
-    const int64_t pb = static_cast<int64_t>(q) * a.pairs + pair;
-    const int64_t o64 = pb * 32 * kBwdD + 8 * lane, orr = pb * 32 * RD + 8 * lane;
+  const int q = blockIdx.x % a.q_c, h = (blockIdx.x / a.q_c) % H;
+  const int t = w >> 2, e0 = w & 3;
+  const int64_t s0 = blockIdx.x / (a.q_c * H);
+  const int64_t pstep = gridDim.x / (a.q_c * H);
+  const int64_t n_iter = (a.pairs - s0 + pstep - 1) / pstep;  // same for every wave
+  const uint32_t cbytes = static_cast<uint32_t>(a.q_c * a.pairs * 32 * kBwdD * 2);
+  const uint32_t rbytes = static_cast<uint32_t>(a.q_c * a.pairs * 32 * RD * 2);
+  // This wave's three copies per pair: fragments f = w, w + 12, w + 24 of the pair's 36
+  // (f < 12: channel-side tensor f / 4, fragment f % 4; else row-side j = f - 12: tensor j / 8,
+  // local row block (j % 8) / 2, K step j % 2).
+  __amdgpu_buffer_rsrc_t rs[3];
+  uint32_t fo[3];  // byte offset of the fragment within the pair
+  bool rside[3];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int64_t o = o64 + (2 * b + g) * kFragElems;
-        f.pu[b][g] = *reinterpret_cast<const u32x4*>(a.pu + o);
-        f.pv[b][g] = *reinterpret_cast<const u32x4*>(a.pv + o);
-        f.dw[b][g] = *reinterpret_cast<const u32x4*>(a.dw + o);
-      }
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int64_t o = orr + (2 * e + g) * kFragElems;
-      f.du[g] = *reinterpret_cast<const u32x4*>(a.du + o);
-      f.dv[g] = *reinterpret_cast<const u32x4*>(a.dv + o);
-      f.z[g] = *reinterpret_cast<const u32x4*>(a.z + o);
+  for (int c = 0; c < 3; ++c) {
+    const int f = w + kReduceWaves * c;
+    if (f < 12) {
+      const int tc = f >> 2;
+      rs[c] = buffer_rsrc(tc == 0 ? a.pu : tc == 1 ? a.pv : a.dw, cbytes);
+      fo[c] = static_cast<uint32_t>((f & 3) * kFragElems * 2);
+      rside[c] = false;
+    } else {
+      const int j = f - 12, tr = j >> 3, k = (j & 7) >> 1, g = j & 1;
+      rs[c] = buffer_rsrc(tr == 0 ? a.du : tr == 1 ? a.dv : a.z, rbytes);
+      fo[c] = static_cast<uint32_t>((2 * (k + 4 * h) + g) * kFragElems * 2);
+      rside[c] = true;
     }
-  };
-  f32x16 U[2] = {}, V[2] = {}, O[2] = {};
-  int64_t pair = blockIdx.x / a.q_c;
-  Frags cur, nxt;
-  if (pair < a.pairs) load(pair, cur);
-  for (; pair < a.pairs; pair += pstep) {
-    if (pair + pstep < a.pairs) load(pair + pstep, nxt);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        U[m] = Ty::mma32(cur.pu[m][g], cur.du[g], U[m]);  // channels 32 m .. x rows 32 e ..
-        V[m] = Ty::mma32(cur.pv[m][g], cur.dv[g], V[m]);
-        O[m] = Ty::mma32(cur.z[g], cur.dw[m][g], O[m]);   // rows 32 e .. x channels 32 m ..
-      }
-    }
-    cur = nxt;
   }
+  auto issue = [&](int64_t i) {  // copies of the workgroup's i-th pair into stage i % kRedStages
+    const int64_t pair = s0 + i * pstep;
+    const bool ok = pair < a.pairs;
+    const uint32_t pb = static_cast<uint32_t>(q * a.pairs + pair);
+    const uint32_t stage = lds_addr(&st[i % kRedStages][0][0]);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const uint32_t base = rside[c] ? pb * 32u * RD * 2u : pb * 32u * kBwdD * 2u;
+      tile_copy(rs[c], ok ? base + fo[c] + 16u * lane : kOffOut,
+                stage + static_cast<uint32_t>((w + kReduceWaves * c) * 1024));
+    }
+  };
+  f32x16 acc[2] = {};
+#pragma unroll
+  for (int i = 0; i < kRedStages - 1; ++i) issue(i);
+  for (int64_t i = 0; i < n_iter; ++i) {
+    // This wave's copies of pair i landed (those of pairs i + 1 .. i + kRedStages - 2 may be in
+    // flight); the barrier makes every wave's visible and means every wave is done with stage
+    // (i - 1) % kRedStages, which pair i + kRedStages - 1 takes.
+    wait_vmcnt<3 * (kRedStages - 2)>();
+    __syncthreads();
+    issue(i + kRedStages - 1);
+    const u32x4(*sf)[64] = st[i % kRedStages];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const u32x4 r = sf[12 + 8 * t + 2 * e0 + g][lane];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) acc[m] = Ty::mma32(sf[4 * t + 2 * m + g][lane], r, acc[m]);
+    }
+  }
+  wait_vmcnt<0>();  // the trailing copies (past the end: zeros) are done before the exit
   mfma_drain();
-  // Accumulator register i of lane (l32, hh): row kord(i, hh) of the product's first operand,
-  // column l32 of the second.
-  float* out = a.partial + static_cast<int64_t>(blockIdx.x) * (3 * kBwdD * RD);
+  // Accumulator register i of lane (l32, hh): channel 32 m + kord(i, hh), row 32 e + l32.
+  float* out = a.partial + (s0 * a.q_c + q) * (3 * kBwdD * RD);
+  const int e = e0 + 4 * h;
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int r = 8 * (i >> 2) + 4 * hh + (i & 3);
-      out[(32 * m + r) * RD + 32 * e + l32] = U[m][i];
-      out[kBwdD * RD + (32 * m + r) * RD + 32 * e + l32] = V[m][i];
-      out[2 * kBwdD * RD + (32 * e + r) * kBwdD + 32 * m + l32] = O[m][i];
+      const int c = 32 * m + 8 * (i >> 2) + 4 * hh + (i & 3), r = 32 * e + l32;
+      const int64_t o = t < 2 ? t * kBwdD * RD + c * RD + r : 2 * kBwdD * RD + r * kBwdD + c;
+      out[o] = acc[m][i];
     }
 }
 
-int64_t bwd_param_reduce64_grid(int64_t pairs, int32_t q_c) {
-  // Two workgroups per CU, at least one pair each; a multiple of q_c.
-  int64_t per_q = (2 * static_cast<int64_t>(device_cus()) + q_c - 1) / q_c;
-  if (per_q > pairs) per_q = pairs;
-  return per_q * q_c;
+// Pair ranges S of the reduction (partial rows S q_c; grid S q_c rd / 128): about one
+// workgroup of 12 waves per CU, at least one pair per range.
+int64_t bwd_param_reduce64_ranges(int64_t pairs, int32_t q_c, int32_t rd) {
+  const int64_t per = static_cast<int64_t>(q_c) * (rd / 128);
+  int64_t ranges = (static_cast<int64_t>(device_cus()) + per - 1) / per;
+  return ranges > pairs ? pairs : ranges;
 }
 
 template <int NCH>
 int launch_param_reduce64(const ParamReduceArgs& a, int64_t grid, int32_t dtype, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL((bwd_param_reduce64_kernel<BF16, NCH>), g, dim3(64 * NCH), 0, s, a);
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<BF16, NCH>), g, dim3(64 * kReduceWaves), 0, s, a);
   else
-    hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, NCH>), g, dim3(64 * NCH), 0, s, a);
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, NCH>), g, dim3(64 * kReduceWaves), 0, s, a);
   return hip_status(hipGetLastError(), "bwd_param_reduce64_kernel launch");
 }
 
@@ -2075,9 +2101,9 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
   return OW_OK;
 }
 
-int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c) {
-  if (q_c < 1 || slots <= 0 || slots % 32) return 0;
-  return ow::bwd_param_reduce64_grid(slots / 32, q_c);
+int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c, int32_t rd) {
+  if (q_c < 1 || slots <= 0 || slots % 32 || (rd != 128 && rd != 256)) return 0;
+  return ow::bwd_param_reduce64_ranges(slots / 32, q_c, rd) * q_c;
 }
 
 int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du, const void* dv,
@@ -2091,9 +2117,12 @@ int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const 
     ow::clear_error();
     return OW_OK;
   }
-  const int64_t grid = ow_bwd_param_reduce64_partials(slots, q_c);
-  OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_param_reduce64_partials)",
-               (long long)n_partial, (long long)grid);
+  const int64_t rows = ow_bwd_param_reduce64_partials(slots, q_c, rd);
+  OW_CHECK_ARG(n_partial == rows, "partial holds %lld rows; %lld needed (ow_bwd_param_reduce64_partials)",
+               (long long)n_partial, (long long)rows);
+  const int64_t grid = rows * (rd / 128);
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31),
+               "intermediates of %lld slots exceed 2 GiB (buffer addressing)", (long long)slots);
   OW_CHECK_ARG(pu && pv && dw && z && du && dv && partial, "tensor pointer is NULL");
   for (const void* p : {pu, pv, dw, z, du, dv})
     OW_CHECK_ARG(ow::aligned16(p), "fragment buffers must be 16-byte aligned");

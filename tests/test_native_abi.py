@@ -158,6 +158,22 @@ def test_bwd_channel_entries_reject_bad_arguments_without_touching_the_gpu() -> 
     assert chan2_routed(npart=n_part + 1) == 1 and b"ow_bwd_channel_partials" in lib.ow_last_error()
     assert chan2_routed(g=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
 
+    # The d = 64 parameter-gradient reduction over the fused kernel's fragment-ordered tiles.
+    n_red = lib.ow_bwd_param_reduce64_partials(64 * 32, 2, 128)
+    assert n_red > 0 and n_red % 2 == 0
+    assert lib.ow_bwd_param_reduce64_partials(64 * 32 + 16, 2, 128) == 0
+    assert lib.ow_bwd_param_reduce64_partials(64 * 32, 2, 192) == 0
+
+    def reduce64(n=n_red, s=64 * 32, rd=128, pu=P):
+        return lib.ow_bwd_param_reduce64(pu, P, P, P, P, P, P, n, s, 2, rd, bf16, None)
+
+    assert reduce64(rd=192) == 2 and b"rd in {128, 256}" in lib.ow_last_error()
+    assert reduce64(s=64 * 32 + 16) == 1 and b"multiple of 32" in lib.ow_last_error()
+    assert reduce64(n=n_red + 2) == 1 and b"ow_bwd_param_reduce64_partials" in lib.ow_last_error()
+    assert reduce64(pu=None) == 1 and b"NULL" in lib.ow_last_error()
+    assert reduce64(pu=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
+    assert reduce64(s=0, n=0) == 0  # empty: nothing launched
+
 
 def test_hip_is_supported_reasons_on_cpu() -> None:
     plan = build_route_plan(14, 14, 512, 16, 128, "local")
