@@ -20,10 +20,12 @@
 //     (omniweave/models/routing.py:107-121): the wave's row pieces go through v_perm_b32 to
 //     its group's elements (strided_pack), in order, so the tile and the math are the same;
 //   * the residual round(x + round(delta)) is written into the tile, which the wave then stores
-//     as whole 16-byte row pieces, or (SG) as one full row per 2-byte store instruction (the
-//     other group's wave, on the same XCD, fills the rest of each line in L2).  Those stores
-//     cost ~8 us at 56x56x128 x 128 images over 16-byte ones, and ~11 us at q_c = 4, where the
-//     resident kernel is faster: the interleaved q_c = 4 groups take that kernel.
+//     as whole 16-byte row pieces.  SG: one workgroup of eight waves holds both groups' weights
+//     (96 KB) and computes four pairs at a time, waves w and w ^ 4 the two groups of one pair;
+//     after a workgroup barrier each of the two stores half of the pair's rows whole, the two
+//     tiles' columns interleaved with v_perm_b32.  (Each group storing its own columns as 2-byte
+//     elements cost ~8 us at 56x56x128 x 128 images, and ~11 us at q_c = 4, where four groups'
+//     weights do not fit one workgroup: the interleaved q_c = 4 groups take the resident kernel.)
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -43,12 +45,15 @@ constexpr int kGroupFrags = kNCH * kFrCh;     // 48 fragments = 48 KB per channe
 constexpr int kLdt = kD + 8;                  // tile row stride (elements)
 constexpr int kWavesWg = 4;
 
+// NG channel groups' weights and NW waves' tiles: (1, 4) for the per-group workgroups, (2, 8) for
+// the interleaved q_c = 2 groups (SG), where one workgroup holds both groups of four pairs.
+template <int NG, int NW>
 struct WaveLds {
-  u32x4 w[kGroupFrags][64];        // the group's packed weights
+  u32x4 w[NG * kGroupFrags][64];   // the groups' packed weights
   u32x4 tok_ops[3][64];            // token-side operand rows A_u, A_v, A_o (read per unit)
-  uint16_t tile[kWavesWg][32 * kLdt];  // per wave: the pair's rows, group columns
-  float rsc[kWavesWg][32];         // per wave: RMSNorm scale of each token of the pair
-  int32_t rows[kWavesWg][32];      // per wave: output row of each token (-1: not stored)
+  uint16_t tile[NW][32 * kLdt];    // per wave: the pair's rows, group columns
+  float rsc[NW][32];               // per wave: RMSNorm scale of each token of the pair
+  int32_t rows[NW][32];            // per wave: output row of each token (-1: not stored)
 };
 
 // Logical workgroup id such that ids q_c m .. q_c m + q_c - 1 run on one XCD (workgroups are
@@ -136,7 +141,7 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t ro
 }
 
 template <class Ty, int QC, bool OM, bool DROP, bool SG>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+__global__ void __attribute__((amdgpu_flat_work_group_size(SG ? 512 : 256, SG ? 512 : 256), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr int C = QC * kD;
   constexpr int NV = C / 16;  // row pieces per lane
@@ -146,22 +151,26 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr bool STREAM = QC == 4;
   constexpr int NX = STREAM ? 4 : NV;  // pieces carried from one unit to the next
   static_assert(!SG || QC == 2, "interleaved channel groups: q_c = 2");
-  __shared__ __attribute__((aligned(16))) WaveLds sh;
+  // SG: waves 0-3 take group 0 and waves 4-7 group 1 of the same four pairs (wave w and w ^ 4
+  // share a pair), so the pair's output rows are put together in LDS and stored whole.
+  constexpr int NG = SG ? 2 : 1, NW = SG ? 8 : kWavesWg;
+  __shared__ __attribute__((aligned(16))) WaveLds<NG, NW> sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
-  const int lid = wave_xcd_remap(blockIdx.x, gridDim.x);
-  const int g = lid % QC;
-  const int team = lid / QC;
-  const int n_team = gridDim.x / QC;
+  const int lid = SG ? static_cast<int>(blockIdx.x) : wave_xcd_remap(blockIdx.x, gridDim.x);
+  const int g = SG ? wave >> 2 : lid % QC;
+  const int team = SG ? lid : lid / QC;
+  const int n_team = SG ? static_cast<int>(gridDim.x) : static_cast<int>(gridDim.x) / QC;
   const int64_t stride = static_cast<int64_t>(n_team) * kWavesWg;
-  const int64_t first = static_cast<int64_t>(team) * kWavesWg + wave;
+  const int64_t first = static_cast<int64_t>(team) * kWavesWg + (wave & (kWavesWg - 1));
   // SG: the group's first channel (its residue mod q_c), wave-uniform.
   const int res = SG ? __builtin_amdgcn_readfirstlane(a.chan[g * kD]) & (QC - 1) : 0;
 
-  // The group's weights into LDS (1 KB per wave and copy), the token operands into registers.
+  // The group's (SG: both groups') weights into LDS (1 KB per wave and copy), the token
+  // operands into registers.
   {
-    const uint16_t* src = a.packed + kHeadElems + static_cast<size_t>(g) * kGroupFrags * kFragElems;
-    for (int f = wave; f < kGroupFrags; f += kWavesWg)
+    const uint16_t* src = a.packed + kHeadElems + static_cast<size_t>(SG ? 0 : g) * kGroupFrags * kFragElems;
+    for (int f = wave; f < NG * kGroupFrags; f += NW)
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(f) * kFragElems + lane * 8),
           (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
@@ -169,7 +178,9 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (first >= n_pairs) return;  // after the only workgroup barrier
+  // After the kernel's first workgroup barrier; SG: every wave of the workgroup runs the same
+  // number of units (the later barriers), those past the end on pad rows.
+  if ((SG ? static_cast<int64_t>(team) * kWavesWg : first) >= n_pairs) return;
 
   uint16_t* tile = sh.tile[wave];
   float* rsc = sh.rsc[wave];
@@ -266,7 +277,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     // products.  The weight fragments come from LDS DEPTH reads ahead of their MFMAs
     // (lds_read_async: no compiler wait per read; lds_wait before each use).
     f32x16 W[kMB] = {};
-    const uint32_t wbase = lds_addr(&sh.w[0][lane]);
+    const uint32_t wbase = lds_addr(&sh.w[SG ? g * kGroupFrags : 0][lane]);
     constexpr int DEPTH = 4;
     u32x4 vb[4];  // streamed batch in flight
     auto step = [&](auto e_tag, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
@@ -369,19 +380,34 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     wave_lds_sync();
 
     // The tile's rows to memory: 32 rows x 8 pieces of the group's columns, 4 per lane; pad
-    // rows go past the buffer.  SG: one row per instruction, lane l storing group column
-    // 2 (l % 32) + hh (channel res + q_c column) as a 2-byte element.
+    // rows go past the buffer.  SG: after a workgroup barrier (the partner wave w ^ 4 has its
+    // group's columns of the same pair in its tile) wave w stores rows 16 g .. 16 g + 15 whole:
+    // lane (row 16 g + lane / 16 + 4 j, piece c = lane % 16) takes columns 4c .. 4c + 3 of the
+    // even-channel group's tile and of the odd one's and interleaves them into channels
+    // 8c .. 8c + 7 (v_perm_b32).
     if constexpr (SG) {
-      const int32_t my_row = rows[l32];
-      const uint32_t voff = 2u * static_cast<uint32_t>(res + QC * (2 * l32 + hh));
+      __syncthreads();
+      const uint16_t* te = sh.tile[res == 0 ? wave : wave ^ 4];
+      const uint16_t* to = sh.tile[res == 0 ? wave ^ 4 : wave];
+      const int c = lane & 15;
+      u32x4 ov[4];
+      int32_t orow[4];
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(&tile[r * kLdt + 2 * l32]);
-        const int32_t orow = __builtin_amdgcn_readlane(my_row, r);
-        const uint32_t rb = orow >= 0 ? static_cast<uint32_t>(orow) * static_cast<uint32_t>(C * 2) : kOutOfRange;
-        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(hh ? w >> 16 : w), ro, voff, rb, 0);
+      for (int j = 0; j < 4; ++j) {
+        const int r = 16 * g + (lane >> 4) + 4 * j;
+        orow[j] = rows[r];
+        const u32x2 e = *reinterpret_cast<const u32x2*>(&te[r * kLdt + 4 * c]);
+        const u32x2 o = *reinterpret_cast<const u32x2*>(&to[r * kLdt + 4 * c]);
+        ov[j] = u32x4{__builtin_amdgcn_perm(o[0], e[0], 0x05040100u), __builtin_amdgcn_perm(o[0], e[0], 0x07060302u),
+                      __builtin_amdgcn_perm(o[1], e[1], 0x05040100u), __builtin_amdgcn_perm(o[1], e[1], 0x07060302u)};
       }
-      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t rb = orow[j] >= 0 ? static_cast<uint32_t>(orow[j]) * static_cast<uint32_t>(C * 2) : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b128(ov[j], ro, rb + 16u * static_cast<uint32_t>(c), 0, 0);
+      }
+      // Both waves of the pair are done reading the tiles before the next unit writes them.
+      __syncthreads();
       out_c = out_n;
       return;
     }
@@ -426,20 +452,29 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     load_pieces<NV>(rx, in0, C, hh, x);
   }
   ent = next_entry();
+  // SG: the workgroup's trip count (from its first pair), the same for all eight waves.
+  const int64_t base0 = SG ? static_cast<int64_t>(team) * kWavesWg : first;
 #pragma unroll 1
-  for (int64_t p = first; p < n_pairs; p += stride) unit(p, x, ssq, ent, out_c);
+  for (int64_t p0 = base0; p0 < n_pairs; p0 += stride) unit(p0 + (first - base0), x, ssq, ent, out_c);
 }
 
 template <class Ty, int QC, bool SG>
 int launch_qc(const ResidentArgs& a, hipStream_t stream) {
   // Two workgroups of four waves per CU (~67 KB of LDS each); whole teams of QC workgroups.
+  // SG: one workgroup of eight waves per CU (~138 KB), four pairs of both groups at a time.
   const int32_t n_pairs = a.n_pairs;
-  int64_t grid = static_cast<int64_t>(device_cus()) * 2;
   const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWavesWg - 1) / kWavesWg;
-  if (grid / QC > teams_needed) grid = teams_needed * QC;
-  grid -= grid % QC;
+  int64_t grid;
+  if (SG) {
+    grid = static_cast<int64_t>(device_cus());
+    if (grid > teams_needed) grid = teams_needed;
+  } else {
+    grid = static_cast<int64_t>(device_cus()) * 2;
+    if (grid / QC > teams_needed) grid = teams_needed * QC;
+    grid -= grid % QC;
+  }
   if (grid <= 0) return OW_OK;
-  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  const dim3 g(static_cast<unsigned>(grid)), b(SG ? 512 : 256);
   if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   if (a.out_tok)
     hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false, SG>), g, b, 0, stream, a, n_pairs);
