@@ -2225,31 +2225,26 @@ int bwd_channel(const void* xt, const void* dyt, const float* a_u, const float* 
   return rc;
 }
 
-// The routing of ow_bwd_channel_routed / ow_bwd_channel2_routed: plan checks and the row
-// arguments (slots = batch * q_s * 16).
-int routed128(const OwPlan* plan, int32_t batch, const void* x, const void* dy, const float* rscale,
-              const int32_t* token_index, int64_t& slots, int32_t& q_c, int32_t& d, const uint16_t*& rx,
-              const uint16_t*& rdy, const float*& rrs, const int32_t*& rtok, int32_t& rq_s, int32_t& rn_tok,
-              int32_t& rc_) {
-  int32_t q_s = 0;
-  if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
-  d = plan->channel_tile;
-  const int32_t c = plan->channels;
+// The routing of ow_bwd_channel_routed / ow_bwd_channel2_routed: plan checks, and the row
+// tables of the kernels' routed mode (slots = batch * q_s * 16).
+struct Routed128 {
+  int64_t slots = 0;
+  int32_t q_c = 0, d = 0, q_s = 0, n_tok = 0, channels = 0;
+};
+int routed128(const OwPlan* plan, int32_t batch, const void* x, const void* dy, const int32_t* token_index,
+              Routed128& r) {
+  if (int rc = ow_plan_dims(plan, &r.q_s, &r.q_c)) return rc;
+  r.d = plan->channel_tile;
+  r.channels = plan->channels;
   OW_CHECK_SUPPORTED(plan->spatial_tile == kG, "unsupported spatial tile g=%d; expected 16", plan->spatial_tile);
-  OW_CHECK_SUPPORTED(d == kB2D && c == q_c * kB2D && (plan->radix_level == 0 || q_c == 1),
+  OW_CHECK_SUPPORTED(r.d == kB2D && r.channels == r.q_c * kB2D && (plan->radix_level == 0 || r.q_c == 1),
                      "routed backward needs the identity channel order with C = q_c * 128");
-  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * q_s < (int64_t(1) << 27), "bad batch %d", batch);
-  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * c * 2 < (int64_t(1) << 31),
+  OW_CHECK_ARG(batch >= 0 && static_cast<int64_t>(batch) * r.q_s < (int64_t(1) << 27), "bad batch %d", batch);
+  OW_CHECK_ARG(static_cast<int64_t>(batch) * plan->height * plan->width * r.channels * 2 < (int64_t(1) << 31),
                "x, dy and g must be below 2 GiB (buffer addressing)");
   OW_CHECK_ARG(x && dy && token_index, "tensor pointer is NULL");
-  slots = static_cast<int64_t>(batch) * q_s * kG;
-  rx = static_cast<const uint16_t*>(x);
-  rdy = static_cast<const uint16_t*>(dy);
-  rrs = rscale;
-  rtok = token_index;
-  rq_s = q_s;
-  rn_tok = plan->height * plan->width;
-  rc_ = c;
+  r.slots = static_cast<int64_t>(batch) * r.q_s * kG;
+  r.n_tok = plan->height * plan->width;
   return OW_OK;
 }
 }  // namespace
@@ -2266,14 +2261,18 @@ int ow_bwd_channel_routed(const void* x, const void* dy, const float* rscale, co
                           const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
                           const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
                           void* dv, int32_t rd, int32_t dtype, void* stream) {
+  ow::Routed128 rt;
+  if (int rc = ow::routed128(plan, batch, x, dy, token_index, rt)) return rc;
   ow::BwdChanArgs r{};
-  int64_t slots = 0;
-  int32_t q_c = 0, d = 0;
-  if (int rc = ow::routed128(plan, batch, x, dy, rscale, token_index, slots, q_c, d, r.x, r.dy, r.rscale, r.tok,
-                             r.q_s, r.n_tok, r.channels))
-    return rc;
-  return ow::bwd_channel(nullptr, nullptr, a_u, a_v, a_o, packed, packed_bytes, pu, pv, dw, z, du, dv, slots, q_c, d,
-                         rd, dtype, r, stream);
+  r.x = static_cast<const uint16_t*>(x);
+  r.dy = static_cast<const uint16_t*>(dy);
+  r.rscale = rscale;
+  r.tok = token_index;
+  r.q_s = rt.q_s;
+  r.n_tok = rt.n_tok;
+  r.channels = rt.channels;
+  return ow::bwd_channel(nullptr, nullptr, a_u, a_v, a_o, packed, packed_bytes, pu, pv, dw, z, du, dv, rt.slots,
+                         rt.q_c, rt.d, rd, dtype, r, stream);
 }
 
 int64_t ow_bwd_channel_partials(int64_t slots, int32_t q_c) {
@@ -2342,16 +2341,20 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
                            const void* dv, const float* a_u, const float* a_v, const void* packed, size_t packed_bytes,
                            const int32_t* token_index, const OwPlan* plan, int32_t batch, void* g, float* partial,
                            int64_t n_partial, int32_t rd, int32_t dtype, void* stream) {
-  ow::BwdChan2Args r{};
-  int64_t slots = 0;
-  int32_t q_c = 0, d = 0;
-  if (int rc = ow::routed128(plan, batch, x, dy, rscale, token_index, slots, q_c, d, r.x, r.dy, r.rscale, r.tok,
-                             r.q_s, r.n_tok, r.channels))
-    return rc;
+  ow::Routed128 rt;
+  if (int rc = ow::routed128(plan, batch, x, dy, token_index, rt)) return rc;
   OW_CHECK_ARG(g, "tensor pointer is NULL");
+  ow::BwdChan2Args r{};
+  r.x = static_cast<const uint16_t*>(x);
+  r.dy = static_cast<const uint16_t*>(dy);
+  r.rscale = rscale;
+  r.tok = token_index;
   r.g = static_cast<uint16_t*>(g);
-  return ow::bwd_channel2(x, dy, z, du, dv, a_u, a_v, packed, packed_bytes, nullptr, partial, n_partial, slots, q_c,
-                          d, rd, dtype, r, stream);
+  r.q_s = rt.q_s;
+  r.n_tok = rt.n_tok;
+  r.channels = rt.channels;
+  return ow::bwd_channel2(x, dy, z, du, dv, a_u, a_v, packed, packed_bytes, nullptr, partial, n_partial, rt.slots,
+                          rt.q_c, rt.d, rd, dtype, r, stream);
 }
 
 int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
