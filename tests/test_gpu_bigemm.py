@@ -105,6 +105,24 @@ def test_fused_block_matches_oracle(stage, route, level, dtype) -> None:
     assert torch.equal(out.cpu(), expected)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_interleaved_groups_ragged_pairs(dtype) -> None:
+    """56x56x128-style interleaved channel groups (radix 1, q_c = 2, the wave kernel's eight-wave
+    workgroups of four pairs) on 5x9 tokens x 3 images: 9 token groups, 5 pairs (the last half
+    pad), so the second workgroup runs one live and three empty units through its barriers."""
+    announce(f"interleaved q_c=2 ragged pairs 5x9x128 radix1 dtype={dtype} B=3 seed=5")
+    plan, x, params, norm_w = make_case(3, 5, 9, 128, 64, "radix", 1, dtype, seed=5)
+    assert plan.token_indices.shape[0] == 3 and plan.channel_indices.shape[0] == 2
+    xd, dp = x.to(DEV), to_dev(params)
+    delta = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp, residual=False)
+    out = bigemm_block_hip(xd, norm_w.to(DEV), plan, **dp)
+    torch.cuda.synchronize()
+    ref = oracle_delta(rmsnorm_reference(x, norm_w), plan, params, dtype)
+    err = rel_l2(delta.cpu(), ref)
+    assert err <= TOL[dtype], f"rel-L2 {err:.3e}"
+    assert torch.equal(out.cpu(), (x.float() + delta.cpu().float()).to(dtype))
+
+
 def test_fused_block_past_2gib_matches_small_batches() -> None:
     """x of 56x56x128 bf16 rows past 2 GiB (2,676 images): the wave kernel's 32-bit offsets do not
     reach, so the launch takes the resident kernel.  Images are independent, so the first and
