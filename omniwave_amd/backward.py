@@ -136,9 +136,24 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     if any(w.dtype != wdtype for w in ws) or wdtype not in _DTYPE_CODE:
         wdtype = torch.float32
         ws = [w.float() for w in ws]
-    nw = _fp32(norm_weight, dev) if fuse_norm else None
-    gm = _fp32(gamma, dev)
-    au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
+    # The small fp32 operands (norm weight, gamma, token matrices): one concatenation and one
+    # cast instead of a conversion kernel each, when they share a 16-bit dtype.
+    small = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o]
+    if len({t.dtype for t in small}) == 1 and small[0].dtype != torch.float32 and all(t.device == dev for t in small):
+        flat = torch.cat([t.detach().reshape(-1) for t in small]).to(torch.float32)
+        parts = list(torch.split(flat, [t.numel() for t in small]))
+        nw = parts.pop(0) if fuse_norm else None
+        gm, au, av, ao = parts[0], parts[1].view(16, 16), parts[2].view(16, 16), parts[3].view(16, 16)
+    else:
+        nw = _fp32(norm_weight, dev) if fuse_norm else None
+        gm = _fp32(gamma, dev)
+        au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
+    # The fp32 parameter gradients in one buffer (norm weight, gamma, the token matrices, then
+    # B_u, B_v, B_o), so that parameters of one dtype are cast back with one kernel.
+    n_c = (2 if fuse_norm else 1) * plan.channels
+    nb = q_c * d * rd
+    g_all = torch.empty(n_c + 768 + 3 * nb, dtype=torch.float32, device=dev)
+    g_a = g_all[n_c:n_c + 768].view(3, 256)
 
     with torch.cuda.device(dev):
         if drop_scale is not None:
@@ -201,7 +216,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                stream), "ow_bwd_fused")
                 del xt, dyt
-            g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
+            torch.sum(partial, dim=0, out=g_a)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates.
             n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c, rd)
@@ -251,7 +266,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                   dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
                                                   dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                   stream), "ow_bwd_channel2")
-            g_a = partial.sum(dim=0)  # [3, 256]: dA_u, dA_v, dA_o
+            torch.sum(partial, dim=0, out=g_a)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
             d_bv = _slot_reduce(pv, dv)
@@ -310,14 +325,12 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                          else None, grad.data_ptr(), dx.data_ptr(), n_rows, plan.channels,
                                          int(residual), code, stream), "ow_bwd_rmsnorm")
 
-        # Parameter gradients from the folded ones.
-        # One buffer per output dtype group, so each group is cast with one kernel below; every
-        # element is written (each channel of the permutation exactly once).
-        nb = q_c * d * rd
-        g_b = torch.empty(3 * nb, dtype=torch.float32, device=dev)
+        # Parameter gradients from the folded ones, into g_all (every element is written: each
+        # channel of the permutation exactly once).
+        g_b = g_all[n_c + 768:]
         g_bu, g_bv = g_b[:nb].view(q_c, d, rd), g_b[nb:2 * nb].view(q_c, d, rd)
         g_bo = g_b[2 * nb:].view(q_c, rd, d)
-        g_c = torch.empty(2 if fuse_norm else 1, plan.channels, dtype=torch.float32, device=dev)
+        g_c = g_all[:n_c].view(-1, plan.channels)
         g_gamma = g_c[0]
         g_nw = g_c[1] if fuse_norm else None
         _native.check(lib.ow_bwd_params(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],
@@ -326,6 +339,16 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                         g_bu.data_ptr(), g_bv.data_ptr(), g_bo.data_ptr(), g_gamma.data_ptr(),
                                         g_nw.data_ptr() if g_nw is not None else None, stream), "ow_bwd_params")
 
+    params = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o, b_u, b_v, b_o]
+    in_all = all(t.untyped_storage().data_ptr() == g_all.untyped_storage().data_ptr() for t in (g_au, g_av, g_ao))
+    if len({t.dtype for t in params}) == 1 and in_all:
+        # One cast of the whole buffer; the gradients are views of it.
+        out = g_all.to(params[0].dtype)
+        o_c = out[:n_c].view(-1, plan.channels)
+        o_a = out[n_c:n_c + 768].view(3, 16, 16)
+        o_b = out[n_c + 768:]
+        return (dx, o_c[1] if fuse_norm else None, o_c[0], o_a[0], o_a[1], o_a[2],
+                o_b[:nb].view(q_c, d, rd), o_b[nb:2 * nb].view(q_c, d, rd), o_b[2 * nb:].view(q_c, rd, d))
     return (
         dx,
         g_nw.to(norm_weight.dtype) if g_nw is not None else None,
