@@ -1,5 +1,9 @@
-// BiGEMM backward: the routing, gating and normalisation parts as HIP kernels; the channel
-// products are plain batched GEMMs the caller runs between them (hipBLASLt).
+// BiGEMM backward.  bf16 / fp16 with d = 64: one fused kernel (token side, channel side and
+// gate, dX', token-matrix gradients) and the parameter-gradient reduction over its
+// fragment-ordered intermediates; with d = 128: two persistent channel kernels, the
+// parameter-gradient reductions left to batched GEMMs; fp32 and other shapes: the routing,
+// gating and token-mixing kernels here around batched GEMMs the caller runs (hipBLASLt).  The
+// RMSNorm backward and the parameter fold-back are shared.
 //
 // Gradients are taken with respect to the folded weights the forward evaluates (per channel
 // group q, token slot k of the flattened (image, token group, row) order, channel c < d,
@@ -12,9 +16,9 @@
 //     delta = A_o W'_tile                                          (reference.py:162-171)
 // Backward for dY = d delta:
 //     dW' = A_o^T dY_tile,  dZ = dW' B_o''^T
-//     dU' = dZ V' s (1 - ln2 U' (1 - s)),  dV' = dZ U' s                   (bwd_gate_kernel)
-//     dB_u'' = P_u^T dU', dB_v'' = P_v^T dV', dB_o'' = Z^T dW'             (GEMMs)
-//     dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,  dX' = A_u^T dP_u + A_v^T dP_v   (GEMMs)
+//     dU' = dZ V' s (1 - ln2 U' (1 - s)),  dV' = dZ U' s
+//     dB_u'' = P_u^T dU', dB_v'' = P_v^T dV', dB_o'' = Z^T dW'   (sums over all slots)
+//     dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,  dX' = A_u^T dP_u + A_v^T dP_v
 //     dx = r g - x r^3 / C sum_c(g x),  g = dX' scattered to NHWC    (bwd_rmsnorm_kernel)
 // and the parameter gradients follow from the folded ones (bwd_params_kernel).
 #include <hip/hip_runtime.h>
