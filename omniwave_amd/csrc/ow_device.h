@@ -175,6 +175,16 @@ __device__ __forceinline__ void tile_copy(__amdgpu_buffer_rsrc_t rx, uint32_t vo
                : "memory", "m0");
 #pragma clang diagnostic pop
 }
+// The same with the non-temporal cache policy, for data read exactly once.
+__device__ __forceinline__ void tile_copy_nt(__amdgpu_buffer_rsrc_t rx, uint32_t voff, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"(voff), "s"(rx),
+               "s"(lds)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
 
 // A wave-uniform pointer the compiler may not prove uniform (the scalar operand of a copy).
 __device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
