@@ -224,10 +224,13 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
             _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
                                                     du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,
                                                     rd, code, stream), "ow_bwd_param_reduce64")
-            g_b3 = red.view(n_red // q_c, q_c, 3 * d * rd).sum(dim=0)
-            d_bu = g_b3[:, :d * rd].reshape(q_c, d, rd).contiguous()
-            d_bv = g_b3[:, d * rd:2 * d * rd].reshape(q_c, d, rd).contiguous()
-            d_bo = g_b3[:, 2 * d * rd:].reshape(q_c, rd, d).contiguous()
+            # Summed into [3, q_c, d * rd] through a permuted output view, so each gradient is a
+            # contiguous slice (no copies before ow_bwd_params).
+            g_b3 = torch.empty(3, q_c, d * rd, dtype=torch.float32, device=dev)
+            torch.sum(red.view(n_red // q_c, q_c, 3, d * rd), dim=0, out=g_b3.permute(1, 0, 2))
+            d_bu = g_b3[0].view(q_c, d, rd)
+            d_bv = g_b3[1].view(q_c, d, rd)
+            d_bo = g_b3[2].view(q_c, rd, d)
             del z, du, dv, pu, pv, dw
         elif d == 128 and dtype != torch.float32:
             # Two kernels over 256-slot units: (1) token side P_u, P_v, dW', then U', V', dZ per
