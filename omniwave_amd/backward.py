@@ -75,6 +75,24 @@ def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -
     return partial.sum(dim=2)
 
 
+_ONES: dict = {}
+
+
+def _sum_partials(partial: Tensor, out: Tensor) -> None:
+    """Sum of the per-workgroup fp32 partial rows of ``partial`` ([n, ...]) into ``out``, as one
+    GEMV against a cached vector of ones: torch's multi-block sum clears a semaphore buffer with
+    an extra fill before its reduction.  The ones vector is made outside graph capture only (its
+    memory then belongs to no graph); a capture that finds none uses the plain sum."""
+    n = partial.shape[0]
+    ones = _ONES.get((partial.device, n))
+    if ones is None:
+        if partial.is_cuda and torch.cuda.is_current_stream_capturing():
+            torch.sum(partial, dim=0, out=out)
+            return
+        ones = _ONES[(partial.device, n)] = torch.ones(n, dtype=torch.float32, device=partial.device)
+    torch.mv(partial.view(n, -1).t(), ones, out=out.view(-1))
+
+
 def _slot_reduce(a: Tensor, b: Tensor) -> Tensor:
     """sum over slots of a^T b per channel group ([q_c, S, m] x [q_c, S, n] -> fp32 [q_c, m, n]).
 
@@ -216,7 +234,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                stream), "ow_bwd_fused")
                 del xt, dyt
-            torch.sum(partial, dim=0, out=g_a)  # [3, 256]: dA_u, dA_v, dA_o
+            _sum_partials(partial, g_a)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates.
             n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c, rd)
@@ -269,7 +287,7 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                                   dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
                                                   dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                   stream), "ow_bwd_channel2")
-            torch.sum(partial, dim=0, out=g_a)  # [3, 256]: dA_u, dA_v, dA_o
+            _sum_partials(partial, g_a)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
             d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
             d_bv = _slot_reduce(pv, dv)
