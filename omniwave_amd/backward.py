@@ -82,14 +82,18 @@ def _sum_partials(partial: Tensor, out: Tensor) -> None:
     """Sum of the per-workgroup fp32 partial rows of ``partial`` ([n, ...]) into ``out``, as one
     GEMV against a cached vector of ones: torch's multi-block sum clears a semaphore buffer with
     an extra fill before its reduction.  The ones vector is made outside graph capture only (its
-    memory then belongs to no graph); a capture that finds none uses the plain sum."""
+    memory then belongs to no graph); a capture that finds none uses the plain sum.  Its fill
+    is waited for once, so a later call on any stream reads it filled."""
     n = partial.shape[0]
     ones = _ONES.get((partial.device, n))
     if ones is None:
         if partial.is_cuda and torch.cuda.is_current_stream_capturing():
             torch.sum(partial, dim=0, out=out)
             return
-        ones = _ONES[(partial.device, n)] = torch.ones(n, dtype=torch.float32, device=partial.device)
+        ones = torch.ones(n, dtype=torch.float32, device=partial.device)
+        if ones.is_cuda:
+            torch.cuda.current_stream(partial.device).synchronize()
+        _ONES[(partial.device, n)] = ones
     torch.mv(partial.view(n, -1).t(), ones, out=out.view(-1))
 
 
@@ -121,6 +125,44 @@ def _fp32(t: Tensor, device) -> Tensor:
     return t.detach().to(device=device, dtype=torch.float32).contiguous()
 
 
+# The bf16 / fp16 backward kernels address x, dy, g and the [q_c, slots, rd] intermediates with
+# 32-bit byte offsets (buffer descriptors): each of those buffers must stay below 2 GiB.
+_ADDR_LIMIT = 1 << 31
+
+
+def native_batch_limit(dtype: torch.dtype, plan: RoutePlan, q_c: int, d: int, rd: int) -> int | None:
+    """Largest batch one pass of the 16-bit backward kernels can address (None: no limit).
+
+    Per image, x / dy / g hold H*W*C values and each intermediate (P_u, P_v, dW', Z, dU', dV',
+    the gathered tiles) q_c * Q_s * 16 * max(d, rd); the kernels need every buffer below 2 GiB.
+    The reference backward (omniweave/ops/reference.py:120-173 through autograd) has no batch
+    ceiling, so ``bigemm_backward`` runs larger batches in chunks of at most this many images.
+    """
+    if dtype == torch.float32:
+        return None
+    elt = torch.empty((), dtype=dtype).element_size()
+    q_s = int(plan.token_indices.shape[0])
+    per_image = max(plan.height * plan.width * plan.channels, q_c * q_s * 16 * max(d, rd)) * elt
+    return max(1, (_ADDR_LIMIT - 1) // per_image)
+
+
+def batch_chunks(batch: int, limit: int | None, q_s: int) -> list[tuple[int, int]]:
+    """[start, end) image ranges of at most ``limit`` images covering ``batch``, as even in size
+    as possible; with an odd Q_s the chunk size is kept even where it can be, so each chunk's
+    slot count stays a multiple of 32 (the fused d = 64 kernel)."""
+    if limit is None or batch <= limit:
+        return [(0, batch)]
+    n = -(-batch // limit)
+    size = -(-batch // n)
+    if q_s % 2 and size % 2 and size > 1:
+        size -= 1
+    out, s = [], 0
+    while s < batch:
+        out.append((s, min(batch, s + size)))
+        s += size
+    return out
+
+
 def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
                     a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float,
                     drop_scale: Tensor | None = None):
@@ -130,7 +172,60 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     its input's dtype (``d_norm_weight`` is None without OW_FUSE_NORM).  With ``drop_scale``
     (per-image drop-path factors of the forward) the delta branch receives the upstream
     gradient scaled per image and rounded (``ow_scale_samples``), the residual the plain one.
+    Batches beyond ``native_batch_limit`` run in chunks: dx per chunk, the parameter gradients
+    summed over chunks in fp32 before the cast.
     """
+    fuse_norm = bool(flags & _native.OW_FUSE_NORM)
+    q_c, d, rd = b_u.shape
+    chunks = batch_chunks(x.shape[0], native_batch_limit(x.dtype, plan, q_c, d, rd),
+                          int(plan.token_indices.shape[0]))
+    if len(chunks) == 1:
+        dx, g_all = _backward_once(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan, flags, eps,
+                                   drop_scale)
+    else:
+        dxs, g_all = [], None
+        for s, e in chunks:
+            dx_c, g_c = _backward_once(grad[s:e], x[s:e], norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan,
+                                       flags, eps, drop_scale[s:e] if drop_scale is not None else None)
+            dxs.append(dx_c)
+            g_all = g_c if g_all is None else g_all.add_(g_c)
+        dx = torch.cat(dxs)
+    return _cast_grads(dx, g_all, fuse_norm, plan.channels, q_c, d, rd,
+                       norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o)
+
+
+def _cast_grads(dx, g_all, fuse_norm, channels, q_c, d, rd, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o):
+    """Parameter gradients as views of the fp32 buffer ``g_all`` (norm weight, gamma, the token
+    matrices, B_u, B_v, B_o), cast to each parameter's dtype: one cast of the whole buffer when
+    they share a dtype."""
+    n_c = (2 if fuse_norm else 1) * channels
+    nb = q_c * d * rd
+    params = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o, b_u, b_v, b_o]
+
+    def views(buf):
+        o_c = buf[:n_c].view(-1, channels)
+        o_a = buf[n_c:n_c + 768].view(3, 16, 16)
+        o_b = buf[n_c + 768:]
+        return (o_c[1] if fuse_norm else None, o_c[0], o_a[0], o_a[1], o_a[2],
+                o_b[:nb].view(q_c, d, rd), o_b[nb:2 * nb].view(q_c, d, rd), o_b[2 * nb:].view(q_c, rd, d))
+
+    if len({t.dtype for t in params}) == 1:
+        return (dx, *views(g_all.to(params[0].dtype)))
+    g_nw, g_gamma, g_au, g_av, g_ao, g_bu, g_bv, g_bo = views(g_all)
+    return (
+        dx,
+        g_nw.to(norm_weight.dtype) if g_nw is not None else None,
+        *_cast_group((g_gamma,), (gamma.dtype,)),
+        *_cast_group((g_au, g_av, g_ao), (a_u.dtype, a_v.dtype, a_o.dtype)),
+        *_cast_group((g_bu, g_bv, g_bo), (b_u.dtype, b_v.dtype, b_o.dtype)),
+    )
+
+
+def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
+                   a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float,
+                   drop_scale: Tensor | None):
+    """One pass of the kernels over the whole batch: dx and the fp32 parameter-gradient buffer
+    (layout of ``_cast_grads``)."""
     lib = _native.lib()
     dev = x.device
     dtype = x.dtype
@@ -360,23 +455,10 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
                                         g_bu.data_ptr(), g_bv.data_ptr(), g_bo.data_ptr(), g_gamma.data_ptr(),
                                         g_nw.data_ptr() if g_nw is not None else None, stream), "ow_bwd_params")
 
-    params = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o, b_u, b_v, b_o]
-    in_all = all(t.untyped_storage().data_ptr() == g_all.untyped_storage().data_ptr() for t in (g_au, g_av, g_ao))
-    if len({t.dtype for t in params}) == 1 and in_all:
-        # One cast of the whole buffer; the gradients are views of it.
-        out = g_all.to(params[0].dtype)
-        o_c = out[:n_c].view(-1, plan.channels)
-        o_a = out[n_c:n_c + 768].view(3, 16, 16)
-        o_b = out[n_c + 768:]
-        return (dx, o_c[1] if fuse_norm else None, o_c[0], o_a[0], o_a[1], o_a[2],
-                o_b[:nb].view(q_c, d, rd), o_b[nb:2 * nb].view(q_c, d, rd), o_b[2 * nb:].view(q_c, rd, d))
-    return (
-        dx,
-        g_nw.to(norm_weight.dtype) if g_nw is not None else None,
-        *_cast_group((g_gamma,), (gamma.dtype,)),
-        *_cast_group((g_au, g_av, g_ao), (a_u.dtype, a_v.dtype, a_o.dtype)),
-        *_cast_group((g_bu, g_bv, g_bo), (b_u.dtype, b_v.dtype, b_o.dtype)),
-    )
+    # The token-matrix gradients of the batched-GEMM path are separate tensors: into g_all too.
+    if not all(t.untyped_storage().data_ptr() == g_all.untyped_storage().data_ptr() for t in (g_au, g_av, g_ao)):
+        g_a.copy_(torch.stack([g_au.reshape(256), g_av.reshape(256), g_ao.reshape(256)]))
+    return dx, g_all
 
 
 def _cast_group(ts: tuple[Tensor, ...], dtypes: tuple[torch.dtype, ...]) -> tuple[Tensor, ...]:

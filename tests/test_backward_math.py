@@ -142,3 +142,27 @@ def test_cast_group_one_buffer_and_fallback() -> None:
     out = _cast_group(sep, (torch.bfloat16, torch.float16, torch.float32))
     assert [o.dtype for o in out] == [torch.bfloat16, torch.float16, torch.float32]
     assert all(torch.equal(o, s.to(o.dtype)) for o, s in zip(out, sep))
+
+
+def test_native_batch_limit_and_chunks() -> None:
+    """The 16-bit backward kernels address every buffer with 32-bit byte offsets: the largest
+    batch of one pass keeps x / dy / g and each [q_c, slots, rd] intermediate below 2 GiB, and
+    larger batches are cut into chunks no larger than that."""
+    from omniwave_amd.backward import batch_chunks, native_batch_limit
+    from omniwave_amd.routing import build_route_plan
+
+    s1 = build_route_plan(56, 56, 128, 16, 64, "shifted", 0)
+    s3 = build_route_plan(14, 14, 512, 16, 128, "shifted", 0)
+    lim1 = native_batch_limit(torch.bfloat16, s1, 2, 64, 128)
+    lim3 = native_batch_limit(torch.float16, s3, 4, 128, 256)
+    assert lim1 == 1337 and 2 * 196 * 16 * 128 * 2 * lim1 < 2 ** 31 <= 2 * 196 * 16 * 128 * 2 * (lim1 + 1)
+    assert lim3 == 5041 and 4 * 13 * 16 * 256 * 2 * lim3 < 2 ** 31 <= 4 * 13 * 16 * 256 * 2 * (lim3 + 1)
+    assert native_batch_limit(torch.float32, s1, 2, 64, 128) is None
+    assert batch_chunks(128, lim1, 196) == [(0, 128)]
+    assert batch_chunks(1400, lim1, 196) == [(0, 700), (700, 1400)]
+    chunks = batch_chunks(4000, lim1, 196)
+    assert chunks[0][0] == 0 and chunks[-1][1] == 4000 and all(e - s <= lim1 for s, e in chunks)
+    assert all(chunks[i][1] == chunks[i + 1][0] for i in range(len(chunks) - 1))
+    # odd Q_s (13 at 14x14): even chunk sizes keep each chunk's slot count a multiple of 32
+    assert batch_chunks(11, 5, 13) == [(0, 4), (4, 8), (8, 11)]
+    assert batch_chunks(7, None, 13) == [(0, 7)]

@@ -169,3 +169,26 @@ def test_full_batch_backward_is_per_sample(stage) -> None:
     for k in NAMES + ["norm_weight"]:
         err = rel_l2(full[k], halves[0][k] + halves[1][k])
         assert err <= 5e-3, f"{stage} {k}: batch gradient != sum of halves (rel-L2 {err:.2e})"
+
+
+def test_backward_beyond_the_addressing_limit_runs_in_chunks() -> None:
+    """S1 at B = 1400: one pass's intermediates would reach 2 GiB (32-bit buffer offsets), so the
+    backward runs as two chunks of 700 images.  Three sampled images' dx (one on each side of the
+    chunk boundary) match the oracle, and the parameter gradients equal the sum of two separate
+    700-image backward passes."""
+    from omniwave_amd.backward import batch_chunks, native_batch_limit
+
+    h, w, c, d = 56, 56, 128, 64
+    announce("backward past the 2 GiB addressing limit s1 shifted bf16 B=1400")
+    plan, x, params, dy = make_case(1400, h, w, c, d, "shifted", 0, torch.bfloat16, seed=6)
+    assert batch_chunks(1400, native_batch_limit(torch.bfloat16, plan, 2, d, 2 * d), 196) == [(0, 700), (700, 1400)]
+    full = hip_grads(x, plan, params, dy, fused=True, residual=True)
+    for i in (0, 700, 1399):
+        want = oracle_grads(x[i:i + 1], plan, params, dy[i:i + 1], fused=True, residual=True)
+        check({"x": full["x"][i:i + 1]}, {"x": want["x"]}, dy[i:i + 1], True, torch.bfloat16, f"B=1400 sample {i}")
+    halves = [hip_grads(x[s], plan, params, dy[s], fused=True, residual=True)
+              for s in (slice(0, 700), slice(700, 1400))]
+    assert torch.equal(full["x"], torch.cat([halves[0]["x"], halves[1]["x"]]))
+    for k in NAMES + ["norm_weight"]:
+        err = rel_l2(full[k], halves[0][k] + halves[1][k])
+        assert err <= 1e-6, f"{k}: chunked gradient != sum of the chunks (rel-L2 {err:.2e})"

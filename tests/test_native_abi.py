@@ -187,3 +187,22 @@ def test_check_raises_with_library_message() -> None:
     q = ctypes.c_int32()
     with pytest.raises(ValueError, match="height/width"):
         _native.check(lib.ow_plan_dims(ctypes.byref(plan), ctypes.byref(q), ctypes.byref(q)), "ow_plan_dims")
+
+
+def test_noalloc_rejects_more_rows_than_the_scratch() -> None:
+    """The size check of ow_bigemm_fwd_noalloc runs on the host before any device call, so it is
+    exercised here without a GPU: the pointers are never dereferenced (a regression fails at the
+    device lookup, not in a kernel)."""
+    from omniwave_amd.routing import native_plan
+
+    h, w, c, d = 56, 56, 128, 64
+    plan = build_route_plan(h, w, c, 16, d, "local", 0)
+    b = (1 << 20) // (h * w) + 1
+    lib = _native.lib()
+    oplan = native_plan(plan)
+    nbytes = lib.ow_packed_weight_bytes(c // d, d, 2 * d, _native.OW_DTYPE_BF16)
+    flags = _native.OW_FUSE_NORM | _native.OW_FUSE_RESIDUAL
+    fake = ctypes.c_void_p(18)  # unaligned: element access, which needs the row scales
+    rc = lib.ow_bigemm_fwd_noalloc(fake, ctypes.c_void_p(1 << 20), 1e-6, ctypes.c_void_p(1 << 24), nbytes, fake, fake,
+                                   ctypes.byref(oplan), b, 2 * d, _native.OW_DTYPE_BF16, flags, None)
+    assert rc == 2 and b"scratch" in lib.ow_last_error()

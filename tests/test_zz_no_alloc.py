@@ -55,26 +55,69 @@ def activations(b, h, w, c, dtype, aligned, seed):
     return x
 
 
-def run_both(x, packed, plan, dtype):
+def run_fwd(x, packed, plan, dtype):
+    """ow_bigemm_fwd with a workspace of its own (the entry the no-allocation one must equal)."""
     lib = _native.lib()
     tok, ch = device_tables(plan, DEV)
     oplan = native_plan(plan)
     b = x.shape[0]
     d = int(plan.channel_indices.shape[1])
     out_ref = torch.empty(x.shape, dtype=dtype, device=DEV)
-    out_new = torch.empty(x.shape, dtype=dtype, device=DEV)
     ws_bytes = lib.ow_fwd_workspace_bytes(ctypes.byref(oplan), b, FLAGS)
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=DEV)
     stream = torch.cuda.current_stream(DEV).cuda_stream
-    code = _DTYPE_CODE[dtype]
     _native.check(lib.ow_bigemm_fwd(x.data_ptr(), out_ref.data_ptr(), 1e-6, packed.data_ptr(), packed.numel(),
-                                    tok.data_ptr(), ch.data_ptr(), ctypes.byref(oplan), b, 2 * d, code, FLAGS,
-                                    ws.data_ptr(), ws_bytes, stream), "ow_bigemm_fwd")
+                                    tok.data_ptr(), ch.data_ptr(), ctypes.byref(oplan), b, 2 * d, _DTYPE_CODE[dtype],
+                                    FLAGS, ws.data_ptr(), ws_bytes, stream), "ow_bigemm_fwd")
+    return out_ref
+
+
+def run_both(x, packed, plan, dtype):
+    lib = _native.lib()
+    tok, ch = device_tables(plan, DEV)
+    oplan = native_plan(plan)
+    b = x.shape[0]
+    d = int(plan.channel_indices.shape[1])
+    out_ref = run_fwd(x, packed, plan, dtype)
+    out_new = torch.empty(x.shape, dtype=dtype, device=DEV)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    code = _DTYPE_CODE[dtype]
     _native.check(lib.ow_bigemm_fwd_noalloc(x.data_ptr(), out_new.data_ptr(), 1e-6, packed.data_ptr(),
                                             packed.numel(), tok.data_ptr(), ch.data_ptr(), ctypes.byref(oplan), b,
                                             2 * d, code, FLAGS, stream), "ow_bigemm_fwd_noalloc")
     torch.cuda.synchronize()
     return out_ref, out_new
+
+
+def test_noalloc_inside_graph_capture() -> None:
+    """The entry called first inside a torch.cuda.graph capture (in a process that has not called
+    it before, this is where the per-device scratch lookup happens): every replay of the graph
+    equals ow_bigemm_fwd's eager output bit for bit, with eager work between the replays."""
+    h, w, c, d, dtype = 14, 14, 512, 128, torch.bfloat16
+    announce(f"noalloc inside graph capture {h}x{w}x{c} {dtype} unaligned B=3")
+    plan = omniwave_amd.build_route_plan(h, w, c, 16, d, "shifted", 0)
+    packed = weights(c, d, dtype, plan, seed=5)
+    x = activations(3, h, w, c, dtype, aligned=False, seed=21)  # element access: uses the scratch
+    lib = _native.lib()
+    tok, ch = device_tables(plan, DEV)
+    oplan = native_plan(plan)
+    ref = run_fwd(x, packed, plan, dtype)
+    torch.cuda.synchronize()
+    out = torch.empty(x.shape, dtype=dtype, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stream = torch.cuda.current_stream(DEV).cuda_stream
+        _native.check(lib.ow_bigemm_fwd_noalloc(x.data_ptr(), out.data_ptr(), 1e-6, packed.data_ptr(),
+                                                packed.numel(), tok.data_ptr(), ch.data_ptr(), ctypes.byref(oplan),
+                                                3, 2 * d, _DTYPE_CODE[dtype], FLAGS, stream),
+                      "ow_bigemm_fwd_noalloc (captured)")
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}: {(out != ref).sum().item()} elements differ"
+        run_both(activations(1, h, w, c, dtype, aligned=False, seed=30 + i), packed, plan, dtype)
 
 
 CASES = [  # (H, W, C, d, dtype, aligned, batches): scratch paths first, then the in-kernel one
@@ -95,17 +138,3 @@ def test_noalloc_matches_fwd_on_two_calls(h, w, c, d, dtype, aligned, batches) -
         x = activations(b, h, w, c, dtype, aligned, seed=10 + i)
         ref, new = run_both(x, packed, plan, dtype)
         assert torch.equal(ref, new), f"call {i + 1} (B={b}): {(ref != new).sum().item()} elements differ"
-
-
-def test_noalloc_rejects_more_rows_than_the_scratch() -> None:
-    announce("noalloc size limit")
-    h, w, c, d = 56, 56, 128, 64
-    plan = omniwave_amd.build_route_plan(h, w, c, 16, d, "local", 0)
-    b = SCRATCH_ROWS // (h * w) + 1
-    lib = _native.lib()
-    oplan = native_plan(plan)
-    nbytes = lib.ow_packed_weight_bytes(c // d, d, 2 * d, _native.OW_DTYPE_BF16)
-    fake = ctypes.c_void_p(18)  # unaligned: element access, which needs the row scales
-    rc = lib.ow_bigemm_fwd_noalloc(fake, ctypes.c_void_p(1 << 20), 1e-6, ctypes.c_void_p(1 << 24), nbytes, fake, fake,
-                                   ctypes.byref(oplan), b, 2 * d, _native.OW_DTYPE_BF16, FLAGS, None)
-    assert rc == 2 and b"scratch" in lib.ow_last_error()
