@@ -130,6 +130,20 @@ __device__ __forceinline__ void load_pieces(__amdgpu_buffer_rsrc_t rx, int32_t r
   for (int k = 0; k < NV; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * k, 0, 0);
 }
 
+// q_c = 2, contiguous groups: the row's two channel groups rotated so that group g comes first:
+// registers 4 b .. 4 b + 3 hold pieces 2 k + hh, k = 4 ((b + g) mod 2) .. + 3, so the group's own
+// pieces are always v[0..3] (g is uniform: only the load offsets depend on it).
+__device__ __forceinline__ void load_pieces_rot2(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh, int g,
+                                                 u32x4 (&v)[8]) {
+  const uint32_t base = row >= 0 ? static_cast<uint32_t>(row) * static_cast<uint32_t>(channels * 2) + 16u * hh
+                                 : kOutOfRange;
+  const uint32_t own = 128u * static_cast<uint32_t>(g), other = 128u - own;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + own + 32u * j, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + other + 32u * j, 0, 0);
+}
+
 // Pieces 2 (k0 + k) + hh, k < 4, of this lane's token row (one channel group of a d = 64 row):
 // one batch of the streamed row read.
 __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh, int k0,
@@ -150,6 +164,8 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   // being held whole (64 registers) for a unit.
   constexpr bool STREAM = QC == 4;
   constexpr int NX = STREAM ? 4 : NV;  // pieces carried from one unit to the next
+  // q_c = 2 with contiguous groups: rows loaded with the own group's pieces first.
+  constexpr bool ROT = QC == 2 && !SG;
   static_assert(!SG || QC == 2, "interleaved channel groups: q_c = 2");
   // SG: waves 0-3 take group 0 and waves 4-7 group 1 of the same four pairs (wave w and w ^ 4
   // share a pair), so the pair's output rows are put together in LDS and stored whole.
@@ -216,6 +232,17 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     if (a.norm) {
       if constexpr (STREAM) {
         acc = ssq;
+      } else if constexpr (ROT) {
+        // The two groups' partial sums: with the rotated rows each group's waves add the same
+        // two values (in either order: the same fp32 sum).
+        float part[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[b] = Ty::dot2sq(xc[4 * b + k][e], part[b]);
+        acc = part[0] + part[1];
       } else {
 #pragma unroll
         for (int k = 0; k < NV; ++k)
@@ -229,18 +256,11 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       // piece 2 k + hh of the row holds group columns 8 k + 4 hh .. 8 k + 4 hh + 3.
 #pragma unroll
       for (int k = 0; k < NV; ++k) *reinterpret_cast<u32x2*>(&tile[l32 * kLdt + 8 * k + 4 * hh]) = strided_pack<4>(xc[k], res);
-    } else if constexpr (STREAM || QC == 1) {
+    } else {
+      // q_c = 1, the streamed batch of group g (q_c = 4) or the rotated rows (q_c = 2): the
+      // group's pieces are xc[0..3].
 #pragma unroll
       for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
-    } else {
-      const int k0 = g == 0 ? 0 : 4;  // g is uniform: a scalar select, no dynamic register indexing
-      if (k0 == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[4 + k];
-      }
     }
     if (hh == 0) {
       rsc[l32] = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
@@ -248,8 +268,10 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     }
     if constexpr (STREAM)
       ssq = 0.0f;  // the next pair's batches are read during the chunk loop
+    else if constexpr (ROT)
+      load_pieces_rot2(rx, in_n, C, hh, g, xc);  // the next pair, a unit ahead of its use
     else
-      load_pieces<NV>(rx, in_n, C, hh, xc);  // the next pair, a unit ahead of its use
+      load_pieces<NV>(rx, in_n, C, hh, xc);
     ent = next_entry();
     wave_lds_sync();
 
@@ -306,7 +328,11 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       static_assert(NU == 0 || NO == 0 || 2 * NU == 16, "two gate values per U'/V' product");
       auto read = [&](auto ic) -> u32x4 {
         constexpr int i = decltype(ic)::value;
-        constexpr int f = i < NU ? (E + 1) * kFrCh + ((i & 1) ? kKS + i / 2 : i / 2) : E * kFrCh + 2 * kKS + (i - NU);
+        // B_o products in the order (block 0, K step 0), (block 1, 0), (0, 1), (1, 1): the two
+        // accumulators alternate, so no product waits on the one issued right before it.
+        constexpr int j = i - NU;
+        constexpr int f = i < NU ? (E + 1) * kFrCh + ((i & 1) ? kKS + i / 2 : i / 2)
+                                 : E * kFrCh + 2 * kKS + 2 * (j % kMB) + j / kMB;
         return lds_read_async<f * kFragElems * 2>(wbase);
       };
       u32x4 fr[DEPTH];
@@ -340,7 +366,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
             Vn = Ty::mma32(fr[i % DEPTH], Pv[i / 2], Vn);
         } else {
           constexpr int j = i - NU;
-          W[j / 2] = Ty::mma32(Z[j % 2], fr[i % DEPTH], W[j / 2]);
+          W[j % kMB] = Ty::mma32(Z[j / kMB], fr[i % DEPTH], W[j % kMB]);
         }
         if constexpr (i + DEPTH < NF) fr[i % DEPTH] = read(std::integral_constant<int, i + DEPTH>{});
         if constexpr (NO > 0 && i < NU) {
@@ -448,6 +474,8 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
         for (int k = 0; k < 4; ++k) x[k] = v[k];
       }
     }
+  } else if constexpr (ROT) {
+    load_pieces_rot2(rx, in0, C, hh, g, x);
   } else {
     load_pieces<NV>(rx, in0, C, hh, x);
   }

@@ -37,6 +37,17 @@ constexpr int kHeadElems = 3 * kFragElems;  // token-side operands (A_u, A_v, A_
 constexpr float kNegLog2e = -1.4426950408889634f;
 constexpr float kNegLn2 = -0.6931471805599453f;
 
+__device__ __forceinline__ uint16_t lo16(uint32_t v) { return static_cast<uint16_t>(v & 0xffffu); }
+__device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16_t>(v >> 16); }
+
+// A constant in a scalar register that the compiler cannot fold into an instruction's constant
+// operand (the asm is not volatile, so it is still hoisted and shared).
+__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t c) {
+  uint32_t r;
+  asm("; opaque constant %0" : "=s"(r) : "0"(c));
+  return r;
+}
+
 struct BF16 {
   static __device__ __forceinline__ uint16_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
@@ -51,6 +62,15 @@ struct BF16 {
   static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
     const bf16x2 v = __builtin_bit_cast(bf16x2, a);
     return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  }
+  // x.lo + v.lo (H = 0) or x.hi + v.hi (H = 1) in fp32 with one rounding: a dot product of v with
+  // (1, 0) or (0, 1) accumulated onto the widened half of x (the products are exact).  The
+  // selector goes through a scalar register (opaque_sgpr): as a literal the compiler encodes
+  // (1, 0) as the inline constant 1.0, which this instruction does not read as (1, 0).
+  template <int H>
+  static __device__ __forceinline__ float add_half(uint32_t x, uint32_t v) {
+    const bf16x2 sel = __builtin_bit_cast(bf16x2, opaque_sgpr(H ? 0x3f800000u : 0x00003f80u));
+    return __builtin_amdgcn_fdot2_f32_bf16(sel, __builtin_bit_cast(bf16x2, v), to_f32(H ? hi16(x) : lo16(x)), false);
   }
   static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -75,6 +95,11 @@ struct F16 {
   static __device__ __forceinline__ float dot2sq(uint32_t a, float acc) {
     const f16x2 v = __builtin_bit_cast(f16x2, a);
     return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+  template <int H>
+  static __device__ __forceinline__ float add_half(uint32_t x, uint32_t v) {
+    const f16x2 sel = __builtin_bit_cast(f16x2, opaque_sgpr(H ? 0x3c000000u : 0x00003c00u));
+    return __builtin_amdgcn_fdot2(sel, __builtin_bit_cast(f16x2, v), to_f32(H ? hi16(x) : lo16(x)), false);
   }
   static __device__ __forceinline__ f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -124,14 +149,17 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ uint16_t lo16(uint32_t v) { return static_cast<uint16_t>(v & 0xffffu); }
-__device__ __forceinline__ uint16_t hi16(uint32_t v) { return static_cast<uint16_t>(v >> 16); }
 
 // round(x + v) on two packed values (low and high halves): the residual of the block output,
 // x the input and v the rounded delta.
+//
+// Each half is one 2-element dot product of v with (1, 0) or (0, 1) accumulated onto the widened
+// half of x: the products are exact, so the fp32 result is the rounded sum x + v, as a separate
+// fp32 add forms it (only signed zeros may differ: -0 + -0 can give +0).  Two instructions per
+// value instead of an unpack of each operand and an add.
 template <class Ty>
 __device__ __forceinline__ uint32_t add_residual2(uint32_t x, uint32_t v) {
-  return Ty::pack2(Ty::to_f32(lo16(x)) + Ty::to_f32(lo16(v)), Ty::to_f32(hi16(x)) + Ty::to_f32(hi16(v)));
+  return Ty::pack2(Ty::template add_half<0>(x, v), Ty::template add_half<1>(x, v));
 }
 
 // Direct global -> LDS copy of one 1 KB operand fragment by one wave (16 bytes per lane, LDS
@@ -681,11 +709,12 @@ __device__ __forceinline__ void pair_output_t(const f32x16 (&W)[MB], u32x4 ao, i
   const bool g0 = (lane & 16) == 0;
   const u32x4 ao0 = keep_if(g0, ao), ao1 = keep_if(!g0, ao);
   const f32x16 zero = {};
+  // Both K steps of each block, the blocks interleaved so that no product waits on the one
+  // issued right before it.
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 0), ao0, zero);
-    dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 1), ao1, dl[mb]);
-  }
+  for (int mb = 0; mb < MB; ++mb) dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 0), ao0, zero);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) dl[mb] = Ty::mma32(pack_kstep<Ty>(W[mb], 1), ao1, dl[mb]);
 }
 
 inline int hip_status(hipError_t e, const char* what) {
