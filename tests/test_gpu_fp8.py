@@ -191,3 +191,54 @@ def test_fp8_rejects_training_and_fp32() -> None:
         blk.train()(x)
     with pytest.raises(RuntimeError, match="fp8 variant"):
         blk.eval()(x.float())
+
+
+def test_fp8_large_batch_is_per_sample() -> None:
+    """At the batch of the fp8 sweep's largest point (14x14x512, B = 1024, shifted): three
+    sampled images equal the same images run as a batch of two bit for bit (the quantisation
+    scales are static per weight set, so an image's result depends on that image only), and
+    match the fp32 oracle and the emulation."""
+    h, w, c, d = STAGES["s3"]
+    announce("fp8 block s3 shifted B=1024 (per-sample, sampled images vs oracle)")
+    plan, x, p = make_case(1024, h, w, c, d, "shifted", 0, seed=11)
+    out = run_fp8(x, plan, p, residual=False)
+    oplan = oracle_plan(h, w, c, 16, d, "shifted", 0)
+    for i in (0, 511, 1023):
+        j = i + 1 if i + 1 < 1024 else i - 1
+        sel = [i, j] if j > i else [j, i]
+        pair = run_fp8(x[sel].contiguous(), plan, p, residual=False)
+        k = sel.index(i)
+        assert torch.equal(out[i], pair[k]), f"image {i}: batch 1024 != batch 2"
+        ref = block_reference(x[i:i + 1].float(), oplan, p, residual=False)
+        e_ref = rel_l2(out[i:i + 1], ref)
+        e_emu = rel_l2(out[i:i + 1], emulate_fp8_delta(x[i:i + 1], plan, p))
+        print(f"fp8 B=1024 image {i}: delta vs fp32 {e_ref:.2e}, vs emulation {e_emu:.2e}", flush=True)
+        assert e_ref <= 5e-2 and e_emu <= 1e-2
+
+
+def test_fp8_model_batch_256_sampled_logits(oracle_backend) -> None:
+    """OmniWeave-T with fp8 on its d = 128 blocks at the benchmark's batch (256): the logits of
+    three sampled images against the fp32 oracle model on those images (LayerScale 1, so the
+    blocks move the logits)."""
+    announce("omniweave_t fp8 forward B=256, sampled logits vs the fp32 oracle")
+    torch.manual_seed(0)
+    model = omniwave_amd.create_model("omniweave_t").eval()
+    with torch.no_grad():
+        for stage in model.stages:
+            for blk in stage.blocks:
+                blk.gamma.fill_(1.0)
+    model = model.to(torch.bfloat16)
+    oracle_model = copy.deepcopy(model).float()
+    for stage in oracle_model.stages:
+        for blk in stage.blocks:
+            blk.backend = "reference"
+    omniwave_amd.enable_fp8(model)
+    x = torch.randn(256, 3, 224, 224, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    with torch.inference_mode():
+        got = model.to(DEV)(x.to(DEV)).float().cpu()
+    with torch.no_grad():
+        for i in (0, 128, 255):
+            want = oracle_model(x[i:i + 1].float())
+            err = rel_l2(got[i:i + 1], want)
+            print(f"fp8 B=256 image {i}: logits rel-L2 {err:.2e}", flush=True)
+            assert err <= 5e-2
