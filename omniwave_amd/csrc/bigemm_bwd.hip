@@ -674,7 +674,9 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
   __shared__ __attribute__((aligned(16))) u32x4 tok[5][64];  // A_u, A_v, A_o^T, A_u^T, A_v^T operand rows
   __shared__ float red[4][3][256];
   __shared__ __attribute__((aligned(16))) uint16_t zst[4][32 * kZSt];  // per wave: one chunk output, staged
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave is uniform: readfirstlane keeps it and the pair, slot and tile positions derived from it in
+  // scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, h4 = lane >> 4;
   const bool g0 = (lane & 16) == 0;
   const int64_t wg_per_q = (a.pairs_per_q + 3) / 4;
