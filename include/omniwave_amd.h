@@ -398,18 +398,37 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
                            int64_t n_partial, int32_t rd, int32_t dtype, void* stream);
 
 /* Parameter-gradient reduction of the d = 64 backward (replaces the slot-reduction GEMMs over
- * the intermediates): from pu, pv, dw ([q_c][slots][64]) and z, du, dv ([q_c][slots][rd]) as
- * ow_bwd_fused / ow_bwd_fused_routed write them (per 32-slot pair, 32x32x16 operand fragments
- * whose K runs over the pair's slots), per workgroup w the sums over its slots of
- * dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and dB_o'' = Z^T dW' ([rd][64]) over
- * slot ranges into partial rows (fp32, those three in that order, 3 * 64 * rd floats); row w
- * covers channel group w % q_c, so the caller adds rows w = q, q + q_c, .. for group q
- * (w < n_partial = ow_bwd_param_reduce64_partials(slots, q_c, rd), a multiple of q_c).
+ * the intermediates, omniweave/ops/triton.py:256-292 through autograd): from pu, pv, dw
+ * ([q_c][slots][64]) and z, du, dv ([q_c][slots][rd]) as ow_bwd_fused / ow_bwd_fused_routed
+ * write them (per 32-slot pair, 32x32x16 operand fragments whose K runs over the pair's slots),
+ * the sums over slot ranges of dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and
+ * dB_o'' = Z^T dW' ([rd][64]) per channel group, fp32.  partial holds n_partial =
+ * ow_bwd_param_reduce64_partials(slots, q_c, rd) rows of 3 * 64 * rd floats (a multiple of q_c):
+ * R = n_partial / q_c ranges, each a [3][q_c][64 * rd] block (product, group), so the gradients
+ * are the sum of the R blocks (ow_sum_rows with rows R, cols 3 * q_c * 64 * rd).
  * slots % 32 == 0, rd in {128, 256}, bf16 / f16. */
 int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c, int32_t rd);
 int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
                           const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
                           int32_t dtype, void* stream);
+
+/* The same reduction for d = 128, from the slot-major intermediates of ow_bwd_channel /
+ * ow_bwd_channel_routed (pu, pv, dw [q_c][slots][128]; z, du, dv [q_c][slots][rd], rows in slot
+ * order): partial holds n_partial = ow_bwd_param_reduce128_partials(slots, q_c, rd) rows of
+ * 3 * 128 * rd floats, R = n_partial / q_c blocks [3][q_c][128 * rd] whose sum (ow_sum_rows) is
+ * dB_u'', dB_v'' ([128][rd] per group) and dB_o'' ([rd][128]).  slots % 16 == 0, rd in
+ * {128, 256}, bf16 / f16; each intermediate below 2 GiB. */
+int64_t ow_bwd_param_reduce128_partials(int64_t slots, int32_t q_c, int32_t rd);
+int ow_bwd_param_reduce128(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
+                           const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
+                           int32_t dtype, void* stream);
+
+/* out[c] = sum over r < rows of partial[r * cols + c], fp32, in a fixed order for given rows
+ * and cols (run to run identical): the sums of the per-workgroup partials above and of the
+ * token-matrix partials of ow_bwd_fused / ow_bwd_channel2 (the reference's autograd sums them
+ * inside its GEMMs, omniweave/ops/triton.py:256-292).  cols % 4 == 0, both pointers 16-byte
+ * aligned, rows >= 1. */
+int ow_sum_rows(const float* partial, int64_t rows, int64_t cols, float* out, void* stream);
 
 /* ow_bwd_fused with the routing folded in, for plans whose channel order is the identity
  * (radix level 0 or one channel group) and C = q_c * 64 (replaces ow_bwd_gather and

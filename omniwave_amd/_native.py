@@ -176,6 +176,13 @@ _SIGNATURES = {
         [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                  ctypes.c_void_p],
     ),
+    "ow_bwd_param_reduce128_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
+    "ow_bwd_param_reduce128": (
+        ctypes.c_int,
+        [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                 ctypes.c_void_p],
+    ),
+    "ow_sum_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
     "ow_bwd_fused_routed": (
         ctypes.c_int,
         [ctypes.c_void_p] * 5 + [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_size_t] + [ctypes.c_void_p] * 8

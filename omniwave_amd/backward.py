@@ -18,8 +18,10 @@ accumulation, entirely on the HIP stream of the gradient:
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
   ``ow_bwd_gate``;
-* the parameter-gradient reductions over slots: for d = 64 ``ow_bwd_param_reduce64`` over the
-  fused kernel's fragment-ordered intermediates, otherwise batched GEMMs.
+* the parameter-gradient reductions over slots: ``ow_bwd_param_reduce64`` over the d = 64 fused
+  kernel's fragment-ordered intermediates, ``ow_bwd_param_reduce128`` over the d = 128 channel
+  kernels' slot-major ones (fp32 batched GEMMs for the fp32 path), and every per-workgroup fp32
+  partial summed by ``ow_sum_rows`` in a fixed order.
 
 Gradients are formed for the folded operands the forward evaluates (B_u'' = -log2(e) w B_u,
 B_v'' = -ln(2) w B_v, B_o'' = B_o diag(gamma), SiLU(U) V = U'V' / (1 + 2^U')) and mapped back
@@ -75,26 +77,13 @@ def _tile_outer(lib, in1: Tensor, in2: Tensor, d: int, code: int, stream: int) -
     return partial.sum(dim=2)
 
 
-_ONES: dict = {}
-
-
-def _sum_partials(partial: Tensor, out: Tensor) -> None:
-    """Sum of the per-workgroup fp32 partial rows of ``partial`` ([n, ...]) into ``out``, as one
-    GEMV against a cached vector of ones: torch's multi-block sum clears a semaphore buffer with
-    an extra fill before its reduction.  The ones vector is made outside graph capture only (its
-    memory then belongs to no graph); a capture that finds none uses the plain sum.  Its fill
-    is waited for once, so a later call on any stream reads it filled."""
-    n = partial.shape[0]
-    ones = _ONES.get((partial.device, n))
-    if ones is None:
-        if partial.is_cuda and torch.cuda.is_current_stream_capturing():
-            torch.sum(partial, dim=0, out=out)
-            return
-        ones = torch.ones(n, dtype=torch.float32, device=partial.device)
-        if ones.is_cuda:
-            torch.cuda.current_stream(partial.device).synchronize()
-        _ONES[(partial.device, n)] = ones
-    torch.mv(partial.view(n, -1).t(), ones, out=out.view(-1))
+def _sum_rows(lib, partial: Tensor, rows: int, out: Tensor, stream: int) -> None:
+    """out = the sum of the ``rows`` equal-sized row blocks of the fp32 buffer ``partial``
+    (``ow_sum_rows``: a fixed summation order, so replays and reruns give identical bits).
+    Both buffers are contiguous fp32 and start 16-byte aligned."""
+    cols = out.numel()
+    assert partial.is_contiguous() and out.is_contiguous() and partial.numel() == rows * cols
+    _native.check(lib.ow_sum_rows(partial.data_ptr(), rows, cols, out.data_ptr(), stream), "ow_sum_rows")
 
 
 def _slot_reduce(a: Tensor, b: Tensor) -> Tensor:
@@ -195,17 +184,16 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
 
 
 def _cast_grads(dx, g_all, fuse_norm, channels, q_c, d, rd, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o):
-    """Parameter gradients as views of the fp32 buffer ``g_all`` (norm weight, gamma, the token
-    matrices, B_u, B_v, B_o), cast to each parameter's dtype: one cast of the whole buffer when
-    they share a dtype."""
-    n_c = (2 if fuse_norm else 1) * channels
+    """Parameter gradients as views of the fp32 buffer ``g_all`` (the token matrices, B_u, B_v,
+    B_o, then gamma and the norm weight), cast to each parameter's dtype: one cast of the whole
+    buffer when they share a dtype."""
     nb = q_c * d * rd
     params = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o, b_u, b_v, b_o]
 
     def views(buf):
-        o_c = buf[:n_c].view(-1, channels)
-        o_a = buf[n_c:n_c + 768].view(3, 16, 16)
-        o_b = buf[n_c + 768:]
+        o_a = buf[:768].view(3, 16, 16)
+        o_b = buf[768:768 + 3 * nb]
+        o_c = buf[768 + 3 * nb:].view(-1, channels)
         return (o_c[1] if fuse_norm else None, o_c[0], o_a[0], o_a[1], o_a[2],
                 o_b[:nb].view(q_c, d, rd), o_b[nb:2 * nb].view(q_c, d, rd), o_b[2 * nb:].view(q_c, rd, d))
 
@@ -261,12 +249,13 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
         nw = _fp32(norm_weight, dev) if fuse_norm else None
         gm = _fp32(gamma, dev)
         au, av, ao = (_fp32(a, dev) for a in (a_u, a_v, a_o))
-    # The fp32 parameter gradients in one buffer (norm weight, gamma, the token matrices, then
-    # B_u, B_v, B_o), so that parameters of one dtype are cast back with one kernel.
+    # The fp32 parameter gradients in one buffer (the token matrices, B_u, B_v, B_o, then gamma
+    # and the norm weight: every block that a kernel sums into starts 16-byte aligned), so that
+    # parameters of one dtype are cast back with one kernel.
     n_c = (2 if fuse_norm else 1) * plan.channels
     nb = q_c * d * rd
-    g_all = torch.empty(n_c + 768 + 3 * nb, dtype=torch.float32, device=dev)
-    g_a = g_all[n_c:n_c + 768].view(3, 256)
+    g_all = torch.empty(768 + 3 * nb + n_c, dtype=torch.float32, device=dev)
+    g_a = g_all[:768].view(3, 256)
 
     with torch.cuda.device(dev):
         if drop_scale is not None:
@@ -329,18 +318,17 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
                                                dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                stream), "ow_bwd_fused")
                 del xt, dyt
-            _sum_partials(partial, g_a)  # [3, 256]: dA_u, dA_v, dA_o
+            _sum_rows(lib, partial, n_part, g_a, stream)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
-            # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates.
+            # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates: per slot
+            # range one [3, q_c, d * rd] block, summed over the ranges.
             n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c, rd)
             red = torch.empty(n_red, 3 * d * rd, dtype=torch.float32, device=dev)
             _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
                                                     du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,
                                                     rd, code, stream), "ow_bwd_param_reduce64")
-            # Summed into [3, q_c, d * rd] through a permuted output view, so each gradient is a
-            # contiguous slice (no copies before ow_bwd_params).
             g_b3 = torch.empty(3, q_c, d * rd, dtype=torch.float32, device=dev)
-            torch.sum(red.view(n_red // q_c, q_c, 3, d * rd), dim=0, out=g_b3.permute(1, 0, 2))
+            _sum_rows(lib, red, n_red // q_c, g_b3, stream)
             d_bu = g_b3[0].view(q_c, d, rd)
             d_bv = g_b3[1].view(q_c, d, rd)
             d_bo = g_b3[2].view(q_c, rd, d)
@@ -382,11 +370,19 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
                                                   dv.data_ptr(), au.data_ptr(), av.data_ptr(), wpk.data_ptr(), nbytes,
                                                   dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
                                                   stream), "ow_bwd_channel2")
-            _sum_partials(partial, g_a)  # [3, 256]: dA_u, dA_v, dA_o
+            _sum_rows(lib, partial, n_part, g_a, stream)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
-            d_bu = _slot_reduce(pu, du)   # [q_c, d, rd]
-            d_bv = _slot_reduce(pv, dv)
-            d_bo = _slot_reduce(z, dw)    # [q_c, rd, d]
+            # dB_u'', dB_v'', dB_o'' from the slot-major intermediates, as for d = 64.
+            n_red = lib.ow_bwd_param_reduce128_partials(slots, q_c, rd)
+            red = torch.empty(n_red, 3 * d * rd, dtype=torch.float32, device=dev)
+            _native.check(lib.ow_bwd_param_reduce128(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
+                                                     du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,
+                                                     rd, code, stream), "ow_bwd_param_reduce128")
+            g_b3 = torch.empty(3, q_c, d * rd, dtype=torch.float32, device=dev)
+            _sum_rows(lib, red, n_red // q_c, g_b3, stream)
+            d_bu = g_b3[0].view(q_c, d, rd)
+            d_bv = g_b3[1].view(q_c, d, rd)
+            d_bo = g_b3[2].view(q_c, rd, d)
             del wpk, z, du, dv, pu, pv, dw
             if not routed:
                 del xt, dyt
@@ -443,10 +439,10 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
 
         # Parameter gradients from the folded ones, into g_all (every element is written: each
         # channel of the permutation exactly once).
-        g_b = g_all[n_c + 768:]
+        g_b = g_all[768:768 + 3 * nb]
         g_bu, g_bv = g_b[:nb].view(q_c, d, rd), g_b[nb:2 * nb].view(q_c, d, rd)
         g_bo = g_b[2 * nb:].view(q_c, rd, d)
-        g_c = g_all[:n_c].view(-1, plan.channels)
+        g_c = g_all[768 + 3 * nb:].view(-1, plan.channels)
         g_gamma = g_c[0]
         g_nw = g_c[1] if fuse_norm else None
         _native.check(lib.ow_bwd_params(*[w.data_ptr() for w in ws], _DTYPE_CODE[wdtype],

@@ -1051,9 +1051,10 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
 // t = w / 4 (0: dB_u'', 1: dB_v'', 2: dB_o'' as its transpose dW'^T Z) for row block
 // e = w % 4 + 4 h and both 32-channel blocks, in fp32 registers.  Every workgroup runs the same
 // number of pairs per range; pairs past the end read as zero (out-of-range offsets) and add
-// nothing.  The sums go to the workgroup's blocks of partial[s q_c + q] (dB_u'' [64][rd],
-// dB_v'' [64][rd], dB_o'' [rd][64]; the H row halves fill disjoint blocks), which the caller
-// adds over s for each group.
+// nothing.  The sums go to the workgroup's blocks of range s's partial row, laid out
+// [3][q_c][64 rd] (product t of group q: dB_u'' [64][rd], dB_v'' [64][rd], dB_o'' [rd][64]; the H
+// row halves fill disjoint blocks), so that the sum of the rows over s (ow_sum_rows) is the
+// [3][q_c][64 rd] gradient buffer.
 struct ParamReduceArgs {
   const uint16_t* pu;  // fragments, [q_c][pairs][32 * 64]
   const uint16_t* pv;
@@ -1061,7 +1062,7 @@ struct ParamReduceArgs {
   const uint16_t* z;   // fragments, [q_c][pairs][32 * rd]
   const uint16_t* du;
   const uint16_t* dv;
-  float* partial;      // [rows][2 * 64 * rd + rd * 64]
+  float* partial;      // [ranges][3][q_c][64 * rd]
   int64_t pairs;       // per group
   int32_t q_c;
 };
@@ -1141,15 +1142,14 @@ __global__ void __launch_bounds__(64 * kReduceWaves) bwd_param_reduce64_kernel(P
   wait_vmcnt<0>();  // the trailing copies (past the end: zeros) are done before the exit
   mfma_drain();
   // Accumulator register i of lane (l32, hh): channel 32 m + kord(i, hh), row 32 e + l32.
-  float* out = a.partial + (s0 * a.q_c + q) * (3 * kBwdD * RD);
+  float* out = a.partial + ((s0 * 3 + t) * a.q_c + q) * (kBwdD * RD);
   const int e = e0 + 4 * h;
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int c = 32 * m + 8 * (i >> 2) + 4 * hh + (i & 3), r = 32 * e + l32;
-      const int64_t o = t < 2 ? t * kBwdD * RD + c * RD + r : 2 * kBwdD * RD + r * kBwdD + c;
-      out[o] = acc[m][i];
+      out[t < 2 ? c * RD + r : r * kBwdD + c] = acc[m][i];
     }
 }
 
@@ -1170,6 +1170,205 @@ int launch_param_reduce64(const ParamReduceArgs& a, int64_t grid, int32_t dtype,
     hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, NCH>), g, dim3(64 * kReduceWaves), 0, s, a);
   return hip_status(hipGetLastError(), "bwd_param_reduce64_kernel launch");
 }
+
+// ---- Parameter-gradient reduction, d = 128 -----------------------------------------------
+// dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' ([128][rd]) and dB_o'' = Z^T dW' ([rd][128]), each a
+// sum over the slots of one channel group, from the slot-major intermediates of
+// ow_bwd_channel (P_u, P_v, dW' [q_c][slots][128]; Z, dU', dV' [q_c][slots][rd]).  Workgroup b
+// takes group q = b % q_c, product t = (b / q_c) % 3 and 32-slot steps s, s + R, .. of that
+// group (s = b / (3 q_c), R = gridDim.x / (3 q_c)): per step it needs 32 rows of the product's
+// left tensor A (P_u, P_v or Z; MW channels) and of its right tensor B (dU', dV' or dW'; NW),
+// which its 8 waves copy (buffer_load ... lds, untracked, 1 KB per copy) into one of
+// kR2Stages LDS stages, kR2Stages - 1 steps ahead; one barrier per step.  A row keeps its 16-byte
+// pieces swizzled (piece p of row r at slot p ^ 4 (r & 3)), so the transposed operand reads
+// (ds_read_b64_tr_b16, four rows x 32 channels per 32 lanes) hit distinct banks.  Wave w owns a
+// 2 x NB block rectangle of the [MW][NW] product (32x32 blocks, fp32 registers) and reads its
+// 2 + NB operands per 16 slots.  The sums go to range s's partial row, laid out
+// [3][q_c][128 rd], so that the sum of the rows over s (ow_sum_rows) is the [3][q_c][128 rd]
+// gradient buffer.  Rows past the group's slots read as zero.
+struct ParamReduce128Args {
+  const uint16_t* pu;  // [q_c][slots][128]
+  const uint16_t* pv;
+  const uint16_t* dw;
+  const uint16_t* z;   // [q_c][slots][rd]
+  const uint16_t* du;
+  const uint16_t* dv;
+  float* partial;      // [ranges][3][q_c][128 * rd]
+  int64_t slots;       // per group, a multiple of 16
+  int32_t q_c;
+};
+constexpr int kR2D = 128;  // channel-group width d
+constexpr int kR2Waves = 8;
+constexpr int kR2Stages = 4;
+constexpr int kR2Slots = 32;  // slots per step
+
+// The LDS byte address of channel c of row r in a swizzled [rows][W] tile at base.
+template <int W>
+__device__ __forceinline__ uint32_t r2_at(uint32_t base, int r, int c) {
+  return base + 2u * static_cast<uint32_t>(r * W + ((((c >> 3) ^ (4 * (r & 3)))) << 3) + (c & 7));
+}
+
+template <class Ty, int MW, int NW>
+__device__ __forceinline__ void param_reduce128_product(const ParamReduce128Args& a, const uint16_t* A,
+                                                        const uint16_t* B, uint32_t lds0, int q, int64_t s0,
+                                                        int64_t sstep, float* out) {
+  constexpr int STAGE = kR2Slots * (MW + NW) * 2;         // bytes per stage
+  constexpr int COPIES = (MW + NW) * kR2Slots * 2 / 1024 / kR2Waves;  // per wave and step
+  constexpr int ACH = MW * kR2Slots * 2 / 1024;            // copies of the A rows per step
+  constexpr int NB = MW * NW / (1024 * kR2Waves * 2);      // n blocks per wave (m blocks: 2)
+  constexpr int MP = MW / 64;                              // m-block pairs
+  static_assert(COPIES * kR2Waves * 1024 == STAGE, "whole copies per wave");
+  static_assert(NB >= 1 && (NW / 32) % NB == 0 && MP * (NW / 32 / NB) == kR2Waves, "block rectangles");
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, half = (lane >> 4) & 1;
+  const int mp = w % MP, np = w / MP;
+  const int64_t steps = (a.slots + kR2Slots - 1) / kR2Slots;
+  const int64_t n_iter = s0 < steps ? (steps - s0 + sstep - 1) / sstep : 0;  // same for every wave
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, static_cast<uint32_t>(a.q_c * a.slots * MW * 2));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, static_cast<uint32_t>(a.q_c * a.slots * NW * 2));
+  // This wave's copies per step: 1 KB pieces k = w + 8 c of the stage (k < ACH: A rows, else B
+  // rows).  Lane -> row rr of the step and LDS slot sl of the row, which holds piece sl ^ 4 (rr & 3).
+  uint32_t loff[COPIES], ldsk[COPIES];
+  int lrow[COPIES];
+  bool isa[COPIES];
+#pragma unroll
+  for (int c = 0; c < COPIES; ++c) {
+    const int k = w + kR2Waves * c;
+    isa[c] = k < ACH;
+    const int width = isa[c] ? MW : NW, ppr = width / 8;  // 16-byte pieces per row
+    const int kk = isa[c] ? k : k - ACH;
+    const int rr = kk * (1024 / (2 * width)) + lane / ppr, sl = lane % ppr;
+    lrow[c] = rr;
+    loff[c] = static_cast<uint32_t>((rr * width + 8 * (sl ^ (4 * (rr & 3)))) * 2);
+    ldsk[c] = static_cast<uint32_t>((isa[c] ? 0 : kR2Slots * MW * 2) + kk * 1024);
+  }
+  auto issue = [&](int64_t i) {
+    const int64_t step = s0 + i * sstep;
+    const int64_t slot0 = step * kR2Slots;
+    const uint32_t stage = lds0 + static_cast<uint32_t>((i % kR2Stages) * STAGE);
+    const uint32_t row0 = static_cast<uint32_t>(q * a.slots + slot0);
+#pragma unroll
+    for (int c = 0; c < COPIES; ++c) {
+      const bool ok = step < steps && slot0 + lrow[c] < a.slots;
+      const uint32_t voff = ok ? row0 * static_cast<uint32_t>((isa[c] ? MW : NW) * 2) + loff[c] : kOffOut;
+      tile_copy_nt(isa[c] ? ra : rb, voff, stage + ldsk[c]);
+    }
+  };
+  f32x16 acc[2][NB] = {};
+#pragma unroll
+  for (int i = 0; i < kR2Stages - 1; ++i) issue(i);
+  for (int64_t i = 0; i < n_iter; ++i) {
+    // This wave's copies of step i landed (those of steps i + 1 .. i + kR2Stages - 2 may be in
+    // flight); the barrier makes every wave's visible and means every wave is done with stage
+    // (i - 1) % kR2Stages, which step i + kR2Stages - 1 takes.
+    wait_vmcnt<COPIES * (kR2Stages - 2)>();
+    __syncthreads();
+    issue(i + kR2Stages - 1);
+    const uint32_t sa = lds0 + static_cast<uint32_t>((i % kR2Stages) * STAGE), sb = sa + kR2Slots * MW * 2;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      // Lane (l32, hh) holds channel 32 blk + l32 of rows 16 g + 4 hh + 0..3 and 16 g + 8 + 4 hh
+      // + 0..3 (the K order of both operands).
+      const int r = 16 * g + 4 * hh + (l16 >> 2), cl = 16 * half + 4 * (l16 & 3);
+      u32x4 av[2], bv[NB];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int c = 32 * (2 * mp + m) + cl;
+        const u32x2 x = lds_read_tr16(r2_at<MW>(sa, r, c)), y = lds_read_tr16(r2_at<MW>(sa, r + 8, c));
+        av[m] = u32x4{x[0], x[1], y[0], y[1]};
+      }
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const int c = 32 * (NB * np + n) + cl;
+        const u32x2 x = lds_read_tr16(r2_at<NW>(sb, r, c)), y = lds_read_tr16(r2_at<NW>(sb, r + 8, c));
+        bv[n] = u32x4{x[0], x[1], y[0], y[1]};
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) acc[m][n] = Ty::mma32(av[m], bv[n], acc[m][n]);
+    }
+  }
+  wait_vmcnt<0>();  // the trailing copies (past the end: zeros) are done before the exit
+  mfma_drain();
+  // Accumulator register i of lane (l32, hh): row 32 mb + kord(i, hh), column 32 nb + l32.
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = 32 * (2 * mp + m) + 8 * (i >> 2) + 4 * hh + (i & 3), col = 32 * (NB * np + n) + l32;
+        out[row * NW + col] = acc[m][n][i];
+      }
+}
+
+template <class Ty, int RD>
+__global__ void __launch_bounds__(64 * kR2Waves) bwd_param_reduce128_kernel(ParamReduce128Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t st[kR2Stages][kR2Slots * (kR2D + RD)];
+  const int q = blockIdx.x % a.q_c, t = (blockIdx.x / a.q_c) % 3;
+  const int64_t s0 = blockIdx.x / (3 * a.q_c), sstep = gridDim.x / (3 * a.q_c);
+  float* out = a.partial + ((s0 * 3 + t) * a.q_c + q) * (kR2D * RD);
+  const uint32_t lds0 = lds_addr(&st[0][0]);
+  if (t < 2)
+    param_reduce128_product<Ty, kR2D, RD>(a, t == 0 ? a.pu : a.pv, t == 0 ? a.du : a.dv, lds0, q, s0, sstep, out);
+  else
+    param_reduce128_product<Ty, RD, kR2D>(a, a.z, a.dw, lds0, q, s0, sstep, out);
+}
+
+// Slot ranges R of the d = 128 reduction (grid 3 q_c R, partial rows R): at most one workgroup
+// per CU, at least one 32-slot step per range.
+int64_t bwd_param_reduce128_ranges(int64_t slots, int32_t q_c) {
+  const int64_t steps = (slots + kR2Slots - 1) / kR2Slots;
+  int64_t ranges = static_cast<int64_t>(device_cus()) / (3 * static_cast<int64_t>(q_c));
+  if (ranges < 1) ranges = 1;
+  return ranges > steps ? steps : ranges;
+}
+
+template <int RD>
+int launch_param_reduce128(const ParamReduce128Args& a, int64_t grid, int32_t dtype, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (dtype == OW_DTYPE_BF16)
+    hipLaunchKernelGGL((bwd_param_reduce128_kernel<BF16, RD>), g, dim3(64 * kR2Waves), 0, s, a);
+  else
+    hipLaunchKernelGGL((bwd_param_reduce128_kernel<F16, RD>), g, dim3(64 * kR2Waves), 0, s, a);
+  return hip_status(hipGetLastError(), "bwd_param_reduce128_kernel launch");
+}
+
+// ---- Fixed-order sum of fp32 partial rows -------------------------------------------------
+// out[c] = sum over r of p[r][c] (cols a multiple of 4, 16-byte aligned rows).  Workgroup b sums
+// columns 256 b .. 256 b + 255 (lane: four of them); its W waves take rows w, w + W, .. in
+// order and are then added in wave order, so the result depends on rows, cols and W only.
+__global__ void __launch_bounds__(1024) sum_rows_kernel(const float4* __restrict__ p, int64_t rows, int64_t cols4,
+                                                        float4* __restrict__ out, int W) {
+  __shared__ float4 part[16][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  float4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (c < cols4) {
+    int64_t r = w;
+    for (; r + 3 * W < rows; r += 4 * W) {
+      const float4 x0 = p[r * cols4 + c], x1 = p[(r + W) * cols4 + c];
+      const float4 x2 = p[(r + 2 * W) * cols4 + c], x3 = p[(r + 3 * W) * cols4 + c];
+      s += x0;
+      s += x1;
+      s += x2;
+      s += x3;
+    }
+    for (; r < rows; r += W) s += p[r * cols4 + c];
+  }
+  if (W > 1) {
+    part[w][lane] = s;
+    __syncthreads();
+    if (w == 0)
+      for (int k = 1; k < W; ++k) s += part[k][lane];
+  }
+  if (w == 0 && c < cols4) out[c] = s;
+}
+
+// Waves per workgroup of sum_rows_kernel: enough rows in flight per column for few rows' latency.
+int sum_rows_waves(int64_t rows) { return rows >= 128 ? 16 : rows >= 32 ? 8 : rows >= 8 ? 4 : 1; }
 
 // ---- Channel side of the backward, d = 128: token side, U'/V'/dZ and the gate -------------
 // Eight waves per workgroup, one workgroup per CU, persistent over units of 256 slots x one
@@ -2148,6 +2347,60 @@ int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const 
   const int rc = rd == 128 ? ow::launch_param_reduce64<4>(a, grid, dtype, s) : ow::launch_param_reduce64<8>(a, grid, dtype, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
+}
+
+int64_t ow_bwd_param_reduce128_partials(int64_t slots, int32_t q_c, int32_t rd) {
+  if (q_c < 1 || slots <= 0 || slots % 16 || (rd != 128 && rd != 256)) return 0;
+  return ow::bwd_param_reduce128_ranges(slots, q_c) * q_c;
+}
+
+int ow_bwd_param_reduce128(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
+                           const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
+                           int32_t dtype, void* stream) {
+  OW_CHECK_SUPPORTED(rd == 128 || rd == 256, "parameter reduction needs rd in {128, 256} (got %d)", rd);
+  OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
+  OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 16 == 0, "bad shape q_c=%d slots=%lld (multiple of 16)", q_c,
+               (long long)slots);
+  if (slots == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  const int64_t rows = ow_bwd_param_reduce128_partials(slots, q_c, rd);
+  OW_CHECK_ARG(n_partial == rows, "partial holds %lld rows; %lld needed (ow_bwd_param_reduce128_partials)",
+               (long long)n_partial, (long long)rows);
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31),
+               "intermediates of %lld slots exceed 2 GiB (buffer addressing)", (long long)slots);
+  OW_CHECK_ARG(pu && pv && dw && z && du && dv && partial, "tensor pointer is NULL");
+  for (const void* p : {pu, pv, dw, z, du, dv})
+    OW_CHECK_ARG(ow::aligned16(p), "intermediate buffers must be 16-byte aligned");
+  auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  ow::ParamReduce128Args a{cu(pu), cu(pv), cu(dw), cu(z), cu(du), cu(dv), partial, slots, q_c};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t grid = 3 * rows;
+  const int rc = rd == 128 ? ow::launch_param_reduce128<128>(a, grid, dtype, s)
+                           : ow::launch_param_reduce128<256>(a, grid, dtype, s);
+  if (rc == OW_OK) ow::clear_error();
+  return rc;
+}
+
+int ow_sum_rows(const float* partial, int64_t rows, int64_t cols, float* out, void* stream) {
+  OW_CHECK_ARG(rows >= 1 && cols >= 0 && cols % 4 == 0, "bad shape rows=%lld cols=%lld (cols a multiple of 4)",
+               (long long)rows, (long long)cols);
+  if (cols == 0) {
+    ow::clear_error();
+    return OW_OK;
+  }
+  OW_CHECK_ARG(partial && out, "tensor pointer is NULL");
+  OW_CHECK_ARG(ow::aligned16(partial) && ow::aligned16(out), "partial and out must be 16-byte aligned");
+  const int64_t cols4 = cols / 4, blocks = (cols4 + 63) / 64;
+  OW_CHECK_ARG(blocks < (int64_t(1) << 31), "too many columns (%lld)", (long long)cols);
+  const int W = ow::sum_rows_waves(rows);
+  hipLaunchKernelGGL(ow::sum_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * W), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const float4*>(partial), rows, cols4,
+                     reinterpret_cast<float4*>(out), W);
+  if (int rc = ow::hip_status(hipGetLastError(), "sum_rows_kernel launch")) return rc;
+  ow::clear_error();
+  return OW_OK;
 }
 
 // Workgroups (and partial rows) of ow_bwd_fused: every workgroup loops over rounds of four

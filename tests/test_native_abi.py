@@ -174,6 +174,31 @@ def test_bwd_channel_entries_reject_bad_arguments_without_touching_the_gpu() -> 
     assert reduce64(pu=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
     assert reduce64(s=0, n=0) == 0  # empty: nothing launched
 
+    # The d = 128 reduction over the channel kernels' slot-major intermediates.
+    n128 = lib.ow_bwd_param_reduce128_partials(13 * 16, 3, 256)
+    assert n128 > 0 and n128 % 3 == 0
+    assert lib.ow_bwd_param_reduce128_partials(13 * 16 + 8, 3, 256) == 0
+    assert lib.ow_bwd_param_reduce128_partials(13 * 16, 3, 192) == 0
+
+    def reduce128(n=n128, s=13 * 16, rd=256, pu=P, q_c=3):
+        return lib.ow_bwd_param_reduce128(pu, P, P, P, P, P, P, n, s, q_c, rd, bf16, None)
+
+    assert reduce128(rd=192) == 2 and b"rd in {128, 256}" in lib.ow_last_error()
+    assert reduce128(s=13 * 16 + 8) == 1 and b"multiple of 16" in lib.ow_last_error()
+    assert reduce128(n=n128 + 3) == 1 and b"ow_bwd_param_reduce128_partials" in lib.ow_last_error()
+    assert reduce128(pu=None) == 1 and b"NULL" in lib.ow_last_error()
+    assert reduce128(pu=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
+    assert reduce128(s=1 << 22, n=lib.ow_bwd_param_reduce128_partials(1 << 22, 3, 256)) == 1
+    assert b"2 GiB" in lib.ow_last_error()
+    assert reduce128(s=0, n=0) == 0  # empty: nothing launched
+
+    # The fixed-order row sum.
+    assert lib.ow_sum_rows(P, 4, 6, P, None) == 1 and b"multiple of 4" in lib.ow_last_error()
+    assert lib.ow_sum_rows(P, 0, 8, P, None) == 1 and b"bad shape" in lib.ow_last_error()
+    assert lib.ow_sum_rows(None, 4, 8, P, None) == 1 and b"NULL" in lib.ow_last_error()
+    assert lib.ow_sum_rows(P, 4, 8, ctypes.c_void_p(20), None) == 1 and b"aligned" in lib.ow_last_error()
+    assert lib.ow_sum_rows(P, 4, 0, P, None) == 0  # no columns: nothing launched
+
 
 def test_hip_is_supported_reasons_on_cpu() -> None:
     plan = build_route_plan(14, 14, 512, 16, 128, "local")
