@@ -339,18 +339,17 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
  * channel-side GEMMs; the reference's fp32 autograd recompute, omniweave/ops/triton.py:256-292):
  * from the routed tiles X' and dY ([q_c][slots][64], ow_bwd_gather) and the fp32 [16][16] token
  * matrices, per 32-slot pair: P_u = A_u X', P_v = A_v X', dW' = A_o^T dY (stored to pu, pv, dw,
- * [q_c][slots][64] elements), U'^T, V'^T, dZ^T and the gate backward per 32-row chunk (z, du, dv,
- * [q_c][slots][rd] elements) -- those six in the fragment order ow_bwd_param_reduce64 reads,
- * not row-major --, W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
+ * [q_c][slots][64] elements, each row in the pair-operand channel order: element 16 k + 8 h + j
+ * is channel 16 k + 8 (j / 4) + 4 h + j % 4, as ow_bwd_param_reduce64 reads them), U'^T, V'^T,
+ * dZ^T and the gate backward per 32-row chunk, W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
  * dX' = A_u^T dP_u + A_v^T dP_v (stored to dxt), and the token-matrix gradients dA_u = sum
  * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
  * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c); element 16 t + k),
  * which the caller sums over w.  slots % 32 == 0, bf16 / f16. */
 int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c);
 int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
-                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
-                 void* dv, void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d,
-                 int32_t rd, int32_t dtype, void* stream);
+                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* dxt, float* partial,
+                 int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);
 
 /* The d = 128 backward's token side and first channel-side products in one kernel (replaces
  * ow_tile_mix x3, the U'/V'/dZ GEMMs and ow_bwd_gate of the composed backward; the reference's
@@ -399,18 +398,19 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
 
 /* Parameter-gradient reduction of the d = 64 backward (replaces the slot-reduction GEMMs over
  * the intermediates, omniweave/ops/triton.py:256-292 through autograd): from pu, pv, dw
- * ([q_c][slots][64]) and z, du, dv ([q_c][slots][rd]) as ow_bwd_fused / ow_bwd_fused_routed
- * write them (per 32-slot pair, 32x32x16 operand fragments whose K runs over the pair's slots),
- * the sums over slot ranges of dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and
- * dB_o'' = Z^T dW' ([rd][64]) per channel group, fp32.  partial holds n_partial =
+ * ([q_c][slots][64], as ow_bwd_fused / ow_bwd_fused_routed write them) and the packed weights of
+ * the same call (ow_pack_bwd_weights), U' = P_u B_u'', V' = P_v B_v'', dZ = dW' B_o''^T and the
+ * gate backward (Z, dU', dV') are recomputed per 32-slot pair and the sums over slot ranges of
+ * dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' (each [64][rd]) and dB_o'' = Z^T dW' ([rd][64]) per
+ * channel group are formed, fp32.  partial holds n_partial =
  * ow_bwd_param_reduce64_partials(slots, q_c, rd) rows of 3 * 64 * rd floats (a multiple of q_c):
  * R = n_partial / q_c ranges, each a [3][q_c][64 * rd] block (product, group), so the gradients
  * are the sum of the R blocks (ow_sum_rows with rows R, cols 3 * q_c * 64 * rd).
  * slots % 32 == 0, rd in {128, 256}, bf16 / f16. */
 int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c, int32_t rd);
-int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du,
-                          const void* dv, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd,
-                          int32_t dtype, void* stream);
+int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* packed, size_t packed_bytes,
+                          float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd, int32_t dtype,
+                          void* stream);
 
 /* The same reduction for d = 128, from the slot-major intermediates of ow_bwd_channel /
  * ow_bwd_channel_routed (pu, pv, dw [q_c][slots][128]; z, du, dv [q_c][slots][rd], rows in slot
@@ -438,9 +438,8 @@ int ow_sum_rows(const float* partial, int64_t rows, int64_t cols, float* out, vo
  * ow_bwd_fused (slots = batch * q_s * 16). */
 int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
                         const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
-                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
-                        void* dv, void* g, float* partial, int64_t n_partial, int32_t rd, int32_t dtype,
-                        void* stream);
+                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* g,
+                        float* partial, int64_t n_partial, int32_t rd, int32_t dtype, void* stream);
 
 /* Parameter gradients from the folded ones (dbu, dbv [q_c][d][rd], dbo [q_c][rd][d], fp32):
  * g_bu, g_bv, g_bo (fp32, parameter shapes), g_gamma [C] and, with norm_weight, g_norm_weight

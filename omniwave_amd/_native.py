@@ -144,7 +144,7 @@ _SIGNATURES = {
     "ow_bwd_fused_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32]),
     "ow_bwd_fused": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 6 + [ctypes.c_size_t] + [ctypes.c_void_p] * 8
+        [ctypes.c_void_p] * 6 + [ctypes.c_size_t] + [ctypes.c_void_p] * 5
         + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
            ctypes.c_void_p],
     ),
@@ -173,8 +173,8 @@ _SIGNATURES = {
     "ow_bwd_param_reduce64_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
     "ow_bwd_param_reduce64": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                 ctypes.c_void_p],
+        [ctypes.c_void_p] * 4 + [ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
     "ow_bwd_param_reduce128_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
     "ow_bwd_param_reduce128": (
@@ -185,7 +185,7 @@ _SIGNATURES = {
     "ow_sum_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
     "ow_bwd_fused_routed": (
         ctypes.c_int,
-        [ctypes.c_void_p] * 5 + [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_size_t] + [ctypes.c_void_p] * 8
+        [ctypes.c_void_p] * 5 + [ctypes.c_int32] + [ctypes.c_void_p] * 4 + [ctypes.c_size_t] + [ctypes.c_void_p] * 5
         + [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
     "ow_bwd_params": (

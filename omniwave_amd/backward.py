@@ -7,9 +7,9 @@ accumulation, entirely on the HIP stream of the gradient:
 * routing, RMSNorm, gate and parameter fold-back are the libomniwave_amd.so kernels
   (``ow_bwd_gather``, ``ow_bwd_gate``, ``ow_bwd_scatter``, ``ow_bwd_rmsnorm``,
   ``ow_bwd_params``, ``ow_fold_weights``);
-* for d = 64 one fused MFMA kernel (``ow_bwd_fused``) does the token side (P_u, P_v, dW'), the
-  channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u, dP_v), dX' and the token-matrix
-  gradients (per-workgroup partials); for d = 128 two kernels share that work
+* for d = 64 one fused MFMA kernel (``ow_bwd_fused``) does the token side (P_u, P_v, dW', the
+  only intermediates it stores), the channel side and gate (U', V', dZ, Z, dU', dV', W', dP_u,
+  dP_v), dX' and the token-matrix gradients (per-workgroup partials); for d = 128 two kernels share that work
   (``ow_bwd_channel``: token side, U', V', dZ and the gate; ``ow_bwd_channel2``: dP_u, dP_v,
   dX', W' and the token-matrix gradients; with the identity channel order their ``_routed``
   forms read x / dy and write dX' straight to the NHWC gradient, so neither the gather nor the
@@ -18,8 +18,8 @@ accumulation, entirely on the HIP stream of the gradient:
   ``ow_tile_mix`` / ``ow_tile_outer`` (16x16x16 MFMA) around plain batched GEMMs over all slots
   of a channel group (``torch.bmm`` -> hipBLASLt, every right operand contiguous) and
   ``ow_bwd_gate``;
-* the parameter-gradient reductions over slots: ``ow_bwd_param_reduce64`` over the d = 64 fused
-  kernel's fragment-ordered intermediates, ``ow_bwd_param_reduce128`` over the d = 128 channel
+* the parameter-gradient reductions over slots: ``ow_bwd_param_reduce64`` from the d = 64 fused
+  kernel's P_u, P_v, dW' (recomputing U', V', dZ and the gate), ``ow_bwd_param_reduce128`` over the d = 128 channel
   kernels' slot-major ones (fp32 batched GEMMs for the fp32 path), and every per-workgroup fp32
   partial summed by ``ow_sum_rows`` in a fixed order.
 
@@ -297,8 +297,6 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
                                                   stream), "ow_pack_bwd_weights")
             pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
             pv, dw = torch.empty_like(pu), torch.empty_like(pu)
-            z = torch.empty(q_c, slots, rd, dtype=dtype, device=dev)
-            du, dv = torch.empty_like(z), torch.empty_like(z)
             n_part = lib.ow_bwd_fused_partials(slots, q_c)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
             if routed:
@@ -306,33 +304,31 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
                                                       is not None else None, tok.data_ptr(),
                                                       ctypes.byref(oplan), batch, au.data_ptr(),
                                                       av.data_ptr(), ao.data_ptr(), wpk.data_ptr(), nbytes,
-                                                      pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
-                                                      du.data_ptr(), dv.data_ptr(), g.data_ptr(),
+                                                      pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), g.data_ptr(),
                                                       partial.data_ptr(), n_part, rd, code, stream),
                               "ow_bwd_fused_routed")
             else:
                 dxt = torch.empty_like(xt)
                 _native.check(lib.ow_bwd_fused(xt.data_ptr(), dyt.data_ptr(), au.data_ptr(), av.data_ptr(),
                                                ao.data_ptr(), wpk.data_ptr(), nbytes, pu.data_ptr(), pv.data_ptr(),
-                                               dw.data_ptr(), z.data_ptr(), du.data_ptr(), dv.data_ptr(),
-                                               dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c, d, rd, code,
-                                               stream), "ow_bwd_fused")
+                                               dw.data_ptr(), dxt.data_ptr(), partial.data_ptr(), n_part, slots, q_c,
+                                               d, rd, code, stream), "ow_bwd_fused")
                 del xt, dyt
             _sum_rows(lib, partial, n_part, g_a, stream)  # [3, 256]: dA_u, dA_v, dA_o
             g_au, g_av, g_ao = (g_a[m].view(16, 16) for m in range(3))
-            # dB_u'', dB_v'', dB_o'' from the kernel's fragment-ordered intermediates: per slot
-            # range one [3, q_c, d * rd] block, summed over the ranges.
+            # dB_u'', dB_v'', dB_o'' from P_u, P_v, dW' (the gate recomputed): per slot range one
+            # [3, q_c, d * rd] block, summed over the ranges.
             n_red = lib.ow_bwd_param_reduce64_partials(slots, q_c, rd)
             red = torch.empty(n_red, 3 * d * rd, dtype=torch.float32, device=dev)
-            _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), z.data_ptr(),
-                                                    du.data_ptr(), dv.data_ptr(), red.data_ptr(), n_red, slots, q_c,
-                                                    rd, code, stream), "ow_bwd_param_reduce64")
+            _native.check(lib.ow_bwd_param_reduce64(pu.data_ptr(), pv.data_ptr(), dw.data_ptr(), wpk.data_ptr(), nbytes,
+                                                    red.data_ptr(), n_red, slots, q_c, rd, code, stream),
+                          "ow_bwd_param_reduce64")
             g_b3 = torch.empty(3, q_c, d * rd, dtype=torch.float32, device=dev)
             _sum_rows(lib, red, n_red // q_c, g_b3, stream)
             d_bu = g_b3[0].view(q_c, d, rd)
             d_bv = g_b3[1].view(q_c, d, rd)
             d_bo = g_b3[2].view(q_c, rd, d)
-            del z, du, dv, pu, pv, dw
+            del pu, pv, dw
         elif d == 128 and dtype != torch.float32:
             # Two kernels over 256-slot units: (1) token side P_u, P_v, dW', then U', V', dZ per
             # 32-row chunk and the gate backward (Z, dU', dV'); (2) dP_u, dP_v, dX', W' and the

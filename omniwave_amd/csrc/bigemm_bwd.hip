@@ -569,9 +569,10 @@ __device__ __forceinline__ void bwd_copy_frag(const uint16_t* src, uint16_t* dst
 //   * P_u^T = X'^T (A_u)^T, P_v^T, dW'^T = dY^T A_o (block-diagonal 32x32x16 products over the
 //     pair, as in the forward) from the X' and dY tiles staged in the second weight buffer,
 //     which no copy targets before the first barrier of the chunk loop; P_u, P_v, dW' are also
-//     stored for the parameter-gradient GEMMs;
-//   * the channel loop (U'^T, V'^T, dZ^T per 32-row chunk, gate, Z / dU' / dV' stored,
-//     W' += Z B_o'', dP_u += dU' B_u''^T, dP_v += dV' B_v''^T);
+//     stored (straight from the operand registers, rows in the pair-operand channel order) for
+//     the parameter-gradient reduction, which recomputes the gate from them;
+//   * the channel loop (U'^T, V'^T, dZ^T per 32-row chunk, gate, W' += Z B_o'',
+//     dP_u += dU' B_u''^T, dP_v += dV' B_v''^T);
 //   * dX' = A_u^T dP_u + A_v^T dP_v (block-diagonal, the forward's output product), stored;
 //   * dA_u += dP_u X'^T, dA_v += dP_v X'^T, dA_o += dY W'^T per 16-slot tile with 16x16x16
 //     products over the channels (dP_u, dP_v, W' as rows through a per-wave LDS tile, X' and
@@ -579,7 +580,6 @@ __device__ __forceinline__ void bwd_copy_frag(const uint16_t* src, uint16_t* dst
 // At the end the four waves' dA sums are added in a fixed order and the workgroup writes
 // partial[blockIdx][3][256] (dA_u, dA_v, dA_o, element 16 t + k).
 constexpr int64_t kBwdFusedGrid = 1024;  // at most 2 workgroups per CU x 2 rounds in flight
-constexpr int kZSt = 40;                 // row stride (elements) of the staged chunk outputs
 
 struct BwdFusedArgs {
   const uint16_t* xt;   // [q_c][slots][64] X' tiles
@@ -588,12 +588,9 @@ struct BwdFusedArgs {
   const float* a_v;
   const float* a_o;
   const uint16_t* packed;  // ow_pack_bwd_weights
-  uint16_t* pu;            // [q_c][slots][64] outputs for the parameter GEMMs
-  uint16_t* pv;
+  uint16_t* pu;            // [q_c][slots][64] outputs for the parameter-gradient reduction, rows
+  uint16_t* pv;            // in the pair-operand channel order (bwd_param_reduce64_kernel)
   uint16_t* dw;
-  uint16_t* z;  // [q_c][slots][rd]
-  uint16_t* du;
-  uint16_t* dv;
   uint16_t* dxt;   // [q_c][slots][64]
   float* partial;  // [gridDim][3][256]
   int64_t slots;
@@ -615,36 +612,6 @@ struct BwdFusedArgs {
 template <class Ty>
 __device__ __forceinline__ uint32_t scale2(uint32_t v, float r) {
   return Ty::pack2(Ty::to_f32(static_cast<uint16_t>(v & 0xffffu)) * r, Ty::to_f32(static_cast<uint16_t>(v >> 16)) * r);
-}
-
-// The d = 64 backward's per-pair intermediates (P_u, P_v, dW' [.. 64], Z, dU', dV' [.. rd]) are
-// kept in HBM as slot-K fragments: for the 32 slots of a pair and each 32-wide block b of the
-// other dimension (channels or expanded rows), two 32x32x16 operand fragments (K-step g = slots
-// 16 g ..), lane (l32, hh) holding entry 32 b + l32 at slots 16 g + kord(j, hh), j < 8: 1 KB each,
-// at element (pair (2 b + g)) * 512 + 8 lane of the pair's 32 * width elements.  The fused kernel
-// writes them with coalesced 16-byte stores and the parameter-gradient reduction reads them as
-// MFMA operands directly (P^T dU' etc. contract over the slots).
-// Stores fragments of blocks b0 .. b0 + KS / 2 - 1 of a [32 slots][..] tile staged in LDS
-// (at(r, c): byte address of slot r, entry c within those blocks) at pair base dst.
-// One fragment at a time (the reads of pair_xt_tr, each fragment stored before the next is read),
-// so the caller's live registers grow by one fragment only.  The stores are non-temporal: at a
-// 56x56x128 batch of 128 the fragments are 0.93 GB, far beyond the L2 and the last-level cache, so
-// keeping them there only evicts the weights and tiles being read (fused block forward + backward
-// 0.820 -> 0.785 ms).
-template <int KS, class At>
-__device__ __forceinline__ void pair_frag_store(At at, int lane, uint16_t* dst, int b0) {
-  const int hh = lane >> 5, l16 = lane & 15, half = (lane >> 4) & 1;
-#pragma unroll
-  for (int cb = 0; cb < KS / 2; ++cb) {
-    const int c = 32 * cb + 16 * half + 4 * (l16 & 3);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int r = 16 * g + 4 * hh + (l16 >> 2);
-      const u32x2 lo = lds_read_tr16(at(r, c)), hi = lds_read_tr16(at(r + 8, c));
-      __builtin_nontemporal_store(u32x4{lo[0], lo[1], hi[0], hi[1]},
-                                  reinterpret_cast<u32x4*>(dst + (2 * (b0 + cb) + g) * kFragElems + 8 * lane));
-    }
-  }
 }
 
 // Token-operand fragment of a 16x16 token matrix (lane (t, hh) slot j = M[t % 16][kord(j, hh)],
@@ -673,7 +640,6 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t wb[2][CH_ELEMS];
   __shared__ __attribute__((aligned(16))) u32x4 tok[5][64];  // A_u, A_v, A_o^T, A_u^T, A_v^T operand rows
   __shared__ float red[4][3][256];
-  __shared__ __attribute__((aligned(16))) uint16_t zst[4][32 * kZSt];  // per wave: one chunk output, staged
   // wave is uniform: readfirstlane keeps it and the pair, slot and tile positions derived from it in
   // scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -801,25 +767,16 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     const f32x16 zero = {};
     const int64_t row = slot0 + l32;  // this lane's slot
     if (live) {
-      // P_u, P_v, dW' through the wave's tile (read completely by the token side; no copy targets
-      // it before the chunk loop's first barrier): lane = slot l32, K-step ks slot j -> channel
-      // 16 ks + kord(j, hh), staged [32 slots][64 channels] and stored as the pair's slot-K
-      // fragments (pair_frag_store), four 1 KB stores per tensor.
-      wave_lds_sync();
-      const uint32_t txa = lds_addr(tx);
+      // P_u, P_v, dW' rows: lane (slot l32, hh) holds K-step ks = channels 16 ks + kord(j, hh),
+      // stored as the 16-byte piece at element 16 ks + 8 hh of the slot's row (the pair-operand
+      // channel order).  Non-temporal: at a 56x56x128 batch of 128 they are 0.3 GB, read once by
+      // the reduction after this pass.
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
         const u32x4(&pk)[kBwdKS] = t == 0 ? Pu : t == 1 ? Pv : Dw;
-        uint16_t* dst = t == 0 ? a.pu : t == 1 ? a.pv : a.dw;
+        uint16_t* dst = (t == 0 ? a.pu : t == 1 ? a.pv : a.dw) + row * kBwdD + 8 * hh;
 #pragma unroll
-        for (int ks = 0; ks < kBwdKS; ++ks) {
-          *reinterpret_cast<u32x2*>(&tx[l32 * kLd + 16 * ks + 4 * hh]) = u32x2{pk[ks][0], pk[ks][1]};
-          *reinterpret_cast<u32x2*>(&tx[l32 * kLd + 16 * ks + 8 + 4 * hh]) = u32x2{pk[ks][2], pk[ks][3]};
-        }
-        wave_lds_sync();
-        pair_frag_store<kBwdKS>([&](int r, int c) { return txa + 2u * static_cast<uint32_t>(r * kLd + c); }, lane,
-                                dst + slot0 * kBwdD, 0);
-        wave_lds_sync();
+        for (int ks = 0; ks < kBwdKS; ++ks) __builtin_nontemporal_store(pk[ks], reinterpret_cast<u32x4*>(dst + 16 * ks));
       }
     }
 
@@ -827,13 +784,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
     for (int ec = 0; ec < NCH; ++ec) {
       // Chunk ec's copies: chunk 0 landed before the tile loads the compiler waited on; chunk
-      // ec >= 1 was issued at step ec - 1, and only that step's 6 stores (live waves) follow it.
-      if (ec > 0) {
-        if (live)
-          wait_vmcnt<6>();
-        else
-          wait_vmcnt<0>();
-      }
+      // ec >= 1 was issued at step ec - 1, and nothing follows it.
+      if (ec > 0) wait_vmcnt<0>();
       __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1 (ec = 0: its tiles)
       if (ec + 1 < NCH) issue(ec + 1);
       const u32x4* cf = reinterpret_cast<const u32x4*>(wb[ec & 1]);
@@ -861,26 +813,6 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
         zs[s] = pack_kstep<Ty>(Z, s);
         dus[s] = pack_kstep<Ty>(DU, s);
         dvs[s] = pack_kstep<Ty>(DV, s);
-      }
-      if (live) {
-        // Registers 4b..4b+3 are expanded rows 32 ec + 8b + 4hh + (0..3) of slot l32: each
-        // tensor staged [32 slots][32 rows] in the wave's buffer, then stored as the pair's two
-        // slot-K fragments of row block ec (pair_frag_store), 6 stores per chunk.
-        uint16_t* zw = zst[wave];
-        const uint32_t zwa = lds_addr(zw);
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-          const u32x4(&pk)[2] = t == 0 ? zs : t == 1 ? dus : dvs;
-          uint16_t* dst = t == 0 ? a.z : t == 1 ? a.du : a.dv;
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            *reinterpret_cast<u32x2*>(&zw[l32 * kZSt + 8 * b + 4 * hh]) =
-                u32x2{pk[b >> 1][2 * (b & 1)], pk[b >> 1][2 * (b & 1) + 1]};
-          wave_lds_sync();
-          pair_frag_store<2>([&](int r, int c) { return zwa + 2u * static_cast<uint32_t>(r * kZSt + c); }, lane,
-                             dst + slot0 * RD, ec);
-          wave_lds_sync();  // the reads are done before the next tensor is staged
-        }
       }
 #pragma unroll
       for (int mb = 0; mb < kBwdMB; ++mb)
@@ -1039,135 +971,280 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
   return OW_OK;
 }
 
-// ---- Parameter-gradient reduction, d = 64 ------------------------------------------------
-// dB_u'' = sum over slots of P_u^T dU', dB_v'' = P_v^T dV' ([64][rd]), dB_o'' = Z^T dW' ([rd][64])
-// per channel group, from the slot-K fragments of ow_bwd_fused (pair_frag_store): a fragment
-// is a 32x32x16 operand whose K runs over 16 slots, so each pair contributes two K steps.
-// Workgroup b takes group q = b % q_c, row half h = (b / q_c) % H (H = rd / 128) and pairs s,
-// s + S, .. (s = b / (q_c H), S = gridDim.x / (q_c H)).  Per pair it needs 36 fragments: the
-// 12 channel-side ones (P_u, P_v, dW') and 24 row-side ones (dU', dV', Z of its 4 row blocks),
-// copied by its 12 waves (three each, buffer_load ... lds, untracked) into one of kRedStages
-// LDS stages, kRedStages - 1 pairs ahead; one barrier per pair.  Wave w computes product
-// t = w / 4 (0: dB_u'', 1: dB_v'', 2: dB_o'' as its transpose dW'^T Z) for row block
-// e = w % 4 + 4 h and both 32-channel blocks, in fp32 registers.  Every workgroup runs the same
-// number of pairs per range; pairs past the end read as zero (out-of-range offsets) and add
-// nothing.  The sums go to the workgroup's blocks of range s's partial row, laid out
-// [3][q_c][64 rd] (product t of group q: dB_u'' [64][rd], dB_v'' [64][rd], dB_o'' [rd][64]; the H
-// row halves fill disjoint blocks), so that the sum of the rows over s (ow_sum_rows) is the
-// [3][q_c][64 rd] gradient buffer.
+// ---- Parameter-gradient reduction, d = 64, recomputing the gate --------------------------
+// dB_u'' = P_u^T dU', dB_v'' = P_v^T dV' ([64][rd]) and dB_o'' = Z^T dW' ([rd][64]), summed over
+// the slots of one channel group, from P_u, P_v, dW' alone (as ow_bwd_fused stores them): the
+// chunk products U' = P_u B_u'', V' = P_v B_v'', dZ = dW' B_o''^T and the gate backward (Z, dU',
+// dV') are recomputed here from the same 16-bit operands and packed weights instead of being
+// stored by the fused kernel and read back (at rd = 128 that is 768 bytes per slot more of each).
+// P rows are kept in the pair-operand channel order: element 16 k + 8 h + j of a row is channel
+// 16 k + kord(j, h), so lane (slot, h) of a K-step operand is one 16-byte piece.
+// Workgroup b takes group q = b % q_c and 2-pair steps s, s + R, .. (s = b / q_c, R = gridDim.x /
+// q_c).  Each step's 2 x 3 [32 slots][64] tiles are copied by the 8 waves (buffer_load ... lds, 3
+// per wave, untracked) into one of kR64Stages LDS stages, kR64Ahead steps ahead; one barrier
+// per step.  Wave w owns the 32-row chunk ec = w % (rd / 32) of the expanded dimension
+// (its 12 weight fragments stay in registers) for pair w / (rd / 32) of each step (rd = 256:
+// both pairs): U', V', dZ of its chunk with lane = expanded row, registers = slots (K-step
+// operands read as 16-byte pieces), the gate, then dB_u''[:, ec] += P_u^T dU', dB_v''[:, ec] +=
+// P_v^T dV' and dB_o''[ec, :] += Z^T dW' with the P^T / dW' operands by transposed LDS reads
+// (ds_read_b64_tr_b16) and the gate outputs as the other operand.  Rows hold their 16-byte
+// pieces swizzled (piece p of row r at p ^ kR64Swz(r)), which keeps both read forms free of
+// bank conflicts.  At rd = 128 the two waves of a chunk add their sums through LDS (in a fixed
+// order) before the workgroup writes range s's partial row, laid out [3][q_c][64 rd]; their
+// sum over s (ow_sum_rows) is the [3][q_c][64 rd] gradient buffer.
 struct ParamReduceArgs {
-  const uint16_t* pu;  // fragments, [q_c][pairs][32 * 64]
+  const uint16_t* pu;      // [q_c][pairs * 32][64], pair-operand channel order
   const uint16_t* pv;
   const uint16_t* dw;
-  const uint16_t* z;   // fragments, [q_c][pairs][32 * rd]
-  const uint16_t* du;
-  const uint16_t* dv;
-  float* partial;      // [ranges][3][q_c][64 * rd]
-  int64_t pairs;       // per group
+  const uint16_t* packed;  // ow_pack_bwd_weights, d = 64
+  float* partial;          // [ranges][3][q_c][64 * rd]
+  int64_t pairs;           // per group
   int32_t q_c;
 };
-constexpr int kReduceWaves = 12;
-constexpr int kRedFrags = 36;   // fragments per pair and workgroup
-constexpr int kRedStages = 4;
+constexpr int kR64Waves = 8;
+constexpr int kR64Ahead = 2;   // steps copied ahead
+constexpr int kR64Stages = 4;  // kR64Ahead + 2: the lagging waves still read step i - 1
+constexpr int kR64Pairs = 2;                            // pairs per step
+constexpr int kR64Tile = 32 * kBwdD;                    // elements of one [32][64] tile
+constexpr int kR64Stage = kR64Pairs * 3 * kR64Tile * 2;  // bytes per stage (24 KB)
 
-template <class Ty, int NCH>
-__global__ void __launch_bounds__(64 * kReduceWaves) bwd_param_reduce64_kernel(ParamReduceArgs a) {
-  constexpr int RD = 32 * NCH;
-  constexpr int H = NCH / 4;  // row halves
-  __shared__ __attribute__((aligned(16))) u32x4 st[kRedStages][kRedFrags][64];
+__device__ __forceinline__ int kR64Swz(int r) { return 4 * ((r >> 1) & 1) + ((r >> 2) & 3); }
+// Position of channel c within a stored row (bits 2 and 3 swapped: the pair-operand order).
+__device__ __forceinline__ int r64_pos(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
+// LDS byte address of element position p of row r in a swizzled [32][64] tile at base.
+__device__ __forceinline__ uint32_t r64_at(uint32_t base, int r, int p) {
+  return base + static_cast<uint32_t>(r * 128 + (((p >> 3) ^ kR64Swz(r)) << 4) + 2 * (p & 7));
+}
+
+template <class Ty, int RD>
+__global__ void __launch_bounds__(64 * kR64Waves) bwd_param_reduce64_kernel(ParamReduceArgs a) {
+  constexpr int NCH = RD / 32;
+  constexpr int WPP = kR64Waves / NCH;  // waves per chunk (2 at rd = 128, 1 at rd = 256)
+  constexpr int CH_ELEMS = kBwdFr * kFragElems;
+  constexpr int COMBINE = (WPP - 1) * (kR64Waves / WPP) * 96 * 64 * 4;  // bytes of the rd = 128 combine
+  constexpr int LDS = kR64Stages * kR64Stage > COMBINE ? kR64Stages * kR64Stage : COMBINE;
+  static_assert(WPP == 1 || WPP == 2, "rd in {128, 256}");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hh = lane >> 5, l32 = lane & 31;
-  const int q = blockIdx.x % a.q_c, h = (blockIdx.x / a.q_c) % H;
-  const int t = w >> 2, e0 = w & 3;
-  const int64_t s0 = blockIdx.x / (a.q_c * H);
-  const int64_t pstep = gridDim.x / (a.q_c * H);
-  const int64_t n_iter = (a.pairs - s0 + pstep - 1) / pstep;  // same for every wave
-  const uint32_t cbytes = static_cast<uint32_t>(a.q_c * a.pairs * 32 * kBwdD * 2);
-  const uint32_t rbytes = static_cast<uint32_t>(a.q_c * a.pairs * 32 * RD * 2);
-  // This wave's three copies per pair: fragments f = w, w + 12, w + 24 of the pair's 36
-  // (f < 12: channel-side tensor f / 4, fragment f % 4; else row-side j = f - 12: tensor j / 8,
-  // local row block (j % 8) / 2, K step j % 2).
-  __amdgpu_buffer_rsrc_t rs[3];
-  uint32_t fo[3];  // byte offset of the fragment within the pair
-  bool rside[3];
+  const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, half = (lane >> 4) & 1;
+  const int ec = w % NCH, pp0 = w / NCH;
+  const int q = blockIdx.x % a.q_c;
+  const int64_t s0 = blockIdx.x / a.q_c, sstep = gridDim.x / a.q_c;
+  const int64_t steps = (a.pairs + kR64Pairs - 1) / kR64Pairs;
+  const int64_t n_iter = s0 < steps ? (steps - s0 + sstep - 1) / sstep : 0;  // same for every wave
+  const uint32_t lds0 = lds_addr(lds);
+
+  // The chunk's weight operands (lane = expanded row 32 ec + l32, K = channels): fragments
+  // ks, 4 + ks, 8 + ks of the chunk are B_u'', B_v'', B_o'' for K-step ks.
+  u32x4 wu[kBwdKS], wv[kBwdKS], wo[kBwdKS];
+  {
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.packed + (static_cast<size_t>(q) * NCH + ec) * CH_ELEMS);
+#pragma unroll
+    for (int ks = 0; ks < kBwdKS; ++ks) {
+      wu[ks] = src[ks * (kFragElems / 8) + lane];
+      wv[ks] = src[(kBwdKS + ks) * (kFragElems / 8) + lane];
+      wo[ks] = src[(2 * kBwdKS + ks) * (kFragElems / 8) + lane];
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const uint32_t tbytes = static_cast<uint32_t>(a.q_c * a.pairs * kR64Tile * 2);
+  const __amdgpu_buffer_rsrc_t rt[3] = {buffer_rsrc(a.pu, tbytes), buffer_rsrc(a.pv, tbytes), buffer_rsrc(a.dw, tbytes)};
+  // This wave's copies per step: 1 KB pieces k = w + 8 c (pair k / 12, tensor (k % 12) / 4, rows
+  // 8 (k % 4) .. + 7); lane -> row rr, LDS slot lane % 8 holding piece (lane % 8) ^ kR64Swz(rr).
+  uint32_t loff[3];
+  int kpair[3], ktensor[3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
-    const int f = w + kReduceWaves * c;
-    if (f < 12) {
-      const int tc = f >> 2;
-      rs[c] = buffer_rsrc(tc == 0 ? a.pu : tc == 1 ? a.pv : a.dw, cbytes);
-      fo[c] = static_cast<uint32_t>((f & 3) * kFragElems * 2);
-      rside[c] = false;
-    } else {
-      const int j = f - 12, tr = j >> 3, k = (j & 7) >> 1, g = j & 1;
-      rs[c] = buffer_rsrc(tr == 0 ? a.du : tr == 1 ? a.dv : a.z, rbytes);
-      fo[c] = static_cast<uint32_t>((2 * (k + 4 * h) + g) * kFragElems * 2);
-      rside[c] = true;
-    }
+    const int k = w + kR64Waves * c;
+    kpair[c] = k / 12;
+    ktensor[c] = (k % 12) / 4;
+    const int rr = 8 * (k % 4) + (lane >> 3), sl = lane & 7;
+    loff[c] = static_cast<uint32_t>(rr * 128 + 16 * (sl ^ kR64Swz(rr)));
   }
-  // copies of the workgroup's i-th pair into stage i % kRedStages; an expanded-side fragment is
-  // read by one workgroup, a channel-side one by the rd / 128 row-block workgroups (one at
-  // rd = 128), so the copies are non-temporal (S1 fused block fwd+bwd 0.775 -> 0.759 ms)
   auto issue = [&](int64_t i) {
-    const int64_t pair = s0 + i * pstep;
-    const bool ok = pair < a.pairs;
-    const uint32_t pb = static_cast<uint32_t>(q * a.pairs + pair);
-    const uint32_t stage = lds_addr(&st[i % kRedStages][0][0]);
+    const int64_t st = s0 + i * sstep;
+    const uint32_t stage = lds0 + static_cast<uint32_t>((i % kR64Stages) * kR64Stage);
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      const uint32_t base = rside[c] ? pb * 32u * RD * 2u : pb * 32u * kBwdD * 2u;
-      tile_copy_nt(rs[c], ok ? base + fo[c] + 16u * lane : kOffOut,
-                stage + static_cast<uint32_t>((w + kReduceWaves * c) * 1024));
+      const int k = w + kR64Waves * c;
+      const int64_t pair = st * kR64Pairs + kpair[c];
+      const bool ok = st < steps && pair < a.pairs;
+      const uint32_t voff = ok ? static_cast<uint32_t>((q * a.pairs + pair) * kR64Tile * 2) + loff[c] : kOffOut;
+      tile_copy_nt(ktensor[c] == 0 ? rt[0] : ktensor[c] == 1 ? rt[1] : rt[2], voff, stage + 1024u * k);
     }
   };
-  f32x16 acc[2] = {};
+
+  f32x16 acc_u[kBwdMB] = {}, acc_v[kBwdMB] = {}, acc_o[kBwdMB] = {};
+  auto stage_of = [&](int64_t i) { return lds0 + static_cast<uint32_t>((i % kR64Stages) * kR64Stage); };
+  // U', V', dZ of the chunk for pair pp of a stage: A = the P rows (lane = slot l32, K-step ks =
+  // piece 2 ks + hh), B = the chunk's weights.
+  auto products = [&](uint32_t stage, int pp, f32x16& U, f32x16& V, f32x16& G) {
+    const uint32_t tu = stage + static_cast<uint32_t>(pp * 3 * kR64Tile * 2);
+    const uint32_t tv = tu + kR64Tile * 2, tw = tv + kR64Tile * 2;
+    U = f32x16{};
+    V = f32x16{};
+    G = f32x16{};
 #pragma unroll
-  for (int i = 0; i < kRedStages - 1; ++i) issue(i);
-  for (int64_t i = 0; i < n_iter; ++i) {
-    // This wave's copies of pair i landed (those of pairs i + 1 .. i + kRedStages - 2 may be in
-    // flight); the barrier makes every wave's visible and means every wave is done with stage
-    // (i - 1) % kRedStages, which pair i + kRedStages - 1 takes.
-    wait_vmcnt<3 * (kRedStages - 2)>();
+    for (int ks = 0; ks < kBwdKS; ++ks) {
+      const int pos = 16 * ks + 8 * hh;
+      const u32x4 xu = *reinterpret_cast<const u32x4*>(lds + (r64_at(tu, l32, pos) - lds0));
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(lds + (r64_at(tv, l32, pos) - lds0));
+      const u32x4 xw = *reinterpret_cast<const u32x4*>(lds + (r64_at(tw, l32, pos) - lds0));
+      U = Ty::mma32(xu, wu[ks], U);
+      V = Ty::mma32(xv, wv[ks], V);
+      G = Ty::mma32(xw, wo[ks], G);
+    }
+  };
+  // The gate on U', V', dZ (register i of lane (l32, hh): expanded row 32 ec + l32, slot
+  // kord(i, hh)) and the sums dB_u'' += P_u^T dU', dB_v'' += P_v^T dV', dB_o'' += Z^T dW'.
+  auto gate_sums = [&](uint32_t stage, int pp, const f32x16& U, const f32x16& V, const f32x16& G) {
+    const uint32_t tu = stage + static_cast<uint32_t>(pp * 3 * kR64Tile * 2);
+    const uint32_t tv = tu + kR64Tile * 2, tw = tv + kR64Tile * 2;
+    // Slot-K operands: lane (l32, hh) = channel 32 cb + l32 of P^T / dW', slots 16 s + kord(j, hh):
+    // two transposed reads (rows 16 s + 4 hh + 0..3 and + 8).
+    auto tr = [&](uint32_t t, int cb, int sk) {
+      const int r = 16 * sk + 4 * hh + (l16 >> 2);
+      const int p = r64_pos(32 * cb + 16 * half + 4 * (l16 & 3));
+      const u32x2 x = lds_read_tr16(r64_at(t, r, p)), y = lds_read_tr16(r64_at(t, r + 8, p));
+      return u32x4{x[0], x[1], y[0], y[1]};
+    };
+#pragma unroll
+    for (int sk = 0; sk < 2; ++sk) {
+      // The gate on registers 8 sk .. 8 sk + 7 (slots 16 sk + kord(j, hh)), packed straight into
+      // the K-step sk operands.
+      uint32_t zp[4], dup[4], dvp[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float z2[2], du2[2], dv2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float up = U[8 * sk + j + e], vp = V[8 * sk + j + e], g = G[8 * sk + j + e];
+          const float sg = gate_sigmoid(up);
+          z2[e] = up * vp * sg;
+          du2[e] = g * vp * sg * (1.0f - kLn2 * up * (1.0f - sg));
+          dv2[e] = g * up * sg;
+        }
+        zp[j / 2] = Ty::pack2(z2[0], z2[1]);
+        dup[j / 2] = Ty::pack2(du2[0], du2[1]);
+        dvp[j / 2] = Ty::pack2(dv2[0], dv2[1]);
+      }
+      const u32x4 zs = u32x4{zp[0], zp[1], zp[2], zp[3]}, dus = u32x4{dup[0], dup[1], dup[2], dup[3]},
+                  dvs = u32x4{dvp[0], dvp[1], dvp[2], dvp[3]};
+#pragma unroll
+      for (int cb = 0; cb < kBwdMB; ++cb) {
+        acc_u[cb] = Ty::mma32(tr(tu, cb, sk), dus, acc_u[cb]);
+        acc_v[cb] = Ty::mma32(tr(tv, cb, sk), dvs, acc_v[cb]);
+        acc_o[cb] = Ty::mma32(zs, tr(tw, cb, sk), acc_o[cb]);
+      }
+    }
+  };
+  // Step i is issued at iteration i - kR64Ahead into stage i % kR64Stages; at iteration i the
+  // stages of steps i - 1 .. i + kR64Ahead are in use (see the rd = 128 schedule below).
+  static_assert(kR64Stages == kR64Ahead + 2, "a stage for the lagging waves' previous step");
+#pragma unroll
+  for (int i = 0; i < kR64Ahead; ++i) issue(i);
+  // One iteration's start: this wave's copies of step i landed (those of steps i + 1 ..
+  // i + kR64Ahead - 1 may be in flight); the barrier makes every wave's visible and means every
+  // wave is done with step i - 2, whose stage step i + kR64Ahead takes.  Every wave passes the
+  // same number of barriers (n_iter is the workgroup's).
+  auto next_step = [&](int64_t i) {
+    wait_vmcnt<3 * (kR64Ahead - 1)>();
     __syncthreads();
-    issue(i + kRedStages - 1);
-    const u32x4(*sf)[64] = st[i % kRedStages];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const u32x4 r = sf[12 + 8 * t + 2 * e0 + g][lane];
-#pragma unroll
-      for (int m = 0; m < 2; ++m) acc[m] = Ty::mma32(sf[4 * t + 2 * m + g][lane], r, acc[m]);
+    issue(i + kR64Ahead);
+  };
+  f32x16 U, V, G;
+  if (WPP == 2 && pp0 == 1) {
+    // rd = 128: waves w and w + 4 share a SIMD (and a chunk).  Wave w does step i's pair 0
+    // (products, gate, sums) in iteration i; wave w + 4 runs half a step behind: the gate and
+    // sums of step i - 1's pair 1 (its products held from the last iteration), then step i's
+    // pair 1 products.  So one wave's MFMAs meet the other's gate VALU work instead of both
+    // entering each phase together after the barrier.
+    for (int64_t i = 0; i < n_iter; ++i) {
+      next_step(i);
+      if (i > 0) {
+        mfma_drain();
+        gate_sums(stage_of(i - 1), 1, U, V, G);
+      }
+      products(stage_of(i), 1, U, V, G);
+    }
+    if (n_iter > 0) {
+      // The last step's pair 1 (no copy targets its stage: those are steps up to
+      // n_iter - 1 + kR64Ahead).
+      mfma_drain();
+      gate_sums(stage_of(n_iter - 1), 1, U, V, G);
+    }
+  } else {
+    for (int64_t i = 0; i < n_iter; ++i) {
+      next_step(i);
+#pragma unroll 1
+      for (int pp = pp0; pp < kR64Pairs; pp += WPP) {
+        products(stage_of(i), pp, U, V, G);
+        mfma_drain();
+        gate_sums(stage_of(i), pp, U, V, G);
+      }
     }
   }
-  wait_vmcnt<0>();  // the trailing copies (past the end: zeros) are done before the exit
+  wait_vmcnt<0>();  // the trailing copies (past the end: zeros) are done before LDS is reused
   mfma_drain();
-  // Accumulator register i of lane (l32, hh): channel 32 m + kord(i, hh), row 32 e + l32.
-  float* out = a.partial + ((s0 * 3 + t) * a.q_c + q) * (kBwdD * RD);
-  const int e = e0 + 4 * h;
+  // acc_u / acc_v register i of lane (l32, hh): channel 32 cb + kord(i, hh), expanded row
+  // 32 ec + l32; acc_o: expanded row 32 ec + kord(i, hh), channel 32 cb + l32.
+  if constexpr (WPP == 2) {
+    // The second wave of each chunk hands its sums to the first through LDS.
+    __syncthreads();  // every wave is done with the stages
+    float* cmb = reinterpret_cast<float*>(lds) + static_cast<size_t>(ec) * 96 * 64;
+    if (pp0 == 1) {
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+      for (int cb = 0; cb < kBwdMB; ++cb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = 32 * m + 8 * (i >> 2) + 4 * hh + (i & 3), r = 32 * e + l32;
-      out[t < 2 ? c * RD + r : r * kBwdD + c] = acc[m][i];
+        for (int i2 = 0; i2 < 16; ++i2) {
+          cmb[((0 * kBwdMB + cb) * 16 + i2) * 64 + lane] = acc_u[cb][i2];
+          cmb[((1 * kBwdMB + cb) * 16 + i2) * 64 + lane] = acc_v[cb][i2];
+          cmb[((2 * kBwdMB + cb) * 16 + i2) * 64 + lane] = acc_o[cb][i2];
+        }
+    }
+    __syncthreads();
+    if (pp0 == 1) return;
+#pragma unroll
+    for (int cb = 0; cb < kBwdMB; ++cb)
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        acc_u[cb][i2] += cmb[((0 * kBwdMB + cb) * 16 + i2) * 64 + lane];
+        acc_v[cb][i2] += cmb[((1 * kBwdMB + cb) * 16 + i2) * 64 + lane];
+        acc_o[cb][i2] += cmb[((2 * kBwdMB + cb) * 16 + i2) * 64 + lane];
+      }
+  }
+  float* out_u = a.partial + ((s0 * 3 + 0) * a.q_c + q) * (kBwdD * RD);
+  float* out_v = a.partial + ((s0 * 3 + 1) * a.q_c + q) * (kBwdD * RD);
+  float* out_o = a.partial + ((s0 * 3 + 2) * a.q_c + q) * (kBwdD * RD);
+#pragma unroll
+  for (int cb = 0; cb < kBwdMB; ++cb)
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) {
+      const int k = 32 * cb + 8 * (i2 >> 2) + 4 * hh + (i2 & 3);  // channel (u, v) / expanded row (o)
+      out_u[k * RD + 32 * ec + l32] = acc_u[cb][i2];
+      out_v[k * RD + 32 * ec + l32] = acc_v[cb][i2];
+      out_o[(32 * ec + k - 32 * cb) * kBwdD + 32 * cb + l32] = acc_o[cb][i2];
     }
 }
 
-// Pair ranges S of the reduction (partial rows S q_c; grid S q_c rd / 128): about one
-// workgroup of 12 waves per CU, at least one pair per range.
-int64_t bwd_param_reduce64_ranges(int64_t pairs, int32_t q_c, int32_t rd) {
-  const int64_t per = static_cast<int64_t>(q_c) * (rd / 128);
-  int64_t ranges = (static_cast<int64_t>(device_cus()) + per - 1) / per;
-  return ranges > pairs ? pairs : ranges;
+// Step ranges S of the reduction (partial rows S q_c; grid S q_c): about one workgroup of 8 waves
+// per CU, at least one 2-pair step per range.
+int64_t bwd_param_reduce64_ranges(int64_t pairs, int32_t q_c) {
+  const int64_t steps = (pairs + kR64Pairs - 1) / kR64Pairs;
+  int64_t ranges = static_cast<int64_t>(device_cus()) / q_c;
+  if (ranges < 1) ranges = 1;
+  return ranges > steps ? steps : ranges;
 }
 
-template <int NCH>
+template <int RD>
 int launch_param_reduce64(const ParamReduceArgs& a, int64_t grid, int32_t dtype, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
   if (dtype == OW_DTYPE_BF16)
-    hipLaunchKernelGGL((bwd_param_reduce64_kernel<BF16, NCH>), g, dim3(64 * kReduceWaves), 0, s, a);
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<BF16, RD>), g, dim3(64 * kR64Waves), 0, s, a);
   else
-    hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, NCH>), g, dim3(64 * kReduceWaves), 0, s, a);
+    hipLaunchKernelGGL((bwd_param_reduce64_kernel<F16, RD>), g, dim3(64 * kR64Waves), 0, s, a);
   return hip_status(hipGetLastError(), "bwd_param_reduce64_kernel launch");
 }
 
@@ -2318,16 +2395,18 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
 
 int64_t ow_bwd_param_reduce64_partials(int64_t slots, int32_t q_c, int32_t rd) {
   if (q_c < 1 || slots <= 0 || slots % 32 || (rd != 128 && rd != 256)) return 0;
-  return ow::bwd_param_reduce64_ranges(slots / 32, q_c, rd) * q_c;
+  return ow::bwd_param_reduce64_ranges(slots / 32, q_c) * q_c;
 }
 
-int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* z, const void* du, const void* dv,
+int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const void* packed, size_t packed_bytes,
                           float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t rd, int32_t dtype,
                           void* stream) {
   OW_CHECK_SUPPORTED(rd == 128 || rd == 256, "parameter reduction needs rd in {128, 256} (got %d)", rd);
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
   OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 32 == 0, "bad shape q_c=%d slots=%lld (multiple of 32)", q_c,
                (long long)slots);
+  OW_CHECK_ARG(packed && packed_bytes == ow_bwd_packed_bytes(q_c, ow::kBwdD, rd),
+               "packed backward weights hold %zu bytes", packed_bytes);
   if (slots == 0) {
     ow::clear_error();
     return OW_OK;
@@ -2335,16 +2414,16 @@ int ow_bwd_param_reduce64(const void* pu, const void* pv, const void* dw, const 
   const int64_t rows = ow_bwd_param_reduce64_partials(slots, q_c, rd);
   OW_CHECK_ARG(n_partial == rows, "partial holds %lld rows; %lld needed (ow_bwd_param_reduce64_partials)",
                (long long)n_partial, (long long)rows);
-  const int64_t grid = rows * (rd / 128);
-  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * rd * 2 < (int64_t(1) << 31),
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * ow::kBwdD * 2 < (int64_t(1) << 31),
                "intermediates of %lld slots exceed 2 GiB (buffer addressing)", (long long)slots);
-  OW_CHECK_ARG(pu && pv && dw && z && du && dv && partial, "tensor pointer is NULL");
-  for (const void* p : {pu, pv, dw, z, du, dv})
-    OW_CHECK_ARG(ow::aligned16(p), "fragment buffers must be 16-byte aligned");
+  OW_CHECK_ARG(pu && pv && dw && partial, "tensor pointer is NULL");
+  for (const void* p : {pu, pv, dw, packed})
+    OW_CHECK_ARG(ow::aligned16(p), "intermediates and packed weights must be 16-byte aligned");
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
-  ow::ParamReduceArgs a{cu(pu), cu(pv), cu(dw), cu(z), cu(du), cu(dv), partial, slots / 32, q_c};
+  ow::ParamReduceArgs a{cu(pu), cu(pv), cu(dw), cu(packed), partial, slots / 32, q_c};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int rc = rd == 128 ? ow::launch_param_reduce64<4>(a, grid, dtype, s) : ow::launch_param_reduce64<8>(a, grid, dtype, s);
+  const int rc = rd == 128 ? ow::launch_param_reduce64<128>(a, rows, dtype, s)
+                           : ow::launch_param_reduce64<256>(a, rows, dtype, s);
   if (rc == OW_OK) ow::clear_error();
   return rc;
 }
@@ -2412,9 +2491,8 @@ int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c) {
 }
 
 int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
-                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du, void* dv,
-                 void* dxt, float* partial, int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd,
-                 int32_t dtype, void* stream) {
+                 const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* dxt, float* partial,
+                 int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream) {
   OW_CHECK_SUPPORTED(d == ow::kBwdD && (rd == 128 || rd == 256), "fused backward needs d = 64, rd in {128, 256}");
   OW_CHECK_SUPPORTED(dtype == OW_DTYPE_BF16 || dtype == OW_DTYPE_F16, "unsupported dtype %d", dtype);
   OW_CHECK_ARG(q_c >= 1 && slots >= 0 && slots % 32 == 0, "bad shape q_c=%d slots=%lld (multiple of 32)", q_c,
@@ -2428,16 +2506,14 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
   const int64_t grid = ow_bwd_fused_partials(slots, q_c);
   OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
                (long long)n_partial, (long long)grid);
-  OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && z && du && dv && dxt && partial,
-               "tensor pointer is NULL");
+  OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && dxt && partial, "tensor pointer is NULL");
   for (const void* p : {xt, dyt, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
-                        static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
-                        static_cast<const void*>(dv), static_cast<const void*>(dxt)})
+                        static_cast<const void*>(dw), static_cast<const void*>(dxt)})
     OW_CHECK_ARG(ow::aligned16(p), "tiles and packed weights must be 16-byte aligned");
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
-  ow::BwdFusedArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
-                     mu(dxt), partial, slots, slots / 32, 0, q_c};
+  ow::BwdFusedArgs a{cu(xt), cu(dyt), a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(dxt), partial, slots,
+                     slots / 32, 0, q_c};
   a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
   return ow::launch_bwd_fused<false>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
 }
@@ -2628,9 +2704,8 @@ int ow_bwd_channel2_routed(const void* x, const void* dy, const float* rscale, c
 
 int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, const int32_t* token_index,
                         const OwPlan* plan, int32_t batch, const float* a_u, const float* a_v, const float* a_o,
-                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* z, void* du,
-                        void* dv, void* g, float* partial, int64_t n_partial, int32_t rd, int32_t dtype,
-                        void* stream) {
+                        const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* g,
+                        float* partial, int64_t n_partial, int32_t rd, int32_t dtype, void* stream) {
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   const int32_t d = plan->channel_tile, c = plan->channels, n = plan->height * plan->width;
@@ -2652,16 +2727,15 @@ int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, cons
   const int64_t grid = ow_bwd_fused_partials(slots, q_c);
   OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
                (long long)n_partial, (long long)grid);
-  OW_CHECK_ARG(x && dy && token_index && a_u && a_v && a_o && pu && pv && dw && z && du && dv && g && partial,
+  OW_CHECK_ARG(x && dy && token_index && a_u && a_v && a_o && pu && pv && dw && g && partial,
                "tensor pointer is NULL");
   for (const void* p : {x, dy, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
-                        static_cast<const void*>(dw), static_cast<const void*>(z), static_cast<const void*>(du),
-                        static_cast<const void*>(dv), static_cast<const void*>(g)})
+                        static_cast<const void*>(dw), static_cast<const void*>(g)})
     OW_CHECK_ARG(ow::aligned16(p), "tensors and packed weights must be 16-byte aligned");
   auto cu = [](const void* p) { return static_cast<const uint16_t*>(p); };
   auto mu = [](void* p) { return static_cast<uint16_t*>(p); };
-  ow::BwdFusedArgs a{nullptr, nullptr, a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), mu(z), mu(du), mu(dv),
-                     nullptr, partial, slots, slots / 32, 0, q_c};
+  ow::BwdFusedArgs a{nullptr, nullptr, a_u, a_v, a_o, cu(packed), mu(pu), mu(pv), mu(dw), nullptr, partial, slots,
+                     slots / 32, 0, q_c};
   a.rounds = static_cast<int64_t>(q_c) * ((a.pairs_per_q + 3) / 4);
   a.x = cu(x);
   a.dy = cu(dy);

@@ -164,14 +164,19 @@ def test_bwd_channel_entries_reject_bad_arguments_without_touching_the_gpu() -> 
     assert lib.ow_bwd_param_reduce64_partials(64 * 32 + 16, 2, 128) == 0
     assert lib.ow_bwd_param_reduce64_partials(64 * 32, 2, 192) == 0
 
-    def reduce64(n=n_red, s=64 * 32, rd=128, pu=P):
-        return lib.ow_bwd_param_reduce64(pu, P, P, P, P, P, P, n, s, 2, rd, bf16, None)
+    NB64 = lib.ow_bwd_packed_bytes(2, 64, 128)
+
+    def reduce64(n=n_red, s=64 * 32, rd=128, pu=P, nb=NB64):
+        return lib.ow_bwd_param_reduce64(pu, P, P, P, nb, P, n, s, 2, rd, bf16, None)
 
     assert reduce64(rd=192) == 2 and b"rd in {128, 256}" in lib.ow_last_error()
     assert reduce64(s=64 * 32 + 16) == 1 and b"multiple of 32" in lib.ow_last_error()
+    assert reduce64(nb=NB64 - 2) == 1 and b"packed backward weights" in lib.ow_last_error()
     assert reduce64(n=n_red + 2) == 1 and b"ow_bwd_param_reduce64_partials" in lib.ow_last_error()
     assert reduce64(pu=None) == 1 and b"NULL" in lib.ow_last_error()
     assert reduce64(pu=ctypes.c_void_p(18)) == 1 and b"aligned" in lib.ow_last_error()
+    assert reduce64(s=1 << 24, n=lib.ow_bwd_param_reduce64_partials(1 << 24, 2, 128)) == 1
+    assert b"2 GiB" in lib.ow_last_error()
     assert reduce64(s=0, n=0) == 0  # empty: nothing launched
 
     # The d = 128 reduction over the channel kernels' slot-major intermediates.
