@@ -662,6 +662,35 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] = 0.0f;
 
+  // Routed: the token-table entry of slot l32 of this wave's pair in round rnd (its first tile
+  // 2 pair = b q_s + s; the load only, so that the next round's is in flight during this one)
+  // and the NHWC row it gives (-1 for pads and waves past the end).
+  struct RoundTok {
+    int32_t b, tk;
+    bool live;
+  };
+  auto round_tok = [&](int64_t rnd) {
+    RoundTok t{0, -1, false};
+    if constexpr (RT) {
+      const int64_t pair = (rnd % wg_per_q) * 4 + wave;
+      t.live = rnd < a.rounds && pair < a.pairs_per_q;
+      const uint32_t tile0 = static_cast<uint32_t>(2 * (t.live ? pair : 0));
+      int32_t b = static_cast<int32_t>(tile0 / static_cast<uint32_t>(a.q_s));
+      int32_t st = static_cast<int32_t>(tile0 - static_cast<uint32_t>(b) * static_cast<uint32_t>(a.q_s)) + (l32 >> 4);
+      if (st == a.q_s) {
+        st = 0;
+        ++b;
+      }
+      t.b = b;
+      t.tk = a.tok[st * kG + (l32 & 15)];
+    }
+    return t;
+  };
+  auto tok_row = [&](const RoundTok& t) -> int32_t {  // < 2^31: host check
+    return (t.live && t.b < a.batch && t.tk >= 0 && t.tk < a.n_tok) ? t.b * a.n_tok + t.tk : -1;
+  };
+  RoundTok cur_tok = round_tok(blockIdx.x);
+
   for (int64_t round = blockIdx.x; round < a.rounds; round += gridDim.x) {
     const int q = static_cast<int>(round / wg_per_q);
     const int64_t pair = (round % wg_per_q) * 4 + wave;
@@ -674,23 +703,6 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     __syncthreads();  // the previous round is done with both weight buffers; tok is written
     issue(0);
     const int64_t slot0 = static_cast<int64_t>(q) * a.slots + (live ? pair : 0) * 32;
-    // Routed mode: the pair's first tile 2 pair = b0 q_s + s0 (uniform), and the NHWC row of
-    // its slot r (-1 for pads and waves past the end).
-    int32_t b0 = 0, s0 = 0;
-    if constexpr (RT) {
-      const uint32_t tile0 = static_cast<uint32_t>(2 * (live ? pair : 0));
-      b0 = static_cast<int32_t>(tile0 / static_cast<uint32_t>(a.q_s));
-      s0 = static_cast<int32_t>(tile0 - static_cast<uint32_t>(b0) * static_cast<uint32_t>(a.q_s));
-    }
-    auto nhwc_row = [&](int r) -> int64_t {
-      int32_t b = b0, st = s0 + (r >> 4);
-      if (st == a.q_s) {
-        st = 0;
-        ++b;
-      }
-      const int32_t tk = a.tok[st * kG + (r & 15)];
-      return (live && b < a.batch && tk >= 0 && tk < a.n_tok) ? static_cast<int64_t>(b) * a.n_tok + tk : -1;
-    };
     const int64_t cbase = static_cast<int64_t>(q) * kBwdD;  // routed: first channel of group q
 
     // Token side, X' first, then dY, through the wave's tile [32][kLd] in the second weight
@@ -699,47 +711,53 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     // Routed rows through buffer loads (pads and rows past the end read as zero): every load of
     // a tile is issued before any is waited on.
     const uint32_t nbytes_rows = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
+    const uint32_t tile_bytes = static_cast<uint32_t>(a.q_c * a.slots * kBwdD * 2);
     const __amdgpu_buffer_rsrc_t rrs =
         buffer_rsrc(a.rscale, a.rscale ? static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * 4) : 0u);
     auto row_off = [&](int64_t nr, int64_t c) {
       return nr >= 0 ? static_cast<uint32_t>((nr * a.channels + cbase + c) * 2) : kOffOut;
     };
-    auto row_scale = [&](int64_t nr) {
-      return __uint_as_float(
-          __builtin_amdgcn_raw_buffer_load_b32(rrs, nr >= 0 ? static_cast<uint32_t>(nr * 4) : kOffOut, 0, 0));
-    };
-    auto stage_tile = [&](const uint16_t* src, bool scale) {
+    // Routed: the NHWC row of this lane's slot l32 (lanes l32 and l32 + 32 alike) and its RMSNorm
+    // scale, looked up once per round; every other use takes slot r's from lane r (__shfl).
+    int32_t my_row = -1;
+    float my_rs = 1.0f;
+    if constexpr (RT) {
+      my_row = tok_row(cur_tok);
+      if (a.rscale)
+        my_rs = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rrs, my_row >= 0 ? static_cast<uint32_t>(my_row) * 4u : kOffOut, 0, 0));
+    }
+    auto row_of = [&](int r) { return __shfl(my_row, r); };
+    // A tile's rows (lane: row (lane + 64 k) / 8, channels 8 ((lane + 64 k) % 8) ..), every load
+    // issued before any is waited on; pads and rows past the end read as zero.
+    auto load_rows = [&](const uint16_t* src, u32x4 (&val)[4]) {
       if constexpr (RT) {
         const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(src, nbytes_rows);
-        uint32_t voff[4], soff[4];
-        u32x4 val[4];
-        float rs[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int64_t nr = nhwc_row((lane + 64 * k) >> 3);
-          voff[k] = row_off(nr, ((lane + 64 * k) & 7) * 8);
-          soff[k] = nr >= 0 ? static_cast<uint32_t>(nr * 4) : kOffOut;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          val[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff[k], 0, 0);
-          rs[k] = (scale && a.rscale) ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrs, soff[k], 0, 0)) : 1.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-          if (scale && a.rscale) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) val[k][w] = scale2<Ty>(val[k][w], rs[k]);
-          }
-          *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = val[k];
-        }
+        for (int k = 0; k < 4; ++k)
+          val[k] = __builtin_amdgcn_raw_buffer_load_b128(
+              rsrc, row_off(row_of((lane + 64 * k) >> 3), ((lane + 64 * k) & 7) * 8), 0, 0);
       } else {
+        // The gathered tiles (below 2 GiB: host check), through 32-bit buffer offsets.
+        const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(src, tile_bytes);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
-          *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = *reinterpret_cast<const u32x4*>(src + (slot0 + r) * kBwdD + c8);
+          val[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<uint32_t>(((slot0 + r) * kBwdD + c8) * 2), 0, 0);
         }
+      }
+    };
+    // The rows into the wave's tile [32][kLd]; routed X rows times their RMSNorm scales (X').
+    auto write_tile = [&](u32x4 (&val)[4], bool scale) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int v = lane + 64 * k, r = v >> 3, c8 = (v & 7) * 8;
+        if (RT && scale && a.rscale) {
+          const float rs = __shfl(my_rs, r);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) val[k][w] = scale2<Ty>(val[k][w], rs);
+        }
+        *reinterpret_cast<u32x4*>(tx + r * kLd + c8) = val[k];
       }
       wave_lds_sync();
     };
@@ -758,12 +776,19 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       }
     };
     u32x4 Pu[kBwdKS], Pv[kBwdKS], Dw[kBwdKS];
-    stage_tile(RT ? a.x : a.xt, true);
-    token_side(tok[0][lane], Pu);
-    token_side(tok[1][lane], Pv);
-    wave_lds_sync();
-    stage_tile(RT ? a.dy : a.dyt, false);
-    token_side(tok[2][lane], Dw);
+    {
+      // X and dY rows requested together; dY's land while X's token side runs.
+      u32x4 vx[4], vy[4];
+      load_rows(RT ? a.x : a.xt, vx);
+      load_rows(RT ? a.dy : a.dyt, vy);
+      cur_tok = round_tok(round + gridDim.x);  // the next round's entry, used at its start
+      write_tile(vx, true);
+      token_side(tok[0][lane], Pu);
+      token_side(tok[1][lane], Pv);
+      wave_lds_sync();
+      write_tile(vy, false);
+      token_side(tok[2][lane], Dw);
+    }
     const f32x16 zero = {};
     const int64_t row = slot0 + l32;  // this lane's slot
     if (live) {
@@ -825,6 +850,37 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     }
     mfma_drain();
 
+    // The rows of the dA products, requested before the dX' products so that they land
+    // meanwhile: rows 16 g + l16 of X (routed: x, scaled at use) and of dY, channels
+    // 16 ks + 4 h4 .. + 3 (waves past the end read pads or their group's first rows, unused).
+    int64_t orow[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if constexpr (RT)
+        orow[g] = row_of(16 * g + l16);
+      else
+        orow[g] = slot0 + 16 * g + l16;
+    }
+    auto other_rows = [&](const uint16_t* tiles, const uint16_t* rows, int g, int ks) -> u32x2 {
+      if constexpr (RT) {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             buffer_rsrc(rows, nbytes_rows), row_off(orow[g], 16 * ks + 4 * h4), 0, 0));
+      } else {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             buffer_rsrc(tiles, tile_bytes),
+                                             static_cast<uint32_t>((orow[g] * kBwdD + 16 * ks + 4 * h4) * 2), 0, 0));
+      }
+    };
+    u32x2 xo[2][kBwdKS], yo[2][kBwdKS];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kBwdKS; ++ks) xo[g][ks] = other_rows(a.xt, a.x, g, ks);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kBwdKS; ++ks) yo[g][ks] = other_rows(a.dyt, a.dy, g, ks);
+
     // dX' = A_u^T dP_u + A_v^T dP_v (lane = channel 32 mb + l32, register i = slot
     // pair_token_row(i, hh)).
     f32x16 DX[kBwdMB];
@@ -855,40 +911,20 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     };
     // dA_m += sum over the pair's two tiles of rows(stage) rows(other)^T: A operand lane (t, h4)
     // = stage row 16 g + t, channels 16 ks + 4 h4 .. + 3; B operand = row 16 g + l16 of other.
-    // Rows 16 g + l16 of X' (scaled) or dY, channels 16 ks + 4 h4 .. + 3.
-    int64_t orow[2];
-    float oscale[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      if constexpr (RT) {
-        orow[g] = nhwc_row(16 * g + l16);
-        oscale[g] = a.rscale ? row_scale(orow[g]) : 1.0f;
-      } else {
-        orow[g] = slot0 + 16 * g + l16;
-        oscale[g] = 1.0f;
-      }
-    }
-    auto other_rows = [&](const uint16_t* tiles, const uint16_t* rows, bool scale, int g, int ks) -> u32x2 {
-      if constexpr (RT) {
-        u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                buffer_rsrc(rows, nbytes_rows), row_off(orow[g], 16 * ks + 4 * h4), 0, 0));
-        if (scale && a.rscale) v = u32x2{scale2<Ty>(v[0], oscale[g]), scale2<Ty>(v[1], oscale[g])};
-        return v;
-      } else {
-        return *reinterpret_cast<const u32x2*>(tiles + orow[g] * kBwdD + 16 * ks + 4 * h4);
-      }
-    };
     auto staged_row = [&](int g, int ks) {
       return *reinterpret_cast<const u32x2*>(stage + (16 * g + l16) * kLd + 16 * ks + 4 * h4);
     };
     f32x4 dA[3] = {};
     if (live) {
-      // X' rows read once (all loads before the products) for both dA_u and dA_v.
-      u32x2 xo[2][kBwdKS];
+      if (RT && a.rscale) {
+        // X' = x r for the routed rows.
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
+        for (int g = 0; g < 2; ++g) {
+          const float rs = __shfl(my_rs, 16 * g + l16);
 #pragma unroll
-        for (int ks = 0; ks < kBwdKS; ++ks) xo[g][ks] = other_rows(a.xt, a.x, true, g, ks);
+          for (int ks = 0; ks < kBwdKS; ++ks) xo[g][ks] = u32x2{scale2<Ty>(xo[g][ks][0], rs), scale2<Ty>(xo[g][ks][1], rs)};
+        }
+      }
       put(DPu);
 #pragma unroll
       for (int g = 0; g < 2; ++g)
@@ -901,14 +937,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
 #pragma unroll
         for (int ks = 0; ks < kBwdKS; ++ks) dA[1] = Ty::mma16(staged_row(g, ks), xo[g][ks], dA[1]);
       wave_lds_sync();
-    }
-    // dA_o = dY W'^T: A operand from dY rows, B from the staged W' rows.
-    if (live) {
-      u32x2 yo[2][kBwdKS];
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int ks = 0; ks < kBwdKS; ++ks) yo[g][ks] = other_rows(a.dyt, a.dy, false, g, ks);
+      // dA_o = dY W'^T: A operand from dY rows, B from the staged W' rows.
       put(W);
 #pragma unroll
       for (int g = 0; g < 2; ++g)
@@ -921,7 +950,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       if constexpr (RT) {
         uint32_t goff[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) goff[k] = row_off(nhwc_row((lane + 64 * k) >> 3), ((lane + 64 * k) & 7) * 8);
+        for (int k = 0; k < 4; ++k) goff[k] = row_off(row_of((lane + 64 * k) >> 3), ((lane + 64 * k) & 7) * 8);
         const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.g, nbytes_rows);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -2506,6 +2535,8 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
   const int64_t grid = ow_bwd_fused_partials(slots, q_c);
   OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
                (long long)n_partial, (long long)grid);
+  OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * ow::kBwdD * 2 < (int64_t(1) << 31),
+               "tiles of %lld slots exceed 2 GiB (buffer addressing)", (long long)slots);
   OW_CHECK_ARG(xt && dyt && a_u && a_v && a_o && pu && pv && dw && dxt && partial, "tensor pointer is NULL");
   for (const void* p : {xt, dyt, packed, static_cast<const void*>(pu), static_cast<const void*>(pv),
                         static_cast<const void*>(dw), static_cast<const void*>(dxt)})
