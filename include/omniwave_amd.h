@@ -344,9 +344,9 @@ int ow_pack_bwd_weights(const void* b_u, const void* b_v, const void* b_o, int32
  * dZ^T and the gate backward per 32-row chunk, W' = Z B_o'', dP_u = dU' B_u''^T, dP_v = dV' B_v''^T,
  * dX' = A_u^T dP_u + A_v^T dP_v (stored to dxt), and the token-matrix gradients dA_u = sum
  * dP_u X'^T, dA_v = sum dP_v X'^T, dA_o = sum dY W'^T as per-workgroup fp32 partials
- * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c); element 16 t + k),
+ * partial[w][3][256] (w < n_partial = ow_bwd_fused_partials(slots, q_c, rd); element 16 t + k),
  * which the caller sums over w.  slots % 32 == 0, bf16 / f16. */
-int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c);
+int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c, int32_t rd);
 int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float* a_v, const float* a_o,
                  const void* packed, size_t packed_bytes, void* pu, void* pv, void* dw, void* dxt, float* partial,
                  int64_t n_partial, int64_t slots, int32_t q_c, int32_t d, int32_t rd, int32_t dtype, void* stream);

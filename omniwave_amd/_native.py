@@ -141,7 +141,7 @@ _SIGNATURES = {
         [ctypes.c_void_p] * 3 + [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         + [ctypes.c_int32] * 5 + [ctypes.c_void_p, ctypes.c_void_p],
     ),
-    "ow_bwd_fused_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32]),
+    "ow_bwd_fused_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
     "ow_bwd_fused": (
         ctypes.c_int,
         [ctypes.c_void_p] * 6 + [ctypes.c_size_t] + [ctypes.c_void_p] * 5

@@ -297,7 +297,7 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
                                                   stream), "ow_pack_bwd_weights")
             pu = torch.empty(q_c, slots, d, dtype=dtype, device=dev)
             pv, dw = torch.empty_like(pu), torch.empty_like(pu)
-            n_part = lib.ow_bwd_fused_partials(slots, q_c)
+            n_part = lib.ow_bwd_fused_partials(slots, q_c, rd)
             partial = torch.empty(n_part, 3, 256, dtype=torch.float32, device=dev)
             if routed:
                 _native.check(lib.ow_bwd_fused_routed(x.data_ptr(), grad_delta.data_ptr(), rscale.data_ptr() if rscale

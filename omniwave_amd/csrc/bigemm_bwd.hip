@@ -630,22 +630,36 @@ __device__ __forceinline__ u32x4 token_frag(const float* m, int lane) {
   return v;
 }
 
-template <class Ty, int RD, bool RT>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+// RES (rd = 128): the resident-weights organisation.  One workgroup of 8 waves per CU holds its
+// channel group's packed weights (4 chunks, 96 KB) in LDS for the whole launch: workgroup b
+// takes group b % q_c, and its waves take the group's pairs w, w + 8 R, .. (R = gridDim.x /
+// q_c workgroups per group) independently, with no barrier and no weight copy after the start
+// (the forward wave kernel's scheme); the dA sums stay in registers until the end.  Otherwise
+// (rd = 256, whose 192 KB of weights do not fit): 4 waves per workgroup, rounds of 4 pairs, the
+// chunks streamed through two LDS buffers with a barrier per chunk, as described above.
+constexpr int kBwdResWaves = 8;
+
+template <class Ty, int RD, bool RT, bool RES>
+__global__ void __attribute__((amdgpu_flat_work_group_size(RES ? 512 : 256, RES ? 512 : 256), amdgpu_waves_per_eu(2, 2)))
 bwd_fused_d64_kernel(BwdFusedArgs a) {
   constexpr int NCH = RD / 32;
   constexpr int CH_ELEMS = kBwdFr * kFragElems;
   constexpr int kLd = kBwdD + 8;  // staged tile row stride (elements): conflict-free columns
-  static_assert(4 * 32 * kLd <= CH_ELEMS, "a tile per wave fits in one weight buffer");
-  __shared__ __attribute__((aligned(16))) uint16_t wb[2][CH_ELEMS];
+  constexpr int NW = RES ? kBwdResWaves : 4;
+  static_assert(!RES || RD == 128, "resident weights: rd = 128");
+  static_assert(RES || 4 * 32 * kLd <= CH_ELEMS, "a tile per wave fits in one weight buffer");
+  static_assert(!RES || NW * 3 * 256 * 4 <= NW * 32 * kLd * 2, "the final dA sums fit in the tiles");
+  // RES: the group's NCH chunks; else two chunk buffers.
+  __shared__ __attribute__((aligned(16))) uint16_t wb[RES ? NCH : 2][CH_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[RES ? NW : 1][32 * kLd];  // RES: per wave
   __shared__ __attribute__((aligned(16))) u32x4 tok[5][64];  // A_u, A_v, A_o^T, A_u^T, A_v^T operand rows
-  __shared__ float red[4][3][256];
+  __shared__ float red[RES ? 1 : 4][3][256];
   // wave is uniform: readfirstlane keeps it and the pair, slot and tile positions derived from it in
   // scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int hh = lane >> 5, l32 = lane & 31, l16 = lane & 15, h4 = lane >> 4;
   const bool g0 = (lane & 16) == 0;
-  const int64_t wg_per_q = (a.pairs_per_q + 3) / 4;
+  const int64_t wg_per_q = (a.pairs_per_q + 3) / 4;  // rounds per group (not RES)
 
   if (wave == 0) {
     tok[0][lane] = token_frag<Ty, false>(a.a_u, lane);
@@ -655,26 +669,27 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     tok[3][lane] = token_frag<Ty, true>(a.a_u, lane);
     tok[4][lane] = token_frag<Ty, true>(a.a_v, lane);
   }
-  // red[wave]: the wave's running dA sums (lane (l16, h4) element (4 h4 + i) * 16 + l16), kept
-  // in LDS rather than registers across the channel loop.
+  // Not RES: red[wave] holds the wave's running dA sums (lane (l16, h4) element (4 h4 + i) * 16 +
+  // l16), in LDS rather than registers across the channel loop.  RES: registers.
+  f32x4 dA_run[3] = {};
+  if constexpr (!RES) {
 #pragma unroll
-  for (int m = 0; m < 3; ++m)
+    for (int m = 0; m < 3; ++m)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] = 0.0f;
+      for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] = 0.0f;
+  }
 
-  // Routed: the token-table entry of slot l32 of this wave's pair in round rnd (its first tile
-  // 2 pair = b q_s + s; the load only, so that the next round's is in flight during this one)
-  // and the NHWC row it gives (-1 for pads and waves past the end).
-  struct RoundTok {
+  // Routed: the token-table entry of slot l32 of a pair (its first tile 2 pair = b q_s + s; the
+  // load only, so that the next pair's is in flight during this one) and the NHWC row it gives
+  // (-1 for pads and waves past the end).
+  struct PairTok {
     int32_t b, tk;
     bool live;
   };
-  auto round_tok = [&](int64_t rnd) {
-    RoundTok t{0, -1, false};
+  auto pair_tok = [&](int64_t pair, bool live) {
+    PairTok t{0, -1, live};
     if constexpr (RT) {
-      const int64_t pair = (rnd % wg_per_q) * 4 + wave;
-      t.live = rnd < a.rounds && pair < a.pairs_per_q;
-      const uint32_t tile0 = static_cast<uint32_t>(2 * (t.live ? pair : 0));
+      const uint32_t tile0 = static_cast<uint32_t>(2 * (live ? pair : 0));
       int32_t b = static_cast<int32_t>(tile0 / static_cast<uint32_t>(a.q_s));
       int32_t st = static_cast<int32_t>(tile0 - static_cast<uint32_t>(b) * static_cast<uint32_t>(a.q_s)) + (l32 >> 4);
       if (st == a.q_s) {
@@ -686,39 +701,26 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     }
     return t;
   };
-  auto tok_row = [&](const RoundTok& t) -> int32_t {  // < 2^31: host check
+  auto tok_row = [&](const PairTok& t) -> int32_t {  // < 2^31: host check
     return (t.live && t.b < a.batch && t.tk >= 0 && t.tk < a.n_tok) ? t.b * a.n_tok + t.tk : -1;
   };
-  RoundTok cur_tok = round_tok(blockIdx.x);
+  const uint32_t nbytes_rows = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
+  const uint32_t tile_bytes = static_cast<uint32_t>(a.q_c * a.slots * kBwdD * 2);
+  const __amdgpu_buffer_rsrc_t rrs =
+      buffer_rsrc(a.rscale, a.rscale ? static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * 4) : 0u);
 
-  for (int64_t round = blockIdx.x; round < a.rounds; round += gridDim.x) {
-    const int q = static_cast<int>(round / wg_per_q);
-    const int64_t pair = (round % wg_per_q) * 4 + wave;
-    const bool live = pair < a.pairs_per_q;  // waves past the end still take part in the barriers
-    const uint16_t* wsrc = a.packed + static_cast<int64_t>(q) * NCH * CH_ELEMS;
-    auto issue = [&](int ec) {
-      for (int f = wave; f < kBwdFr; f += 4)
-        bwd_copy_frag(wsrc + static_cast<int64_t>(ec) * CH_ELEMS + f * kFragElems, wb[ec & 1] + f * kFragElems, lane);
-    };
-    __syncthreads();  // the previous round is done with both weight buffers; tok is written
-    issue(0);
+  // One pair of group q (32 slots from slot0): token side, channel loop, dX', dA.  tx: the wave's
+  // tile [32][kLd] for X, dY and the dA rows; next: the token-table entry of the wave's next pair;
+  // chunk_begin(ec) / chunk_frag(ec): the chunk loop's synchronisation and chunk ec's fragments.
+  auto do_pair = [&](int q, int64_t pair, bool live, PairTok& cur_tok, const PairTok& next_tok, uint16_t* tx,
+                     uint16_t* stage, auto chunk_begin, auto chunk_frags) {
     const int64_t slot0 = static_cast<int64_t>(q) * a.slots + (live ? pair : 0) * 32;
     const int64_t cbase = static_cast<int64_t>(q) * kBwdD;  // routed: first channel of group q
-
-    // Token side, X' first, then dY, through the wave's tile [32][kLd] in the second weight
-    // buffer.
-    uint16_t* tx = wb[1] + wave * 32 * kLd;
-    // Routed rows through buffer loads (pads and rows past the end read as zero): every load of
-    // a tile is issued before any is waited on.
-    const uint32_t nbytes_rows = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.channels * 2);
-    const uint32_t tile_bytes = static_cast<uint32_t>(a.q_c * a.slots * kBwdD * 2);
-    const __amdgpu_buffer_rsrc_t rrs =
-        buffer_rsrc(a.rscale, a.rscale ? static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * 4) : 0u);
     auto row_off = [&](int64_t nr, int64_t c) {
       return nr >= 0 ? static_cast<uint32_t>((nr * a.channels + cbase + c) * 2) : kOffOut;
     };
     // Routed: the NHWC row of this lane's slot l32 (lanes l32 and l32 + 32 alike) and its RMSNorm
-    // scale, looked up once per round; every other use takes slot r's from lane r (__shfl).
+    // scale, looked up once per pair; every other use takes slot r's from lane r (__shfl).
     int32_t my_row = -1;
     float my_rs = 1.0f;
     if constexpr (RT) {
@@ -761,9 +763,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       }
       wave_lds_sync();
     };
-    const bool g0b = g0;
     auto token_side = [&](u32x4 f, u32x4 (&out)[kBwdKS]) {
-      const u32x4 f0 = keep_if(g0b, f), f1 = keep_if(!g0b, f);
+      const u32x4 f0 = keep_if(g0, f), f1 = keep_if(!g0, f);
       const f32x16 zero = {};
 #pragma unroll
       for (int cb = 0; cb < kBwdMB; ++cb) {
@@ -781,7 +782,7 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       u32x4 vx[4], vy[4];
       load_rows(RT ? a.x : a.xt, vx);
       load_rows(RT ? a.dy : a.dyt, vy);
-      cur_tok = round_tok(round + gridDim.x);  // the next round's entry, used at its start
+      cur_tok = next_tok;  // the next pair's entry (requested by the caller), used at its start
       write_tile(vx, true);
       token_side(tok[0][lane], Pu);
       token_side(tok[1][lane], Pv);
@@ -808,12 +809,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     // Channel side.
     f32x16 W[kBwdMB] = {}, DPu[kBwdMB] = {}, DPv[kBwdMB] = {};
     for (int ec = 0; ec < NCH; ++ec) {
-      // Chunk ec's copies: chunk 0 landed before the tile loads the compiler waited on; chunk
-      // ec >= 1 was issued at step ec - 1, and nothing follows it.
-      if (ec > 0) wait_vmcnt<0>();
-      __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1 (ec = 0: its tiles)
-      if (ec + 1 < NCH) issue(ec + 1);
-      const u32x4* cf = reinterpret_cast<const u32x4*>(wb[ec & 1]);
+      chunk_begin(ec);
+      const u32x4* cf = chunk_frags(ec);
       auto frag = [&](int f) { return cf[f * (kFragElems / 8) + lane]; };
       f32x16 U = {}, V = {}, G = {};
 #pragma unroll
@@ -861,13 +858,13 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
       else
         orow[g] = slot0 + 16 * g + l16;
     }
-    auto other_rows = [&](const uint16_t* tiles, const uint16_t* rows, int g, int ks) -> u32x2 {
+    auto other_rows = [&](const uint16_t* tiles_src, const uint16_t* rows, int g, int ks) -> u32x2 {
       if constexpr (RT) {
         return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                                              buffer_rsrc(rows, nbytes_rows), row_off(orow[g], 16 * ks + 4 * h4), 0, 0));
       } else {
         return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                             buffer_rsrc(tiles, tile_bytes),
+                                             buffer_rsrc(tiles_src, tile_bytes),
                                              static_cast<uint32_t>((orow[g] * kBwdD + 16 * ks + 4 * h4) * 2), 0, 0));
       }
     };
@@ -898,10 +895,8 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
     }
     mfma_drain();
 
-    // Through the wave's LDS tile [32 slots][kLd] (the buffer of chunk NCH: no copy targets it
-    // after the last barrier of the loop): dP_u, dP_v, W' as rows for the dA products, dX' as
-    // 16-byte row vectors to memory.
-    uint16_t* stage = wb[NCH & 1] + wave * 32 * kLd;
+    // Through the wave's staging tile [32 slots][kLd]: dP_u, dP_v, W' as rows for the dA
+    // products, dX' as 16-byte row vectors to memory.
     auto put = [&](const f32x16 (&m)[kBwdMB]) {
 #pragma unroll
       for (int mb = 0; mb < kBwdMB; ++mb)
@@ -965,20 +960,97 @@ bwd_fused_d64_kernel(BwdFusedArgs a) {
                                       reinterpret_cast<u32x4*>(a.dxt + (slot0 + r) * kBwdD + c8));
         }
       }
+      wave_lds_sync();  // the staging tile is read before the next pair's rows replace it
     }
     mfma_drain();
+    if constexpr (RES) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) dA_run[m] += dA[m];
+    } else {
+#pragma unroll
+      for (int m = 0; m < 3; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] += dA[m][i];
+    }
+  };
+
+  float(*sums)[3][256];  // the waves' dA sums for the final fixed-order addition
+  if constexpr (RES) {
+    // The group's weights into LDS once (12 KB per wave); then every wave on its own.
+    const int q = static_cast<int>(blockIdx.x % a.q_c);
+    const int64_t wg_in_q = blockIdx.x / a.q_c, wpg = gridDim.x / a.q_c;
+    const uint16_t* wsrc = a.packed + static_cast<int64_t>(q) * NCH * CH_ELEMS;
+    for (int f = wave; f < NCH * kBwdFr; f += NW) bwd_copy_frag(wsrc + f * kFragElems, &wb[0][0] + f * kFragElems, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // weights and tok are written
+    uint16_t* tx = tiles[wave];
+    const int64_t pstride = wpg * NW;
+    int64_t pair = wg_in_q * NW + wave;
+    PairTok cur_tok = pair_tok(pair, pair < a.pairs_per_q);
+    for (; pair < a.pairs_per_q; pair += pstride) {
+      const int64_t nxt = pair + pstride;
+      const PairTok next_tok = pair_tok(nxt, nxt < a.pairs_per_q);
+      do_pair(q, pair, true, cur_tok, next_tok, tx, tx, [](int) {},
+              [&](int ec) { return reinterpret_cast<const u32x4*>(wb[ec]); });
+    }
+    __syncthreads();  // every wave is done with its tile
+    sums = reinterpret_cast<float(*)[3][256]>(&tiles[0][0]);
 #pragma unroll
     for (int m = 0; m < 3; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] += dA[m][i];
+      for (int i = 0; i < 4; ++i) sums[wave][m][(4 * h4 + i) * 16 + l16] = dA_run[m][i];
+  } else {
+    PairTok cur_tok = pair_tok((blockIdx.x % wg_per_q) * 4 + wave,
+                               blockIdx.x < a.rounds && (blockIdx.x % wg_per_q) * 4 + wave < a.pairs_per_q);
+    for (int64_t round = blockIdx.x; round < a.rounds; round += gridDim.x) {
+      const int q = static_cast<int>(round / wg_per_q);
+      const int64_t pair = (round % wg_per_q) * 4 + wave;
+      const bool live = pair < a.pairs_per_q;  // waves past the end still take part in the barriers
+      const uint16_t* wsrc = a.packed + static_cast<int64_t>(q) * NCH * CH_ELEMS;
+      auto issue = [&](int ec) {
+        for (int f = wave; f < kBwdFr; f += 4)
+          bwd_copy_frag(wsrc + static_cast<int64_t>(ec) * CH_ELEMS + f * kFragElems, wb[ec & 1] + f * kFragElems, lane);
+      };
+      __syncthreads();  // the previous round is done with both weight buffers; tok is written
+      issue(0);
+      const int64_t nr = round + gridDim.x;
+      const int64_t npair = (nr % wg_per_q) * 4 + wave;
+      const PairTok next_tok = pair_tok(npair, nr < a.rounds && npair < a.pairs_per_q);
+      // The token side's tile is in the second weight buffer (no copy targets it before the
+      // first barrier of the chunk loop); the dA staging in the buffer of chunk NCH, which no copy
+      // targets after the loop's last barrier.
+      do_pair(q, pair, live, cur_tok, next_tok, wb[1] + wave * 32 * kLd, wb[NCH & 1] + wave * 32 * kLd,
+              [&](int ec) {
+                // Chunk ec's copies: chunk 0 landed before the tile loads the compiler waited on;
+                // chunk ec >= 1 was issued at step ec - 1, and nothing follows it.
+                if (ec > 0) wait_vmcnt<0>();
+                __syncthreads();  // chunk ec landed; every wave is done with chunk ec - 1 (ec = 0: its tiles)
+                if (ec + 1 < NCH) issue(ec + 1);
+              },
+              [&](int ec) { return reinterpret_cast<const u32x4*>(wb[ec & 1]); });
+    }
+    __syncthreads();
+    sums = red;
   }
-
-  // The workgroup's dA sums, the waves added in order 0..3.
-  __syncthreads();
-  for (int e = threadIdx.x; e < 3 * 256; e += 256) {
+  // The workgroup's dA sums, the waves added in order.
+  if constexpr (RES) __syncthreads();
+  for (int e = threadIdx.x; e < 3 * 256; e += 64 * NW) {
     const int m = e >> 8, k = e & 255;
-    a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = ((red[0][m][k] + red[1][m][k]) + red[2][m][k]) + red[3][m][k];
+    float v = sums[0][m][k];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += sums[w][m][k];
+    a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = v;
   }
+}
+
+// Workgroups of the resident-weights kernel: about one per CU, a multiple of q_c (at least one
+// per group), no more per group than it has 8-pair rows.
+int64_t bwd_fused_res_grid(int64_t pairs, int32_t q_c) {
+  int64_t per = static_cast<int64_t>(device_cus()) / q_c;
+  const int64_t need = (pairs + kBwdResWaves - 1) / kBwdResWaves;
+  if (per > need) per = need;
+  if (per < 1) per = 1;
+  return per * q_c;
 }
 
 template <bool RT>
@@ -986,14 +1058,14 @@ int launch_bwd_fused(const BwdFusedArgs& a, int64_t grid, int32_t rd, int32_t dt
   const dim3 g(static_cast<unsigned>(grid));
   if (dtype == OW_DTYPE_BF16) {
     if (rd == 128)
-      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 128, RT>), g, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 128, RT, true>), g, dim3(64 * kBwdResWaves), 0, s, a);
     else
-      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 256, RT>), g, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<BF16, 256, RT, false>), g, dim3(256), 0, s, a);
   } else {
     if (rd == 128)
-      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 128, RT>), g, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 128, RT, true>), g, dim3(64 * kBwdResWaves), 0, s, a);
     else
-      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 256, RT>), g, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((bwd_fused_d64_kernel<F16, 256, RT, false>), g, dim3(256), 0, s, a);
   }
   if (int rc = hip_status(hipGetLastError(), "bwd_fused_d64_kernel launch")) return rc;
   clear_error();
@@ -2511,10 +2583,12 @@ int ow_sum_rows(const float* partial, int64_t rows, int64_t cols, float* out, vo
   return OW_OK;
 }
 
-// Workgroups (and partial rows) of ow_bwd_fused: every workgroup loops over rounds of four
-// pairs, so the dA partials stay few.
-int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c) {
-  if (q_c < 1 || slots <= 0 || slots % 32) return 0;
+// Workgroups (and partial rows) of ow_bwd_fused: rd = 128 about one resident-weights workgroup
+// per CU; rd = 256 rounds of four pairs, grid-strided over at most kBwdFusedGrid workgroups, so
+// the dA partials stay few.
+int64_t ow_bwd_fused_partials(int64_t slots, int32_t q_c, int32_t rd) {
+  if (q_c < 1 || slots <= 0 || slots % 32 || (rd != 128 && rd != 256)) return 0;
+  if (rd == 128) return ow::bwd_fused_res_grid(slots / 32, q_c);
   const int64_t rounds = static_cast<int64_t>(q_c) * ((slots / 32 + 3) / 4);
   return rounds < ow::kBwdFusedGrid ? rounds : ow::kBwdFusedGrid;
 }
@@ -2532,7 +2606,7 @@ int ow_bwd_fused(const void* xt, const void* dyt, const float* a_u, const float*
     ow::clear_error();
     return OW_OK;
   }
-  const int64_t grid = ow_bwd_fused_partials(slots, q_c);
+  const int64_t grid = ow_bwd_fused_partials(slots, q_c, rd);
   OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
                (long long)n_partial, (long long)grid);
   OW_CHECK_ARG(static_cast<int64_t>(q_c) * slots * ow::kBwdD * 2 < (int64_t(1) << 31),
@@ -2755,7 +2829,7 @@ int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, cons
     ow::clear_error();
     return OW_OK;
   }
-  const int64_t grid = ow_bwd_fused_partials(slots, q_c);
+  const int64_t grid = ow_bwd_fused_partials(slots, q_c, rd);
   OW_CHECK_ARG(n_partial == grid, "partial holds %lld workgroup rows; %lld needed (ow_bwd_fused_partials)",
                (long long)n_partial, (long long)grid);
   OW_CHECK_ARG(x && dy && token_index && a_u && a_v && a_o && pu && pv && dw && g && partial,
