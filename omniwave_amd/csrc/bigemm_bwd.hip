@@ -1803,8 +1803,9 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
 // Same units as bwd_chan_d128_kernel.  Per 32-slot pair (one per wave):
 //   * pass 1 over the chunks of the expanded dimension: dP_u^T... as accumulators DPu[mb] +=
 //     dU' B_u''^T, DPv[mb] += dV' B_v''^T (lane = channel 32 mb + l32, register i = slot
-//     kord(i, hh)), the pair's dU', dV' chunk rows copied to the wave's LDS region and the
-//     chunk's B-operand fragments shared by the eight waves (three LDS buffers);
+//     kord(i, hh)), the pair's dU', dV' chunk rows copied two chunks ahead into the wave's LDS
+//     region (three buffers) and the chunk's B-operand fragments shared by the eight waves
+//     (three LDS buffers);
 //   * dX'^T = dP_u^T A_u + dP_v^T A_v with the operands swapped (lane = slot, registers =
 //     channels), stored as 8-byte row pieces;
 //   * dA_u += dP_u X'^T, dA_v += dP_v X'^T per 16-slot tile on 16x16x16 MFMAs over the channels:
@@ -1837,12 +1838,20 @@ struct BwdChan2Args {
 
 constexpr int kB2FrB = 16;  // B-operand fragments of pass 1 per chunk (B_u''^T, B_v''^T)
 
+// Rows in the wave's region are 64 bytes (32 values); their 16-byte pieces are XOR-swizzled so
+// that the row-operand reads (one row per lane) and the staged dP / W' writes and transposed
+// reads spread over the LDS banks: chunk rows (slot r) keep piece p at p ^ c2_rswz(r), the
+// staged [128 channels][32 slots] set (channel c) at p ^ c2_sswz(c).
+__device__ __forceinline__ int c2_rswz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int c2_sswz(int c) { return (2 * ((c >> 2) & 1)) ^ ((c >> 3) & 1); }
+constexpr int kB2RowBuf = 4096;  // bytes of one chunk-row buffer (pass 1: dU' then dV', 2 KB each)
+
 struct BwdChan2Lds {
-  uint16_t r[kB2Waves][32 * kB2D];      // per wave: operand chunk rows, then staged dP / W' (8 KB)
-  uint16_t w[3][kB2FrB * kFragElems];   // chunk buffers
-  u32x4 tok[2][64];                     // A_u^T, A_v^T token-operand rows
-  float red[kB2Waves][3][256];          // per-wave dA sums
+  uint16_t r[kB2Waves][3 * kB2RowBuf / 2];  // per wave: three chunk-row buffers; staged dP / W' in the first 8 KB
+  uint16_t w[3][kB2FrB * kFragElems];      // chunk buffers
+  u32x4 tok[2][64];                        // A_u^T, A_v^T token-operand rows
 };
+static_assert(kB2Waves * 3 * 256 * 4 <= sizeof(BwdChan2Lds::r), "the final dA sums fit in the row regions");
 
 template <class Ty, int RD, bool RT>
 __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int32_t n_units) {
@@ -1878,20 +1887,25 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
     const int64_t row0 = static_cast<int64_t>(q) * a.slots + slot0;
     const uint16_t* pk = a.packed + static_cast<size_t>(q) * NCH * PACK_CH;
     // Chunk rows of one [slots][RD] tensor (32 slots x 32 values, 2 KB) into the wave's region
-    // at byte offset `at`: two copies, lane -> slot 16 c + lane / 4, 16 bytes at value 8 (lane % 4).
+    // at byte offset `at`: two copies, lane -> slot 16 c + lane / 4, LDS piece lane % 4 holding
+    // the row's piece (lane % 4) ^ c2_rswz(slot).
     auto copy_rows = [&](__amdgpu_buffer_rsrc_t r, int ec, uint32_t at) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int sl = 16 * c + (lane >> 2);
+        const int pc = (lane & 3) ^ c2_rswz(sl);
         const uint32_t voff =
-            slot0 + sl < a.slots ? static_cast<uint32_t>((row0 + sl) * RD + 32 * ec + 8 * (lane & 3)) * 2u : kOffOut;
+            slot0 + sl < a.slots ? static_cast<uint32_t>((row0 + sl) * RD + 32 * ec + 8 * pc) * 2u : kOffOut;
         tile_copy(r, voff, rlds + at + 1024u * c);
       }
     };
-    // K-step operand s of a staged chunk (lane (slot l32, hh): values 16 s + 4 hh + 0..3 and + 8).
+    // K-step operand s of a staged chunk (lane (slot l32, hh): values 16 s + 4 hh + 0..3 and + 8,
+    // the 8-byte halves hh of pieces 2 s and 2 s + 1).
     auto row_op = [&](uint32_t at, int s2) {
-      const uint16_t* base = sh.r[wave] + at / 2 + l32 * 32 + 16 * s2 + 4 * hh;
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(base), hi = *reinterpret_cast<const u32x2*>(base + 8);
+      const uint16_t* base = sh.r[wave] + at / 2 + l32 * 32 + 4 * hh;
+      const int sw = c2_rswz(l32);
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(base + 8 * ((2 * s2) ^ sw));
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(base + 8 * ((2 * s2 + 1) ^ sw));
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
     auto copy_w = [&](int ec, int off, int nfr) {  // nfr / 8 fragments per wave
@@ -1906,17 +1920,21 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
     // channel-major: region [128 channels][32 slots], bf16.
     auto stage = [&](const f32x16 (&m)[MB]) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb) {
+        const int c = 32 * mb + l32;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          *reinterpret_cast<u32x2*>(&sh.r[wave][(32 * mb + l32) * 32 + 8 * b + 4 * hh]) =
+          *reinterpret_cast<u32x2*>(&sh.r[wave][c * 32 + 8 * (b ^ c2_sswz(c)) + 4 * hh]) =
               u32x2{Ty::pack2(m[mb][4 * b], m[mb][4 * b + 1]), Ty::pack2(m[mb][4 * b + 2], m[mb][4 * b + 3])};
+      }
       wave_lds_sync();
     };
     // Rows 16 g + l16, channels 16 ks + 4 h4 .. + 3 of the staged set, by transposed reads (the
-    // 16x16x16 operand: lane (t = l16, h4)).
+    // 16x16x16 operand: lane (t = l16, h4)); the lane's address: channel 16 ks + 4 h4 + l16 / 4,
+    // slots 16 g + 4 (l16 % 4) .. + 3.
     auto staged_op = [&](int g, int ks) {
-      const uint32_t addr = rlds + 2u * static_cast<uint32_t>((16 * ks + 4 * h4 + (l16 >> 2)) * 32 + 16 * g + 4 * (l16 & 3));
+      const int c = 16 * ks + 4 * h4 + (l16 >> 2), sl = 16 * g + 4 * (l16 & 3);
+      const uint32_t addr = rlds + 2u * static_cast<uint32_t>(c * 32 + 8 * ((sl >> 3) ^ c2_sswz(c)) + (sl & 7));
       return lds_read_tr16(addr);
     };
     // RT: the NHWC rows of the lane's slots 16 g + l16 (g < 2) and, for X', their RMSNorm scales.
@@ -1930,8 +1948,8 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
       }
     }
     // Rows 16 g + l16 of a [slots][128] tensor, channels 16 ks + 4 h4 .. + 3 (zero past the slots);
-    // RT: of x (XS: times the row's scale and rounded, X' as the gather forms it) or dy.
-    auto mem_op = [&](__amdgpu_buffer_rsrc_t r, int g, int ks, bool xs) {
+    // RT: of x or dy (the loads only: x_scaled forms X' as the gather does).
+    auto mem_op = [&](__amdgpu_buffer_rsrc_t r, int g, int ks) {
       uint32_t o;
       if constexpr (RT)
         o = grow[g] >= 0 ? static_cast<uint32_t>(grow[g] * a.channels + kB2D * q + 16 * ks + 4 * h4) * 2u : kOffOut;
@@ -1939,20 +1957,26 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
         o = slot0 + 16 * g + l16 < a.slots
                 ? static_cast<uint32_t>((row0 + 16 * g + l16) * kB2D + 16 * ks + 4 * h4) * 2u
                 : kOffOut;
-      u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+      return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+    };
+    auto x_scaled = [&](u32x2 v, int g) {
       if constexpr (RT) {
-        if (xs && a.rscale) v = u32x2{scale2<Ty>(v[0], grs[g]), scale2<Ty>(v[1], grs[g])};
+        if (a.rscale) v = u32x2{scale2<Ty>(v[0], grs[g]), scale2<Ty>(v[1], grs[g])};
       }
       return v;
     };
 
     __syncthreads();  // the previous unit is done with every buffer; tok is written
-    // Pass 1.  Step ec: [wait: chunk ec's rows and fragments] [barrier] [rows of ec + 1: 4]
-    // [fragments of ec + 2: 2] [products].  Only the fragments of the next step may be in flight.
+    // Pass 1.  Step ec: [wait: chunk ec's rows and fragments] [barrier] [rows and fragments of
+    // ec + 2: 4 + 2] [products].  Chunk ec + 1's copies may be in flight (6, none at the last step).
     copy_rows(rdu, 0, 0);
     copy_rows(rdv, 0, 2048);
     copy_w(0, OFF_BU, kB2FrB);
-    copy_w(1, OFF_BU, kB2FrB);
+    if (NCH > 1) {
+      copy_rows(rdu, 1, kB2RowBuf);
+      copy_rows(rdv, 1, kB2RowBuf + 2048);
+      copy_w(1, OFF_BU, kB2FrB);
+    }
     f32x16 DPu[MB], DPv[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -1962,16 +1986,16 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
 #pragma unroll 1
     for (int ec = 0; ec < NCH; ++ec) {
       if (ec + 1 < NCH)
-        wait_vmcnt<2>();
+        wait_vmcnt<6>();
       else
         wait_vmcnt<0>();
-      __syncthreads();
-      const uint32_t cur = 4096u * (ec & 1), nxt = 4096u * ((ec + 1) & 1);
-      if (ec + 1 < NCH) {
-        copy_rows(rdu, ec + 1, nxt);
-        copy_rows(rdv, ec + 1, nxt + 2048);
+      __syncthreads();  // chunk ec is in LDS for every wave; every wave is done with chunk ec - 1
+      const uint32_t cur = kB2RowBuf * (ec % 3), nxt2 = kB2RowBuf * ((ec + 2) % 3);
+      if (ec + 2 < NCH) {
+        copy_rows(rdu, ec + 2, nxt2);
+        copy_rows(rdv, ec + 2, nxt2 + 2048);
+        copy_w(ec + 2, OFF_BU, kB2FrB);
       }
-      if (ec + 2 < NCH) copy_w(ec + 2, OFF_BU, kB2FrB);
       const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
@@ -2016,38 +2040,52 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
         }
       }
     }
-    // dA_u, dA_v.
+    // dA_u, dA_v: the X rows requested before the staging of dP_u.
+    u32x2 xo[2][kB2KS];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) xo[g][ks] = mem_op(rxt, g, ks);
     stage(DPu);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[0] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks, true), dA[0]);
+      for (int ks = 0; ks < kB2KS; ++ks) xo[g][ks] = x_scaled(xo[g][ks], g);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) dA[0] = Ty::mma16(staged_op(g, ks), xo[g][ks], dA[0]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     stage(DPv);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[1] = Ty::mma16(staged_op(g, ks), mem_op(rxt, g, ks, true), dA[1]);
+      for (int ks = 0; ks < kB2KS; ++ks) dA[1] = Ty::mma16(staged_op(g, ks), xo[g][ks], dA[1]);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // nothing in flight before pass 2's copies
 
-    // Pass 2: W'[mb] += Z B_o''; [wait] [barrier] [Z rows of ec + 1: 2] [fragments of ec + 2: 1].
+    // Pass 2: W'[mb] += Z B_o''; [wait] [barrier] [Z rows and fragments of ec + 2: 2 + 1].
     __syncthreads();  // every wave is done with pass 1's chunk buffers
     copy_rows(rz, 0, 0);
     copy_w(0, OFF_BO, 2 * MB);
-    copy_w(1, OFF_BO, 2 * MB);
+    if (NCH > 1) {
+      copy_rows(rz, 1, kB2RowBuf);
+      copy_w(1, OFF_BO, 2 * MB);
+    }
     f32x16 W[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) W[mb] = f32x16{};
 #pragma unroll 1
     for (int ec = 0; ec < NCH; ++ec) {
       if (ec + 1 < NCH)
-        wait_vmcnt<1>();
+        wait_vmcnt<3>();
       else
         wait_vmcnt<0>();
       __syncthreads();
-      const uint32_t cur = 2048u * (ec & 1), nxt = 2048u * ((ec + 1) & 1);
-      if (ec + 1 < NCH) copy_rows(rz, ec + 1, nxt);
-      if (ec + 2 < NCH) copy_w(ec + 2, OFF_BO, 2 * MB);
+      const uint32_t cur = kB2RowBuf * (ec % 3), nxt2 = kB2RowBuf * ((ec + 2) % 3);
+      if (ec + 2 < NCH) {
+        copy_rows(rz, ec + 2, nxt2);
+        copy_w(ec + 2, OFF_BO, 2 * MB);
+      }
       const u32x4* cf = reinterpret_cast<const u32x4*>(sh.w[ec % 3]);
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
@@ -2058,25 +2096,33 @@ __global__ void __launch_bounds__(512) bwd_chan2_d128_kernel(BwdChan2Args a, int
     }
     mfma_drain();
     // dA_o = dY W'^T: A = dY rows from memory, B = staged W' rows.
+    u32x2 yo[2][kB2KS];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int ks = 0; ks < kB2KS; ++ks) yo[g][ks] = mem_op(rdy, g, ks);
     stage(W);
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int ks = 0; ks < kB2KS; ++ks) dA[2] = Ty::mma16(mem_op(rdy, g, ks, false), staged_op(g, ks), dA[2]);
+      for (int ks = 0; ks < kB2KS; ++ks) dA[2] = Ty::mma16(yo[g][ks], staged_op(g, ks), dA[2]);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   }
 
-  // The workgroup's dA sums, waves added in order.
+  // The workgroup's dA sums, waves added in order (in the row regions, which every wave is done
+  // with after the barrier).
   mfma_drain();
+  __syncthreads();
+  float(*red)[3][256] = reinterpret_cast<float(*)[3][256]>(&sh.r[0][0]);
 #pragma unroll
   for (int m = 0; m < 3; ++m)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sh.red[wave][m][(4 * h4 + i) * 16 + l16] = dA[m][i];
+    for (int i = 0; i < 4; ++i) red[wave][m][(4 * h4 + i) * 16 + l16] = dA[m][i];
   __syncthreads();
   for (int e = threadIdx.x; e < 3 * 256; e += 512) {
     const int m = e >> 8, k = e & 255;
     float v = 0.0f;
-    for (int w = 0; w < kB2Waves; ++w) v += sh.red[w][m][k];
+    for (int w = 0; w < kB2Waves; ++w) v += red[w][m][k];
     a.partial[static_cast<int64_t>(blockIdx.x) * 768 + e] = v;
   }
 }
