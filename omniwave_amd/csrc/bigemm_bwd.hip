@@ -1554,7 +1554,7 @@ int sum_rows_waves(int64_t rows) { return rows >= 128 ? 16 : rows >= 32 ? 8 : ro
 //   * P_u = A_u X', P_v = A_v X' from the wave's 32 X' rows, then dW' = A_o^T dY from its 32 dY
 //     rows: the forward's block-diagonal token-side products (32x32x16 MFMAs), the X^T operands
 //     by transposed LDS reads of the rows, which buffer_load ... lds copies into the wave's
-//     swizzled tile (piece p of row r at slot p ^ 4 ((r >> 2) & 1)); P_u, P_v, dW' are stored;
+//     swizzled tile (piece p of row r at slot p ^ tile128_swz(r)); P_u, P_v, dW' are stored;
 //   * per 32-row chunk ec of the expanded dimension: U'^T = B_u''^T P_u^T, V'^T, dZ^T = B_o''
 //     dW'^T (the chunk's 24 A-operand fragments of ow_pack_bwd_weights, shared by the eight
 //     waves through three LDS buffers), the gate backward (as bwd_gate_kernel), and Z, dU', dV'
@@ -1665,12 +1665,12 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
       if (hh == 0) sh.rs[wave][l32] = (a.rscale && my_grow >= 0) ? a.rscale[my_grow] : 1.0f;
     }
     // Copy k: rows 4k .. 4k + 3 of the wave; lane -> row 4k + lane / 16, LDS slot lane % 16,
-    // which holds the row's piece (lane % 16) ^ 4 (k & 1); rows past the slots read as zero.
+    // which holds the row's piece (lane % 16) ^ tile128_swz(row); rows past the slots read as zero.
     auto copy_tile = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int rr = 4 * k + (lane >> 4);
-        const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ (4 * (k & 1)));
+        const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ tile128_swz(rr));
         uint32_t voff;
         if constexpr (RT) {
           const int32_t gr = __shfl(my_grow, rr);
@@ -1693,7 +1693,7 @@ __global__ void __launch_bounds__(512) bwd_chan_d128_kernel(BwdChanArgs a, int32
       }
     };
     auto at = [&](int r, int c) {
-      return xlds + 2u * static_cast<uint32_t>(r * kB2D + (c ^ (32 * ((r >> 2) & 1))));
+      return xlds + 2u * static_cast<uint32_t>(r * kB2D + (c ^ (8 * tile128_swz(r))));
     };
     // Lane (slot l32, hh) of K-step operand ks holds channels 16 ks + 4 hh + (0..3, 8..11).
     const int64_t my_row = row0 + l32;

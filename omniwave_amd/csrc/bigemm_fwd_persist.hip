@@ -26,8 +26,8 @@
 //   * the output: delta = A_o W, rounded (and scaled by the drop-path factor), is staged per
 //     wave in the chunk buffers that the loop no longer reads, and stored as 16-byte row pieces
 //     with the residual round(x + delta), x from the tile.
-// Tile layout: row r holds its 128 channels, 16-byte piece p at slot p ^ (4 ((r >> 2) & 1)), so
-// the two lane halves of a token-side column read (rows 4 apart) hit different LDS banks.
+// Tile layout: row r holds its 128 channels, 16-byte piece p at slot p ^ tile128_swz(r), so
+// the rows of a token-side transposed read hit different LDS banks.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -90,8 +90,8 @@ __device__ __forceinline__ void strided_write(uint16_t* xw, int lane, int res, i
   constexpr int M = 8 / NS;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const int r = 4 * (p0 + p) + (lane >> 4);  // row of the wave; swizzle bit (r >> 2) & 1 = (p0 + p) & 1
-    const int sw = 32 * ((p0 + p) & 1);
+    const int r = 4 * (p0 + p) + (lane >> 4);  // row of the wave
+    const int sw = 8 * tile128_swz(r);          // the swizzle in channels
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int c0 = M * ((lane & 15) + 16 * j);
@@ -198,14 +198,14 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     }
   };
   // This wave's 32 tile rows of unit u (slot s): copy k covers rows 4k .. 4k + 3, lane -> row
-  // 4k + lane / 16, slot lane % 16, which holds the row's piece (lane % 16) ^ (4 (k & 1)).
+  // 4k + lane / 16, slot lane % 16, which holds the row's piece (lane % 16) ^ tile128_swz(row).
   auto issue_tile = [&](int32_t u, int s) {
     const uint32_t col0 = static_cast<uint32_t>((u % a.q_c) * kD * 2);
 #pragma unroll
     for (int k = 0; k < kTileOps; ++k) {
       const int r = 32 * wave + 4 * k + (lane >> 4);
       const int32_t id = sh.rowid[s][r];
-      const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ (4 * (k & 1)));
+      const uint32_t piece = static_cast<uint32_t>((lane & 15) ^ tile128_swz(r));
       const uint32_t voff = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) + col0 + 16u * piece
                                     : kOffOut;
       tile_copy(rx, voff, lds_addr(&sh.x[(32 * wave_u + 4 * k) * kD]));
@@ -329,10 +329,10 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       // The token operands are read per unit from LDS rather than kept live through the loop.
       const u32x4 fAu = sh.tok_ops[0][lane];
       const u32x4 fAv = sh.tok_ops[1][lane];
-      // X^T operands by transposed reads; channel c of tile row r sits at c ^ (32 ((r >> 2) & 1)).
+      // X^T operands by transposed reads; channel c of tile row r sits at c ^ 8 tile128_swz(r).
       const uint32_t xb = lds_addr(sh.x) + 2u * static_cast<uint32_t>(32 * kD * wave);
       pair_xt_tr<kKS>(
-          [&](int r, int c) { return xb + 2u * static_cast<uint32_t>(r * kD + (c ^ (32 * ((r >> 2) & 1)))); }, lane,
+          [&](int r, int c) { return xb + 2u * static_cast<uint32_t>(r * kD + (c ^ (8 * tile128_swz(r)))); }, lane,
           xk);
       u32x4 bu = fAu, bv = fAv;
       if (a.norm != kNormNone) {
@@ -580,12 +580,12 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         *reinterpret_cast<u32x2*>(&st[l32 * kLdo + 32 * mb + 8 * q + 4 * hh]) = u32x2{v0, v1};
       }
     // Pass k covers piece lane % 16 of rows lane / 16 + 4 k of the wave (tile slot of the piece:
-    // piece ^ 4 (k & 1)).
+    // piece ^ tile128_swz(row)).
     u32x4 xv[8], val[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int rr = (lane >> 4) + 4 * k;
-      xv[k] = *reinterpret_cast<const u32x4*>(&sh.x[(32 * wave + rr) * kD + ((piece ^ (4 * (k & 1))) * 8)]);
+      xv[k] = *reinterpret_cast<const u32x4*>(&sh.x[(32 * wave + rr) * kD + ((piece ^ tile128_swz(rr)) * 8)]);
     }
     wave_lds_sync();
 #pragma unroll

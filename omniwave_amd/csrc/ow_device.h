@@ -392,6 +392,11 @@ __device__ __forceinline__ void pair_token_side_mma(const u32x4 (&xk)[KS / 2][2]
   }
 }
 
+// 16-byte piece swizzle of a [rows][128] 16-bit tile (256-byte rows): piece p of row r sits at
+// slot p ^ tile128_swz(r).  The four rows that a 16-lane transposed read (pair_xt_tr) or a 1 KB
+// copy covers then fall in four different 64-byte bank windows.
+__device__ __forceinline__ int tile128_swz(int r) { return 4 * (r & 3); }
+
 // X^T operands of a pair (as pair_token_side reads them) by transposed LDS reads
 // (ds_read_b64_tr_b16): in each group of 16 lanes, lane L reads the 8 bytes of row r0 + L / 4 at
 // channel c0 + 4 (L % 4), and lane i of the group then holds channel c0 + i of rows r0 .. r0 + 3
