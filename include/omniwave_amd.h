@@ -450,6 +450,13 @@ int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t wei
                   const float* dbv, const float* dbo, float* g_bu, float* g_bv, float* g_bo,
                   float* g_gamma, float* g_norm_weight, void* stream);
 
+/* The backward's small parameters (norm weight, gamma, A_u, A_v, A_o; the reference's autograd
+ * takes them in fp32, omniweave/ops/triton.py:256-292) converted into one fp32 buffer in one
+ * launch: source k (dtype[k] in OW_DTYPE_*, count[k] values) goes to dst at the sum of the
+ * counts before it.  1 <= n <= 8. */
+int ow_small_to_f32(const void* const* src, const int32_t* dtype, const int64_t* count, int32_t n, float* dst,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -237,12 +237,19 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
     if any(w.dtype != wdtype for w in ws) or wdtype not in _DTYPE_CODE:
         wdtype = torch.float32
         ws = [w.float() for w in ws]
-    # The small fp32 operands (norm weight, gamma, token matrices): one concatenation and one
-    # cast instead of a conversion kernel each, when they share a 16-bit dtype.
+    # The small fp32 operands (norm weight, gamma, token matrices): one conversion kernel into
+    # one buffer (ow_small_to_f32).
     small = ([norm_weight] if fuse_norm else []) + [gamma, a_u, a_v, a_o]
-    if len({t.dtype for t in small}) == 1 and small[0].dtype != torch.float32 and all(t.device == dev for t in small):
-        flat = torch.cat([t.detach().reshape(-1) for t in small]).to(torch.float32)
-        parts = list(torch.split(flat, [t.numel() for t in small]))
+    if all(t.device == dev and t.dtype in _DTYPE_CODE for t in small):
+        srcs = [t.detach().contiguous() for t in small]
+        counts = [t.numel() for t in srcs]
+        flat = torch.empty(sum(counts), dtype=torch.float32, device=dev)
+        n = len(srcs)
+        _native.check(lib.ow_small_to_f32((ctypes.c_void_p * n)(*[t.data_ptr() for t in srcs]),
+                                          (ctypes.c_int32 * n)(*[_DTYPE_CODE[t.dtype] for t in srcs]),
+                                          (ctypes.c_int64 * n)(*counts), n, flat.data_ptr(), _stream(dev)),
+                      "ow_small_to_f32")
+        parts = list(torch.split(flat, counts))
         nw = parts.pop(0) if fuse_norm else None
         gm, au, av, ao = parts[0], parts[1].view(16, 16), parts[2].view(16, 16), parts[3].view(16, 16)
     else:

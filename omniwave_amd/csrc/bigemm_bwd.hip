@@ -331,37 +331,122 @@ struct ParamArgs {
   int32_t wdtype, q_c, d, rd, channels;
 };
 
-// One wave per (q, c): the folded gradients mapped back to the parameters, the per-channel
-// sums over the expanded dim reduced across the wave.
-__global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (i >= static_cast<int64_t>(a.q_c) * a.d) return;
-  const int32_t c = static_cast<int32_t>(i % a.d);
-  const int32_t q = static_cast<int32_t>(i / a.d);
-  const int32_t ch = a.chan[q * a.d + c];
+// The folded gradients mapped back to the parameters.  Blocks [0, n_a): one wave per (q, c):
+// dB_u, dB_v and the norm-weight gradient (a sum over the expanded dimension of the [d][rd] rows,
+// reduced across the wave).  Blocks [n_a, ..): 16 channels of one group per block, thread t
+// taking channel 16 b + t % 16 and every 16th expanded row from t / 16, so that the [rd][d]
+// rows of dB_o'' and B_o are read 16 channels at a time: dB_o and the gamma gradient, the 16
+// partial sums of a channel added in a fixed order.
+constexpr int kParamC = 16;  // channels per dB_o block
+__global__ void __launch_bounds__(256) bwd_params_kernel(ParamArgs a, int32_t n_a) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (static_cast<int32_t>(blockIdx.x) < n_a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + wv;
+    if (i >= static_cast<int64_t>(a.q_c) * a.d) return;
+    const int32_t c = static_cast<int32_t>(i % a.d);
+    const int32_t q = static_cast<int32_t>(i / a.d);
+    const int32_t ch = a.chan[q * a.d + c];
+    const bool ok = ch >= 0 && ch < a.channels;
+    const float w = ok ? (a.norm_w ? a.norm_w[ch] : 1.0f) : 0.0f;
+    // Every load of the row is issued before the stores (rd <= 4 * 64 here: the loop runs once
+    // for rd in {128, 256}).
+    const float* __restrict__ dbu = a.dbu;
+    const float* __restrict__ dbv = a.dbv;
+    float* __restrict__ gbu = a.g_bu;
+    float* __restrict__ gbv = a.g_bv;
+    float sum_w = 0.0f;
+    for (int32_t e0 = 0; e0 < a.rd; e0 += 4 * 64) {
+      float du[4], dv[4], bu[4], bv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int32_t e = e0 + 64 * k + lane;
+        const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;
+        const bool in = e < a.rd;
+        du[k] = in ? dbu[cd] : 0.0f;
+        dv[k] = in ? dbv[cd] : 0.0f;
+        bu[k] = in ? load_any(a.b_u, cd, a.wdtype) : 0.0f;
+        bv[k] = in ? load_any(a.b_v, cd, a.wdtype) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int32_t e = e0 + 64 * k + lane;
+        const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;
+        if (e < a.rd) {
+          gbu[cd] = du[k] * kNegLog2e * w;
+          gbv[cd] = dv[k] * kNegLn2 * w;
+        }
+        sum_w += du[k] * kNegLog2e * bu[k] + dv[k] * kNegLn2 * bv[k];
+      }
+    }
+    for (int m = 32; m > 0; m >>= 1) sum_w += __shfl_xor(sum_w, m);
+    if (ok && lane == 0 && a.g_norm_w) a.g_norm_w[ch] = sum_w;
+    return;
+  }
+  __shared__ float part[256 / kParamC][kParamC];
+  const int32_t cblocks = (a.d + kParamC - 1) / kParamC;
+  const int32_t b = static_cast<int32_t>(blockIdx.x) - n_a;
+  const int32_t q = b / cblocks;
+  const int32_t c = (b % cblocks) * kParamC + (threadIdx.x % kParamC);
+  const int32_t eg = threadIdx.x / kParamC;  // 0 .. 15
+  const bool in = c < a.d;
+  const int32_t ch = in ? a.chan[q * a.d + c] : -1;
   const bool ok = ch >= 0 && ch < a.channels;
-  const float w = ok ? (a.norm_w ? a.norm_w[ch] : 1.0f) : 0.0f;
   const float gm = ok ? (a.gamma ? a.gamma[ch] : 1.0f) : 0.0f;
-  float sum_w = 0.0f, sum_g = 0.0f;
-  for (int32_t e = lane; e < a.rd; e += 64) {
-    const int64_t cd = (static_cast<int64_t>(q) * a.d + c) * a.rd + e;
-    const int64_t ec = (static_cast<int64_t>(q) * a.rd + e) * a.d + c;
-    const float du = a.dbu[cd], dv = a.dbv[cd], dob = a.dbo[ec];
-    a.g_bu[cd] = du * kNegLog2e * w;
-    a.g_bv[cd] = dv * kNegLn2 * w;
-    a.g_bo[ec] = dob * gm;
-    sum_w += du * kNegLog2e * load_any(a.b_u, cd, a.wdtype) + dv * kNegLn2 * load_any(a.b_v, cd, a.wdtype);
-    sum_g += dob * load_any(a.b_o, ec, a.wdtype);
+  const float* __restrict__ dbo = a.dbo;
+  float* __restrict__ gbo = a.g_bo;
+  float sum_g = 0.0f;
+  if (in) {
+    constexpr int kBatch = 8;
+    for (int32_t e0 = eg; e0 < a.rd; e0 += kBatch * (256 / kParamC)) {
+      float dob[kBatch], bo[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int32_t e = e0 + k * (256 / kParamC);
+        const int64_t ec = (static_cast<int64_t>(q) * a.rd + e) * a.d + c;
+        dob[k] = e < a.rd ? dbo[ec] : 0.0f;
+        bo[k] = e < a.rd ? load_any(a.b_o, ec, a.wdtype) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int32_t e = e0 + k * (256 / kParamC);
+        if (e < a.rd) gbo[(static_cast<int64_t>(q) * a.rd + e) * a.d + c] = dob[k] * gm;
+        sum_g += dob[k] * bo[k];
+      }
+    }
   }
-  for (int m = 32; m > 0; m >>= 1) {
-    sum_w += __shfl_xor(sum_w, m);
-    sum_g += __shfl_xor(sum_g, m);
+  part[eg][threadIdx.x % kParamC] = sum_g;
+  __syncthreads();
+  if (threadIdx.x < kParamC && ok) {
+    float v = part[0][threadIdx.x];
+#pragma unroll
+    for (int k = 1; k < 256 / kParamC; ++k) v += part[k][threadIdx.x];
+    a.g_gamma[ch] = v;
   }
-  if (ok && lane == 0) {
-    a.g_gamma[ch] = sum_g;
-    if (a.g_norm_w) a.g_norm_w[ch] = sum_w;
-  }
+}
+
+// The small parameters of the backward (norm weight, gamma, the token matrices) as one fp32
+// buffer: source k (dtype[k], off[k + 1] - off[k] values) into dst[off[k] ..].
+struct SmallF32Args {
+  const void* src[8];
+  int32_t dtype[8];
+  int64_t off[9];
+  int32_t n;
+  float* dst;
+};
+__global__ void __launch_bounds__(256) small_to_f32_kernel(SmallF32Args a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= a.off[a.n]) return;
+  const void* src = a.src[0];
+  int32_t dt = a.dtype[0];
+  int64_t o = 0;
+#pragma unroll
+  for (int k = 1; k < 8; ++k)
+    if (k < a.n && i >= a.off[k]) {
+      src = a.src[k];
+      dt = a.dtype[k];
+      o = a.off[k];
+    }
+  a.dst[i] = load_any(src, i - o, dt);
 }
 
 // Token mixing per 16-row tile: out = M1 in1 (+ M2 in2), M* [16][16] fp32, in/out tiles
@@ -2900,6 +2985,34 @@ int ow_bwd_fused_routed(const void* x, const void* dy, const float* rscale, cons
   return ow::launch_bwd_fused<true>(a, grid, rd, dtype, static_cast<hipStream_t>(stream));
 }
 
+int ow_small_to_f32(const void* const* src, const int32_t* dtype, const int64_t* count, int32_t n, float* dst,
+                    void* stream) {
+  OW_CHECK_ARG(n >= 1 && n <= 8, "between 1 and 8 sources (got %d)", n);
+  OW_CHECK_ARG(src && dtype && count && dst, "argument pointer is NULL");
+  ow::SmallF32Args a{};
+  a.n = n;
+  a.dst = dst;
+  a.off[0] = 0;
+  for (int k = 0; k < n; ++k) {
+    OW_CHECK_ARG(dtype[k] >= OW_DTYPE_F32 && dtype[k] <= OW_DTYPE_F16, "unknown dtype %d of source %d", dtype[k], k);
+    OW_CHECK_ARG(count[k] >= 0, "bad count %lld of source %d", (long long)count[k], k);
+    OW_CHECK_ARG(src[k] || count[k] == 0, "source %d is NULL", k);
+    a.src[k] = src[k];
+    a.dtype[k] = dtype[k];
+    a.off[k + 1] = a.off[k] + count[k];
+  }
+  for (int k = n + 1; k < 9; ++k) a.off[k] = a.off[n];
+  const int64_t total = a.off[n];
+  if (total > 0) {
+    OW_CHECK_ARG(total < (int64_t(1) << 31), "too many values (%lld)", (long long)total);
+    hipLaunchKernelGGL(ow::small_to_f32_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+    if (int rc = ow::hip_status(hipGetLastError(), "small_to_f32_kernel launch")) return rc;
+  }
+  ow::clear_error();
+  return OW_OK;
+}
+
 int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t weight_dtype, const float* norm_weight,
                   const float* gamma, const int32_t* channel_index, int32_t channels, int32_t q_c, int32_t d, int32_t rd,
                   const float* dbu, const float* dbv, const float* dbo, float* g_bu, float* g_bv, float* g_bo,
@@ -2912,8 +3025,11 @@ int ow_bwd_params(const void* b_u, const void* b_v, const void* b_o, int32_t wei
   ow::ParamArgs a{b_u, b_v, b_o, norm_weight, gamma, channel_index, dbu, dbv, dbo, g_bu, g_bv, g_bo, g_gamma,
                   g_norm_weight, weight_dtype, q_c, d, rd, channels};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>((static_cast<int64_t>(q_c) * d + 3) / 4);
-  hipLaunchKernelGGL(ow::bwd_params_kernel, dim3(blocks), dim3(256), 0, s, a);
+  const int64_t n_a = (static_cast<int64_t>(q_c) * d + 3) / 4;
+  const int64_t n_b = static_cast<int64_t>(q_c) * ((d + ow::kParamC - 1) / ow::kParamC);
+  OW_CHECK_ARG(n_a + n_b < (int64_t(1) << 31), "too many channels (q_c=%d d=%d)", q_c, d);
+  hipLaunchKernelGGL(ow::bwd_params_kernel, dim3(static_cast<unsigned>(n_a + n_b)), dim3(256), 0, s, a,
+                     static_cast<int32_t>(n_a));
   if (int rc = ow::hip_status(hipGetLastError(), "bwd_params_kernel launch")) return rc;
   ow::clear_error();
   return OW_OK;

@@ -5,11 +5,12 @@ group, the sums over slots that the reference's autograd forms inside its GEMMs,
 omniweave/ops/triton.py:256-292) is compared with float64 products of the same 16-bit
 intermediates: the products of 16-bit values are exact in fp32, so only the fp32 summation
 order differs (rel-L2 <= 1e-5).  ``ow_sum_rows`` is compared with a float64 sum and must give
-identical bits on a second call.
+identical bits on a second call; ``ow_small_to_f32`` equals torch's (exact) widening conversion.
 """
 
 from __future__ import annotations
 
+import ctypes
 import sys
 
 import pytest
@@ -98,3 +99,23 @@ def test_sum_rows_matches_float64_and_repeats_bitwise(rows, cols) -> None:
     err = rel_l2(outs[0], want)
     assert err <= 1e-6, f"rel-L2 {err:.2e}"
     assert torch.equal(outs[0], outs[1]), "two calls on the same input differ"
+
+
+def test_small_to_f32_converts_each_source_exactly() -> None:
+    """ow_small_to_f32: bf16, fp16 and fp32 sources of ragged lengths into one fp32 buffer,
+    equal to torch's conversion of each (a widening conversion: exact)."""
+    announce("small_to_f32 bf16 / fp16 / fp32 sources")
+    gen = torch.Generator().manual_seed(5)
+    srcs = [torch.randn(n, generator=gen).to(dt).to(DEV)
+            for n, dt in ((7, torch.bfloat16), (256, torch.float16), (33, torch.float32), (1, torch.bfloat16))]
+    lib = _native.lib()
+    n = len(srcs)
+    out = torch.full((sum(t.numel() for t in srcs),), float("nan"), device=DEV)
+    code = {torch.bfloat16: _native.OW_DTYPE_BF16, torch.float16: _native.OW_DTYPE_F16,
+            torch.float32: _native.OW_DTYPE_F32}
+    _native.check(lib.ow_small_to_f32((ctypes.c_void_p * n)(*[t.data_ptr() for t in srcs]),
+                                      (ctypes.c_int32 * n)(*[code[t.dtype] for t in srcs]),
+                                      (ctypes.c_int64 * n)(*[t.numel() for t in srcs]), n, out.data_ptr(),
+                                      torch.cuda.current_stream(DEV).cuda_stream), "ow_small_to_f32")
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), torch.cat([t.float() for t in srcs]).cpu())

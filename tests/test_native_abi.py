@@ -204,6 +204,20 @@ def test_bwd_channel_entries_reject_bad_arguments_without_touching_the_gpu() -> 
     assert lib.ow_sum_rows(P, 4, 8, ctypes.c_void_p(20), None) == 1 and b"aligned" in lib.ow_last_error()
     assert lib.ow_sum_rows(P, 4, 0, P, None) == 0  # no columns: nothing launched
 
+    # The small-parameter conversion.
+    srcs = (ctypes.c_void_p * 2)(16, 32)
+    dts = (ctypes.c_int32 * 2)(bf16, _native.OW_DTYPE_F32)
+    cnt = (ctypes.c_int64 * 2)(4, 8)
+    assert lib.ow_small_to_f32(srcs, dts, cnt, 0, P, None) == 1 and b"between 1 and 8" in lib.ow_last_error()
+    assert lib.ow_small_to_f32(srcs, dts, cnt, 9, P, None) == 1
+    assert lib.ow_small_to_f32(srcs, (ctypes.c_int32 * 2)(bf16, 7), cnt, 2, P, None) == 1
+    assert b"unknown dtype" in lib.ow_last_error()
+    assert lib.ow_small_to_f32(srcs, dts, (ctypes.c_int64 * 2)(4, -1), 2, P, None) == 1
+    assert lib.ow_small_to_f32((ctypes.c_void_p * 2)(None, 32), dts, cnt, 2, P, None) == 1
+    assert b"source 0 is NULL" in lib.ow_last_error()
+    assert lib.ow_small_to_f32(srcs, dts, cnt, 2, None, None) == 1 and b"NULL" in lib.ow_last_error()
+    assert lib.ow_small_to_f32((ctypes.c_void_p * 2)(None, None), dts, (ctypes.c_int64 * 2)(0, 0), 2, P, None) == 0
+
 
 def test_hip_is_supported_reasons_on_cpu() -> None:
     plan = build_route_plan(14, 14, 512, 16, 128, "local")
