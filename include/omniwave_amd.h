@@ -221,6 +221,21 @@ int ow_bigemm_fwd_chain(const void* x, void* out, float eps,
                         int32_t* stats_written, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ow_bigemm_fwd (drop_scale NULL) or ow_bigemm_fwd_drop for training, also handing the RMSNorm
+ * row scales r = 1 / sqrt(mean_c x^2 + eps) that the launch applied to the backward (the
+ * reference's autograd keeps its normalised activations, omniweave/models/block.py:83-108, and
+ * ow_bwd_rmsnorm / ow_bwd_fused_routed need r): where the launch forms every row's scale in one
+ * place -- the statistics pass, or the d = 64 wave kernel -- it writes them to row_scale
+ * ([batch * H * W] fp32, device) and sets *scales_written to 1; otherwise *scales_written is 0
+ * and the caller forms them with ow_rms_scale.  Needs OW_FUSE_NORM for any scales to be written.
+ */
+int ow_bigemm_fwd_scales(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                         const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan,
+                         int32_t batch, int32_t rd, int32_t dtype, int32_t flags, const float* drop_scale,
+                         float* row_scale, int32_t* scales_written, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
  * ow_bigemm_fwd for training with per-sample drop-path (stochastic depth,
  * omniweave/models/block.py:99-107): drop_scale [batch] (fp32, device) multiplies each image's
  * rounded delta before the residual, out = round(x + round(round(delta) * drop_scale[b])) (or

@@ -81,6 +81,16 @@ _SIGNATURES = {
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ],
     ),
+    "ow_bigemm_fwd_scales": (
+        ctypes.c_int,
+        [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.POINTER(OwPlan), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32), ctypes.c_void_p,
+            ctypes.c_size_t, ctypes.c_void_p,
+        ],
+    ),
     "ow_bigemm_fwd_drop": (
         ctypes.c_int,
         [

@@ -154,7 +154,7 @@ def batch_chunks(batch: int, limit: int | None, q_s: int) -> list[tuple[int, int
 
 def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
                     a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float,
-                    drop_scale: Tensor | None = None):
+                    drop_scale: Tensor | None = None, row_scale: Tensor | None = None):
     """Gradients of ``bigemm_fwd(x, norm_weight, gamma, a_u, .., b_o, plan, flags, eps, drop_scale)``.
 
     Returns ``(dx, d_norm_weight, d_gamma, d_a_u, d_a_v, d_a_o, d_b_u, d_b_v, d_b_o)``, each in
@@ -162,20 +162,25 @@ def bigemm_backward(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: 
     (per-image drop-path factors of the forward) the delta branch receives the upstream
     gradient scaled per image and rounded (``ow_scale_samples``), the residual the plain one.
     Batches beyond ``native_batch_limit`` run in chunks: dx per chunk, the parameter gradients
-    summed over chunks in fp32 before the cast.
+    summed over chunks in fp32 before the cast.  ``row_scale`` ([B * H * W] fp32, or None): the
+    RMSNorm row scales the forward applied (``ow_bigemm_fwd_scales``), else formed here.
     """
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
     q_c, d, rd = b_u.shape
     chunks = batch_chunks(x.shape[0], native_batch_limit(x.dtype, plan, q_c, d, rd),
                           int(plan.token_indices.shape[0]))
+    n_tok = plan.height * plan.width
+    if row_scale is not None and row_scale.numel() != x.shape[0] * n_tok:
+        row_scale = None
     if len(chunks) == 1:
         dx, g_all = _backward_once(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan, flags, eps,
-                                   drop_scale)
+                                   drop_scale, row_scale)
     else:
         dxs, g_all = [], None
         for s, e in chunks:
             dx_c, g_c = _backward_once(grad[s:e], x[s:e], norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan,
-                                       flags, eps, drop_scale[s:e] if drop_scale is not None else None)
+                                       flags, eps, drop_scale[s:e] if drop_scale is not None else None,
+                                       row_scale[s * n_tok:e * n_tok] if row_scale is not None else None)
             dxs.append(dx_c)
             g_all = g_c if g_all is None else g_all.add_(g_c)
         dx = torch.cat(dxs)
@@ -211,7 +216,7 @@ def _cast_grads(dx, g_all, fuse_norm, channels, q_c, d, rd, norm_weight, gamma, 
 
 def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: Tensor, a_u: Tensor, a_v: Tensor,
                    a_o: Tensor, b_u: Tensor, b_v: Tensor, b_o: Tensor, plan: RoutePlan, flags: int, eps: float,
-                   drop_scale: Tensor | None):
+                   drop_scale: Tensor | None, row_scale: Tensor | None = None):
     """One pass of the kernels over the whole batch: dx and the fp32 parameter-gradient buffer
     (layout of ``_cast_grads``)."""
     lib = _native.lib()
@@ -271,7 +276,9 @@ def _backward_once(grad: Tensor, x: Tensor, norm_weight: Tensor | None, gamma: T
             _native.check(lib.ow_scale_samples(grad.data_ptr(), scale.data_ptr(), grad_delta.data_ptr(), batch,
                                                grad.numel() // max(batch, 1), code, stream), "ow_scale_samples")
         rscale = None
-        if fuse_norm:
+        if fuse_norm and row_scale is not None:
+            rscale = row_scale.to(device=dev, dtype=torch.float32).contiguous()  # the forward's own scales
+        elif fuse_norm:
             rscale = torch.empty(n_rows, dtype=torch.float32, device=dev)
             _native.check(lib.ow_rms_scale(x.data_ptr(), rscale.data_ptr(), n_rows, plan.channels, eps, code,
                                            stream), "ow_rms_scale")

@@ -1290,8 +1290,10 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
                             const OwPlan* plan, int32_t batch, int32_t rd, int32_t dtype, int32_t flags,
                             const float* stats_in, int32_t stats_in_parts, float* stats_out,
                             int32_t* stats_written, const float* drop_scale, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            size_t workspace_bytes, void* stream, float* scale_out = nullptr,
+                            int32_t* scale_written = nullptr) {
   if (stats_written) *stats_written = 0;
+  if (scale_written) *scale_written = 0;
   int32_t q_s = 0, q_c = 0;
   if (int rc = ow_plan_dims(plan, &q_s, &q_c)) return rc;
   OW_CHECK_ARG(batch >= 0, "batch must be >= 0 (got %d)", batch);
@@ -1326,12 +1328,20 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   const bool resident = path.resident && rd == 2 * d;
   const int32_t mode = path.mode;
   float* scale = nullptr;
+  // scale_out (ow_bigemm_fwd_scales): the row scales go to the caller's buffer where the launch
+  // forms them in one place (the statistics pass, or the wave kernel below).
+  const bool want_scales = scale_out && norm && !out_rows;
   if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr, batch)) {
-    const size_t need = ow_fwd_workspace_bytes(plan, batch, flags);
-    OW_CHECK_ARG(workspace && workspace_bytes >= need, "workspace holds %zu bytes; %zu needed", workspace_bytes,
-                 need);
-    scale = static_cast<float*>(workspace);
+    if (want_scales) {
+      scale = scale_out;
+    } else {
+      const size_t need = ow_fwd_workspace_bytes(plan, batch, flags);
+      OW_CHECK_ARG(workspace && workspace_bytes >= need, "workspace holds %zu bytes; %zu needed", workspace_bytes,
+                   need);
+      scale = static_cast<float*>(workspace);
+    }
     if (int rc = ow_rms_scale(x, scale, static_cast<int64_t>(batch) * n, c, eps, dtype, stream)) return rc;
+    if (want_scales) *scale_written = 1;
   }
 
   if (fp32) {
@@ -1361,9 +1371,13 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.eps = eps;
     r.drop_scale = drop_scale;
     const int64_t x_elems = static_cast<int64_t>(batch) * n * c;
-    const int rc = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems)
-                       ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s)
-                       : ow::launch_fwd_resident(r, dtype, s);
+    const bool wave = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems);
+    if (wave && want_scales) {
+      r.rs_out = scale_out;
+      *scale_written = 1;
+    }
+    const int rc = wave ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s) : ow::launch_fwd_resident(r, dtype, s);
+    if (rc != OW_OK && scale_written) *scale_written = 0;
     if (rc == OW_OK) ow::clear_error();
     return rc;
   }
@@ -1494,6 +1508,19 @@ int ow_bigemm_fwd_chain(const void* x, void* out, float eps, const void* packed,
   return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, out_rows, plan, batch, rd,
                           dtype, flags, stats_in, stats_in_parts, stats_out, stats_written, nullptr, workspace,
                           workspace_bytes, stream);
+}
+
+int ow_bigemm_fwd_scales(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,
+                         const int32_t* token_index, const int32_t* channel_index, const OwPlan* plan,
+                         int32_t batch, int32_t rd, int32_t dtype, int32_t flags, const float* drop_scale,
+                         float* row_scale, int32_t* scales_written, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  OW_CHECK_ARG(scales_written, "scales_written is NULL");
+  *scales_written = 0;
+  OW_CHECK_ARG(row_scale || batch == 0, "row_scale is NULL");
+  return bigemm_fwd_entry(x, out, eps, packed, packed_bytes, token_index, channel_index, nullptr, plan, batch, rd,
+                          dtype, flags, nullptr, 0, nullptr, nullptr, drop_scale, workspace, workspace_bytes, stream,
+                          row_scale, scales_written);
 }
 
 int ow_bigemm_fwd_drop(const void* x, void* out, float eps, const void* packed, size_t packed_bytes,

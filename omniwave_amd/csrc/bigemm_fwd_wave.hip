@@ -263,8 +263,12 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
     }
     if (hh == 0) {
-      rsc[l32] = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
+      const float sc = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
+      rsc[l32] = sc;
       rows[l32] = out_c;
+      // The row scales for the backward: every group's waves form the same value, group 0's
+      // write it (out_c is the input row without an output-row table).
+      if (a.rs_out && g == 0 && out_c >= 0) a.rs_out[out_c] = sc;
     }
     if constexpr (STREAM)
       ssq = 0.0f;  // the next pair's batches are read during the chunk loop

@@ -758,6 +758,7 @@ struct ResidentArgs {
   int32_t residual; // write x + delta instead of delta
   float eps;
   const float* drop_scale;  // [batch] per-image multiplier of the rounded delta; NULL: none
+  float* rs_out;            // wave kernel: the RMSNorm scale of every input row it normalises; NULL: none
 };
 
 bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);

@@ -203,10 +203,14 @@ def bigemm_fwd(
     flags: int,
     eps: float,
     drop_scale: Tensor | None,
-) -> Tensor:
-    """delta (flags=0) or x + delta with the block's RMSNorm fused (flags=3), NHWC; flag
-    OW_FUSE_FP8 selects the fp8 channel side.  ``drop_scale`` ([B] fp32 or None): per-image
-    multiplier of the rounded delta, the drop-path of training (``ow_bigemm_fwd_drop``)."""
+    want_scales: bool,
+) -> tuple[Tensor, Tensor]:
+    """(out, row_scale): out = delta (flags=0) or x + delta with the block's RMSNorm fused
+    (flags=3), NHWC; flag OW_FUSE_FP8 selects the fp8 channel side.  ``drop_scale`` ([B] fp32 or
+    None): per-image multiplier of the rounded delta, the drop-path of training.  With
+    ``want_scales`` and the RMSNorm fused, row_scale is [B * H * W] fp32, the RMSNorm scale of
+    every row of x, which the backward needs (``ow_bigemm_fwd_scales``: the forward's own values
+    where its kernel forms them in one place, else ``ow_rms_scale``); otherwise it is empty."""
     plan = _plan_from_desc(plan_desc)
     x = x.contiguous()
     fuse_norm = bool(flags & _native.OW_FUSE_NORM)
@@ -223,15 +227,26 @@ def bigemm_fwd(
     workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
     common = (x.data_ptr(), out.data_ptr(), eps, packed.data_ptr(), packed.numel(), tok.data_ptr(), ch.data_ptr(),
               ctypes.byref(oplan), x.shape[0], b_u.shape[2], _DTYPE_CODE[x.dtype], flags)
+    n_rows = x.shape[0] * plan.height * plan.width
+    scales = torch.empty(n_rows if (want_scales and fuse_norm) else 0, dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        if drop_scale is None:
+        if scales.numel():
+            written = ctypes.c_int32(0)
+            scale = _drop_scale_arg(drop_scale, x) if drop_scale is not None else None
+            _native.check(lib.ow_bigemm_fwd_scales(*common, scale.data_ptr() if scale is not None else None,
+                                                   scales.data_ptr(), ctypes.byref(written), workspace.data_ptr(),
+                                                   ws_bytes, _stream_ptr(x.device)), "ow_bigemm_fwd_scales")
+            if not written.value:
+                _native.check(lib.ow_rms_scale(x.data_ptr(), scales.data_ptr(), n_rows, plan.channels, eps,
+                                               _DTYPE_CODE[x.dtype], _stream_ptr(x.device)), "ow_rms_scale")
+        elif drop_scale is None:
             _native.check(lib.ow_bigemm_fwd(*common, workspace.data_ptr(), ws_bytes, _stream_ptr(x.device)),
                           "ow_bigemm_fwd")
         else:
             scale = _drop_scale_arg(drop_scale, x)
             _native.check(lib.ow_bigemm_fwd_drop(*common, scale.data_ptr(), workspace.data_ptr(), ws_bytes,
                                                  _stream_ptr(x.device)), "ow_bigemm_fwd_drop")
-    return out
+    return out, scales
 
 
 def _drop_scale_arg(drop_scale: Tensor, x: Tensor) -> Tensor:
@@ -242,26 +257,36 @@ def _drop_scale_arg(drop_scale: Tensor, x: Tensor) -> Tensor:
 
 
 @bigemm_fwd.register_fake
-def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale):
-    return torch.empty_like(x, memory_format=torch.contiguous_format)
+def _bigemm_fwd_fake(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale,
+                     want_scales):
+    h, w = plan_desc[0], plan_desc[1]
+    n = x.shape[0] * h * w if (want_scales and flags & _native.OW_FUSE_NORM) else 0
+    return (torch.empty_like(x, memory_format=torch.contiguous_format),
+            torch.empty(n, dtype=torch.float32, device=x.device))
 
 
 def _bigemm_fwd_setup_context(ctx, inputs, output):
-    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale = inputs
-    ctx.save_for_backward(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale)
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, plan_desc, flags, eps, drop_scale, want_scales = inputs
+    _, scales = output
+    ctx.mark_non_differentiable(scales)
+    ctx.set_materialize_grads(False)  # no zero-filled gradient for the scales output
+    ctx.save_for_backward(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale, scales)
     ctx.plan_desc, ctx.flags, ctx.eps = list(plan_desc), int(flags), float(eps)
 
 
-def _bigemm_fwd_backward(ctx, grad):
+def _bigemm_fwd_backward(ctx, grad, grad_scales):
     from omniwave_amd.backward import bigemm_backward
 
     if ctx.flags & _native.OW_FUSE_FP8:
         raise NotImplementedError("the fp8 BiGEMM variant is inference-only (no backward)")
-    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale = ctx.saved_tensors
+    if grad is None:
+        return (None,) * 14
+    x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, drop_scale, scales = ctx.saved_tensors
     grads = bigemm_backward(grad, x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o,
-                            _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps, drop_scale=drop_scale)
+                            _plan_from_desc(ctx.plan_desc), ctx.flags, ctx.eps, drop_scale=drop_scale,
+                            row_scale=scales if scales.numel() else None)
     grads = tuple(g if need else None for g, need in zip(grads, ctx.needs_input_grad))
-    return grads + (None, None, None, None)
+    return grads + (None, None, None, None, None)
 
 
 bigemm_fwd.register_autograd(_bigemm_fwd_backward, setup_context=_bigemm_fwd_setup_context)
@@ -276,7 +301,7 @@ def _require(x, plan, b_u) -> None:
 def bigemm_delta_hip(*, x, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma) -> Tensor:
     """delta for pre-normalised x (omniweave/ops/reference.py:120-173 semantics)."""
     _require(x, plan, b_u)
-    return bigemm_fwd(x, None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), 0, 0.0, None)
+    return bigemm_fwd(x, None, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), 0, 0.0, None, False)[0]
 
 
 def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, eps: float = 1e-6,
@@ -292,8 +317,11 @@ def bigemm_block_hip(x, norm_weight, plan, a_u, a_v, a_o, b_u, b_v, b_o, gamma, 
     if fp8 and x.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError(f"hip backend not supported: the fp8 variant takes bf16 or fp16 activations, not {x.dtype}")
     flags = _native.OW_FUSE_NORM | (_native.OW_FUSE_RESIDUAL if residual else 0) | (_native.OW_FUSE_FP8 if fp8 else 0)
+    # The RMSNorm row scales are kept for the backward when one will run.
+    want_scales = (not fp8 and torch.is_grad_enabled()
+                   and any(t.requires_grad for t in (x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o)))
     return bigemm_fwd(x, norm_weight, gamma, a_u, a_v, a_o, b_u, b_v, b_o, _plan_desc(plan), flags, float(eps),
-                      drop_scale)
+                      drop_scale, want_scales)[0]
 
 
 def drop_path_scale(batch: int, drop_path_rate: float, dtype: torch.dtype, device) -> Tensor:

@@ -192,3 +192,41 @@ def test_backward_beyond_the_addressing_limit_runs_in_chunks() -> None:
     for k in NAMES + ["norm_weight"]:
         err = rel_l2(full[k], halves[0][k] + halves[1][k])
         assert err <= 1e-6, f"{k}: chunked gradient != sum of the chunks (rel-L2 {err:.2e})"
+
+
+SCALE_CASES = [  # (B, H, W, C, d, route, level): the wave kernel, the statistics pass, neither
+    ("wave", (2, 56, 56, 128, 64, "shifted", 0)),
+    ("statistics-pass", (2, 14, 14, 512, 128, "shifted", 0)),
+    ("resident-fallback", (2, 28, 28, 256, 64, "radix", 1)),
+]
+
+
+@pytest.mark.parametrize("name,case", SCALE_CASES, ids=[n for n, _ in SCALE_CASES])
+def test_forward_hands_its_row_scales_to_the_backward(name, case) -> None:
+    """bigemm_fwd with want_scales returns every row's RMSNorm scale (the forward's own values,
+    or ow_rms_scale's where the kernel does not form them in one place), equal to a separate
+    ow_rms_scale pass to within the fp32 summation order, and the same output bits as without."""
+    import ctypes
+    from omniwave_amd import _native
+    from omniwave_amd.hip import _plan_desc
+
+    b, h, w, c, d, route, level = case
+    announce(f"forward row scales {name} B={b} {h}x{w}x{c}")
+    plan, x, params, _ = make_case(b, h, w, c, d, route, level, torch.bfloat16, seed=6)
+    xs = x.to(DEV)
+    ps = {k: v.to(DEV) for k, v in params.items()}
+    args = (xs, ps["norm_weight"], ps["gamma"], ps["a_u"], ps["a_v"], ps["a_o"], ps["b_u"], ps["b_v"], ps["b_o"],
+            _plan_desc(plan), _native.OW_FUSE_NORM | _native.OW_FUSE_RESIDUAL, 1e-6, None)
+    with torch.no_grad():
+        out_s, scales = torch.ops.omniwave_amd.bigemm_fwd(*args, True)
+        out, none = torch.ops.omniwave_amd.bigemm_fwd(*args, False)
+    rows = b * h * w
+    want = torch.empty(rows, dtype=torch.float32, device=DEV)
+    lib = _native.lib()
+    _native.check(lib.ow_rms_scale(xs.data_ptr(), want.data_ptr(), rows, c, ctypes.c_float(1e-6), _native.OW_DTYPE_BF16,
+                                   torch.cuda.current_stream(DEV).cuda_stream), "ow_rms_scale")
+    torch.cuda.synchronize()
+    assert none.numel() == 0 and scales.shape == (rows,)
+    err = float(((scales - want).abs() / want.abs()).max())
+    assert err <= 2e-6, f"{name}: row scales differ from the statistics pass by {err:.2e} (relative)"
+    assert torch.equal(out_s, out), f"{name}: output changed when the scales were requested"
