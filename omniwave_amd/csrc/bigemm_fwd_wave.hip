@@ -4,13 +4,16 @@
 //
 // Same math and operand packing as the other forward kernels (reference
 // omniweave/ops/reference.py:147-171; operand scheme in ow_device.h).  Organisation:
-//   * a workgroup owns one channel group g: its 48 KB of packed weights (4 chunks of the
-//     expanded dimension) are copied to LDS once and read from there by all four waves;
+//   * a workgroup of eight waves (one per CU) owns one channel group g: its 48 KB of packed
+//     weights (4 chunks of the expanded dimension) are copied to LDS once and read from there by
+//     all eight waves;
 //   * each wave processes whole units: the 32 tokens of a pair of token groups against all
 //     128 expanded rows of group g, so the token side is computed once per unit and no partial
 //     sums cross waves — no workgroup barrier after the weight copy;
 //   * the q_c workgroups of a team (logical ids q_c m .. q_c m + q_c - 1, one per channel group,
-//     placed on one XCD) walk the same pairs; each wave reads its pair's whole rows (the
+//     placed on one XCD) walk the same contiguous range of pairs, each wave drawing its next pair
+//     from its workgroup's LDS counter, so the two waves of a SIMD stay busy to the end whatever
+//     their issue priority; each wave reads its pair's whole rows (the
 //     RMSNorm statistics need all C channels) one pair ahead into registers, in the 32x32x16
 //     operand layout (lane = token, 8 channels per 16-byte piece), sums the squares with
 //     v_dot2_f32 and writes only its group's columns to its own LDS tile; the other group's
@@ -54,6 +57,7 @@ struct WaveLds {
   uint16_t tile[NW][32 * kLdt];    // per wave: the pair's rows, group columns
   float rsc[NW][32];               // per wave: RMSNorm scale of each token of the pair
   int32_t rows[NW][32];            // per wave: output row of each token (-1: not stored)
+  int32_t next_pair;               // per-group workgroups: the next pair of the team's range
 };
 
 // Logical workgroup id such that ids q_c m .. q_c m + q_c - 1 run on one XCD (workgroups are
@@ -85,6 +89,20 @@ __device__ __forceinline__ void pos_advance(PairPos& pos, int32_t step_b, int32_
     pos.s -= q_s;
     ++pos.b;
   }
+}
+
+// Position of pair p (wave-uniform).
+__device__ __forceinline__ PairPos pair_pos(int32_t p, int32_t q_s) {
+  const int32_t t = 2 * p, b = t / q_s;
+  return PairPos{b, t - b * q_s};
+}
+
+// One pair index of the workgroup's counter, taken by lane 0 (the value is read a unit later,
+// through readfirstlane, so the LDS atomic's latency is not waited on).
+__device__ __forceinline__ int32_t take_pair(int32_t* counter, int lane) {
+  int32_t v = 0;
+  if (lane == 0) v = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return v;
 }
 
 // Token-table entries of this lane's token (lane % 32) for the pair at `pos`: only loads here;
@@ -155,7 +173,7 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t ro
 }
 
 template <class Ty, int QC, bool OM, bool DROP, bool SG>
-__global__ void __attribute__((amdgpu_flat_work_group_size(SG ? 512 : 256, SG ? 512 : 256), amdgpu_waves_per_eu(2, 2)))
+__global__ void __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr int C = QC * kD;
   constexpr int NV = C / 16;  // row pieces per lane
@@ -168,8 +186,14 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr bool ROT = QC == 2 && !SG;
   static_assert(!SG || QC == 2, "interleaved channel groups: q_c = 2");
   // SG: waves 0-3 take group 0 and waves 4-7 group 1 of the same four pairs (wave w and w ^ 4
-  // share a pair), so the pair's output rows are put together in LDS and stored whole.
-  constexpr int NG = SG ? 2 : 1, NW = SG ? 8 : kWavesWg;
+  // share a pair), so the pair's output rows are put together in LDS and stored whole; every
+  // wave walks a fixed pair sequence (the workgroup's barriers keep the eight in step).
+  // Otherwise the eight waves of a workgroup all take group g and draw their pairs one at a time
+  // from the team's contiguous range [lo, hi) through an LDS counter: the hardware issues from
+  // the older of a SIMD's two waves first, so under a fixed split one wave of each SIMD finishes
+  // its share long before the other and leaves the SIMD with one wave; drawn pairs keep both
+  // busy to the end.
+  constexpr int NG = SG ? 2 : 1, NW = 8;
   __shared__ __attribute__((aligned(16))) WaveLds<NG, NW> sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -179,6 +203,8 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   const int n_team = SG ? static_cast<int>(gridDim.x) : static_cast<int>(gridDim.x) / QC;
   const int64_t stride = static_cast<int64_t>(n_team) * kWavesWg;
   const int64_t first = static_cast<int64_t>(team) * kWavesWg + (wave & (kWavesWg - 1));
+  const int32_t lo = static_cast<int32_t>(static_cast<int64_t>(team) * n_pairs / n_team);
+  const int32_t hi = static_cast<int32_t>(static_cast<int64_t>(team + 1) * n_pairs / n_team);
   // SG: the group's first channel (its residue mod q_c), wave-uniform.
   const int res = SG ? __builtin_amdgcn_readfirstlane(a.chan[g * kD]) & (QC - 1) : 0;
 
@@ -192,11 +218,12 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
           (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
   }
   if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
+  if (!SG && threadIdx.x == 0) sh.next_pair = lo;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   // After the kernel's first workgroup barrier; SG: every wave of the workgroup runs the same
   // number of units (the later barriers), those past the end on pad rows.
-  if ((SG ? static_cast<int64_t>(team) * kWavesWg : first) >= n_pairs) return;
+  if (SG ? static_cast<int64_t>(team) * kWavesWg >= n_pairs : lo >= hi) return;
 
   uint16_t* tile = sh.tile[wave];
   float* rsc = sh.rsc[wave];
@@ -211,11 +238,21 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   PairPos pos{static_cast<int32_t>(2 * first / a.q_s), 0};
   pos.s = static_cast<int32_t>(2 * first - static_cast<int64_t>(pos.b) * a.q_s);
   int64_t pos_pair = first;
+  // Drawn pairs: `pend` (lane 0) holds the index taken a unit before it is read; p_ent is the
+  // pair whose table entries next_entry returned last.
+  int32_t pend = 0, p_ent = 0;
+  if constexpr (!SG) pend = take_pair(&sh.next_pair, lane);
   auto next_entry = [&]() {
-    const TokEntry e = tok_entry<OM>(a, pos, pos_pair < n_pairs, l32);
-    pos_advance(pos, step_b, step_s, a.q_s);
-    pos_pair += stride;
-    return e;
+    if constexpr (SG) {
+      const TokEntry e = tok_entry<OM>(a, pos, pos_pair < n_pairs, l32);
+      pos_advance(pos, step_b, step_s, a.q_s);
+      pos_pair += stride;
+      return e;
+    } else {
+      p_ent = __builtin_amdgcn_readfirstlane(pend);
+      pend = take_pair(&sh.next_pair, lane);
+      return tok_entry<OM>(a, pair_pos(p_ent, a.q_s), p_ent < hi, l32);
+    }
   };
 
   // One unit: pair p from xc (this lane's pieces, loaded a unit ago), output row out_c of this
@@ -462,6 +499,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   u32x4 x[NX];
   float ssq = 0.0f;
   TokEntry ent = next_entry();
+  const int32_t p_first = p_ent;
   int32_t in0, out_c;
   unit_row<OM>(a, ent, in0, out_c);
   if constexpr (STREAM) {
@@ -484,29 +522,43 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     load_pieces<NV>(rx, in0, C, hh, x);
   }
   ent = next_entry();
-  // SG: the workgroup's trip count (from its first pair), the same for all eight waves.
-  const int64_t base0 = SG ? static_cast<int64_t>(team) * kWavesWg : first;
+  if constexpr (SG) {
+    // The workgroup's trip count (from its first pair), the same for all eight waves.
+    const int64_t base0 = static_cast<int64_t>(team) * kWavesWg;
 #pragma unroll 1
-  for (int64_t p0 = base0; p0 < n_pairs; p0 += stride) unit(p0 + (first - base0), x, ssq, ent, out_c);
+    for (int64_t p0 = base0; p0 < n_pairs; p0 += stride) unit(p0 + (first - base0), x, ssq, ent, out_c);
+  } else {
+    // ent holds the entries of the pair after the current one; the unit reads its rows and
+    // draws the next.
+    int32_t p = p_first;
+#pragma unroll 1
+    while (p < hi) {
+      const int32_t following = p_ent;
+      unit(p, x, ssq, ent, out_c);
+      p = following;
+    }
+  }
 }
 
 template <class Ty, int QC, bool SG>
 int launch_qc(const ResidentArgs& a, hipStream_t stream) {
-  // Two workgroups of four waves per CU (~67 KB of LDS each); whole teams of QC workgroups.
-  // SG: one workgroup of eight waves per CU (~138 KB), four pairs of both groups at a time.
+  // One workgroup of eight waves per CU.  Per-group workgroups (~89 KB of LDS): whole teams of
+  // QC workgroups, each team a contiguous pair range of at least eight pairs where the batch
+  // allows.  SG (~138 KB): four pairs of both groups at a time.
   const int32_t n_pairs = a.n_pairs;
-  const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWavesWg - 1) / kWavesWg;
   int64_t grid;
   if (SG) {
+    const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWavesWg - 1) / kWavesWg;
     grid = static_cast<int64_t>(device_cus());
     if (grid > teams_needed) grid = teams_needed;
   } else {
-    grid = static_cast<int64_t>(device_cus()) * 2;
+    const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + 7) / 8;
+    grid = static_cast<int64_t>(device_cus());
     if (grid / QC > teams_needed) grid = teams_needed * QC;
     grid -= grid % QC;
   }
   if (grid <= 0) return OW_OK;
-  const dim3 g(static_cast<unsigned>(grid)), b(SG ? 512 : 256);
+  const dim3 g(static_cast<unsigned>(grid)), b(512);
   if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   if (a.out_tok)
     hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false, SG>), g, b, 0, stream, a, n_pairs);
