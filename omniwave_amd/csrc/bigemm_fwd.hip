@@ -897,6 +897,55 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
   static_cast<uint16_t*>(p.packed)[idx] = Ty::from_f32(val);
 }
 
+// Second section for d = 64, rd = 128 (the 16-token wave kernel, bigemm_fwd_wave16.hip), after
+// the 32x32x16 fragments: per (q, chunk ec) 12 operands of v_mfma_f32_16x16x32 (64 lanes x 8),
+// K order kord16(j, h) = 16 (j / 4) + 4 h + j % 4 for lane l = 16 h + l16, slot j:
+//   BU'' (eb, s), BV'' (eb, s) for eb, s in {0, 1} (A operands): row e = 32 ec + 16 eb + l16,
+//                               channel 32 s + kord16(j, h)
+//   BO (cb), cb < 4 (B operand): channel 16 cb + l16, expanded index 32 ec + kord16(j, h)
+// (the rows of the kernel's 16x16 accumulators, so each accumulator pair is the next operand).
+template <class Ty>
+__global__ void __launch_bounds__(256) pack16_kernel(PackArgs p, int64_t base, int64_t n) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n) return;
+  constexpr int kD16 = 64, kRD16 = 128, kFrames = 12;
+  const int per_q = (kRD16 / 32) * kFrames * kFragElems;
+  const int q = static_cast<int>(idx / per_q);
+  int rem = static_cast<int>(idx - static_cast<int64_t>(q) * per_q);
+  const int ec = rem / (kFrames * kFragElems);
+  rem -= ec * kFrames * kFragElems;
+  const int fr = rem / kFragElems, e = rem % kFragElems;
+  const int lane = e / 8, j = e % 8;
+  const int l16 = lane & 15, h = lane >> 4;
+  const int k = 16 * (j / 4) + 4 * h + (j % 4);
+  float val;
+  if (fr < 8) {
+    const bool is_u = fr < 4;
+    const int eb = (fr & 3) >> 1, sk = fr & 1;
+    const int col = 32 * ec + 16 * eb + l16;  // expanded row
+    const int c = 32 * sk + k;                // channel of the group
+    const int64_t src = (static_cast<int64_t>(q) * kD16 + c) * kRD16 + col;
+    float w = 1.0f;
+    if (p.chan) {
+      const int gc = p.chan[q * kD16 + c];
+      w = (gc >= 0 && gc < p.channels) ? (p.norm_w ? p.norm_w[gc] : 1.0f) : 0.0f;
+    }
+    val = load_f32(is_u ? p.b_u : p.b_v, src, p.wdtype) * w * (is_u ? kNegLog2e : kNegLn2);
+  } else {
+    const int cb = fr - 8;
+    const int c = 16 * cb + l16;
+    const int ee = 32 * ec + k;
+    const int64_t src = (static_cast<int64_t>(q) * kRD16 + ee) * kD16 + c;
+    float w = 1.0f;
+    if (p.chan) {
+      const int gc = p.chan[q * kD16 + c];
+      w = (gc >= 0 && gc < p.channels) ? (p.gamma ? p.gamma[gc] : 1.0f) : 0.0f;
+    }
+    val = load_f32(p.b_o, src, p.wdtype) * w;
+  }
+  static_cast<uint16_t*>(p.packed)[base + idx] = Ty::from_f32(val);
+}
+
 // fp8 channel side: per-tensor scales, in three launches (f8_zero, f8_amax, f8_finalize).
 // f8_amax: absmax of the folded B_v'' over all channel groups, 8 values per thread, wave
 // maxima combined with atomic max on the (non-negative) float bits.
@@ -1024,6 +1073,10 @@ __global__ void __launch_bounds__(256) pack_f8_kernel(PackArgs p, const float* s
 int64_t packed_elems(int32_t q_c, int32_t d, int32_t rd) {
   const int64_t per_chunk = static_cast<int64_t>(2 * (d / 16) + 2 * (d / 32)) * kFragElems;
   return kHeadElems + static_cast<int64_t>(q_c) * (rd / 32) * per_chunk;
+}
+
+int64_t packed16_elems(int32_t q_c, int32_t d, int32_t rd) {
+  return d == 64 && rd == 128 ? static_cast<int64_t>(q_c) * 3 * d * rd : 0;
 }
 
 template <class Ty>
@@ -1163,8 +1216,8 @@ extern "C" {
 
 size_t ow_packed_weight_bytes(int32_t q_c, int32_t d, int32_t rd, int32_t compute_dtype) {
   if (q_c < 1 || d < 32 || rd < 32 || d % 32 || rd % 32) return 0;
-  const size_t elem = compute_dtype == OW_DTYPE_F32 ? 4 : 2;
-  return static_cast<size_t>(ow::packed_elems(q_c, d, rd)) * elem;
+  if (compute_dtype == OW_DTYPE_F32) return static_cast<size_t>(ow::packed_elems(q_c, d, rd)) * 4;
+  return static_cast<size_t>(ow::packed_elems(q_c, d, rd) + ow::packed16_elems(q_c, d, rd)) * 2;
 }
 
 size_t ow_fwd_workspace_bytes(const OwPlan* plan, int32_t batch, int32_t flags) {
@@ -1204,6 +1257,14 @@ int ow_pack_weights(const void* a_u, const void* a_v, const void* a_o, const voi
   else
     hipLaunchKernelGGL(ow::pack_kernel<ow::F16>, dim3(blocks), dim3(256), 0, s, p);
   if (int rc = ow::hip_status(hipGetLastError(), "pack_kernel launch")) return rc;
+  if (const int64_t n16 = ow::packed16_elems(q_c, d, rd)) {
+    const unsigned blocks16 = static_cast<unsigned>((n16 + 255) / 256);
+    if (compute_dtype == OW_DTYPE_BF16)
+      hipLaunchKernelGGL(ow::pack16_kernel<ow::BF16>, dim3(blocks16), dim3(256), 0, s, p, p.total, n16);
+    else
+      hipLaunchKernelGGL(ow::pack16_kernel<ow::F16>, dim3(blocks16), dim3(256), 0, s, p, p.total, n16);
+    if (int rc = ow::hip_status(hipGetLastError(), "pack16_kernel launch")) return rc;
+  }
   ow::clear_error();
   return OW_OK;
 }
@@ -1371,12 +1432,15 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.eps = eps;
     r.drop_scale = drop_scale;
     const int64_t x_elems = static_cast<int64_t>(batch) * n * c;
-    const bool wave = ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems);
-    if (wave && want_scales) {
+    const bool wave16 = ow::wave16_supported(d, rd, c, q_c, x_elems);
+    const bool wave = !wave16 && ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems);
+    if ((wave16 || wave) && want_scales) {
       r.rs_out = scale_out;
       *scale_written = 1;
     }
-    const int rc = wave ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s) : ow::launch_fwd_resident(r, dtype, s);
+    const int rc = wave16 ? ow::launch_fwd_wave16(r, plan->radix_level, dtype, s)
+                   : wave ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s)
+                          : ow::launch_fwd_resident(r, dtype, s);
     if (rc != OW_OK && scale_written) *scale_written = 0;
     if (rc == OW_OK) ow::clear_error();
     return rc;

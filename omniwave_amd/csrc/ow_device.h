@@ -80,6 +80,10 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
                                                      __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 mma16k32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  }
 };
 
 struct F16 {
@@ -108,6 +112,10 @@ struct F16 {
   static __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
                                                  __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16k32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
   }
 };
 
@@ -818,6 +826,10 @@ bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_
 // level 0, else (q_c = 2) the plan's interleaved groups (channels congruent to g + level mod 2).
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems);
 int launch_fwd_wave(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream);
+// 16-token-unit forward for d = 64, rd = 128, C = 128 (q_c = 2, contiguous or interleaved groups,
+// bigemm_fwd_wave16.hip); reads the packed weights' second section (packed16_elems).
+bool wave16_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
+int launch_fwd_wave16(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream);
 
 // fp32 path (bigemm_fwd_f32.hip): operand packing, RMSNorm row scales and the forward.
 int pack_weights_f32(const void* a_u, const void* a_v, const void* a_o, const void* b_u, const void* b_v,

@@ -54,7 +54,10 @@ def test_packed_weight_bytes() -> None:
     lib = _native.lib()
     # head (3 token-operand rows of 64 lanes x 8) + q_c * 3*d*rd elements, 2 bytes each
     assert lib.ow_packed_weight_bytes(4, 128, 256, _native.OW_DTYPE_BF16) == 2 * (1536 + 4 * 3 * 128 * 256)
-    assert lib.ow_packed_weight_bytes(2, 64, 128, _native.OW_DTYPE_F16) == 2 * (1536 + 2 * 3 * 64 * 128)
+    # d = 64, rd = 128: a second section of 16x16x32 fragments, the same element count again
+    assert lib.ow_packed_weight_bytes(2, 64, 128, _native.OW_DTYPE_F16) == 2 * (1536 + 2 * 2 * 3 * 64 * 128)
+    assert lib.ow_packed_weight_bytes(2, 64, 256, _native.OW_DTYPE_F16) == 2 * (1536 + 2 * 3 * 64 * 256)
+    assert lib.ow_packed_weight_bytes(2, 64, 128, _native.OW_DTYPE_F32) == 4 * (1536 + 2 * 3 * 64 * 128)
     assert lib.ow_packed_weight_bytes(0, 64, 128, _native.OW_DTYPE_F16) == 0
 
 
