@@ -1439,7 +1439,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
       *scale_written = 1;
     }
     const int rc = wave16 ? ow::launch_fwd_wave16(r, plan->radix_level, dtype, s)
-                   : wave ? ow::launch_fwd_wave(r, plan->radix_level, dtype, s)
+                   : wave ? ow::launch_fwd_wave(r, dtype, s)
                           : ow::launch_fwd_resident(r, dtype, s);
     if (rc != OW_OK && scale_written) *scale_written = 0;
     if (rc == OW_OK) ow::clear_error();

@@ -1,6 +1,6 @@
-// Persistent BiGEMM forward for d = 64, rd = 128 and C = q_c * 64 with q_c in {1, 2, 4} (the
-// 56x56x128 and 28x28x256 stages of OmniWeave-T), one (pair, channel group) unit per wave at a
-// time.
+// Persistent BiGEMM forward for d = 64, rd = 128 and contiguous channel groups with C = q_c * 64,
+// q_c in {1, 4} (the 28x28x256 stage of OmniWeave-T at radix level 0), one (pair, channel group)
+// unit per wave at a time.  q_c = 2 (56x56x128) takes bigemm_fwd_wave16.hip.
 //
 // Same math and operand packing as the other forward kernels (reference
 // omniweave/ops/reference.py:147-171; operand scheme in ow_device.h).  Organisation:
@@ -13,22 +13,15 @@
 //   * the q_c workgroups of a team (logical ids q_c m .. q_c m + q_c - 1, one per channel group,
 //     placed on one XCD) walk the same contiguous range of pairs, each wave drawing its next pair
 //     from its workgroup's LDS counter, so the two waves of a SIMD stay busy to the end whatever
-//     their issue priority; each wave reads its pair's whole rows (the
-//     RMSNorm statistics need all C channels) one pair ahead into registers, in the 32x32x16
-//     operand layout (lane = token, 8 channels per 16-byte piece), sums the squares with
-//     v_dot2_f32 and writes only its group's columns to its own LDS tile; the other group's
-//     wave reads the same rows, which its XCD's L2 serves;
-//   * rows come from the token table; group g is channels 64 g .. 64 g + 63 at radix level 0 or
-//     with one group, else (SG, q_c = 2) the channels res + 2 t, t < 64, res = (g + level) mod 2
-//     (omniweave/models/routing.py:107-121): the wave's row pieces go through v_perm_b32 to
-//     its group's elements (strided_pack), in order, so the tile and the math are the same;
+//     their issue priority (the hardware issues from the older wave first: under a fixed split
+//     one wave of each SIMD finished its share long before the other);
+//   * each wave reads its pair's whole rows (the RMSNorm statistics need all C channels) a pair
+//     ahead in the 32x32x16 operand layout (lane = token, 8 channels per 16-byte piece), at
+//     q_c = 4 in four batches of one group each during the chunk loop, sums the squares with
+//     v_dot2_f32 and writes only its group's columns to its own LDS tile; the other groups'
+//     waves read the same rows, which their XCD's L2 serves;
 //   * the residual round(x + round(delta)) is written into the tile, which the wave then stores
-//     as whole 16-byte row pieces.  SG: one workgroup of eight waves holds both groups' weights
-//     (96 KB) and computes four pairs at a time, waves w and w ^ 4 the two groups of one pair;
-//     after a workgroup barrier each of the two stores half of the pair's rows whole, the two
-//     tiles' columns interleaved with v_perm_b32.  (Each group storing its own columns as 2-byte
-//     elements cost ~8 us at 56x56x128 x 128 images, and ~11 us at q_c = 4, where four groups'
-//     weights do not fit one workgroup: the interleaved q_c = 4 groups take the resident kernel.)
+//     as whole 16-byte row pieces of its group's columns.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -46,18 +39,15 @@ constexpr int kNCH = kRD / 32;                // 32-row chunks of the expanded d
 constexpr int kFrCh = 2 * kKS + 2 * kMB;      // fragments per chunk (B_u'^T, B_v'^T, B_o)
 constexpr int kGroupFrags = kNCH * kFrCh;     // 48 fragments = 48 KB per channel group
 constexpr int kLdt = kD + 8;                  // tile row stride (elements)
-constexpr int kWavesWg = 4;
+constexpr int kWaves = 8;
 
-// NG channel groups' weights and NW waves' tiles: (1, 4) for the per-group workgroups, (2, 8) for
-// the interleaved q_c = 2 groups (SG), where one workgroup holds both groups of four pairs.
-template <int NG, int NW>
 struct WaveLds {
-  u32x4 w[NG * kGroupFrags][64];   // the groups' packed weights
+  u32x4 w[kGroupFrags][64];        // the group's packed weights
   u32x4 tok_ops[3][64];            // token-side operand rows A_u, A_v, A_o (read per unit)
-  uint16_t tile[NW][32 * kLdt];    // per wave: the pair's rows, group columns
-  float rsc[NW][32];               // per wave: RMSNorm scale of each token of the pair
-  int32_t rows[NW][32];            // per wave: output row of each token (-1: not stored)
-  int32_t next_pair;               // per-group workgroups: the next pair of the team's range
+  uint16_t tile[kWaves][32 * kLdt];  // per wave: the pair's rows, group columns
+  float rsc[kWaves][32];           // per wave: RMSNorm scale of each token of the pair
+  int32_t rows[kWaves][32];        // per wave: output row of each token (-1: not stored)
+  int32_t next_pair;               // the next pair of the team's range
 };
 
 // Logical workgroup id such that ids q_c m .. q_c m + q_c - 1 run on one XCD (workgroups are
@@ -76,20 +66,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tensor_rsrc(const void* p, uin
 }
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a byte offset past every buffer
 
-// Position of a pair's first token group 2 pair = b q_s + s (image b, group s of the image),
-// advanced along the wave's pair sequence with additions only.
+// Position of a pair's first token group 2 pair = b q_s + s (image b, group s of the image).
 struct PairPos {
   int32_t b, s;
 };
-
-__device__ __forceinline__ void pos_advance(PairPos& pos, int32_t step_b, int32_t step_s, int32_t q_s) {
-  pos.b += step_b;
-  pos.s += step_s;
-  if (pos.s >= q_s) {
-    pos.s -= q_s;
-    ++pos.b;
-  }
-}
 
 // Position of pair p (wave-uniform).
 __device__ __forceinline__ PairPos pair_pos(int32_t p, int32_t q_s) {
@@ -148,20 +128,6 @@ __device__ __forceinline__ void load_pieces(__amdgpu_buffer_rsrc_t rx, int32_t r
   for (int k = 0; k < NV; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * k, 0, 0);
 }
 
-// q_c = 2, contiguous groups: the row's two channel groups rotated so that group g comes first:
-// registers 4 b .. 4 b + 3 hold pieces 2 k + hh, k = 4 ((b + g) mod 2) .. + 3, so the group's own
-// pieces are always v[0..3] (g is uniform: only the load offsets depend on it).
-__device__ __forceinline__ void load_pieces_rot2(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh, int g,
-                                                 u32x4 (&v)[8]) {
-  const uint32_t base = row >= 0 ? static_cast<uint32_t>(row) * static_cast<uint32_t>(channels * 2) + 16u * hh
-                                 : kOutOfRange;
-  const uint32_t own = 128u * static_cast<uint32_t>(g), other = 128u - own;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + own + 32u * j, 0, 0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + other + 32u * j, 0, 0);
-}
-
 // Pieces 2 (k0 + k) + hh, k < 4, of this lane's token row (one channel group of a d = 64 row):
 // one batch of the streamed row read.
 __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t row, int channels, int hh, int k0,
@@ -172,8 +138,8 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rx, int32_t ro
   for (int k = 0; k < 4; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 32u * (k0 + k), 0, 0);
 }
 
-template <class Ty, int QC, bool OM, bool DROP, bool SG>
-__global__ void __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+template <class Ty, int QC, bool OM, bool DROP>
+__global__ void __attribute__((amdgpu_flat_work_group_size(64 * kWaves, 64 * kWaves), amdgpu_waves_per_eu(2, 2)))
 bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   constexpr int C = QC * kD;
   constexpr int NV = C / 16;  // row pieces per lane
@@ -182,48 +148,27 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   // being held whole (64 registers) for a unit.
   constexpr bool STREAM = QC == 4;
   constexpr int NX = STREAM ? 4 : NV;  // pieces carried from one unit to the next
-  // q_c = 2 with contiguous groups: rows loaded with the own group's pieces first.
-  constexpr bool ROT = QC == 2 && !SG;
-  static_assert(!SG || QC == 2, "interleaved channel groups: q_c = 2");
-  // SG: waves 0-3 take group 0 and waves 4-7 group 1 of the same four pairs (wave w and w ^ 4
-  // share a pair), so the pair's output rows are put together in LDS and stored whole; every
-  // wave walks a fixed pair sequence (the workgroup's barriers keep the eight in step).
-  // Otherwise the eight waves of a workgroup all take group g and draw their pairs one at a time
-  // from the team's contiguous range [lo, hi) through an LDS counter: the hardware issues from
-  // the older of a SIMD's two waves first, so under a fixed split one wave of each SIMD finishes
-  // its share long before the other and leaves the SIMD with one wave; drawn pairs keep both
-  // busy to the end.
-  constexpr int NG = SG ? 2 : 1, NW = 8;
-  __shared__ __attribute__((aligned(16))) WaveLds<NG, NW> sh;
+  __shared__ __attribute__((aligned(16))) WaveLds sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
-  const int lid = SG ? static_cast<int>(blockIdx.x) : wave_xcd_remap(blockIdx.x, gridDim.x);
-  const int g = SG ? wave >> 2 : lid % QC;
-  const int team = SG ? lid : lid / QC;
-  const int n_team = SG ? static_cast<int>(gridDim.x) : static_cast<int>(gridDim.x) / QC;
-  const int64_t stride = static_cast<int64_t>(n_team) * kWavesWg;
-  const int64_t first = static_cast<int64_t>(team) * kWavesWg + (wave & (kWavesWg - 1));
+  const int lid = wave_xcd_remap(blockIdx.x, gridDim.x);
+  const int g = lid % QC, team = lid / QC, n_team = static_cast<int>(gridDim.x) / QC;
   const int32_t lo = static_cast<int32_t>(static_cast<int64_t>(team) * n_pairs / n_team);
   const int32_t hi = static_cast<int32_t>(static_cast<int64_t>(team + 1) * n_pairs / n_team);
-  // SG: the group's first channel (its residue mod q_c), wave-uniform.
-  const int res = SG ? __builtin_amdgcn_readfirstlane(a.chan[g * kD]) & (QC - 1) : 0;
 
-  // The group's (SG: both groups') weights into LDS (1 KB per wave and copy), the token
-  // operands into registers.
+  // The group's weights into LDS (1 KB per wave and copy), the token operands into LDS.
   {
-    const uint16_t* src = a.packed + kHeadElems + static_cast<size_t>(SG ? 0 : g) * kGroupFrags * kFragElems;
-    for (int f = wave; f < NG * kGroupFrags; f += NW)
+    const uint16_t* src = a.packed + kHeadElems + static_cast<size_t>(g) * kGroupFrags * kFragElems;
+    for (int f = wave; f < kGroupFrags; f += kWaves)
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(f) * kFragElems + lane * 8),
           (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
   }
   if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
-  if (!SG && threadIdx.x == 0) sh.next_pair = lo;
+  if (threadIdx.x == 0) sh.next_pair = lo;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  // After the kernel's first workgroup barrier; SG: every wave of the workgroup runs the same
-  // number of units (the later barriers), those past the end on pad rows.
-  if (SG ? static_cast<int64_t>(team) * kWavesWg >= n_pairs : lo >= hi) return;
+  if (lo >= hi) return;
 
   uint16_t* tile = sh.tile[wave];
   float* rsc = sh.rsc[wave];
@@ -231,28 +176,13 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
   const uint32_t bytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * C * 2);
   const __amdgpu_buffer_rsrc_t rx = tensor_rsrc(a.x, bytes), ro = tensor_rsrc(a.out, bytes);
 
-  // The wave's pairs are first, first + stride, ...  `pos` is the position of the pair whose
-  // table entries are read next (two pairs ahead of the one computed).
-  const int32_t step_b = static_cast<int32_t>(2 * stride / a.q_s);
-  const int32_t step_s = static_cast<int32_t>(2 * stride - static_cast<int64_t>(step_b) * a.q_s);
-  PairPos pos{static_cast<int32_t>(2 * first / a.q_s), 0};
-  pos.s = static_cast<int32_t>(2 * first - static_cast<int64_t>(pos.b) * a.q_s);
-  int64_t pos_pair = first;
   // Drawn pairs: `pend` (lane 0) holds the index taken a unit before it is read; p_ent is the
   // pair whose table entries next_entry returned last.
-  int32_t pend = 0, p_ent = 0;
-  if constexpr (!SG) pend = take_pair(&sh.next_pair, lane);
+  int32_t pend = take_pair(&sh.next_pair, lane), p_ent = 0;
   auto next_entry = [&]() {
-    if constexpr (SG) {
-      const TokEntry e = tok_entry<OM>(a, pos, pos_pair < n_pairs, l32);
-      pos_advance(pos, step_b, step_s, a.q_s);
-      pos_pair += stride;
-      return e;
-    } else {
-      p_ent = __builtin_amdgcn_readfirstlane(pend);
-      pend = take_pair(&sh.next_pair, lane);
-      return tok_entry<OM>(a, pair_pos(p_ent, a.q_s), p_ent < hi, l32);
-    }
+    p_ent = __builtin_amdgcn_readfirstlane(pend);
+    pend = take_pair(&sh.next_pair, lane);
+    return tok_entry<OM>(a, pair_pos(p_ent, a.q_s), p_ent < hi, l32);
   };
 
   // One unit: pair p from xc (this lane's pieces, loaded a unit ago), output row out_c of this
@@ -269,17 +199,6 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     if (a.norm) {
       if constexpr (STREAM) {
         acc = ssq;
-      } else if constexpr (ROT) {
-        // The two groups' partial sums: with the rotated rows each group's waves add the same
-        // two values (in either order: the same fp32 sum).
-        float part[2] = {0.0f, 0.0f};
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) part[b] = Ty::dot2sq(xc[4 * b + k][e], part[b]);
-        acc = part[0] + part[1];
       } else {
 #pragma unroll
         for (int k = 0; k < NV; ++k)
@@ -288,17 +207,10 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
       }
       acc += __shfl_xor(acc, 32);
     }
-    // The group's columns into the tile; the row scale (0 for pad tokens) and output row.
-    if constexpr (SG) {
-      // piece 2 k + hh of the row holds group columns 8 k + 4 hh .. 8 k + 4 hh + 3.
+    // The group's columns into the tile (q_c = 1: the row; q_c = 4: the streamed batch of group
+    // g, xc[0..3]); the row scale (0 for pad tokens) and output row.
 #pragma unroll
-      for (int k = 0; k < NV; ++k) *reinterpret_cast<u32x2*>(&tile[l32 * kLdt + 8 * k + 4 * hh]) = strided_pack<4>(xc[k], res);
-    } else {
-      // q_c = 1, the streamed batch of group g (q_c = 4) or the rotated rows (q_c = 2): the
-      // group's pieces are xc[0..3].
-#pragma unroll
-      for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
-    }
+    for (int k = 0; k < 4; ++k) *reinterpret_cast<u32x4*>(&tile[l32 * kLdt + 16 * k + 8 * hh]) = xc[k];
     if (hh == 0) {
       const float sc = a.norm ? rms_scale<Ty>(acc / static_cast<float>(C), a.eps) : 1.0f;
       rsc[l32] = sc;
@@ -309,10 +221,8 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     }
     if constexpr (STREAM)
       ssq = 0.0f;  // the next pair's batches are read during the chunk loop
-    else if constexpr (ROT)
-      load_pieces_rot2(rx, in_n, C, hh, g, xc);  // the next pair, a unit ahead of its use
     else
-      load_pieces<NV>(rx, in_n, C, hh, xc);
+      load_pieces<NV>(rx, in_n, C, hh, xc);  // the next pair, a unit ahead of its use
     ent = next_entry();
     wave_lds_sync();
 
@@ -340,7 +250,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     // products.  The weight fragments come from LDS DEPTH reads ahead of their MFMAs
     // (lds_read_async: no compiler wait per read; lds_wait before each use).
     f32x16 W[kMB] = {};
-    const uint32_t wbase = lds_addr(&sh.w[SG ? g * kGroupFrags : 0][lane]);
+    const uint32_t wbase = lds_addr(&sh.w[0][lane]);
     constexpr int DEPTH = 4;
     u32x4 vb[4];  // streamed batch in flight
     auto step = [&](auto e_tag, f32x16& Un, f32x16& Vn, const f32x16& Uc, const f32x16& Vc) {
@@ -447,37 +357,7 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
     wave_lds_sync();
 
     // The tile's rows to memory: 32 rows x 8 pieces of the group's columns, 4 per lane; pad
-    // rows go past the buffer.  SG: after a workgroup barrier (the partner wave w ^ 4 has its
-    // group's columns of the same pair in its tile) wave w stores rows 16 g .. 16 g + 15 whole:
-    // lane (row 16 g + lane / 16 + 4 j, piece c = lane % 16) takes columns 4c .. 4c + 3 of the
-    // even-channel group's tile and of the odd one's and interleaves them into channels
-    // 8c .. 8c + 7 (v_perm_b32).
-    if constexpr (SG) {
-      __syncthreads();
-      const uint16_t* te = sh.tile[res == 0 ? wave : wave ^ 4];
-      const uint16_t* to = sh.tile[res == 0 ? wave ^ 4 : wave];
-      const int c = lane & 15;
-      u32x4 ov[4];
-      int32_t orow[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 16 * g + (lane >> 4) + 4 * j;
-        orow[j] = rows[r];
-        const u32x2 e = *reinterpret_cast<const u32x2*>(&te[r * kLdt + 4 * c]);
-        const u32x2 o = *reinterpret_cast<const u32x2*>(&to[r * kLdt + 4 * c]);
-        ov[j] = u32x4{__builtin_amdgcn_perm(o[0], e[0], 0x05040100u), __builtin_amdgcn_perm(o[0], e[0], 0x07060302u),
-                      __builtin_amdgcn_perm(o[1], e[1], 0x05040100u), __builtin_amdgcn_perm(o[1], e[1], 0x07060302u)};
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t rb = orow[j] >= 0 ? static_cast<uint32_t>(orow[j]) * static_cast<uint32_t>(C * 2) : kOutOfRange;
-        __builtin_amdgcn_raw_buffer_store_b128(ov[j], ro, rb + 16u * static_cast<uint32_t>(c), 0, 0);
-      }
-      // Both waves of the pair are done reading the tiles before the next unit writes them.
-      __syncthreads();
-      out_c = out_n;
-      return;
-    }
+    // rows go past the buffer.
     u32x4 ov[4];
     int32_t orow[4];
 #pragma unroll
@@ -516,81 +396,63 @@ bigemm_fwd_wave_kernel(ResidentArgs a, int32_t n_pairs) {
         for (int k = 0; k < 4; ++k) x[k] = v[k];
       }
     }
-  } else if constexpr (ROT) {
-    load_pieces_rot2(rx, in0, C, hh, g, x);
   } else {
     load_pieces<NV>(rx, in0, C, hh, x);
   }
   ent = next_entry();
-  if constexpr (SG) {
-    // The workgroup's trip count (from its first pair), the same for all eight waves.
-    const int64_t base0 = static_cast<int64_t>(team) * kWavesWg;
+  // ent holds the entries of the pair after the current one; the unit reads its rows and draws
+  // the next.
+  int32_t p = p_first;
 #pragma unroll 1
-    for (int64_t p0 = base0; p0 < n_pairs; p0 += stride) unit(p0 + (first - base0), x, ssq, ent, out_c);
-  } else {
-    // ent holds the entries of the pair after the current one; the unit reads its rows and
-    // draws the next.
-    int32_t p = p_first;
-#pragma unroll 1
-    while (p < hi) {
-      const int32_t following = p_ent;
-      unit(p, x, ssq, ent, out_c);
-      p = following;
-    }
+  while (p < hi) {
+    const int32_t following = p_ent;
+    unit(p, x, ssq, ent, out_c);
+    p = following;
   }
 }
 
-template <class Ty, int QC, bool SG>
+template <class Ty, int QC>
 int launch_qc(const ResidentArgs& a, hipStream_t stream) {
-  // One workgroup of eight waves per CU.  Per-group workgroups (~89 KB of LDS): whole teams of
-  // QC workgroups, each team a contiguous pair range of at least eight pairs where the batch
-  // allows.  SG (~138 KB): four pairs of both groups at a time.
+  // One workgroup of eight waves per CU (~89 KB of LDS): whole teams of QC workgroups, each team
+  // a contiguous pair range of at least eight pairs where the batch allows.
   const int32_t n_pairs = a.n_pairs;
-  int64_t grid;
-  if (SG) {
-    const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWavesWg - 1) / kWavesWg;
-    grid = static_cast<int64_t>(device_cus());
-    if (grid > teams_needed) grid = teams_needed;
-  } else {
-    const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + 7) / 8;
-    grid = static_cast<int64_t>(device_cus());
-    if (grid / QC > teams_needed) grid = teams_needed * QC;
-    grid -= grid % QC;
-  }
+  const int64_t teams_needed = (static_cast<int64_t>(n_pairs) + kWaves - 1) / kWaves;
+  int64_t grid = static_cast<int64_t>(device_cus());
+  if (grid / QC > teams_needed) grid = teams_needed * QC;
+  grid -= grid % QC;
   if (grid <= 0) return OW_OK;
-  const dim3 g(static_cast<unsigned>(grid)), b(512);
+  const dim3 g(static_cast<unsigned>(grid)), b(64 * kWaves);
   if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   if (a.out_tok)
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false, SG>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, true, false>), g, b, 0, stream, a, n_pairs);
   else if (a.drop_scale)
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, true, SG>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, true>), g, b, 0, stream, a, n_pairs);
   else
-    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, false, SG>), g, b, 0, stream, a, n_pairs);
+    hipLaunchKernelGGL((bigemm_fwd_wave_kernel<Ty, QC, false, false>), g, b, 0, stream, a, n_pairs);
   return hip_status(hipGetLastError(), "bigemm_fwd_wave_kernel launch");
 }
 
 template <class Ty>
-int launch_ty(const ResidentArgs& a, bool strided, hipStream_t stream) {
+int launch_ty(const ResidentArgs& a, hipStream_t stream) {
   switch (a.q_c) {
-    case 1: return launch_qc<Ty, 1, false>(a, stream);
-    case 2: return strided ? launch_qc<Ty, 2, true>(a, stream) : launch_qc<Ty, 2, false>(a, stream);
-    case 4: return launch_qc<Ty, 4, false>(a, stream);
-    default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 2, 4} (got %d)", a.q_c);
+    case 1: return launch_qc<Ty, 1>(a, stream);
+    case 4: return launch_qc<Ty, 4>(a, stream);
+    default: return fail(OW_ERR_UNSUPPORTED, "wave-unit forward needs q_c in {1, 4} (got %d)", a.q_c);
   }
 }
 
 }  // namespace
 
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems) {
-  // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.
-  return d == kD && rd == kRD && (q_c == 1 || q_c == 2 || (q_c == 4 && radix_level == 0)) && channels == q_c * kD &&
+  // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.  q_c = 2 runs on
+  // bigemm_fwd_wave16.hip; interleaved q_c = 4 groups (radix levels >= 1) on the resident kernel.
+  return d == kD && rd == kRD && (q_c == 1 || (q_c == 4 && radix_level == 0)) && channels == q_c * kD &&
          x_elems * 2 < (int64_t(1) << 31);
 }
 
-int launch_fwd_wave(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream) {
-  const bool strided = radix_level != 0 && a.q_c > 1;  // routing.py:107-121
-  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, strided, stream);
-  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, strided, stream);
+int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream) {
+  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, stream);
+  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, stream);
   return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
 }
 

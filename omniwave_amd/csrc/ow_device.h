@@ -825,7 +825,7 @@ bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_
 // d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2, 4}; channel groups in channel order at radix
 // level 0, else (q_c = 2) the plan's interleaved groups (channels congruent to g + level mod 2).
 bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems);
-int launch_fwd_wave(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream);
+int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
 // 16-token-unit forward for d = 64, rd = 128, C = 128 (q_c = 2, contiguous or interleaved groups,
 // bigemm_fwd_wave16.hip); reads the packed weights' second section (packed16_elems).
 bool wave16_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
