@@ -8,7 +8,7 @@ weights are resident in HBM before timing; a step is replayed from a HIP graph.
 
 Prints ONE JSON line.  ``value`` = algorithmic TFLOP/s of the whole step (cheapest
 association, F_tile = 6 g d (g + rd) per 16-token x d-channel tile, pad rows included);
-``roofline`` is for the kernel with the largest share of the step time; ``cpu_baseline`` is the
+``roofline`` is for the case with the largest cold-cache launch time; ``cpu_baseline`` is the
 oracle (the reference backend's algorithm, fp32, PyTorch on the host CPU) on a bounded sample.
 """
 

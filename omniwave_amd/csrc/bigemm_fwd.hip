@@ -1390,7 +1390,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   const int32_t mode = path.mode;
   float* scale = nullptr;
   // scale_out (ow_bigemm_fwd_scales): the row scales go to the caller's buffer where the launch
-  // forms them in one place (the statistics pass, or the wave kernel below).
+  // forms them in one place (the statistics pass, or the d = 64 wave kernels below).
   const bool want_scales = scale_out && norm && !out_rows;
   if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr, batch)) {
     if (want_scales) {

@@ -194,8 +194,8 @@ def test_backward_beyond_the_addressing_limit_runs_in_chunks() -> None:
         assert err <= 1e-6, f"{k}: chunked gradient != sum of the chunks (rel-L2 {err:.2e})"
 
 
-SCALE_CASES = [  # (B, H, W, C, d, route, level): the wave kernel, the statistics pass, neither
-    ("wave", (2, 56, 56, 128, 64, "shifted", 0)),
+SCALE_CASES = [  # (B, H, W, C, d, route, level): the 16-token kernel, the statistics pass, neither
+    ("wave16", (2, 56, 56, 128, 64, "shifted", 0)),
     ("statistics-pass", (2, 14, 14, 512, 128, "shifted", 0)),
     ("resident-fallback", (2, 28, 28, 256, 64, "radix", 1)),
 ]

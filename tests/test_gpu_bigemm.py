@@ -107,9 +107,10 @@ def test_fused_block_matches_oracle(stage, route, level, dtype) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_interleaved_groups_ragged_pairs(dtype) -> None:
-    """56x56x128-style interleaved channel groups (radix 1, q_c = 2, the wave kernel's eight-wave
-    workgroups of four pairs) on 5x9 tokens x 3 images: 9 token groups, 5 pairs (the last half
-    pad), so the second workgroup runs one live and three empty units through its barriers."""
+    """56x56x128-style interleaved channel groups (radix 1, q_c = 2, the 16-token kernel) on 5x9
+    tokens x 3 images: 9 units of 16 tokens (each image's last one 13 pad rows) for one
+    twelve-wave workgroup, so three waves draw no unit and leave, and pad rows read as zero and
+    store nowhere."""
     announce(f"interleaved q_c=2 ragged pairs 5x9x128 radix1 dtype={dtype} B=3 seed=5")
     plan, x, params, norm_w = make_case(3, 5, 9, 128, 64, "radix", 1, dtype, seed=5)
     assert plan.token_indices.shape[0] == 3 and plan.channel_indices.shape[0] == 2
@@ -124,9 +125,9 @@ def test_interleaved_groups_ragged_pairs(dtype) -> None:
 
 
 def test_fused_block_past_2gib_matches_small_batches() -> None:
-    """x of 56x56x128 bf16 rows past 2 GiB (2,676 images): the wave kernel's 32-bit offsets do not
-    reach, so the launch takes the resident kernel.  Images are independent, so the first and
-    last two images of the big batch must match the same images run as a batch of 2 (wave
+    """x of 56x56x128 bf16 rows past 2 GiB (2,676 images): the 16-token kernel's 32-bit offsets do
+    not reach, so the launch takes the resident kernel.  Images are independent, so the first and
+    last two images of the big batch must match the same images run as a batch of 2 (16-token
     kernel, checked against the oracle above) to bf16 rounding, and the oracle directly."""
     h, w, c, d = STAGES["s1"]
     b = 2676

@@ -34,8 +34,8 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 NAMES = ["a_u", "a_v", "a_o", "b_u", "b_v", "b_o", "gamma"]
 TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-3, torch.float32: 1e-4}
-CASES = [  # (H, W, C, d, route, level, dtype): wave kernel (contiguous and interleaved channel
-    # groups), resident kernel (interleaved q_c = 4), persistent / streamed kernels, fp32 kernel
+CASES = [  # (H, W, C, d, route, level, dtype): wave-unit kernel (S2 shifted), 16-token kernel
+    # (interleaved groups), resident kernel (interleaved q_c = 4), persistent / streamed kernels, fp32 kernel
     (28, 28, 256, 64, "shifted", 0, torch.bfloat16),
     (56, 56, 128, 64, "radix", 1, torch.bfloat16),
     (28, 28, 256, 64, "radix", 1, torch.bfloat16),
