@@ -1,25 +1,33 @@
-// Forward for d = 64, rd = 128, C = 128 (q_c = 2: the 56x56x128 stage of OmniWeave-T), with
-// contiguous channel groups or the interleaved groups of radix levels >= 1, on 16x16 MFMAs.
+// Forward for d = 64, rd = 128, C = 64 q_c with q_c in {2, 4} (the 56x56x128 and 28x28x256
+// stages of OmniWeave-T), with contiguous channel groups or the interleaved groups of radix
+// levels >= 1, on 16x16 MFMAs.
 //
 // Same math as the other forward kernels (reference omniweave/ops/reference.py:147-171, the
 // block's RMSNorm and residual omniweave/models/block.py:83-108); the folded operands are those
 // of ow_device.h (U' = -log2(e) w U, V' = -ln(2) w V, SiLU(U) V = U' V' / (1 + 2^U')).
 // Organisation:
-//   * a unit is one 16-token group of one image and BOTH channel groups: a wave reads the unit's
-//     16 rows once (256 bytes each, four rows per 16-byte-per-lane load, so every load is four
-//     whole rows), forms the RMSNorm scales from them and writes both groups' columns into its
-//     LDS tile, group-major (interleaved groups are split with v_perm_b32);
+//   * a unit is one 16-token group of one image and two channel groups (q_c = 2: both): a wave
+//     reads the unit's 16 rows once (four rows per 16-byte-per-lane load, so every load covers
+//     four whole rows, or their halves), forms the RMSNorm scales from them and writes its two
+//     groups' columns into its LDS tile, group-major (interleaved groups are split with
+//     v_perm_b32);
+//   * q_c = 4: the workgroups come in pairs on one XCD, blocks 16 m + x and 16 m + 8 + x (the
+//     dispatcher places block b on XCD b % 8), which walk the same unit range: half ph = 0 of the
+//     pair computes the groups of channels 0 .. 127 (contiguous) or of residues 0, 1 mod 4
+//     (interleaved), half 1 the others.  Each reads whole rows for the RMSNorm sums; the
+//     second read of a row comes from the XCD's L2.  Interleaved halves store 4-byte words
+//     (the two residues of a word are the half's two groups), one row per store instruction;
 //   * per group: the token side P^T = X^T (A diag r)^T on v_mfma_f32_16x16x16 (A operand by
 //     transposed LDS reads of the tile), the channel side on v_mfma_f32_16x16x32 over four
 //     32-row chunks of the expanded dimension (U'^T, V'^T, the gate, W += Z B_o), the output
 //     delta^T = W^T A_o^T on v_mfma_f32_16x16x16, lane = token, four consecutive channels per
 //     register quad; rounded, plus x, written back into the tile;
-//   * the tile's rows then leave as whole 16-byte row pieces (interleaved groups re-joined with
-//     v_perm_b32): four stores of four whole rows each;
+//   * the tile's rows then leave as 16-byte row pieces (q_c = 2 interleaved groups re-joined with
+//     v_perm_b32): four stores of four rows each;
 //   * the accumulator of each 16x16 product is, pair of accumulators by pair, the next product's
 //     operand: its rows 4h + i (h = lane / 16) are the K slots kord16(j, h) = 16 (j / 4) + 4h +
 //     j % 4 of the next 16x16x32 operand, the order the packed weights use (pack16_kernel);
-//   * twelve waves (three per SIMD) per CU, both groups' packed weights (96 KB) in LDS, units
+//   * twelve waves (three per SIMD) per CU, two groups' packed weights (96 KB) in LDS, units
 //     drawn one at a time from the workgroup's range through an LDS counter.
 #include <hip/hip_runtime.h>
 
@@ -32,16 +40,17 @@ namespace {
 
 constexpr int kD = 64;
 constexpr int kRD = 128;
-constexpr int kC = 2 * kD;              // 128 channels: two groups
+constexpr int kC = 2 * kD;              // tile width: the two groups a workgroup computes
 constexpr int kNCH = kRD / 32;          // 4 chunks of 32 expanded rows
 constexpr int kFr = 12;                 // 16x16x32 fragments per chunk: BU(eb, s) x4, BV(eb, s) x4, BO(cb) x4
 constexpr int kGroupFr = kNCH * kFr;    // 48 fragments (48 KB) per channel group
 constexpr int kWaves = 12;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMainElems = kHeadElems + 2 * kNCH * 12 * kFragElems;  // the 32x32x16 part before the second section
+// Elements of the packed weights' 32x32x16 part, before the second section.
+constexpr int main_elems(int q_c) { return kHeadElems + q_c * kNCH * 12 * kFragElems; }
 
 struct Wave16Lds {
-  u32x4 w[2 * kGroupFr][64];       // both groups' 16x16x32 fragments
+  u32x4 w[2 * kGroupFr][64];       // the two groups' 16x16x32 fragments
   u32x2 tok_ops[3][64];            // A_u, A_v, A_o: lane l holds A[l % 16][4 (l / 16) .. + 3]
   uint16_t tile[kWaves][16 * kC];  // per wave: the unit's 16 rows, group-major columns
   float rsc[kWaves][16];           // RMSNorm scale of each token of the unit
@@ -92,23 +101,42 @@ struct UnitEntry {
   int32_t tk, to, b;
 };
 
-template <class Ty, bool SG, bool OM, bool DROP>
+template <class Ty, int QC, bool SG, bool OM, bool DROP>
 __global__ void __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(3, 3)))
 bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
+  static_assert(QC == 2 || QC == 4, "two or four channel groups");
+  constexpr int kCT = QC * kD;  // channels of a row of x and out
   __shared__ __attribute__((aligned(16))) Wave16Lds sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 4, l16 = lane & 15;
-  const int32_t lo = static_cast<int32_t>(static_cast<int64_t>(blockIdx.x) * n_units / gridDim.x);
-  const int32_t hi = static_cast<int32_t>(static_cast<int64_t>(blockIdx.x + 1) * n_units / gridDim.x);
-  // Interleaved groups (group q = channels res_q + 2 t): the region holding the even channels.
-  const int q_even = SG ? (__builtin_amdgcn_readfirstlane(a.chan[0]) & 1) : 0;
+  // q_c = 4: half ph of the XCD pair (see above) and the pair's unit range rb of gridDim / 2.
+  const int ph = QC == 4 ? static_cast<int>((blockIdx.x >> 3) & 1) : 0;
+  const int64_t n_ranges = QC == 4 ? gridDim.x / 2 : gridDim.x;
+  const int64_t rb = QC == 4 ? ((blockIdx.x & 7) | ((blockIdx.x >> 4) << 3)) : blockIdx.x;
+  const int32_t lo = static_cast<int32_t>(rb * n_units / n_ranges);
+  const int32_t hi = static_cast<int32_t>((rb + 1) * n_units / n_ranges);
+  // q_c = 2 interleaved groups (group q = channels res_q + 2 t): the region holding the even channels.
+  const int q_even = (QC == 2 && SG) ? (__builtin_amdgcn_readfirstlane(a.chan[0]) & 1) : 0;
+  // The channel groups of the tile's two regions: q_c = 2 both, in order; q_c = 4 contiguous
+  // groups 2 ph, 2 ph + 1; q_c = 4 interleaved (group q = channels (rot + q) % 4 + 4 t) the
+  // groups of residues 2 ph and 2 ph + 1.
+  int q0 = 0;
+  if constexpr (QC == 4) {
+    const int rot = SG ? (__builtin_amdgcn_readfirstlane(a.chan[0]) & 3) : 0;
+    q0 = (2 * ph - rot) & 3;
+  }
+  const int q1 = QC == 4 ? ((q0 + 1) & 3) : 1;
 
   {
-    const uint16_t* src = a.packed + kMainElems;
-    for (int f = wave; f < 2 * kGroupFr; f += kWaves)
+    const uint16_t* src = a.packed + main_elems(QC);
+    for (int f = wave; f < 2 * kGroupFr; f += kWaves) {
+      const int q = f < kGroupFr ? q0 : q1;
+      const int ff = f < kGroupFr ? f : f - kGroupFr;
       __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(f) * kFragElems + lane * 8),
+          (const __attribute__((address_space(1))) void*)(src + static_cast<size_t>(q * kGroupFr + ff) * kFragElems +
+                                                          lane * 8),
           (__attribute__((address_space(3))) void*)(&sh.w[f][0]), 16, 0, 0);
+    }
   }
   if (wave < 3) {
     // The 32x32x16 head row of lane l16 + 32 (h & 1) holds A[l16][4 (h & 1) + 8 (j / 4) + j % 4].
@@ -121,15 +149,17 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
   if (lo >= hi) return;
 
   uint16_t* tile = sh.tile[wave];
-  const uint32_t bytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * kC * 2);
+  const uint32_t bytes = static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * kCT * 2);
   const __amdgpu_buffer_rsrc_t rx = tensor_rsrc16(a.x, bytes), ro = tensor_rsrc16(a.out, bytes);
 
-  // Drawn units: `pend` (lane 0) holds the index taken a unit before it is read.
-  int32_t pend = 0, u_ent = 0;
-  if (lane == 0) pend = __hip_atomic_fetch_add(&sh.next_unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  // Units are drawn one at a time, the next one while the current one's first group is computed
+  // (its rows are read during the second group): a wave holds at most one unit it has not
+  // started, so at the end of the range no wave sits on units that idle waves could take.
+  int32_t u_ent = 0;
   auto next_entry = [&]() {
-    u_ent = __builtin_amdgcn_readfirstlane(pend);
-    if (lane == 0) pend = __hip_atomic_fetch_add(&sh.next_unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int32_t t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(&sh.next_unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    u_ent = __builtin_amdgcn_readfirstlane(t);
     const int32_t b = u_ent / a.q_s, s = u_ent - b * a.q_s;  // s < q_s for any unit index
     UnitEntry e;
     e.b = u_ent < hi ? b : a.batch;
@@ -145,14 +175,17 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
     out = in;
     if (OM) out = (ok & (e.to >= 0) & (e.to < a.n_tok)) ? base + e.to : -1;
   };
-  // Rows of the unit whose token-l16 input row is `in`: load k holds token 4k + h, piece l16.
-  u32x4 xr[4];
+  // Rows of the unit whose token-l16 input row is `in`: load k holds token 4k + h, piece l16
+  // (q_c = 4: xr the piece of the 256-byte half at byte own_off, xo of the other half).
+  const uint32_t own_off = (QC == 4 && !SG) ? 256u * ph : 0u;
+  u32x4 xr[4], xo[QC == 4 ? 4 : 1];
   auto load_rows = [&](int32_t in) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int32_t row = __shfl(in, 4 * k + h, 16);
-      const uint32_t off = row >= 0 ? static_cast<uint32_t>(row) * (kC * 2u) + 16u * l16 : kOutOfRange;
-      xr[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+      const uint32_t off = row >= 0 ? static_cast<uint32_t>(row) * (kCT * 2u) + 16u * l16 : kOutOfRange;
+      xr[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + own_off, 0, 0);
+      if constexpr (QC == 4) xo[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off + (256u - own_off), 0, 0);
     }
   };
 
@@ -213,17 +246,15 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
     static_assert(kNCH == 4, "four chunks: the step sequence above");
   };
 
-  // Prologue: the first unit's entries and rows; the second unit's entries.
+  // Prologue: the first unit's entries and rows.
   UnitEntry ent = next_entry();
   int32_t u_cur = u_ent;
-  int32_t in_c, out_c;
+  int32_t in_c, out_c, in_n = -1, out_n = -1;
   unit_row(ent, in_c, out_c);
   load_rows(in_c);
-  ent = next_entry();
 
 #pragma unroll 1
   while (u_cur < hi) {
-    const int32_t u_following = u_ent;
     // RMSNorm scales of the unit's tokens 4k + h (every lane of row h holds the total).
     float sc[4];
 #pragma unroll
@@ -232,15 +263,32 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
       if (a.norm) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) part = Ty::dot2sq(xr[k][e], part);
+        if constexpr (QC == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part = Ty::dot2sq(xo[k][e], part);
+        }
         part = group_sum<16>(part);
       }
-      sc[k] = a.norm ? rms_scale<Ty>(part / static_cast<float>(kC), a.eps) : 1.0f;
+      sc[k] = a.norm ? rms_scale<Ty>(part / static_cast<float>(kCT), a.eps) : 1.0f;
     }
     // The rows into the tile, group-major; scales and output rows into LDS.
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int t = 4 * k + h;
-      if constexpr (SG) {
+      if constexpr (QC == 4 && SG) {
+        // Piece p (channels 8 p .. 8 p + 7): residue 2 ph + j holds channels 8 p + 2 ph + j and
+        // 8 p + 2 ph + j + 4, i.e. columns 2 p, 2 p + 1 of region j, the halves j of words ph and
+        // ph + 2.
+        int pl = l16;
+        asm volatile("" : "+v"(pl));
+        auto put = [&](const u32x4& v, int p) {
+          const uint32_t wl = ph ? v[1] : v[0], wh = ph ? v[3] : v[2];
+          *reinterpret_cast<uint32_t*>(&tile[toff(t, 2 * p)]) = __builtin_amdgcn_perm(wh, wl, 0x05040100u);
+          *reinterpret_cast<uint32_t*>(&tile[toff(t, 64 + 2 * p)]) = __builtin_amdgcn_perm(wh, wl, 0x07060302u);
+        };
+        put(xr[k], pl);
+        put(xo[k], 16 + pl);
+      } else if constexpr (SG) {
         *reinterpret_cast<u32x2*>(&tile[toff(t, 64 * q_even + 4 * l16)]) = strided_pack<4>(xr[k], 0);
         *reinterpret_cast<u32x2*>(&tile[toff(t, 64 * (q_even ^ 1) + 4 * l16)]) = strided_pack<4>(xr[k], 1);
       } else {
@@ -249,14 +297,10 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
       if (l16 == 0) sh.rsc[wave][t] = sc[k];
     }
     if (h == 0) sh.rows[wave][l16] = out_c;
-    // The next unit's rows (its entries were read a unit ago), then the entries of the one after.
-    int32_t in_n, out_n;
-    unit_row(ent, in_n, out_n);
-    load_rows(in_n);
-    ent = next_entry();
     wave_lds_sync();
-    // The row scales for the backward (out_c is the input row without an output-row table).
-    if (a.rs_out && h == 0 && out_c >= 0) a.rs_out[out_c] = sh.rsc[wave][l16];
+    // The row scales for the backward (out_c is the input row without an output-row table);
+    // q_c = 4: half 0 of the pair writes them.
+    if (a.rs_out && ph == 0 && h == 0 && out_c >= 0) a.rs_out[out_c] = sh.rsc[wave][l16];
 
     // Token-side operands: lane l holds (A diag r)^T column l16, rows 4h .. 4h + 3.
     const float4 r4 = *reinterpret_cast<const float4*>(&sh.rsc[wave][4 * h]);
@@ -286,6 +330,7 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
           Pv[sk] = join16<Ty>(pv[2 * sk], pv[2 * sk + 1]);
         }
       }
+      if (g == 0) ent = next_entry();  // the next unit, read during the first group's channel side
       channel_side(g);
       // delta^T block cb = W^T A_o^T (lane = token l16, channels 16 cb + 4h + i), rounded, times
       // the drop-path scale, plus x, back into the tile.
@@ -314,13 +359,34 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
         }
         *p = u32x2{v0, v1};
       }
+      if (g == 0) {  // the next unit's rows, read during the second group
+        unit_row(ent, in_n, out_n);
+        load_rows(in_n);
+      }
     }
 
-    // The tile's rows to memory: store k writes tokens 4k .. 4k + 3 whole (lane: token 4k + h,
-    // piece l16); pad rows go past the buffer.
+    // The tile's rows to memory; pad rows go past the buffer.
     wave_lds_sync();
+    if constexpr (QC == 4 && SG) {
+      // Store r writes row r's words of this half: lane l the residues 2 ph, 2 ph + 1 of
+      // channel block 4 l, i.e. columns l of both regions, at byte 8 l + 4 ph of the row.
+      // (The lane id passes through an empty asm, so that the compiler forms these addresses
+      // here instead of keeping 32 of them live across the loop.)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int32_t my_row = sh.rows[wave][ln & 15];
+#pragma unroll 2
+      for (int r = 0; r < 16; ++r) {
+        const int32_t orow = __builtin_amdgcn_readlane(my_row, r);
+        const uint32_t v = static_cast<uint32_t>(tile[toff(r, ln)]) |
+                           (static_cast<uint32_t>(tile[toff(r, 64 + ln)]) << 16);
+        const uint32_t off =
+            orow >= 0 ? static_cast<uint32_t>(orow) * (kCT * 2u) + 8u * ln + 4u * ph : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b32(v, ro, off, 0, 0);
+      }
+    }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < (QC == 4 && SG ? 0 : 4); ++k) {
       const int t = 4 * k + h;
       const int32_t orow = sh.rows[wave][t];
       u32x4 ov;
@@ -332,45 +398,62 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
       } else {
         ov = *reinterpret_cast<const u32x4*>(&tile[toff(t, 8 * l16)]);
       }
-      const uint32_t off = orow >= 0 ? static_cast<uint32_t>(orow) * (kC * 2u) + 16u * l16 : kOutOfRange;
+      const uint32_t off =
+          orow >= 0 ? static_cast<uint32_t>(orow) * (kCT * 2u) + own_off + 16u * l16 : kOutOfRange;
       __builtin_amdgcn_raw_buffer_store_b128(ov, ro, off, 0, 0);
     }
     // The next unit overwrites the tile and the tables: every lane's reads above are done.
     wave_lds_sync();
     out_c = out_n;
-    u_cur = u_following;
+    u_cur = u_ent;
   }
 }
 
-template <class Ty, bool SG>
+template <class Ty, int QC, bool SG>
 int launch_sg(const ResidentArgs& a, hipStream_t stream) {
   const int32_t n_units = static_cast<int32_t>(static_cast<int64_t>(a.batch) * a.q_s);
-  int64_t grid = static_cast<int64_t>(device_cus());
-  const int64_t want = (static_cast<int64_t>(n_units) + kWaves - 1) / kWaves;
-  if (grid > want) grid = want;
-  if (grid <= 0) return OW_OK;
+  const int64_t want = (static_cast<int64_t>(n_units) + kWaves - 1) / kWaves;  // unit ranges
+  if (want <= 0) return OW_OK;
+  int64_t grid;
+  if constexpr (QC == 4) {
+    // Ranges in multiples of 8 (one per XCD), each computed by two workgroups.
+    int64_t ranges = static_cast<int64_t>(device_cus()) / 16 * 8;
+    if (ranges > (want + 7) / 8 * 8) ranges = (want + 7) / 8 * 8;
+    if (ranges < 8) ranges = 8;
+    grid = 2 * ranges;
+  } else {
+    grid = static_cast<int64_t>(device_cus());
+    if (grid > want) grid = want;
+  }
   if (a.out_tok && a.drop_scale) return fail(OW_ERR_UNSUPPORTED, "an output-row table with a drop-path scale");
   const dim3 g(static_cast<unsigned>(grid)), b(kThreads);
   if (a.out_tok)
-    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, SG, true, false>), g, b, 0, stream, a, n_units);
+    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, QC, SG, true, false>), g, b, 0, stream, a, n_units);
   else if (a.drop_scale)
-    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, SG, false, true>), g, b, 0, stream, a, n_units);
+    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, QC, SG, false, true>), g, b, 0, stream, a, n_units);
   else
-    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, SG, false, false>), g, b, 0, stream, a, n_units);
+    hipLaunchKernelGGL((bigemm_fwd_wave16_kernel<Ty, QC, SG, false, false>), g, b, 0, stream, a, n_units);
   return hip_status(hipGetLastError(), "bigemm_fwd_wave16_kernel launch");
+}
+
+template <class Ty>
+int launch_ty(const ResidentArgs& a, bool interleaved, hipStream_t stream) {
+  if (a.q_c == 4) return interleaved ? launch_sg<Ty, 4, true>(a, stream) : launch_sg<Ty, 4, false>(a, stream);
+  return interleaved ? launch_sg<Ty, 2, true>(a, stream) : launch_sg<Ty, 2, false>(a, stream);
 }
 
 }  // namespace
 
 bool wave16_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems) {
   // Byte offsets are 32-bit and kOutOfRange (2^31) must lie past x and out.
-  return d == kD && rd == kRD && q_c == 2 && channels == kC && x_elems * 2 < (int64_t(1) << 31);
+  return d == kD && rd == kRD && (q_c == 2 || q_c == 4) && channels == q_c * kD && x_elems * 2 < (int64_t(1) << 31);
 }
 
 int launch_fwd_wave16(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream) {
-  const bool interleaved = radix_level != 0;  // routing.py:107-121: q_c = 2 groups alternate channels
-  if (dtype == OW_DTYPE_BF16) return interleaved ? launch_sg<BF16, true>(a, stream) : launch_sg<BF16, false>(a, stream);
-  if (dtype == OW_DTYPE_F16) return interleaved ? launch_sg<F16, true>(a, stream) : launch_sg<F16, false>(a, stream);
+  // routing.py:107-121: at radix levels >= 1 group q holds the channels of one residue mod q_c.
+  const bool interleaved = radix_level != 0;
+  if (dtype == OW_DTYPE_BF16) return launch_ty<BF16>(a, interleaved, stream);
+  if (dtype == OW_DTYPE_F16) return launch_ty<F16>(a, interleaved, stream);
   return fail(OW_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
 }
 
