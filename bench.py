@@ -60,7 +60,7 @@ def case_work(batch, h, w, c, d, rd=None, elem=2):
 def kernel_of(c: int, d: int, level: int = 0, rd: int | None = None) -> str:
     """HIP kernel(s) that carry a fused bf16 launch with 16-byte aligned rows (the dispatch rule of
     ow_bigemm_fwd): d=64/rd=128 with C = 128 or 256 (q_c in {2, 4}, contiguous or interleaved
-    groups) runs the 16-token-unit kernel, with q_c = 1 the one-pair-per-wave kernel; d=128/rd=256
+    groups) runs the 16-token-unit kernel, with q_c = 1 the resident-weight kernel; d=128/rd=256
     with contiguous groups runs the RMSNorm statistics kernel, then the persistent kernel, and with
     strided groups (q_c in {2, 4, 8}) the persistent kernel alone (it reads whole rows and forms
     the statistics itself); the rest runs the streamed tile kernel."""
@@ -71,7 +71,7 @@ def kernel_of(c: int, d: int, level: int = 0, rd: int | None = None) -> str:
         if q_c in (2, 4):
             return "bigemm_fwd_wave16_kernel"
         if q_c == 1:
-            return "bigemm_fwd_wave_kernel"
+            return "bigemm_fwd_resident_kernel"
     if d == 128 and rd == 256 and c == q_c * 128 and contiguous:
         return "rms_rows16_kernel+bigemm_fwd_persist_kernel"
     if d == 128 and rd == 256 and c == q_c * 128 and q_c in (2, 4, 8):

@@ -225,7 +225,7 @@ int ow_bigemm_fwd_chain(const void* x, void* out, float eps,
  * row scales r = 1 / sqrt(mean_c x^2 + eps) that the launch applied to the backward (the
  * reference's autograd keeps its normalised activations, omniweave/models/block.py:83-108, and
  * ow_bwd_rmsnorm / ow_bwd_fused_routed need r): where the launch forms every row's scale in one
- * place -- the statistics pass, or the d = 64 wave kernels -- it writes them to row_scale
+ * place -- the statistics pass, or the d = 64 16-token kernel -- it writes them to row_scale
  * ([batch * H * W] fp32, device) and sets *scales_written to 1; otherwise *scales_written is 0
  * and the caller forms them with ow_rms_scale.  Needs OW_FUSE_NORM for any scales to be written.
  */

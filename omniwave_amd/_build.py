@@ -19,7 +19,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libomniwave_amd.so"
-SOURCES = ["route.cpp", "bigemm_fwd.hip", "bigemm_fwd_resident.hip", "bigemm_fwd_wave.hip", "bigemm_fwd_wave16.hip", "bigemm_fwd_persist.hip", "bigemm_fwd_f32.hip", "bigemm_bwd.hip", "bigemm_bwd_f32.hip", "stem.hip", "fwd_noalloc.hip"]
+SOURCES = ["route.cpp", "bigemm_fwd.hip", "bigemm_fwd_resident.hip", "bigemm_fwd_wave16.hip", "bigemm_fwd_persist.hip", "bigemm_fwd_f32.hip", "bigemm_bwd.hip", "bigemm_bwd_f32.hip", "stem.hip", "fwd_noalloc.hip"]
 ARCH = "gfx950"
 
 

@@ -897,7 +897,7 @@ __global__ void __launch_bounds__(256) pack_kernel(PackArgs p) {
   static_cast<uint16_t*>(p.packed)[idx] = Ty::from_f32(val);
 }
 
-// Second section for d = 64, rd = 128 (the 16-token wave kernel, bigemm_fwd_wave16.hip), after
+// Second section for d = 64, rd = 128 (the 16-token kernel, bigemm_fwd_wave16.hip), after
 // the 32x32x16 fragments: per (q, chunk ec) 12 operands of v_mfma_f32_16x16x32 (64 lanes x 8),
 // K order kord16(j, h) = 16 (j / 4) + 4 h + j % 4 for lane l = 16 h + l16, slot j:
 //   BU'' (eb, s), BV'' (eb, s) for eb, s in {0, 1} (A operands): row e = 32 ec + 16 eb + l16,
@@ -1390,7 +1390,7 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
   const int32_t mode = path.mode;
   float* scale = nullptr;
   // scale_out (ow_bigemm_fwd_scales): the row scales go to the caller's buffer where the launch
-  // forms them in one place (the statistics pass, or the d = 64 wave kernels below).
+  // forms them in one place (the statistics pass, or the 16-token kernel below).
   const bool want_scales = scale_out && norm && !out_rows;
   if (ow::fwd_needs_scale_buffer(x, out, plan, rd, dtype, flags, stats_in != nullptr, batch)) {
     if (want_scales) {
@@ -1433,14 +1433,12 @@ static int bigemm_fwd_entry(const void* x, void* out, float eps, const void* pac
     r.drop_scale = drop_scale;
     const int64_t x_elems = static_cast<int64_t>(batch) * n * c;
     const bool wave16 = ow::wave16_supported(d, rd, c, q_c, x_elems);
-    const bool wave = !wave16 && ow::wave_supported(d, rd, c, q_c, plan->radix_level, x_elems);
-    if ((wave16 || wave) && want_scales) {
+    if (wave16 && want_scales) {
       r.rs_out = scale_out;
       *scale_written = 1;
     }
-    const int rc = wave16 ? ow::launch_fwd_wave16(r, plan->radix_level, dtype, s)
-                   : wave ? ow::launch_fwd_wave(r, dtype, s)
-                          : ow::launch_fwd_resident(r, dtype, s);
+    const int rc =
+        wave16 ? ow::launch_fwd_wave16(r, plan->radix_level, dtype, s) : ow::launch_fwd_resident(r, dtype, s);
     if (rc != OW_OK && scale_written) *scale_written = 0;
     if (rc == OW_OK) ow::clear_error();
     return rc;

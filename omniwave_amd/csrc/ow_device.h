@@ -766,7 +766,7 @@ struct ResidentArgs {
   int32_t residual; // write x + delta instead of delta
   float eps;
   const float* drop_scale;  // [batch] per-image multiplier of the rounded delta; NULL: none
-  float* rs_out;            // wave kernel: the RMSNorm scale of every input row it normalises; NULL: none
+  float* rs_out;            // 16-token kernel: the RMSNorm scale of every input row it normalises; NULL: none
 };
 
 bool resident_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c);
@@ -821,13 +821,9 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream);
 bool fwd_uses_persist(const void* x, const void* out, const OwPlan* plan, int32_t rd, int32_t dtype, int32_t flags,
                       int32_t batch);
 
-// One (pair, channel group) unit per wave, the group's weights in LDS (bigemm_fwd_wave.hip):
-// d = 64, rd = 128, C = q_c * 64 with q_c in {1, 2, 4}; channel groups in channel order at radix
-// level 0, else (q_c = 2) the plan's interleaved groups (channels congruent to g + level mod 2).
-bool wave_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int32_t radix_level, int64_t x_elems);
-int launch_fwd_wave(const ResidentArgs& a, int32_t dtype, hipStream_t stream);
-// 16-token-unit forward for d = 64, rd = 128, C = 128 (q_c = 2, contiguous or interleaved groups,
-// bigemm_fwd_wave16.hip); reads the packed weights' second section (packed16_elems).
+// 16-token-unit forward for d = 64, rd = 128, C = 64 q_c with q_c in {2, 4} (contiguous groups,
+// or the interleaved groups of radix levels >= 1; bigemm_fwd_wave16.hip); reads the packed
+// weights' second section (packed16_elems).
 bool wave16_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int64_t x_elems);
 int launch_fwd_wave16(const ResidentArgs& a, int32_t radix_level, int32_t dtype, hipStream_t stream);
 

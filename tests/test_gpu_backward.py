@@ -196,8 +196,9 @@ def test_backward_beyond_the_addressing_limit_runs_in_chunks() -> None:
 
 SCALE_CASES = [  # (B, H, W, C, d, route, level): the 16-token kernel, the statistics pass, neither
     ("wave16", (2, 56, 56, 128, 64, "shifted", 0)),
+    ("wave16-q4-interleaved", (2, 28, 28, 256, 64, "radix", 1)),
     ("statistics-pass", (2, 14, 14, 512, 128, "shifted", 0)),
-    ("resident-fallback", (2, 28, 28, 256, 64, "radix", 1)),
+    ("resident-fallback", (2, 16, 16, 64, 64, "shifted", 0)),
 ]
 
 

@@ -34,11 +34,12 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 NAMES = ["a_u", "a_v", "a_o", "b_u", "b_v", "b_o", "gamma"]
 TOL = {torch.bfloat16: 1e-2, torch.float16: 5e-3, torch.float32: 1e-4}
-CASES = [  # (H, W, C, d, route, level, dtype): wave-unit kernel (S2 shifted), 16-token kernel
-    # (interleaved groups), resident kernel (interleaved q_c = 4), persistent / streamed kernels, fp32 kernel
+CASES = [  # (H, W, C, d, route, level, dtype): 16-token kernel (contiguous q_c = 4, interleaved
+    # q_c = 2 and 4), resident kernel (q_c = 1), persistent / streamed kernels, fp32 kernel
     (28, 28, 256, 64, "shifted", 0, torch.bfloat16),
     (56, 56, 128, 64, "radix", 1, torch.bfloat16),
     (28, 28, 256, 64, "radix", 1, torch.bfloat16),
+    (16, 16, 64, 64, "shifted", 0, torch.bfloat16),
     (14, 14, 512, 128, "radix", 1, torch.bfloat16),
     (7, 7, 1024, 128, "local", 0, torch.float16),
     (14, 14, 512, 128, "local", 0, torch.float32),
