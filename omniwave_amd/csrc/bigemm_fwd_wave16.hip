@@ -255,22 +255,26 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
 
 #pragma unroll 1
   while (u_cur < hi) {
-    // RMSNorm scales of the unit's tokens 4k + h (every lane of row h holds the total).
-    float sc[4];
+    // RMSNorm scales of the unit's tokens: the sums of squares of rows 4k + h (every lane of
+    // row h holds the totals), then one scale per lane, for row 4 (l16 % 4) + h.
+    float part[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float part = 0.0f;
+      part[k] = 0.0f;
       if (a.norm) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) part = Ty::dot2sq(xr[k][e], part);
+        for (int e = 0; e < 4; ++e) part[k] = Ty::dot2sq(xr[k][e], part[k]);
         if constexpr (QC == 4) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) part = Ty::dot2sq(xo[k][e], part);
+          for (int e = 0; e < 4; ++e) part[k] = Ty::dot2sq(xo[k][e], part[k]);
         }
-        part = group_sum<16>(part);
+        part[k] = group_sum<16>(part[k]);
       }
-      sc[k] = a.norm ? rms_scale<Ty>(part / static_cast<float>(kCT), a.eps) : 1.0f;
     }
+    const int kq = l16 & 3;
+    const float mine = kq == 0 ? part[0] : kq == 1 ? part[1] : kq == 2 ? part[2] : part[3];
+    const float sc = a.norm ? rms_scale<Ty>(mine / static_cast<float>(kCT), a.eps) : 1.0f;
+    if (l16 < 4) sh.rsc[wave][4 * l16 + h] = sc;
     // The rows into the tile, group-major; scales and output rows into LDS.
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -294,7 +298,6 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
       } else {
         *reinterpret_cast<u32x4*>(&tile[toff(t, 8 * l16)]) = xr[k];
       }
-      if (l16 == 0) sh.rsc[wave][t] = sc[k];
     }
     if (h == 0) sh.rows[wave][l16] = out_c;
     wave_lds_sync();
