@@ -276,22 +276,39 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
     const float sc = a.norm ? rms_scale<Ty>(mine / static_cast<float>(kCT), a.eps) : 1.0f;
     if (l16 < 4) sh.rsc[wave][4 * l16 + h] = sc;
     // The rows into the tile, group-major; scales and output rows into LDS.
+    if constexpr (QC == 4 && SG) {
+      // Piece p (channels 8 p .. 8 p + 7): residue 2 ph + j holds channels 8 p + 2 ph + j and
+      // 8 p + 2 ph + j + 4, i.e. columns 2 p, 2 p + 1 of region j, the halves j of words ph and
+      // ph + 2.  Row t = 4 k + h: toff(t, 2 p) = 512 k + o[k % 2][p / 16], with the lane's four
+      // offsets o formed once (t & 7 = 4 (k % 2) + h); region 1 is 64 elements further.
+      int pl = l16;
+      asm volatile("" : "+v"(pl));
+      int o[2][2];
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) o[kp][j] = h * kC + ((((2 * (16 * j + pl)) >> 3) ^ (4 * kp + h)) << 3) + ((2 * pl) & 7);
+      // Word ph of a word pair by one v_perm_b32 (byte selector in a scalar register; a plain
+      // ph ? a : b would become a dynamic vector index and a chain of selects).
+      uint32_t wsel = ph ? 0x07060504u : 0x03020100u;
+      asm volatile("" : "+s"(wsel));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const u32x4& v = j == 0 ? xr[k] : xo[k];
+          const uint32_t wl = __builtin_amdgcn_perm(v[1], v[0], wsel), wh = __builtin_amdgcn_perm(v[3], v[2], wsel);
+          uint16_t* dst = tile + 4 * k * kC + o[k & 1][j];
+          *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(wh, wl, 0x05040100u);
+          *reinterpret_cast<uint32_t*>(dst + 64) = __builtin_amdgcn_perm(wh, wl, 0x07060302u);
+        }
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int t = 4 * k + h;
       if constexpr (QC == 4 && SG) {
-        // Piece p (channels 8 p .. 8 p + 7): residue 2 ph + j holds channels 8 p + 2 ph + j and
-        // 8 p + 2 ph + j + 4, i.e. columns 2 p, 2 p + 1 of region j, the halves j of words ph and
-        // ph + 2.
-        int pl = l16;
-        asm volatile("" : "+v"(pl));
-        auto put = [&](const u32x4& v, int p) {
-          const uint32_t wl = ph ? v[1] : v[0], wh = ph ? v[3] : v[2];
-          *reinterpret_cast<uint32_t*>(&tile[toff(t, 2 * p)]) = __builtin_amdgcn_perm(wh, wl, 0x05040100u);
-          *reinterpret_cast<uint32_t*>(&tile[toff(t, 64 + 2 * p)]) = __builtin_amdgcn_perm(wh, wl, 0x07060302u);
-        };
-        put(xr[k], pl);
-        put(xo[k], 16 + pl);
+        // (written above)
       } else if constexpr (SG) {
         *reinterpret_cast<u32x2*>(&tile[toff(t, 64 * q_even + 4 * l16)]) = strided_pack<4>(xr[k], 0);
         *reinterpret_cast<u32x2*>(&tile[toff(t, 64 * (q_even ^ 1) + 4 * l16)]) = strided_pack<4>(xr[k], 1);
@@ -378,13 +395,17 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
       const int32_t my_row = sh.rows[wave][ln & 15];
-#pragma unroll 2
+      // toff(r, ln) = 128 r + cb[r & 7], toff(r, 64 + ln) = toff(r, ln) + 64.
+      int cb[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) cb[m] = ((((ln >> 3) ^ m)) << 3) + (ln & 7);
+      const uint32_t vb = 8u * ln + 4u * ph;
+#pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int32_t orow = __builtin_amdgcn_readlane(my_row, r);
-        const uint32_t v = static_cast<uint32_t>(tile[toff(r, ln)]) |
-                           (static_cast<uint32_t>(tile[toff(r, 64 + ln)]) << 16);
-        const uint32_t off =
-            orow >= 0 ? static_cast<uint32_t>(orow) * (kCT * 2u) + 8u * ln + 4u * ph : kOutOfRange;
+        const uint16_t* tr = tile + r * kC + cb[r & 7];
+        const uint32_t v = static_cast<uint32_t>(tr[0]) | (static_cast<uint32_t>(tr[64]) << 16);
+        const uint32_t off = (orow >= 0 ? static_cast<uint32_t>(orow) * (kCT * 2u) : kOutOfRange) + vb;
         __builtin_amdgcn_raw_buffer_store_b32(v, ro, off, 0, 0);
       }
     }
