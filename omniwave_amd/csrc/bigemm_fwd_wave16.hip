@@ -255,24 +255,28 @@ bigemm_fwd_wave16_kernel(ResidentArgs a, int32_t n_units) {
 
 #pragma unroll 1
   while (u_cur < hi) {
-    // RMSNorm scales of the unit's tokens: the sums of squares of rows 4k + h (every lane of
-    // row h holds the totals), then one scale per lane, for row 4 (l16 % 4) + h.
-    float part[4];
+    // RMSNorm scales of the unit's tokens, one per lane: row 4 (l16 % 4) + h.  part[k] is the
+    // lane's partial sum of squares of row 4 k + h; a transposed reduction keeps, across lane
+    // bit 0 and then bit 1, the partials of the rows whose k matches the lane's bits, then adds
+    // the four quads of the 16-lane row (rotations by 4 and 8).
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.norm) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      part[k] = 0.0f;
-      if (a.norm) {
+      for (int k = 0; k < 4; ++k) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[k] = Ty::dot2sq(xr[k][e], part[k]);
         if constexpr (QC == 4) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) part[k] = Ty::dot2sq(xo[k][e], part[k]);
         }
-        part[k] = group_sum<16>(part[k]);
       }
     }
-    const int kq = l16 & 3;
-    const float mine = kq == 0 ? part[0] : kq == 1 ? part[1] : kq == 2 ? part[2] : part[3];
+    const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
+    const float q0 = (b0 ? part[1] : part[0]) + dpp_f32<0xb1, 0xf>(b0 ? part[0] : part[1]);  // quad_perm 1,0,3,2
+    const float q1 = (b0 ? part[3] : part[2]) + dpp_f32<0xb1, 0xf>(b0 ? part[2] : part[3]);
+    float mine = (b1 ? q1 : q0) + dpp_f32<0x4e, 0xf>(b1 ? q0 : q1);  // quad_perm 2,3,0,1
+    mine += dpp_f32<0x124, 0xf>(mine);  // row_ror:4
+    mine += dpp_f32<0x128, 0xf>(mine);  // row_ror:8
     const float sc = a.norm ? rms_scale<Ty>(mine / static_cast<float>(kCT), a.eps) : 1.0f;
     if (l16 < 4) sh.rsc[wave][4 * l16 + h] = sc;
     // The rows into the tile, group-major; scales and output rows into LDS.
