@@ -4,12 +4,14 @@
 //
 // Same math and operand packing as bigemm_fwd.hip (reference omniweave/ops/reference.py:147-171;
 // operand scheme in ow_device.h).  Organisation:
-//   * one workgroup of eight waves per CU (145 KB of LDS), persistent over units of 256 token
-//     rows (16 token groups: one 32-token pair per wave) x one channel group; unit u is row chunk
-//     u / q_c, channel group u % q_c, and workgroup b takes units b, b + grid, ...  With the grid
-//     a multiple of 8 (and q_c dividing 8) all units of workgroup b are of channel group b % q_c,
-//     and so are all units of its XCD (workgroups are dispatched round-robin over the 8 XCDs):
-//     an XCD's L2 holds the weights of one channel group;
+//   * one workgroup of eight waves per CU (149 KB of LDS), persistent over units of up to 8
+//     32-token pairs (256 token rows, one pair per wave) x one channel group.  With at most one
+//     unit per CU each workgroup runs one unit; with more, each channel group's pairs are split
+//     evenly over grid / q_c workgroups, which run their range as full units and one partial
+//     last unit whose waves without a pair compute nothing (so a tail of 2 pairs per CU runs
+//     one wave per SIMD instead of a last round of whole units on a quarter of the CUs).  With
+//     contiguous groups every workgroup of an XCD (dispatched round-robin over the 8 XCDs) is of
+//     one channel group, so an XCD's L2 holds one group's weights;
 //   * the eight waves share one stream of weight chunks (24 KB per 32-row chunk of the expanded
 //     dimension, three LDS buffers, copied global -> LDS with global_load_lds), with the chunk
 //     loop of bigemm_fwd.hip: chunk ec + 1's U'/V' products issued with chunk ec's gate values
@@ -116,8 +118,14 @@ struct TokLoad {
 // NS: 1 for contiguous channel groups (tile rows by DMA), else the channel stride of the
 // strided groups (q_c = NS; whole rows through registers, QW = NS pieces per lane and row, which
 // also give the RMSNorm scales; output by 2-byte stores).
+// Scheduling (a unit is up to 8 consecutive 32-token pairs of one channel group, pair p = token
+// groups 2p, 2p + 1): n_pairs == 0: one unit per workgroup, unit u = pairs 8 (u / q_c) .. + 7
+// of group u % q_c (the grid covers the n_units units); n_pairs < 0: the grid is a multiple of
+// 8 and of q_c, and workgroup b runs units b, b + grid, ...; n_pairs > 0: the same grid, and each
+// channel group's n_pairs pairs are split evenly over its grid / q_c workgroups, which run their
+// range as full units and one partial last unit.
 template <class Ty, bool F8, int NS>
-__global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units) {
+__global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units, int32_t n_pairs) {
   constexpr int QW = NS > 1 ? NS : 0;  // register-tile fetch width (0: DMA tile)
   constexpr int SNP = QW == 8 ? 1 : 2;  // register tiles: passes (4 rows each) per batch
   constexpr int CHU = F8 ? f8_chunk_units(kD) : kFrCh;      // 1 KB copy units per chunk
@@ -139,11 +147,54 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   const int64_t n_groups = static_cast<int64_t>(a.batch) * a.q_s;
   const bool tok_lds = a.q_s * kG <= kTokLds;  // token tables copied to LDS at the start
 
-  // Row l < 32 of this wave in unit u (lanes < 32): the token-table loads of meta_write.
-  auto meta_load = [&](int32_t u) {
+  // This workgroup's channel group qc and 32-token pairs [p_lo, p_hi).  Contiguous groups: all
+  // workgroups of an XCD (dispatched round-robin over the 8 XCDs) are of one group, so an XCD's
+  // L2 holds one group's weights.  Strided groups: the q_c workgroups of one pair range run on
+  // one XCD, so their whole-row reads and the 2-byte stores of their interleaved columns meet in
+  // one L2.
+  int qc;
+  int32_t p_lo, p_hi;
+  int32_t p_step = kWaves;  // pairs from one of the workgroup's units to the next
+  if (n_pairs <= 0) {
+    int32_t u = blockIdx.x;
+    if constexpr (QW > 0) {
+      const int nwg = gridDim.x, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+      const int per = nwg >> 3, rem = nwg & 7;
+      u = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+    }
+    if (u >= n_units) return;
+    qc = u % a.q_c;
+    p_lo = (u / a.q_c) * kWaves;
+    p_hi = p_lo + kWaves;
+    if (n_pairs < 0) {  // units u + j grid: the same group, pairs 8 grid / q_c further each
+      p_step = kWaves * static_cast<int32_t>(gridDim.x / a.q_c);
+      p_hi = (n_units / a.q_c) * kWaves;
+    }
+  } else {
+    const int nwg = gridDim.x, per = nwg >> 3, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    int k;
+    if (QW > 0 || 8 % a.q_c != 0) {  // (contiguous groups: only when q_c does not divide 8)
+      const int idx = QW > 0 ? xcd * per + slot : static_cast<int>(blockIdx.x);
+      qc = idx % a.q_c;
+      k = idx / a.q_c;
+    } else {
+      qc = xcd % a.q_c;
+      k = (xcd / a.q_c) * per + slot;
+    }
+    const int64_t wg = nwg / a.q_c;
+    p_lo = static_cast<int32_t>(k * static_cast<int64_t>(n_pairs) / wg);
+    p_hi = static_cast<int32_t>((k + 1) * static_cast<int64_t>(n_pairs) / wg);
+    if (p_lo >= p_hi) return;
+  }
+  // The group's first channel mod NS (its residue; strided groups).
+  const int res_g = NS > 1 ? (a.chan[qc * kD] & (NS - 1)) : 0;
+
+  // Row l < 32 of this wave in the unit of pairs p0 .. p0 + np - 1 (lanes < 32): the token-table
+  // loads of meta_write.  Waves past the unit's pairs get pad rows.
+  auto meta_load = [&](int32_t p0, int np) {
     TokLoad e{-1, -1, -1, 1.0f};
-    if (lane < 32) {
-      const int64_t tg = static_cast<int64_t>(u / a.q_c) * kGroups + 2 * wave + (lane >> 4);
+    if (lane < 32 && wave < np) {
+      const int64_t tg = 2 * (static_cast<int64_t>(p0) + wave) + (lane >> 4);
       if (tg < n_groups) {
         e.b = static_cast<int32_t>(tg / a.q_s);
         const int32_t sg = static_cast<int32_t>(tg - static_cast<int64_t>(e.b) * a.q_s);
@@ -197,10 +248,10 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       sh.rsc[s][32 * wave + lane] = r;
     }
   };
-  // This wave's 32 tile rows of unit u (slot s): copy k covers rows 4k .. 4k + 3, lane -> row
+  // This wave's 32 tile rows of slot s: copy k covers rows 4k .. 4k + 3, lane -> row
   // 4k + lane / 16, slot lane % 16, which holds the row's piece (lane % 16) ^ tile128_swz(row).
-  auto issue_tile = [&](int32_t u, int s) {
-    const uint32_t col0 = static_cast<uint32_t>((u % a.q_c) * kD * 2);
+  auto issue_tile = [&](int s) {
+    const uint32_t col0 = static_cast<uint32_t>(qc * kD * 2);
 #pragma unroll
     for (int k = 0; k < kTileOps; ++k) {
       const int r = 32 * wave + 4 * k + (lane >> 4);
@@ -211,8 +262,8 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       tile_copy(rx, voff, lds_addr(&sh.x[(32 * wave_u + 4 * k) * kD]));
     }
   };
-  auto issue_chunk = [&](int32_t u, int ec) {
-    const uint16_t* src = uniform_ptr(a.packed + HEAD + (static_cast<size_t>(u % a.q_c) * kNCH + ec) * CH_ELEMS);
+  auto issue_chunk = [&](int ec) {
+    const uint16_t* src = uniform_ptr(a.packed + HEAD + (static_cast<size_t>(qc) * kNCH + ec) * CH_ELEMS);
     uint16_t* dst = sh.w[ec % 3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
@@ -231,17 +282,6 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   };
   using E0 = std::integral_constant<int, 0>;
 
-  // Strided groups: the q_c units of a row chunk (consecutive logical ids) run on one XCD, so
-  // their whole-row reads and the 2-byte stores of their interleaved columns meet in one L2.
-  int32_t u = blockIdx.x;
-  if constexpr (QW > 0) {
-    const int nwg = gridDim.x, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    const int per = nwg >> 3, rem = nwg & 7;
-    u = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
-  }
-  if (u >= n_units) return;
-  // First channel of a group, mod NS (the group's residue) for unit u.
-  auto group_res = [&](int32_t uu) { return NS > 1 ? (a.chan[(uu % a.q_c) * kD] & (NS - 1)) : 0; };
   // Register tiles (QW > 0), one batch of passes p0 .. p0 + SNP - 1: tile_fetch issues the loads
   // of whole rows (16 lanes per row), tile_put writes the group's columns to the tile and, with
   // kNormInline, the rows' RMSNorm scales: sum of squares over the 16 lanes (DPP), the total in
@@ -250,9 +290,9 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   auto tile_fetch = [&](int ss, int p0, TileBatch& v) {
     if constexpr (QW > 0) strided_fetch<NS, SNP>(rx, &sh.rowid[ss][32 * wave], a.channels, lane, p0, v);
   };
-  auto tile_put = [&](int32_t uu, int ss, int p0, const TileBatch& v) {
+  auto tile_put = [&](int ss, int p0, const TileBatch& v) {
     if constexpr (QW > 0) {
-      strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, group_res(uu), p0, v);
+      strided_write<NS, SNP>(sh.x + 32 * wave * kD, lane, res_g, p0, v);
       if (a.norm == kNormInline) {
 #pragma unroll
           for (int p = 0; p < SNP; ++p) {
@@ -274,20 +314,21 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   // The whole register tile of unit uu, slot ss (after the unit's stores; batch 0 already
   // requested into va): each batch's loads go out before the previous batch is put (two batches
   // of registers in flight).
-  auto strided_tile = [&](int32_t uu, int ss, TileBatch& va) {
+  auto strided_tile = [&](int ss, TileBatch& va) {
     if constexpr (QW > 0) {
       TileBatch vb;
 #pragma unroll
       for (int p0 = 0; p0 < 8; p0 += 2 * SNP) {
         tile_fetch(ss, p0 + SNP, vb);
-        tile_put(uu, ss, p0, va);
+        tile_put(ss, p0, va);
         if (p0 + 2 * SNP < 8) tile_fetch(ss, p0 + 2 * SNP, va);
-        tile_put(uu, ss, p0 + SNP, vb);
+        tile_put(ss, p0 + SNP, vb);
       }
       wave_lds_sync();
     }
   };
   int s = 0;
+  int32_t pu = p_lo;  // the unit's first pair
   if (wave < 3) sh.tok_ops[wave][lane] = reinterpret_cast<const u32x4*>(a.packed)[wave * 64 + lane];
   if (tok_lds) {
     for (int i = threadIdx.x; i < a.q_s * kG; i += kThreads) {
@@ -297,35 +338,41 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   }
   __syncthreads();
   {
-    const int32_t id = meta_write(meta_load(u), 0);
-    if constexpr (QW == 0) issue_tile(u, 0);
-    issue_chunk(u, 0);
+    const int32_t id = meta_write(meta_load(pu, p_hi - pu < kWaves ? p_hi - pu : kWaves), 0);
+    if constexpr (QW == 0) issue_tile(0);
+    issue_chunk(0);
     TileBatch va0;
     tile_fetch(0, 0, va0);
-    strided_tile(u, 0, va0);
+    strided_tile(0, va0);
     stats_write(stats_load(id), id, 0);
     wave_lds_sync();
     wait_chunk(E0{});  // this wave's tile rows; chunk 0 may still be in flight
   }
 
 #pragma unroll 1
-  for (; u < n_units; u += gridDim.x, s ^= 1) {
+  for (; pu < p_hi; pu += p_step, s ^= 1) {
     asm volatile("" : "+v"(lane), "+v"(wave));
     hh = lane >> 5;
     l32 = lane & 31;
     lane16 = 16u * static_cast<uint32_t>(lane);
-    const int32_t un = u + static_cast<int32_t>(gridDim.x);
-    const bool has_next = un < n_units;
-    const int qc = u % a.q_c;
+    const int np = p_hi - pu < kWaves ? p_hi - pu : kWaves;  // the unit's pairs
+    const int32_t pn = pu + p_step;
+    const bool has_next = pn < p_hi;
+    const int np_next = p_hi - pn < kWaves ? p_hi - pn : kWaves;
+    // Strided groups: a wave with no pair in this unit (a partial last unit, or pad token groups
+    // only) copies its share of the weight chunks and meets the barriers, but computes nothing;
+    // such a unit is the last of the workgroup's range.  (Contiguous groups compute pad rows as
+    // zeros instead: the branches cost their chunk loop more than the idle waves give back.)
+    const bool act = NS == 1 || (wave_u < np && 2 * (static_cast<int64_t>(pu) + wave_u) < n_groups);
     TokLoad en{-1, -1, -1, 1.0f};
-    if (has_next) en = meta_load(un);  // consumed after the token side
+    if (has_next) en = meta_load(pn, np_next);  // consumed after the token side
 
     // Token side of this wave's pair (rows 32 wave .. + 31 of the tile).
     constexpr int KV = F8 ? kKS / 4 : kKS;
     using VOp = std::conditional_t<F8, u32x8, u32x4>;
     u32x4 Pu[kKS], xk[kKS / 2][2];
     VOp Pv[KV];
-    {
+    if (act) {
       // The token operands are read per unit from LDS rather than kept live through the loop.
       const u32x4 fAu = sh.tok_ops[0][lane];
       const u32x4 fAv = sh.tok_ops[1][lane];
@@ -358,8 +405,8 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // stay exact).
     wait_lds_dma();
     __syncthreads();
-    issue_chunk(u, 1);
-    issue_chunk(u, 2);
+    issue_chunk(1);
+    issue_chunk(2);
     float snext = 0.0f;
     if (has_next) snext = stats_load(id_next);
 
@@ -528,13 +575,15 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
         else
           wait_lds_dma();
         __syncthreads();
-        if (ec >= 1 && ec + 2 < kNCH) issue_chunk(u, ec + 2);
-        if constexpr (F8) {
-          stream8(std::true_type{}, std::true_type{}, ec + 1, ec, Un, Vn, Uc, Vc);
-        } else {
-          stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+        if (ec >= 1 && ec + 2 < kNCH) issue_chunk(ec + 2);
+        if (act) {
+          if constexpr (F8) {
+            stream8(std::true_type{}, std::true_type{}, ec + 1, ec, Un, Vn, Uc, Vc);
+          } else {
+            stream(Nu{}, No{}, base(ec + 1), bo, Un, Vn, Uc, Vc);
+          }
         }
-      } else {
+      } else if (act) {
         if constexpr (F8)
           stream8(std::false_type{}, std::true_type{}, ec, ec, Un, Vn, Uc, Vc);
         else
@@ -542,10 +591,12 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
       }
     };
     f32x16 Ua, Va, Ub = {}, Vb = {};
-    if constexpr (F8)
-      stream8(std::true_type{}, std::false_type{}, 0, 0, Ua, Va, Ub, Vb);
-    else
-      stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
+    if (act) {
+      if constexpr (F8)
+        stream8(std::true_type{}, std::false_type{}, 0, 0, Ua, Va, Ub, Vb);
+      else
+        stream(Nu{}, Zero{}, base(0), 0u, Ua, Va, Ub, Vb);
+    }
 #pragma unroll
     for (int ec = 0; ec < kNCH; ec += 2) {
       step(ec, Ua, Va, Ub, Vb);
@@ -557,6 +608,7 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // this unit's tile rows, read from LDS before the next unit's tile rows replace them.
     mfma_drain();
     __syncthreads();
+    if (act) {
     const int piece = lane & 15;
     const int64_t colq = static_cast<int64_t>(qc) * kD;
     const u32x4 fAo = sh.tok_ops[2][lane];
@@ -594,9 +646,8 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
     // (strided groups: fetched through registers after the stores).
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if constexpr (QW == 0) {
-      if (has_next) issue_tile(un, s ^ 1);
+      if (has_next) issue_tile(s ^ 1);
     }
-    const int res_u = group_res(u);
     const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(a.out, xbytes);
     const __amdgpu_buffer_rsrc_t rs =
         buffer_rsrc(a.stats_out, static_cast<uint32_t>(static_cast<int64_t>(a.batch) * a.n_tok * a.q_c * 4));
@@ -639,24 +690,27 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
           const int t = 64 * h + lane;
           const uint16_t v = st[rr * kLdo + t];
           const uint32_t ob = id >= 0 ? static_cast<uint32_t>(id) * static_cast<uint32_t>(a.channels * 2) +
-                                            2u * static_cast<uint32_t>(res_u + t * NS)
+                                            2u * static_cast<uint32_t>(res_g + t * NS)
                                       : kOffOut;
           __builtin_amdgcn_raw_buffer_store_b16(v, ro, ob, 0, 0);
         }
       }
     }
+    } else if constexpr (QW == 0) {
+      if (has_next) issue_tile(s ^ 1);
+    }
     if constexpr (QW > 0) {
       if (has_next) {
         TileBatch vpre;
         tile_fetch(s ^ 1, 0, vpre);
-        strided_tile(un, s ^ 1, vpre);
+        strided_tile(s ^ 1, vpre);
       }
     }
     if (has_next) {
       stats_write(snext, id_next, s ^ 1);
       wave_lds_sync();
       __syncthreads();  // every wave is done with its staging rows, which chunk 0 overwrites
-      issue_chunk(un, 0);
+      issue_chunk(0);
       // The next unit's tile rows have landed once at most this unit's stores (8 row pieces, 8
       // statistics values) and chunk 0's copies, all issued after them, are outstanding
       // (strided groups: the rows were written by this wave).
@@ -677,11 +731,11 @@ bool persist_supported(int32_t d, int32_t rd, int32_t channels, int32_t q_c, int
 }
 
 template <class Ty>
-void launch_stride(const PersistArgs& a, dim3 g, int32_t n, hipStream_t stream) {
+void launch_stride(const PersistArgs& a, dim3 g, int32_t n, int32_t n_pairs, hipStream_t stream) {
   auto go = [&](auto f8_tag, auto ns_tag) {
     constexpr bool F8 = decltype(f8_tag)::value;
     constexpr int NS = decltype(ns_tag)::value;
-    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<Ty, F8, NS>), g, dim3(kThreads), 0, stream, a, n);
+    hipLaunchKernelGGL((bigemm_fwd_persist_kernel<Ty, F8, NS>), g, dim3(kThreads), 0, stream, a, n, n_pairs);
   };
   auto by_ns = [&](auto f8_tag) {
     switch (a.stride) {
@@ -702,13 +756,22 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
   const int64_t units = chunks * a.q_c;
   if (units == 0) return OW_OK;
   if (units > 0x7fffffff) return fail(OW_ERR_UNSUPPORTED, "grid too large (%lld units)", (long long)units);
-  // One workgroup per CU; with more units than CUs a multiple of 8 (whole XCD rounds), so that
-  // every unit of a workgroup belongs to one channel group; with fewer, one unit per workgroup.
-  int64_t grid = device_cus();
-  if (grid >= units)
-    grid = units;
-  else if (grid >= 8)
-    grid -= grid % 8;
+  // With at most one unit per CU, one workgroup per unit.  With more, one workgroup per CU, the
+  // grid a multiple of 8 (whole XCD rounds) and of q_c.  Contiguous groups: whole units round
+  // robin (workgroup b, and so its XCD, keeps group b % q_c).  Strided groups: each group's
+  // pairs split evenly over its grid / q_c workgroups, so that the last round's 2-byte stores
+  // come from all 8 XCDs (at 416 units on 256 CUs, 14x14x512 batch 128, a round robin left the
+  // second round on 5 of them) and from partial units whose idle waves store nothing.
+  const int64_t cus = device_cus();
+  int64_t grid = units;
+  int32_t n_pairs = 0;
+  if (cus < units) {
+    int64_t m = 8;
+    while (m % a.q_c) m += 8;  // lcm(8, q_c)
+    grid = cus - cus % m;
+    if (grid < m) grid = m;
+    n_pairs = a.stride > 1 ? static_cast<int32_t>((static_cast<int64_t>(a.batch) * a.q_s + 1) / 2) : -1;
+  }
   const dim3 g(static_cast<unsigned>(grid));
   if (a.norm == kNormInline && a.stride == 1)
     return fail(OW_ERR_INVALID, "the persistent forward with contiguous groups takes precomputed row statistics");
@@ -719,9 +782,9 @@ int launch_fwd_persist(const PersistArgs& a, int32_t dtype, hipStream_t stream) 
     return fail(OW_ERR_UNSUPPORTED, "persistent forward: channel stride %d", a.stride);
   if (a.stride != 1 && a.stride != a.q_c) return fail(OW_ERR_INVALID, "strided groups need stride == q_c");
   if (dtype == OW_DTYPE_BF16)
-    launch_stride<BF16>(a, g, n, stream);
+    launch_stride<BF16>(a, g, n, n_pairs, stream);
   else
-    launch_stride<F16>(a, g, n, stream);
+    launch_stride<F16>(a, g, n, n_pairs, stream);
   return hip_status(hipGetLastError(), "bigemm_fwd_persist_kernel launch");
 }
 

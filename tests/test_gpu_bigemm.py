@@ -151,6 +151,35 @@ def test_fused_block_past_2gib_matches_small_batches() -> None:
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("stage,route,level,b,dtype", [
+    ("s3", "local", 0, 255, torch.bfloat16),
+    ("s3", "radix", 1, 256, torch.float16),
+    ("s4", "shifted", 0, 300, torch.bfloat16),
+    ("s4", "radix", 1, 300, torch.bfloat16),
+])
+def test_persistent_pair_ranges_match_small_batches(stage, route, level, b, dtype) -> None:
+    """d = 128 batches with more units than CUs: each channel group's 32-token pairs are split
+    evenly over the workgroups, which end on a partial unit (25-26 pairs per workgroup at
+    14x14x512 B = 255 / 256, 18-19 at 7x7x1024 B = 300; B = 255 has an odd token-group count, so
+    the last pair is half pad).  Every image must equal, bit for bit, the same images run in
+    batches of at most 64 (one unit per workgroup), and the first image the oracle."""
+    h, w, c, d = STAGES[stage]
+    announce(f"persistent pair ranges {stage} {route}{level} {dtype} B={b} seed=8")
+    plan, x, params, norm_w = make_case(b, h, w, c, d, route, level, dtype, seed=8)
+    dp = to_dev(params)
+    xd, nw = x.to(DEV), norm_w.to(DEV)
+    for residual in (False, True):
+        out = bigemm_block_hip(xd, nw, plan, **dp, residual=residual)
+        for i0 in range(0, b, 64):
+            sl = slice(i0, min(b, i0 + 64))
+            small = bigemm_block_hip(xd[sl].contiguous(), nw, plan, **dp, residual=residual)
+            assert torch.equal(out[sl], small), f"images {sl}, residual={residual}"
+        if not residual:
+            ref = oracle_delta(rmsnorm_reference(x[:1], norm_w), plan, params, dtype)
+            err = rel_l2(out[:1].cpu(), ref)
+            assert err <= TOL[dtype], f"rel-L2 {err:.3e} vs the oracle"
+
+
 def test_config1_shape_local_bf16() -> None:
     """x [8,14,14,512] ~ N(0,1), local route, g=16, d=128, A ~ N(0,1/16), B ~ N(0,1/fan_in), seed 0."""
     announce("config1 x[8,14,14,512] local bf16 seed=0")
