@@ -151,20 +151,25 @@ def test_fused_block_past_2gib_matches_small_batches() -> None:
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("stage,route,level,b,dtype", [
-    ("s3", "local", 0, 255, torch.bfloat16),
-    ("s3", "radix", 1, 256, torch.float16),
-    ("s4", "shifted", 0, 300, torch.bfloat16),
-    ("s4", "radix", 1, 300, torch.bfloat16),
-])
-def test_persistent_pair_ranges_match_small_batches(stage, route, level, b, dtype) -> None:
-    """d = 128 batches with more units than CUs: each channel group's 32-token pairs are split
-    evenly over the workgroups, which end on a partial unit (25-26 pairs per workgroup at
-    14x14x512 B = 255 / 256, 18-19 at 7x7x1024 B = 300; B = 255 has an odd token-group count, so
-    the last pair is half pad).  Every image must equal, bit for bit, the same images run in
-    batches of at most 64 (one unit per workgroup), and the first image the oracle."""
-    h, w, c, d = STAGES[stage]
-    announce(f"persistent pair ranges {stage} {route}{level} {dtype} B={b} seed=8")
+@pytest.mark.parametrize("shape,route,level,b,dtype", [
+    ((14, 14, 512, 128), "local", 0, 255, torch.bfloat16),
+    ((14, 14, 512, 128), "radix", 1, 256, torch.float16),
+    ((7, 7, 1024, 128), "shifted", 0, 300, torch.bfloat16),
+    ((7, 7, 1024, 128), "radix", 1, 300, torch.bfloat16),
+    ((14, 14, 384, 128), "local", 0, 128, torch.bfloat16),
+    ((14, 14, 128, 128), "shifted", 0, 400, torch.bfloat16),
+], ids=["s3-local-b255", "s3-radix1-b256-f16", "s4-shifted-b300", "s4-radix1-b300", "c384-local-b128",
+        "c128-shifted-b400"])
+def test_persistent_multi_round_matches_small_batches(shape, route, level, b, dtype) -> None:
+    """d = 128 batches with more units than CUs.  Strided groups: each channel group's 32-token
+    pairs are split evenly over the workgroups, which end on a partial unit (25-26 pairs per
+    workgroup at 14x14x512 B = 256, 18-19 at 7x7x1024 B = 300).  Contiguous groups: whole units
+    round robin over a grid that is a multiple of 8 and of q_c (q_c = 3 at C = 384: 240
+    workgroups; q_c = 1 at C = 128).  B = 255 has an odd token-group count, so the last pair is
+    half pad.  Every image must equal, bit for bit, the same images run in batches of at most 64
+    (one unit per workgroup), and the first image the oracle."""
+    h, w, c, d = shape
+    announce(f"persistent multi-round {h}x{w}x{c} {route}{level} {dtype} B={b} seed=8")
     plan, x, params, norm_w = make_case(b, h, w, c, d, route, level, dtype, seed=8)
     dp = to_dev(params)
     xd, nw = x.to(DEV), norm_w.to(DEV)
