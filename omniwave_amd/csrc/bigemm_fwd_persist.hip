@@ -6,12 +6,12 @@
 // operand scheme in ow_device.h).  Organisation:
 //   * one workgroup of eight waves per CU (149 KB of LDS), persistent over units of up to 8
 //     32-token pairs (256 token rows, one pair per wave) x one channel group.  With at most one
-//     unit per CU each workgroup runs one unit; with more, each channel group's pairs are split
-//     evenly over grid / q_c workgroups, which run their range as full units and one partial
-//     last unit whose waves without a pair compute nothing (so a tail of 2 pairs per CU runs
-//     one wave per SIMD instead of a last round of whole units on a quarter of the CUs).  With
-//     contiguous groups every workgroup of an XCD (dispatched round-robin over the 8 XCDs) is of
-//     one channel group, so an XCD's L2 holds one group's weights;
+//     unit per CU each workgroup runs one unit.  With more, contiguous groups take whole units
+//     round robin, and every workgroup of an XCD (dispatched round-robin over the 8 XCDs) keeps
+//     one channel group, so an XCD's L2 holds one group's weights; strided groups split each
+//     group's pairs evenly over grid / q_c workgroups, which run their range as full units and
+//     one partial last unit whose waves without a pair compute nothing, so that the last
+//     round's 2-byte stores come from every XCD;
 //   * the eight waves share one stream of weight chunks (24 KB per 32-row chunk of the expanded
 //     dimension, three LDS buffers, copied global -> LDS with global_load_lds), with the chunk
 //     loop of bigemm_fwd.hip: chunk ec + 1's U'/V' products issued with chunk ec's gate values
@@ -121,9 +121,9 @@ struct TokLoad {
 // Scheduling (a unit is up to 8 consecutive 32-token pairs of one channel group, pair p = token
 // groups 2p, 2p + 1): n_pairs == 0: one unit per workgroup, unit u = pairs 8 (u / q_c) .. + 7
 // of group u % q_c (the grid covers the n_units units); n_pairs < 0: the grid is a multiple of
-// 8 and of q_c, and workgroup b runs units b, b + grid, ...; n_pairs > 0: the same grid, and each
-// channel group's n_pairs pairs are split evenly over its grid / q_c workgroups, which run their
-// range as full units and one partial last unit.
+// 8 and of q_c, and workgroup b runs units b, b + grid, ... (contiguous groups); n_pairs > 0: the
+// same grid, and each channel group's n_pairs pairs are split evenly over its grid / q_c
+// workgroups, which run their range as full units and one partial last unit (strided groups).
 template <class Ty, bool F8, int NS>
 __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArgs a, int32_t n_units, int32_t n_pairs) {
   constexpr int QW = NS > 1 ? NS : 0;  // register-tile fetch width (0: DMA tile)
@@ -173,11 +173,11 @@ __global__ void __launch_bounds__(kThreads) bigemm_fwd_persist_kernel(PersistArg
   } else {
     const int nwg = gridDim.x, per = nwg >> 3, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     int k;
-    if (QW > 0 || 8 % a.q_c != 0) {  // (contiguous groups: only when q_c does not divide 8)
+    if (QW > 0 || 8 % a.q_c != 0) {
       const int idx = QW > 0 ? xcd * per + slot : static_cast<int>(blockIdx.x);
       qc = idx % a.q_c;
       k = idx / a.q_c;
-    } else {
+    } else {  // contiguous groups, q_c dividing 8: one group per XCD
       qc = xcd % a.q_c;
       k = (xcd / a.q_c) * per + slot;
     }
