@@ -279,6 +279,33 @@ def test_chain_consumer_matches_unchained_block(route, level, variant) -> None:
     assert _rel(got.cpu(), ref) <= tol
 
 
+@pytest.mark.parametrize("route,level", [("shifted", 0), ("radix", 1)])
+def test_chain_and_drop_path_multi_round_match_small_batches(route, level) -> None:
+    """14x14x512 at B = 256, the model's batch: 832 units on 256 CUs, so the persistent kernel
+    runs its multi-round schedules (whole units round robin for contiguous groups, each group's
+    pairs split evenly for strided ones).  The chained launch's output and per-group statistics,
+    a consumer's output given them, and a block with per-image drop-path scales must equal, bit
+    for bit, the same images run in batches of 64 (one unit per workgroup)."""
+    b, hw = 256, 14 * 14
+    announce(f"chain + drop path multi-round s3 {route}{level} bf16 B={b}")
+    plan0, x0, p0, nw0 = make_case(b, 14, 14, 512, 128, route, level, torch.bfloat16, seed=6)
+    plan, _, p, nw = make_case(1, 14, 14, 512, 128, route, level, torch.bfloat16, seed=7)
+    ds = torch.rand(b, generator=torch.Generator().manual_seed(8)).add_(0.5).to(DEV)
+    with torch.no_grad():
+        y, st = bigemm_block_chain_hip(x0, None, nw0, plan0, **p0)
+        z, st2 = bigemm_block_chain_hip(y, st, nw, plan, **p)
+        dr = bigemm_block_hip(x0, nw0, plan0, **p0, drop_scale=ds)
+        for i0 in range(0, b, 64):
+            sl, rows = slice(i0, i0 + 64), slice(i0 * hw, (i0 + 64) * hw)
+            ys, sts = bigemm_block_chain_hip(x0[sl].contiguous(), None, nw0, plan0, **p0)
+            zs, st2s = bigemm_block_chain_hip(ys, sts, nw, plan, **p)
+            drs = bigemm_block_hip(x0[sl].contiguous(), nw0, plan0, **p0, drop_scale=ds[sl].contiguous())
+            assert torch.equal(y[sl], ys) and torch.equal(st[rows], sts), f"producer, images {sl}"
+            assert torch.equal(z[sl], zs) and torch.equal(st2[rows], st2s), f"consumer, images {sl}"
+            assert torch.equal(dr[sl], drs), f"drop path, images {sl}"
+    torch.cuda.synchronize()
+
+
 def test_chain_s2d_consumer_and_resident_producer() -> None:
     """factor 2: the chained launch writes the space_to_depth layout and no statistics; a d = 64
     block (the resident kernel) takes no statistics and writes none."""
